@@ -1,0 +1,217 @@
+"""Benchmark of the attention hot path on one MI355X.
+
+A step is one forward pass of the headline workload, flash_attention bf16
+BHSD B=4 H=32 S=4096 D=128 causal (the configuration the metric is quoted
+on). The same run also times paged-KV decode fp16 (64 sequences, H=32, D=128,
+context ~ U{512..8192}, 16-token pages) and reports it under "paged_decode".
+Inputs are synthetic (seeded N(0,1)) and resident in HBM before timing.
+
+Prints ONE JSON line. Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+for _p in (REPO, os.path.join(REPO, "mlx-primitives_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+import torch  # noqa: E402
+
+import workloads as wl  # noqa: E402
+
+PEAK_BF16_TFLOPS = 2516.6   # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def time_steps(fn, steps: int, warmup: int):
+    """Warmup, then `steps` timed calls; returns (wall ms/step, mean event ms/call).
+
+    Events are recorded on torch's current stream, the stream the kernels are
+    launched on, around every call."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        starts[i].record()
+        fn()
+        ends[i].record()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / steps
+    ev = [s.elapsed_time(e) for s, e in zip(starts, ends)]
+    return wall_ms, sum(ev) / len(ev), min(ev)
+
+
+def blas_threads() -> int:
+    try:
+        from threadpoolctl import threadpool_info
+
+        n = [d.get("num_threads", 1) for d in threadpool_info() if d.get("user_api") == "blas"]
+        if n:
+            return int(max(n))
+    except Exception:
+        pass
+    return len(os.sched_getaffinity(0))
+
+
+def cpu_baseline_flash(cfg: dict, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                       budget_s: float) -> dict:
+    """The oracle's restatement of the reference's BHSD branch (dense masked
+    softmax, flash.py:172-192) in float32 on host cores, over whole heads of the
+    same workload until ~budget_s of CPU work."""
+    import numpy as np
+
+    from oracle import attention as oa
+
+    B, H, S, D = q.shape
+    scale = wl.default_scale(D)
+    heads_done, t_total = 0, 0.0
+    order = [(b, h) for b in range(B) for h in range(H)]
+    for b, h in order:
+        qs, ks, vs = (x[b:b + 1, h:h + 1].float().cpu().numpy() for x in (q, k, v))
+        t0 = time.perf_counter()
+        oa.dense_attention_bhsd(qs, ks, vs, scale, True)
+        t_total += time.perf_counter() - t0
+        heads_done += 1
+        if t_total >= budget_s:
+            break
+    flops = wl.flash_flops(1, heads_done, S, D, True)
+    return {"value": flops / t_total / 1e12, "unit": "TFLOP/s", "cores": blas_threads(),
+            "kind": "port",
+            "sample": f"{heads_done} of {B * H} (batch, head) pairs of the same workload, "
+                      f"oracle dense BHSD branch in float32 numpy, {t_total:.1f} s"}
+
+
+def cpu_baseline_paged(inp, cfg: dict, budget_s: float) -> dict:
+    """The oracle's paged decode (gather + dense masked softmax,
+    paged_attention.py:108-208) in float32 over whole sequences."""
+    from oracle import paged as op
+
+    lens = inp.context_lens.cpu()
+    tables = inp.block_tables.cpu().numpy()
+    t_total, nbytes, done = 0.0, 0.0, 0
+    for b in range(lens.numel()):
+        row = tables[b:b + 1]
+        used = row[row >= 0]
+        kp = inp.k_pool[torch.as_tensor(used, device=inp.k_pool.device).long()].float().cpu().numpy()
+        vp = inp.v_pool[torch.as_tensor(used, device=inp.v_pool.device).long()].float().cpu().numpy()
+        local = row.copy()
+        local[row >= 0] = range(len(used))
+        q = inp.q[b:b + 1].float().cpu().numpy()
+        t0 = time.perf_counter()
+        op.paged_attention_decode(q, kp, vp, local, lens[b:b + 1].numpy(),
+                                  wl.default_scale(cfg["D"]), inp.block_size)
+        t_total += time.perf_counter() - t0
+        nbytes += wl.paged_bytes(lens[b:b + 1], cfg["H"], cfg["D"], 2, row.shape[1])
+        done += 1
+        if t_total >= budget_s:
+            break
+    return {"value": nbytes / t_total / 1e9, "unit": "GB/s", "cores": blas_threads(),
+            "kind": "port",
+            "sample": f"{done} of {lens.numel()} sequences of the same workload, oracle paged "
+                      f"decode in float32 numpy, {t_total:.1f} s"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--cpu-budget", type=float, default=10.0,
+                    help="seconds of CPU work per baseline sample")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
+              "(this build has no multi-GPU path)", file=sys.stderr)
+        return 2
+
+    from mlx_primitives.attention import flash_attention
+    from mlx_primitives.cache import paged_attention
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    # ---- headline: causal flash fwd, bf16 BHSD B=4 H=32 S=4096 D=128 -------------
+    name = "flash_bf16_bhsd"
+    cfg = wl.CONFIGS[name]
+    q, k, v = wl.make_qkv(cfg, device=dev)
+    flops = wl.config_work(name)
+    step = lambda: flash_attention(q, k, v, causal=True, layout="BHSD")
+    log(f"[bench] {name}: warmup {args.warmup}, steps {args.steps}")
+    wall_ms, ev_ms, ev_min = time_steps(step, args.steps, args.warmup)
+    achieved = flops / (ev_ms * 1e-3) / 1e12
+    log(f"[bench] {name}: {wall_ms:.3f} ms/step wall, kernel {ev_ms:.3f} ms "
+        f"(min {ev_min:.3f}) -> {achieved:.1f} TFLOP/s")
+
+    # ---- paged decode, fp16 --------------------------------------------------------
+    pname = "paged_decode_fp16"
+    pcfg = wl.CONFIGS[pname]
+    pin = wl.make_paged(pcfg, device=dev)
+    pbytes = wl.config_work(pname, pin)
+    pstep = lambda: paged_attention(pin.q, pin.k_pool, pin.v_pool, pin.block_tables,
+                                    pin.context_lens, block_size=pin.block_size)
+    log(f"[bench] {pname}: warmup {args.warmup}, steps {args.steps}")
+    p_wall, p_ev, p_min = time_steps(pstep, args.steps, args.warmup)
+    p_gbs = pbytes / (p_ev * 1e-3) / 1e9
+    log(f"[bench] {pname}: {p_wall:.3f} ms/step wall, kernels {p_ev:.3f} ms -> {p_gbs:.1f} GB/s")
+
+    cpu = None
+    pcpu = None
+    if not args.no_cpu_baseline:
+        log("[bench] cpu baselines (oracle restatement on host cores)")
+        cpu = cpu_baseline_flash(cfg, q, k, v, args.cpu_budget)
+        pcpu = cpu_baseline_paged(pin, pcfg, args.cpu_budget)
+
+    result = {
+        "metric": "causal fwd TFLOP/s @S=4096,D=128 + paged-decode HBM GB/s, % of roofline",
+        "value": flops / (wall_ms * 1e-3) / 1e12,
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": wall_ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1), cast to bf16)",
+        "config": {"workload": "flash_attention fwd bf16 BHSD B=4 H=32 S=4096 D=128 causal, "
+                               "scale 1/sqrt(128)",
+                   "global_batch": cfg["B"], "seq_len": cfg["S"], "heads": cfg["H"],
+                   "head_dim": cfg["D"], "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": achieved / PEAK_BF16_TFLOPS, "traffic": None,
+                     "kernel": "fa_fwd16_kernel<128,64,4,bf16>",
+                     "flop_per_launch": flops, "launch_ms": ev_ms},
+        "cpu_baseline": cpu,
+        "paged_decode": {
+            "workload": "paged_attention decode fp16, 64 seqs, H=32, D=128, ctx~U{512..8192}, "
+                        "16-token pages, permuted block table",
+            "value": p_gbs, "unit": "GB/s", "ms_per_step": p_wall, "kernel_ms": p_ev,
+            "bytes_per_step": pbytes,
+            "roofline": {"bound": "hbm", "achieved": p_gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                         "frac": p_gbs / PEAK_HBM_GBS, "traffic": None},
+            "cpu_baseline": pcpu,
+        },
+    }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

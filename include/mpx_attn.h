@@ -1,0 +1,121 @@
+/*
+ * mpx_attn.h — C ABI of libmpx_attn.so, the MI355X (gfx950) attention hot path
+ * behind the mlx-primitives Python API.
+ *
+ * Every entry point:
+ *   - takes raw device pointers, element strides and sizes (no framework types);
+ *   - never allocates or frees device memory (the caller passes the workspace);
+ *   - launches asynchronously on the caller's HIP stream (`stream` is a
+ *     hipStream_t; NULL means the legacy default stream) and never synchronises;
+ *   - returns MPX_OK or a negative MPX_E* code, with a message readable through
+ *     mpx_last_error() on the calling thread.
+ *
+ * dtype codes: MPX_F32 (float), MPX_F16 (IEEE half), MPX_BF16 (bfloat16).
+ * Tensors are addressed through element strides in the logical order
+ * (batch, head, seq); the head dimension must be contiguous (stride 1).
+ */
+#ifndef MPX_ATTN_H
+#define MPX_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MPX_OK 0
+#define MPX_EINVAL (-1)       /* bad argument: the Python layer raises ValueError */
+#define MPX_EUNSUPPORTED (-2) /* valid but not implemented (e.g. head_dim > 128) */
+#define MPX_EHIP (-3)         /* a HIP launch/runtime call failed: RuntimeError */
+
+#define MPX_F32 0
+#define MPX_F16 1
+#define MPX_BF16 2
+
+/* Library version, (major << 16) | minor. */
+int mpx_version(void);
+
+/* Message describing the last failure on this thread ("" if none). */
+const char* mpx_last_error(void);
+
+/*
+ * Exact softmax attention forward, O = softmax(scale * Q K^T + mask) V, with
+ * the row sums normalised as O / (l + 1e-6) like the reference's tiled
+ * online-softmax path.
+ *
+ * Replaces (one entry serves all four reference entry points):
+ *   - flash_attention / FlashAttention  (mlx_primitives/attention/flash.py:52-254,
+ *     tiled path 257-316, BHSD dense branch 172-192, Metal kernel 319-476);
+ *   - sliding_window_attention / SlidingWindowAttention
+ *     (mlx_primitives/attention/sliding_window.py:227-313, tiled 363-511);
+ *   - chunked_cross_attention / ChunkedCrossAttention
+ *     (mlx_primitives/attention/chunked.py:43-169);
+ *   - the per-chunk kernel + merge (mlx_primitives/attention/_online_softmax.py:42-176).
+ *
+ * Shapes: Q (B, H, Sq, D), K and V (B, H, Sk, D), O (B, H, Sq, D) addressed by
+ * the *_strides arrays = {batch, head, seq} element strides, so BSHD and BHSD
+ * tensors are both passed without a transpose.
+ *
+ * Mask, with q and kv absolute positions (top-left aligned, kv <= q when causal):
+ *   causal != 0        -> kv <= q  (window_right is then ignored)
+ *   window_left  >= 0  -> kv >= q - window_left   (-1 = unbounded)
+ *   window_right >= 0  -> kv <= q + window_right  (-1 = unbounded)
+ * Sliding-window semantics of the reference (|q-kv| <= W, plus kv <= q when
+ * causal) are window_left = W with causal = 1, or window_left = window_right = W.
+ *
+ * Supported: D <= 128 (kernels are built for D in {32, 64, 128}; pass D as
+ * one of those, zero-padded by the caller otherwise), dtype f32/f16/bf16,
+ * 16-byte aligned base pointers and seq strides that are multiples of 8
+ * elements (4 for f32).
+ *
+ * workspace: device memory of at least mpx_attn_fwd_workspace_bytes(...) bytes
+ * for the same arguments (0 bytes means no workspace is needed, pass NULL).
+ */
+int mpx_attn_fwd(const void* q, const void* k, const void* v, void* o,
+                 const int64_t* q_strides, const int64_t* k_strides,
+                 const int64_t* v_strides, const int64_t* o_strides,
+                 int B, int H, int Sq, int Sk, int D, float scale, int causal,
+                 int window_left, int window_right, int dtype,
+                 void* workspace, size_t workspace_bytes, void* stream);
+
+/* Workspace needed by mpx_attn_fwd (split-KV partials for long KV / few q tiles). */
+size_t mpx_attn_fwd_workspace_bytes(int B, int H, int Sq, int Sk, int D, int causal,
+                                    int window_left, int window_right, int dtype);
+
+/*
+ * Paged-KV decode attention: one query token per sequence against the
+ * sequence's cached tokens, gathered through a block table.
+ *
+ * Replaces paged_attention(q, k_pool, v_pool, block_tables, context_lens, ...)
+ * with seq_q == 1 (mlx_primitives/cache/paged_attention.py:44-105 -> decode
+ * path 108-208), including the optional ALiBi bias (163-178).
+ *
+ *   q             (B, H, D) via q_strides = {batch, head}, D contiguous
+ *   k_pool/v_pool (num_blocks, block_size, H, D), contiguous
+ *   block_tables  int32 (B, max_blocks), row-major, -1 = no page
+ *   context_lens  int32 (B,)
+ *   alibi_slopes  float32 (H,) or NULL; bias = slope_h * (kv_pos - context_len)
+ *   o             (B, H, D) via o_strides
+ *
+ * Token t of sequence b is valid iff t < context_lens[b] and
+ * 0 <= block_tables[b, t / block_size] < num_blocks; the softmax runs over
+ * valid tokens only (exact, no epsilon). A sequence with no valid token gets
+ * NaN, as the reference's softmax over an all -inf row does.
+ */
+int mpx_paged_decode(const void* q, const void* k_pool, const void* v_pool,
+                     const int32_t* block_tables, const int32_t* context_lens,
+                     const float* alibi_slopes, void* o,
+                     const int64_t* q_strides, const int64_t* o_strides,
+                     int B, int H, int D, int num_blocks, int block_size, int max_blocks,
+                     float scale, int dtype, void* workspace, size_t workspace_bytes,
+                     void* stream);
+
+/* Workspace needed by mpx_paged_decode (per-partition (o, m, l) partials). */
+size_t mpx_paged_decode_workspace_bytes(int B, int H, int D, int block_size, int max_blocks);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MPX_ATTN_H */

@@ -1,0 +1,76 @@
+"""Build libmpx_attn.so (the gfx950 HIP kernels + C ABI) in-tree.
+
+Usage: python mlx-primitives_amd/build.py [--verbose]
+
+The library lands in mlx-primitives_amd/mlx_primitives/_lib/libmpx_attn.so,
+where the Python layer loads it with ctypes. Host-only compilation: no GPU is
+needed to build.
+"""
+
+from __future__ import annotations
+
+import argparse
+import os
+import shutil
+import subprocess
+import sys
+import tempfile
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+REPO = os.path.dirname(HERE)
+CSRC = os.path.join(HERE, "csrc")
+INCLUDE = os.path.join(REPO, "include")
+LIB_DIR = os.path.join(HERE, "mlx_primitives", "_lib")
+LIB_PATH = os.path.join(LIB_DIR, "libmpx_attn.so")
+
+SOURCES = ["abi.hip", "fa_fwd.hip", "paged_decode.hip"]
+ARCH = "gfx950"
+
+
+def hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and os.path.exists(cand):
+            return cand
+    raise RuntimeError("hipcc not found (ROCm is required to build libmpx_attn.so)")
+
+
+def compile_flags() -> list[str]:
+    return [
+        f"--offload-arch={ARCH}",
+        "-O3",
+        "-std=c++17",
+        "-fPIC",
+        "-shared",
+        "-I" + INCLUDE,
+        "-I" + CSRC,
+        # Packed fp32 VALU ops are kept out of the device code.
+        "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        "-Wno-unused-command-line-argument",
+    ]
+
+
+def build(verbose: bool = False) -> str:
+    os.makedirs(LIB_DIR, exist_ok=True)
+    srcs = [os.path.join(CSRC, s) for s in SOURCES]
+    fd, tmp = tempfile.mkstemp(prefix="libmpx_attn.", suffix=".so.tmp", dir=LIB_DIR)
+    os.close(fd)
+    cmd = [hipcc()] + compile_flags() + srcs + ["-o", tmp]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    noise = "is not a recognized feature for this target"
+    err = "\n".join(ln for ln in proc.stderr.splitlines() if noise not in ln)
+    if proc.returncode != 0:
+        os.unlink(tmp)
+        raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{err}")
+    if verbose and err.strip():
+        print(err, file=sys.stderr)
+    os.replace(tmp, LIB_PATH)
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--verbose", action="store_true")
+    args = ap.parse_args()
+    print(build(verbose=args.verbose))

@@ -1,0 +1,757 @@
+// Exact-softmax attention forward for gfx950 (MI355X): flash / sliding-window /
+// chunked-cross attention of mlx-primitives on MFMA.
+//
+// Algorithm: the reference's tiled online softmax
+// (mlx_primitives/attention/_online_softmax.py:42-176, attention/flash.py:257-316),
+// restated for CDNA4:
+//   * one workgroup = BM = 32*NW query rows of one (batch, head) and a range of
+//     KV tiles of BN keys; every wave owns 32 query rows;
+//   * scores are computed transposed, S^T = K Q^T, so that every lane holds 32
+//     scores of a single query row: the row max needs one exchange with lane^32
+//     and the row sum none until the end;
+//   * P^T (bf16/f16) produced in the MFMA accumulator layout is fed straight
+//     back as the B operand of O^T += V^T P^T; V is transposed once per tile
+//     when it is staged into LDS (shared by all waves), K rows are permuted so
+//     that each lane's P^T values are contiguous keys;
+//   * K/V tiles are double-buffered in LDS with one barrier per tile; the
+//     next tile's global loads are in flight while the current one computes;
+//   * masks are index arithmetic (causal, left/right window, Sk tail); whole
+//     tiles outside the mask are never visited (WG range) or skipped (wave);
+//   * softmax in base 2 with scale*log2(e) folded in; the running max is only
+//     moved when a row max grows by more than 2^8, so O is rarely rescaled;
+//   * long KV ranges are split across workgroups (split-KV); partial
+//     (O, m, l) are merged by fa_split_merge_kernel, the reference's
+//     online_softmax_merge.
+#include "mpx_common.h"
+
+#include <algorithm>
+#include <cmath>
+
+namespace mpx {
+
+struct FwdParams {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* o;
+  int64_t q_sb, q_sh, q_ss;
+  int64_t k_sb, k_sh, k_ss;
+  int64_t v_sb, v_sh, v_ss;
+  int64_t o_sb, o_sh, o_ss;
+  float* ws_o;   // split partials O: (splits, B, H, Sq, D) fp32, unnormalised
+  float* ws_ml;  // split partials (m, l): (splits, B, H, Sq, 2) fp32, m in log2 units
+  int B, H, Sq, Sk;
+  int win_left, win_right;  // -1 = unbounded
+  int n_qtiles, num_splits, tiles_per_split;
+  float c;  // |scale| * log2(e)
+  int neg;  // scale < 0: Q is negated on load (exact) and |scale| used
+};
+
+// Rescale threshold of the lazy running max, in log2 units.
+constexpr float kRescaleThreshold = 8.0f;
+
+// Work item of this workgroup. Consecutive workgroup ids are dealt round-robin
+// to the 8 XCDs; the remap gives every XCD a contiguous slice of the work so
+// the q-tiles of one (batch, head) share that XCD's L2 for their K/V reads.
+// Within a (batch, head) the q-tiles run longest (most KV tiles) first.
+struct WorkItem {
+  int b, h, qt, split;
+};
+
+__device__ __forceinline__ WorkItem decode_work(const FwdParams& p) {
+  const int L = blockIdx.x, N = gridDim.x;
+  const int w = (N & 7) == 0 ? (L & 7) * (N >> 3) + (L >> 3) : L;
+  const int per_bh = p.n_qtiles * p.num_splits;
+  const int bh = w / per_bh;
+  const int r = w - bh * per_bh;
+  const int qi = r / p.num_splits;
+  WorkItem wi;
+  wi.qt = p.n_qtiles - 1 - qi;
+  wi.split = r - qi * p.num_splits;
+  wi.b = bh / p.H;
+  wi.h = bh - wi.b * p.H;
+  return wi;
+}
+
+// KV tile range [t_begin, t_end) (tiles of BN keys from kv_lo) for query rows
+// [q0, q0 + BM).
+template <int BM, int BN>
+__device__ __forceinline__ void kv_range(const FwdParams& p, int q0, int split, int& kv_lo,
+                                         int& t_begin, int& t_end) {
+  const int q_last = min(q0 + BM, p.Sq) - 1;
+  int lo = p.win_left >= 0 ? max(0, q0 - p.win_left) : 0;
+  lo -= lo % BN;
+  const int hi = p.win_right >= 0 ? min(p.Sk, q_last + p.win_right + 1) : p.Sk;
+  const int n_tiles = hi > lo ? (hi - lo + BN - 1) / BN : 0;
+  kv_lo = lo;
+  t_begin = split * p.tiles_per_split;
+  t_end = min(n_tiles, t_begin + p.tiles_per_split);
+}
+
+__device__ __forceinline__ bool kv_valid(const FwdParams& p, int q, int kv) {
+  return kv < p.Sk && (p.win_right < 0 || kv <= q + p.win_right) &&
+         (p.win_left < 0 || kv >= q - p.win_left);
+}
+
+// Per-wave classification of the tile [kv0, kv0 + BN) for rows [qa, qb].
+template <int BN>
+__device__ __forceinline__ void classify_tile(const FwdParams& p, int kv0, int qa, int qb,
+                                              bool& skip, bool& full) {
+  skip = kv0 >= p.Sk || (p.win_right >= 0 && kv0 > qb + p.win_right) ||
+         (p.win_left >= 0 && kv0 + BN - 1 < qa - p.win_left);
+  full = kv0 + BN <= p.Sk && (p.win_right < 0 || kv0 + BN - 1 <= qa + p.win_right) &&
+         (p.win_left < 0 || kv0 >= qb - p.win_left);
+}
+
+// ---------------------------------------------------------------------------
+// bf16 / f16 kernel: 32x32x16 MFMA.
+//
+// MFMA 32x32 register layouts used below (lane = j + 32*g, j in [0,32)):
+//   A (32 x 16):  lane holds row j, 8 values of one k-group g;
+//   B (16 x 32):  lane holds column j, 8 values of k-group g (same k-groups as A);
+//   C (32 x 32):  element e of lane holds row 8*(e/4) + 4*g + e%4, column j.
+// S^T = K Q^T: A row i of key block nb is LDS key row 32*nb + swap23(i) (bits 2
+// and 3 of i exchanged); C element e then holds key 32*nb + 16*(e/8) + 8*g + e%8
+// of query j, so elements 8h..8h+7 are 8 consecutive keys: exactly the B operand
+// of the PV step over keys [16*(2nb+h), +16) with k-group g = keys +8g..+8g+7.
+// ---------------------------------------------------------------------------
+template <int D, int BN, int NW, bool BF16>
+__global__ __launch_bounds__(64 * NW) void fa_fwd16_kernel(FwdParams p) {
+  constexpr int BM = 32 * NW, NT = 64 * NW;
+  constexpr int KS = D + 8;   // K row stride (elements): 16-byte pad, conflict-free b128 reads
+  constexpr int VS = BN + 8;  // V^T row stride (elements)
+  constexpr int K_ELEMS = BN * KS, V_ELEMS = D * VS, STAGE = K_ELEMS + V_ELEMS;
+  constexpr int NB = BN / 32, NSL = BN / 16, NKS = D / 16, NDB = D / 32;
+  constexpr int CPR = D / 8;  // 16-byte chunks per row
+  constexpr int K_CHUNKS = BN * CPR;
+  constexpr int K_PER_T = (K_CHUNKS + NT - 1) / NT;
+  constexpr int V_UNITS = (BN / 4) * CPR;  // 4 keys x 8 dims per unit
+  constexpr int V_PER_T = (V_UNITS + NT - 1) / NT;
+  static_assert(D % 32 == 0 && BN % 32 == 0, "tile shape");
+
+  __shared__ __align__(16) uint16_t smem[2 * STAGE];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int j = lane & 31, g = lane >> 5;
+
+  const WorkItem wi = decode_work(p);
+  const int q0 = wi.qt * BM;
+  int kv_lo, t_begin, t_end;
+  kv_range<BM, BN>(p, q0, wi.split, kv_lo, t_begin, t_end);
+
+  const uint16_t* __restrict__ Qp = (const uint16_t*)p.q + wi.b * p.q_sb + wi.h * p.q_sh;
+  const uint16_t* __restrict__ Kp = (const uint16_t*)p.k + wi.b * p.k_sb + wi.h * p.k_sh;
+  const uint16_t* __restrict__ Vp = (const uint16_t*)p.v + wi.b * p.v_sb + wi.h * p.v_sh;
+
+  // Q^T as B operand, k-group g of 16-dim step ks = dims 16*ks + 8*g .. +8.
+  const int wq0 = q0 + wave * 32;
+  const int myq = wq0 + j;
+  u32x4 qreg[NKS];
+  if (myq < p.Sq) {
+    const u32x4* src = (const u32x4*)(Qp + (int64_t)myq * p.q_ss);
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) qreg[ks] = src[2 * ks + g];
+  } else {
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) qreg[ks] = (u32x4){0u, 0u, 0u, 0u};
+  }
+  if (p.neg) {
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) qreg[ks] ^= 0x80008000u;
+  }
+
+  u32x4 kbuf[K_PER_T];
+  u32x4 vbuf[V_PER_T * 4];
+
+  auto load_tile = [&](int kv0) {
+#pragma unroll
+    for (int i = 0; i < K_PER_T; ++i) {
+      const int c = tid + i * NT;
+      if (K_CHUNKS % NT == 0 || c < K_CHUNKS) {
+        const int row = c / CPR, col = c - (c / CPR) * CPR;
+        const int kv = kv0 + row;
+        kbuf[i] = kv < p.Sk ? *(const u32x4*)(Kp + (int64_t)kv * p.k_ss + col * 8)
+                            : (u32x4){0u, 0u, 0u, 0u};
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < V_PER_T; ++i) {
+      const int u = tid + i * NT;
+      if (V_UNITS % NT == 0 || u < V_UNITS) {
+        const int kq = u / CPR, dq = u - (u / CPR) * CPR;
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          const int kv = kv0 + 4 * kq + rr;
+          vbuf[4 * i + rr] = kv < p.Sk ? *(const u32x4*)(Vp + (int64_t)kv * p.v_ss + dq * 8)
+                                       : (u32x4){0u, 0u, 0u, 0u};
+        }
+      }
+    }
+  };
+
+  auto store_tile = [&](int stage) {
+    uint16_t* Ks = smem + stage * STAGE;
+    uint16_t* Vt = Ks + K_ELEMS;
+#pragma unroll
+    for (int i = 0; i < K_PER_T; ++i) {
+      const int c = tid + i * NT;
+      if (K_CHUNKS % NT == 0 || c < K_CHUNKS) {
+        const int row = c / CPR, col = c - (c / CPR) * CPR;
+        *(u32x4*)(Ks + row * KS + col * 8) = kbuf[i];
+      }
+    }
+    // V (4 keys x 8 dims) -> V^T (8 dims x 4 keys).
+#pragma unroll
+    for (int i = 0; i < V_PER_T; ++i) {
+      const int u = tid + i * NT;
+      if (V_UNITS % NT == 0 || u < V_UNITS) {
+        const int kq = u / CPR, dq = u - (u / CPR) * CPR;
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          const u32 r0 = vbuf[4 * i + 0][jj], r1 = vbuf[4 * i + 1][jj];
+          const u32 r2 = vbuf[4 * i + 2][jj], r3 = vbuf[4 * i + 3][jj];
+          const u32x2 lo = {(r0 & 0xffffu) | (r1 << 16), (r2 & 0xffffu) | (r3 << 16)};
+          const u32x2 hi = {(r0 >> 16) | (r1 & 0xffff0000u), (r2 >> 16) | (r3 & 0xffff0000u)};
+          const int d = dq * 8 + 2 * jj;
+          *(u32x2*)(Vt + d * VS + 4 * kq) = lo;
+          *(u32x2*)(Vt + (d + 1) * VS + 4 * kq) = hi;
+        }
+      }
+    }
+  };
+
+  f32x16 o[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) o[db] = (f32x16){};
+  float m_run = -INFINITY;  // reference point of o and l_run (log2 units)
+  float m_max = -INFINITY;  // true running max (log2 units)
+  float l_run = 0.f;        // this lane's half of the row sum
+  const float c = p.c;
+
+  const int krow_perm = (j & ~12) | ((j & 4) << 1) | ((j & 8) >> 1);
+
+  if (t_begin < t_end) {
+    load_tile(kv_lo + t_begin * BN);
+    store_tile(0);
+  }
+  __syncthreads();
+
+  for (int t = t_begin; t < t_end; ++t) {
+    const int stage = (t - t_begin) & 1;
+    const int kv0 = kv_lo + t * BN;
+    const bool has_next = t + 1 < t_end;
+    if (has_next) load_tile(kv0 + BN);
+
+    bool skip, full;
+    classify_tile<BN>(p, kv0, wq0, wq0 + 31, skip, full);
+    if (!skip) {
+      const uint16_t* Ks = smem + stage * STAGE;
+      const uint16_t* Vt = Ks + K_ELEMS;
+
+      f32x16 s[NB];
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        s[nb] = (f32x16){};
+        const u32x4* kp = (const u32x4*)(Ks + (nb * 32 + krow_perm) * KS) + g;
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) s[nb] = mfma32x32x16<BF16>(kp[2 * ks], qreg[ks], s[nb]);
+      }
+
+      if (!full) {
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            const int kv = kv0 + nb * 32 + 16 * (e >> 3) + 8 * g + (e & 7);
+            if (!kv_valid(p, myq, kv)) s[nb][e] = -INFINITY;
+          }
+      }
+
+      float mt = -INFINITY;
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) mt = fmaxf(mt, s[nb][e]);
+      mt = fmaxf(mt, xor32(mt)) * c;
+      m_max = fmaxf(m_max, mt);
+
+      if (__any(mt > m_run + kRescaleThreshold)) {
+        const float m_new = fmaxf(m_run, mt);
+        const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(m_run - m_new);
+        l_run *= alpha;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) o[db][e] *= alpha;
+        m_run = m_new;
+      }
+      const float msub = m_run == -INFINITY ? 0.f : m_run;
+
+      u32x4 pop[NSL];
+      float lsum = 0.f;
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+          for (int e2 = 0; e2 < 4; ++e2) {
+            const float x0 = fast_exp2(s[nb][8 * hh + 2 * e2] * c - msub);
+            const float x1 = fast_exp2(s[nb][8 * hh + 2 * e2 + 1] * c - msub);
+            lsum += x0 + x1;
+            pop[2 * nb + hh][e2] = pack2<BF16>(x0, x1);
+          }
+      l_run += lsum;
+
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) {
+        const u32x4* vp = (const u32x4*)(Vt + (db * 32 + j) * VS) + g;
+#pragma unroll
+        for (int sl = 0; sl < NSL; ++sl) o[db] = mfma32x32x16<BF16>(vp[2 * sl], pop[sl], o[db]);
+      }
+    }
+
+    if (has_next) store_tile(stage ^ 1);
+    __syncthreads();
+  }
+
+  // Epilogue: move o and l to the true max, then normalise (or emit partials).
+  const float l_tot = l_run + xor32(l_run);
+  const float f = m_max == -INFINITY ? 0.f : fast_exp2(m_run - m_max);
+  if (p.num_splits == 1) {
+    if (myq < p.Sq) {
+      const float inv = m_max == -INFINITY ? 0.f : f / (l_tot * f + kSoftmaxEps);
+      uint16_t* Op = (uint16_t*)p.o + wi.b * p.o_sb + wi.h * p.o_sh + (int64_t)myq * p.o_ss;
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int e4 = 0; e4 < 4; ++e4) {
+          const int d = db * 32 + 8 * e4 + 4 * g;
+          const u32x2 val = {pack2<BF16>(o[db][4 * e4] * inv, o[db][4 * e4 + 1] * inv),
+                             pack2<BF16>(o[db][4 * e4 + 2] * inv, o[db][4 * e4 + 3] * inv)};
+          *(u32x2*)(Op + d) = val;
+        }
+    }
+  } else if (myq < p.Sq) {
+    const int64_t row = (((int64_t)wi.split * p.B + wi.b) * p.H + wi.h) * p.Sq + myq;
+    float* wo = p.ws_o + row * D;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int e4 = 0; e4 < 4; ++e4) {
+        const int d = db * 32 + 8 * e4 + 4 * g;
+        *(f32x4*)(wo + d) = (f32x4){o[db][4 * e4] * f, o[db][4 * e4 + 1] * f,
+                                    o[db][4 * e4 + 2] * f, o[db][4 * e4 + 3] * f};
+      }
+    if (g == 0) {
+      p.ws_ml[2 * row] = m_max;
+      p.ws_ml[2 * row + 1] = l_tot * f;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// fp32 kernel: 32x32x2 f32 MFMA (true fp32 products, for fp32 parity).
+// S^T = K Q^T with k index (4-dim run) dims 8*(ks/4) + 4*g + ks%4; C element e
+// of lane (j, g) holds key 32*nb + 8*(e/4) + 4*g + e%4. PV step (nb, e) has
+// k = g <-> that key, so P^T needs no repacking and V stays row-major in LDS.
+// ---------------------------------------------------------------------------
+template <int D, int BN, int NW>
+__global__ __launch_bounds__(64 * NW) void fa_fwd32_kernel(FwdParams p) {
+  constexpr int BM = 32 * NW, NT = 64 * NW;
+  constexpr int KS = D + 4;  // conflict-free 16-byte reads along rows
+  constexpr int VS = D + 8;  // rows kv and kv+4 land on opposite bank halves
+  constexpr int K_ELEMS = BN * KS, V_ELEMS = BN * VS, STAGE = K_ELEMS + V_ELEMS;
+  constexpr int NB = BN / 32, NDB = D / 32, NQ4 = D / 8;
+  constexpr int CPR = D / 4;  // 16-byte chunks per row
+  constexpr int CHUNKS = BN * CPR;
+  constexpr int PER_T = (CHUNKS + NT - 1) / NT;
+  static_assert(D % 32 == 0 && BN % 32 == 0, "tile shape");
+
+  __shared__ __align__(16) float smem[2 * STAGE];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int j = lane & 31, g = lane >> 5;
+
+  const WorkItem wi = decode_work(p);
+  const int q0 = wi.qt * BM;
+  int kv_lo, t_begin, t_end;
+  kv_range<BM, BN>(p, q0, wi.split, kv_lo, t_begin, t_end);
+
+  const float* __restrict__ Qp = (const float*)p.q + wi.b * p.q_sb + wi.h * p.q_sh;
+  const float* __restrict__ Kp = (const float*)p.k + wi.b * p.k_sb + wi.h * p.k_sh;
+  const float* __restrict__ Vp = (const float*)p.v + wi.b * p.v_sb + wi.h * p.v_sh;
+
+  const int wq0 = q0 + wave * 32;
+  const int myq = wq0 + j;
+  f32x4 qf[NQ4];
+  if (myq < p.Sq) {
+    const f32x4* src = (const f32x4*)(Qp + (int64_t)myq * p.q_ss);
+#pragma unroll
+    for (int jj = 0; jj < NQ4; ++jj) qf[jj] = src[2 * jj + g];
+  } else {
+#pragma unroll
+    for (int jj = 0; jj < NQ4; ++jj) qf[jj] = (f32x4){};
+  }
+  if (p.neg) {
+#pragma unroll
+    for (int jj = 0; jj < NQ4; ++jj) qf[jj] = -qf[jj];
+  }
+
+  f32x4 kbuf[PER_T], vbuf[PER_T];
+  auto load_tile = [&](int kv0) {
+#pragma unroll
+    for (int i = 0; i < PER_T; ++i) {
+      const int cc = tid + i * NT;
+      if (CHUNKS % NT == 0 || cc < CHUNKS) {
+        const int row = cc / CPR, col = cc - (cc / CPR) * CPR;
+        const int kv = kv0 + row;
+        const bool ok = kv < p.Sk;
+        kbuf[i] = ok ? *(const f32x4*)(Kp + (int64_t)kv * p.k_ss + col * 4) : (f32x4){};
+        vbuf[i] = ok ? *(const f32x4*)(Vp + (int64_t)kv * p.v_ss + col * 4) : (f32x4){};
+      }
+    }
+  };
+  auto store_tile = [&](int stage) {
+    float* Ks = smem + stage * STAGE;
+    float* Vs = Ks + K_ELEMS;
+#pragma unroll
+    for (int i = 0; i < PER_T; ++i) {
+      const int cc = tid + i * NT;
+      if (CHUNKS % NT == 0 || cc < CHUNKS) {
+        const int row = cc / CPR, col = cc - (cc / CPR) * CPR;
+        *(f32x4*)(Ks + row * KS + col * 4) = kbuf[i];
+        *(f32x4*)(Vs + row * VS + col * 4) = vbuf[i];
+      }
+    }
+  };
+
+  f32x16 o[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) o[db] = (f32x16){};
+  float m_run = -INFINITY, m_max = -INFINITY, l_run = 0.f;
+  const float c = p.c;
+
+  if (t_begin < t_end) {
+    load_tile(kv_lo + t_begin * BN);
+    store_tile(0);
+  }
+  __syncthreads();
+
+  for (int t = t_begin; t < t_end; ++t) {
+    const int stage = (t - t_begin) & 1;
+    const int kv0 = kv_lo + t * BN;
+    const bool has_next = t + 1 < t_end;
+    if (has_next) load_tile(kv0 + BN);
+
+    bool skip, full;
+    classify_tile<BN>(p, kv0, wq0, wq0 + 31, skip, full);
+    if (!skip) {
+      const float* Ks = smem + stage * STAGE;
+      const float* Vs = Ks + K_ELEMS;
+
+      f32x16 s[NB];
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        s[nb] = (f32x16){};
+        const f32x4* kp = (const f32x4*)(Ks + (nb * 32 + j) * KS) + g;
+#pragma unroll
+        for (int jj = 0; jj < NQ4; ++jj) {
+          const f32x4 a = kp[2 * jj];
+#pragma unroll
+          for (int t4 = 0; t4 < 4; ++t4) s[nb] = mfma32x32x2f32(a[t4], qf[jj][t4], s[nb]);
+        }
+      }
+
+      if (!full) {
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            const int kv = kv0 + nb * 32 + 8 * (e >> 2) + 4 * g + (e & 3);
+            if (!kv_valid(p, myq, kv)) s[nb][e] = -INFINITY;
+          }
+      }
+
+      float mt = -INFINITY;
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) mt = fmaxf(mt, s[nb][e]);
+      mt = fmaxf(mt, xor32(mt)) * c;
+      m_max = fmaxf(m_max, mt);
+
+      if (__any(mt > m_run + kRescaleThreshold)) {
+        const float m_new = fmaxf(m_run, mt);
+        const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(m_run - m_new);
+        l_run *= alpha;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) o[db][e] *= alpha;
+        m_run = m_new;
+      }
+      const float msub = m_run == -INFINITY ? 0.f : m_run;
+
+      float lsum = 0.f;
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const float x = fast_exp2(s[nb][e] * c - msub);
+          s[nb][e] = x;
+          lsum += x;
+        }
+      l_run += lsum;
+
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            const int kv = nb * 32 + 8 * (e >> 2) + 4 * g + (e & 3);
+            o[db] = mfma32x32x2f32(Vs[kv * VS + db * 32 + j], s[nb][e], o[db]);
+          }
+    }
+
+    if (has_next) store_tile(stage ^ 1);
+    __syncthreads();
+  }
+
+  const float l_tot = l_run + xor32(l_run);
+  const float f = m_max == -INFINITY ? 0.f : fast_exp2(m_run - m_max);
+  if (p.num_splits == 1) {
+    if (myq < p.Sq) {
+      const float inv = m_max == -INFINITY ? 0.f : f / (l_tot * f + kSoftmaxEps);
+      float* Op = (float*)p.o + wi.b * p.o_sb + wi.h * p.o_sh + (int64_t)myq * p.o_ss;
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int e4 = 0; e4 < 4; ++e4) {
+          const int d = db * 32 + 8 * e4 + 4 * g;
+          *(f32x4*)(Op + d) = (f32x4){o[db][4 * e4] * inv, o[db][4 * e4 + 1] * inv,
+                                      o[db][4 * e4 + 2] * inv, o[db][4 * e4 + 3] * inv};
+        }
+    }
+  } else if (myq < p.Sq) {
+    const int64_t row = (((int64_t)wi.split * p.B + wi.b) * p.H + wi.h) * p.Sq + myq;
+    float* wo = p.ws_o + row * D;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int e4 = 0; e4 < 4; ++e4) {
+        const int d = db * 32 + 8 * e4 + 4 * g;
+        *(f32x4*)(wo + d) = (f32x4){o[db][4 * e4] * f, o[db][4 * e4 + 1] * f,
+                                    o[db][4 * e4 + 2] * f, o[db][4 * e4 + 3] * f};
+      }
+    if (g == 0) {
+      p.ws_ml[2 * row] = m_max;
+      p.ws_ml[2 * row + 1] = l_tot * f;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Split-KV merge: the reference's online_softmax_merge
+// (mlx_primitives/attention/_online_softmax.py:42-106) folded over all splits,
+// then O / (l + 1e-6). One thread per (row, 4 dims).
+// ---------------------------------------------------------------------------
+template <int DT>
+__global__ __launch_bounds__(256) void fa_split_merge_kernel(const float* __restrict__ ws_o,
+                                                             const float* __restrict__ ws_ml,
+                                                             void* o, int64_t o_sb, int64_t o_sh,
+                                                             int64_t o_ss, int B, int H, int Sq,
+                                                             int D, int splits) {
+  const int chunks = D / 4;
+  const int64_t rows = (int64_t)B * H * Sq;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= rows * chunks) return;
+  const int64_t row = idx / chunks;
+  const int c4 = (int)(idx - row * chunks);
+  float M = -INFINITY;
+  for (int s = 0; s < splits; ++s) M = fmaxf(M, ws_ml[2 * (s * rows + row)]);
+  f32x4 acc = {};
+  float L = 0.f;
+  if (M != -INFINITY) {
+    for (int s = 0; s < splits; ++s) {
+      const int64_t r = s * rows + row;
+      const float wgt = fast_exp2(ws_ml[2 * r] - M);
+      L += wgt * ws_ml[2 * r + 1];
+      acc += wgt * *(const f32x4*)(ws_o + r * D + 4 * c4);
+    }
+    acc = acc / (L + kSoftmaxEps);
+  }
+  const int q = (int)(row % Sq);
+  const int bh = (int)(row / Sq);
+  const int b = bh / H, h = bh - (bh / H) * H;
+  const int64_t off = b * o_sb + h * o_sh + (int64_t)q * o_ss + 4 * c4;
+  if constexpr (DT == MPX_F32) {
+    *(f32x4*)((float*)o + off) = acc;
+  } else {
+    const u32x2 val = {pack2<DT == MPX_BF16>(acc[0], acc[1]), pack2<DT == MPX_BF16>(acc[2], acc[3])};
+    *(u32x2*)((uint16_t*)o + off) = val;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host side.
+// ---------------------------------------------------------------------------
+namespace {
+
+constexpr int kNumWaves = 4;          // 4 waves x 32 rows = 128 query rows per workgroup
+constexpr int kTargetWorkgroups = 512; // 256 CUs x 2 resident workgroups
+
+struct Plan {
+  int BM, BN, n_qtiles, splits, tiles_per_split, win_left, win_right;
+  size_t ws_bytes;
+};
+
+int tile_n(int D, int dtype) { return (dtype == MPX_F32 && D > 64) ? 32 : 64; }
+
+Plan make_plan(int B, int H, int Sq, int Sk, int D, int causal, int window_left,
+               int window_right, int dtype) {
+  Plan pl;
+  pl.BM = 32 * kNumWaves;
+  pl.BN = tile_n(D, dtype);
+  pl.win_left = window_left < 0 ? -1 : window_left;
+  pl.win_right = causal ? 0 : (window_right < 0 ? -1 : window_right);
+  pl.n_qtiles = (Sq + pl.BM - 1) / pl.BM;
+  // Widest KV range over all q-tiles.
+  int max_tiles = 0;
+  for (int qt = 0; qt < pl.n_qtiles; ++qt) {
+    const int q0 = qt * pl.BM, q_last = std::min(q0 + pl.BM, Sq) - 1;
+    int lo = pl.win_left >= 0 ? std::max(0, q0 - pl.win_left) : 0;
+    lo -= lo % pl.BN;
+    const int hi = pl.win_right >= 0 ? std::min(Sk, q_last + pl.win_right + 1) : Sk;
+    const int n = hi > lo ? (hi - lo + pl.BN - 1) / pl.BN : 0;
+    max_tiles = std::max(max_tiles, n);
+  }
+  const long base = (long)B * H * pl.n_qtiles;
+  int splits = 1;
+  if (base > 0 && base < kTargetWorkgroups && max_tiles >= 8) {
+    splits = (int)std::min<long>((kTargetWorkgroups + base - 1) / base, max_tiles / 4);
+    splits = std::max(splits, 1);
+  }
+  pl.tiles_per_split = splits > 1 ? (max_tiles + splits - 1) / splits : std::max(max_tiles, 1);
+  if (splits > 1) splits = (max_tiles + pl.tiles_per_split - 1) / pl.tiles_per_split;
+  pl.splits = splits;
+  pl.ws_bytes = splits > 1 ? (size_t)splits * B * H * Sq * (D + 2) * sizeof(float) : 0;
+  return pl;
+}
+
+template <int D, int BN, bool F32, bool BF16>
+hipError_t launch_fwd(const FwdParams& p, int grid, hipStream_t stream) {
+  if constexpr (F32) {
+    hipLaunchKernelGGL((fa_fwd32_kernel<D, BN, kNumWaves>), dim3(grid), dim3(64 * kNumWaves), 0,
+                       stream, p);
+  } else {
+    hipLaunchKernelGGL((fa_fwd16_kernel<D, BN, kNumWaves, BF16>), dim3(grid),
+                       dim3(64 * kNumWaves), 0, stream, p);
+  }
+  return hipGetLastError();
+}
+
+hipError_t dispatch_fwd(const FwdParams& p, int D, int dtype, int grid, hipStream_t st) {
+  if (dtype == MPX_F32) {
+    switch (D) {
+      case 32: return launch_fwd<32, 64, true, false>(p, grid, st);
+      case 64: return launch_fwd<64, 64, true, false>(p, grid, st);
+      default: return launch_fwd<128, 32, true, false>(p, grid, st);
+    }
+  } else if (dtype == MPX_BF16) {
+    switch (D) {
+      case 32: return launch_fwd<32, 64, false, true>(p, grid, st);
+      case 64: return launch_fwd<64, 64, false, true>(p, grid, st);
+      default: return launch_fwd<128, 64, false, true>(p, grid, st);
+    }
+  } else {
+    switch (D) {
+      case 32: return launch_fwd<32, 64, false, false>(p, grid, st);
+      case 64: return launch_fwd<64, 64, false, false>(p, grid, st);
+      default: return launch_fwd<128, 64, false, false>(p, grid, st);
+    }
+  }
+}
+
+bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
+
+}  // namespace
+}  // namespace mpx
+
+using namespace mpx;
+
+extern "C" size_t mpx_attn_fwd_workspace_bytes(int B, int H, int Sq, int Sk, int D, int causal,
+                                               int window_left, int window_right, int dtype) {
+  if (B <= 0 || H <= 0 || Sq <= 0 || Sk <= 0 || D <= 0) return 0;
+  return make_plan(B, H, Sq, Sk, D, causal, window_left, window_right, dtype).ws_bytes;
+}
+
+extern "C" int mpx_attn_fwd(const void* q, const void* k, const void* v, void* o,
+                            const int64_t* q_strides, const int64_t* k_strides,
+                            const int64_t* v_strides, const int64_t* o_strides, int B, int H,
+                            int Sq, int Sk, int D, float scale, int causal, int window_left,
+                            int window_right, int dtype, void* workspace, size_t workspace_bytes,
+                            void* stream) {
+  clear_error();
+  MPX_CHECK_ARG(dtype == MPX_F32 || dtype == MPX_F16 || dtype == MPX_BF16,
+                "mpx_attn_fwd: unknown dtype code %d", dtype);
+  MPX_CHECK_ARG(B >= 0 && H >= 0 && Sq >= 0 && Sk >= 0, "mpx_attn_fwd: negative size");
+  if (D != 32 && D != 64 && D != 128) {
+    set_error("mpx_attn_fwd: head_dim %d not supported (kernels exist for 32, 64, 128)", D);
+    return MPX_EUNSUPPORTED;
+  }
+  MPX_CHECK_ARG(std::isfinite(scale), "mpx_attn_fwd: scale must be finite");
+  if ((long)B * H * Sq == 0) return MPX_OK;
+  MPX_CHECK_ARG(q && k && v && o && q_strides && k_strides && v_strides && o_strides,
+                "mpx_attn_fwd: null pointer argument");
+  MPX_CHECK_ARG(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o),
+                "mpx_attn_fwd: tensors must be 16-byte aligned");
+  const int vec = dtype == MPX_F32 ? 4 : 8;
+  const int64_t* all[4] = {q_strides, k_strides, v_strides, o_strides};
+  for (int t = 0; t < 4; ++t)
+    for (int i = 0; i < 3; ++i)
+      MPX_CHECK_ARG(all[t][i] >= 0 && all[t][i] % vec == 0,
+                    "mpx_attn_fwd: strides must be non-negative multiples of %d elements", vec);
+
+  const Plan pl = make_plan(B, H, Sq, Sk, D, causal, window_left, window_right, dtype);
+  if (pl.splits > 1) {
+    MPX_CHECK_ARG(workspace != nullptr && workspace_bytes >= pl.ws_bytes,
+                  "mpx_attn_fwd: workspace of %zu bytes required, %zu given", pl.ws_bytes,
+                  workspace_bytes);
+    MPX_CHECK_ARG(aligned16(workspace), "mpx_attn_fwd: workspace must be 16-byte aligned");
+  }
+  const long grid_l = (long)B * H * pl.n_qtiles * pl.splits;
+  MPX_CHECK_ARG(grid_l < (1L << 31), "mpx_attn_fwd: problem too large");
+
+  FwdParams p;
+  p.q = q; p.k = k; p.v = v; p.o = o;
+  p.q_sb = q_strides[0]; p.q_sh = q_strides[1]; p.q_ss = q_strides[2];
+  p.k_sb = k_strides[0]; p.k_sh = k_strides[1]; p.k_ss = k_strides[2];
+  p.v_sb = v_strides[0]; p.v_sh = v_strides[1]; p.v_ss = v_strides[2];
+  p.o_sb = o_strides[0]; p.o_sh = o_strides[1]; p.o_ss = o_strides[2];
+  p.ws_o = pl.splits > 1 ? (float*)workspace : nullptr;
+  p.ws_ml = pl.splits > 1 ? (float*)workspace + (size_t)pl.splits * B * H * Sq * D : nullptr;
+  p.B = B; p.H = H; p.Sq = Sq; p.Sk = Sk;
+  p.win_left = pl.win_left; p.win_right = pl.win_right;
+  p.n_qtiles = pl.n_qtiles; p.num_splits = pl.splits; p.tiles_per_split = pl.tiles_per_split;
+  p.c = std::fabs(scale) * kLog2e;
+  p.neg = scale < 0.f ? 1 : 0;
+
+  hipStream_t st = (hipStream_t)stream;
+  MPX_CHECK_HIP(dispatch_fwd(p, D, dtype, (int)grid_l, st));
+  if (pl.splits > 1) {
+    const long threads = (long)B * H * Sq * (D / 4);
+    const int blocks = (int)((threads + 255) / 256);
+    if (dtype == MPX_F32)
+      hipLaunchKernelGGL(fa_split_merge_kernel<MPX_F32>, dim3(blocks), dim3(256), 0, st, p.ws_o,
+                         p.ws_ml, o, p.o_sb, p.o_sh, p.o_ss, B, H, Sq, D, pl.splits);
+    else if (dtype == MPX_BF16)
+      hipLaunchKernelGGL(fa_split_merge_kernel<MPX_BF16>, dim3(blocks), dim3(256), 0, st, p.ws_o,
+                         p.ws_ml, o, p.o_sb, p.o_sh, p.o_ss, B, H, Sq, D, pl.splits);
+    else
+      hipLaunchKernelGGL(fa_split_merge_kernel<MPX_F16>, dim3(blocks), dim3(256), 0, st, p.ws_o,
+                         p.ws_ml, o, p.o_sb, p.o_sh, p.o_ss, B, H, Sq, D, pl.splits);
+    MPX_CHECK_HIP(hipGetLastError());
+  }
+  return MPX_OK;
+}

@@ -1,0 +1,97 @@
+// Shared types and helpers for the gfx950 attention kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <cstdio>
+#include <string>
+
+#include "mpx_attn.h"
+
+namespace mpx {
+
+typedef uint32_t u32;
+typedef __attribute__((ext_vector_type(2))) uint32_t u32x2;
+typedef __attribute__((ext_vector_type(4))) uint32_t u32x4;
+typedef __attribute__((ext_vector_type(4))) float f32x4;
+typedef __attribute__((ext_vector_type(16))) float f32x16;
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
+typedef __attribute__((ext_vector_type(8))) _Float16 f16x8;
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
+typedef __attribute__((ext_vector_type(2))) _Float16 f16x2;
+
+constexpr float kLog2e = 1.4426950408889634f;
+// Normaliser epsilon of the reference's tiled online-softmax path:
+// O / (l + 1e-6) (mlx_primitives/constants.py:110, attention/flash.py:312).
+constexpr float kSoftmaxEps = 1e-6f;
+
+// ---- error reporting -------------------------------------------------------
+
+void set_error(const char* fmt, ...);
+void clear_error();
+
+#define MPX_CHECK_ARG(cond, ...)  \
+  do {                            \
+    if (!(cond)) {                \
+      ::mpx::set_error(__VA_ARGS__); \
+      return MPX_EINVAL;          \
+    }                             \
+  } while (0)
+
+#define MPX_CHECK_HIP(expr)                                              \
+  do {                                                                   \
+    hipError_t _e = (expr);                                              \
+    if (_e != hipSuccess) {                                              \
+      ::mpx::set_error("%s failed: %s", #expr, hipGetErrorString(_e));   \
+      return MPX_EHIP;                                                   \
+    }                                                                    \
+  } while (0)
+
+// ---- device helpers ----------------------------------------------------------
+
+// Raw v_exp_f32 (base-2 exponential); exp2(-inf) = 0.
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Value held by lane (lane ^ 32).
+__device__ __forceinline__ float xor32(float x) { return __shfl_xor(x, 32, 64); }
+
+// 16-bit storage type <-> float.
+template <bool BF16>
+__device__ __forceinline__ float h2f(uint16_t x) {
+  if constexpr (BF16) {
+    return __uint_as_float(((u32)x) << 16);
+  } else {
+    return (float)__builtin_bit_cast(_Float16, x);
+  }
+}
+
+// Two floats -> packed pair of 16-bit values (round to nearest even).
+template <bool BF16>
+__device__ __forceinline__ u32 pack2(float a, float b) {
+  if constexpr (BF16) {
+    bf16x2 r = {(__bf16)a, (__bf16)b};
+    return __builtin_bit_cast(u32, r);
+  } else {
+    f16x2 r = {(_Float16)a, (_Float16)b};
+    return __builtin_bit_cast(u32, r);
+  }
+}
+
+// 32x32x16 MFMA on 8 packed 16-bit values per lane.
+template <bool BF16>
+__device__ __forceinline__ f32x16 mfma32x32x16(u32x4 a, u32x4 b, f32x16 c) {
+  if constexpr (BF16) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+}
+
+__device__ __forceinline__ f32x16 mfma32x32x2f32(float a, float b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
+}  // namespace mpx

@@ -1,0 +1,325 @@
+// Paged-KV decode attention for gfx950 (MI355X).
+//
+// Semantics follow mlx_primitives/cache/paged_attention.py:108-208 (decode
+// path of paged_attention): one query token per sequence, keys/values gathered
+// through block_tables from pools laid out (num_blocks, block_size, H, D);
+// token t is valid iff t < context_len and its page id is >= 0; optional ALiBi
+// bias slope_h * (t - context_len) (163-178); exact softmax.
+//
+// Design (memory bound, ~1 FLOP/byte):
+//   * split-K: each sequence's tokens are cut into partitions of PART tokens;
+//     a workgroup = 4 waves = 4 consecutive heads of one (sequence, partition),
+//     so the four waves stream adjacent 256-byte head rows of the same pages;
+//   * pass 1 streams K: a token row of one head is read by LPT lanes with
+//     16-byte loads (U loads in flight per lane), partial dot products are
+//     reduced across the LPT lanes, scores land in LDS;
+//   * partition max / exp2 / sum over the LDS scores, then pass 2 streams V
+//     and accumulates p * v in fp32;
+//   * per-partition (o, m, l) go to the workspace; paged_decode_merge_kernel
+//     combines them (online-softmax merge) and normalises by the exact sum.
+// The page ids of a partition are staged once in LDS, invalid ids (< 0 or
+// >= num_blocks) are masked and never dereferenced.
+#include "mpx_common.h"
+
+#include <algorithm>
+#include <cmath>
+
+namespace mpx {
+
+struct DecodeParams {
+  const void* q;
+  const void* kpool;
+  const void* vpool;
+  const int32_t* bt;
+  const int32_t* cl;
+  const float* slopes;
+  void* o;
+  int64_t q_sb, q_sh, o_sb, o_sh;
+  float* ws_o;   // (B, H, max_parts, D)
+  float* ws_ml;  // (B, H, max_parts, 2), m in log2 units
+  int B, H, num_blocks, bs, max_blocks, max_parts;
+  float c;  // scale * log2(e)
+};
+
+constexpr int kPart = 512;   // tokens per partition
+constexpr int kHeadsPerWG = 4;
+
+template <int DT>
+__device__ __forceinline__ float elem(const u32x4& v, int i) {
+  if constexpr (DT == MPX_F32) {
+    return __uint_as_float(v[i]);
+  } else {
+    const u32 w = v[i >> 1];
+    const uint16_t x = (uint16_t)((i & 1) ? (w >> 16) : (w & 0xffffu));
+    return h2f<DT == MPX_BF16>(x);
+  }
+}
+
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) x = fmaxf(x, __shfl_xor(x, off, 64));
+  return x;
+}
+
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off, 64);
+  return x;
+}
+
+template <int D, int DT>
+__global__ __launch_bounds__(256) void paged_decode_part_kernel(DecodeParams p) {
+  constexpr int ES = DT == MPX_F32 ? 4 : 2;  // element bytes
+  constexpr int EPC = 16 / ES;               // elements per 16-byte chunk
+  constexpr int LPT = D / EPC;               // lanes per token row
+  constexpr int TPI = 64 / LPT;              // tokens per wave-wide load
+  constexpr int U = 8;                       // loads in flight per lane
+  static_assert(LPT >= 1 && LPT <= 64 && 64 % LPT == 0, "head_dim");
+
+  __shared__ float sc[kHeadsPerWG][kPart];
+  __shared__ int btl[kPart + 1];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int h = blockIdx.x * kHeadsPerWG + wave;
+  const int part = blockIdx.y, b = blockIdx.z;
+  const int ctx = max(0, min(p.cl[b], p.max_blocks * p.bs));
+  const int p0 = part * kPart;
+  if (p0 >= ctx) return;  // uniform over the workgroup
+  const int p1 = min(p0 + kPart, ctx);
+  const int n = p1 - p0;
+  const int pg0 = p0 / p.bs;
+  const int npg = (p1 - 1) / p.bs - pg0 + 1;
+  for (int i = tid; i < npg; i += 256) {
+    const int blk = p.bt[(int64_t)b * p.max_blocks + pg0 + i];
+    btl[i] = (blk >= 0 && blk < p.num_blocks) ? blk : -1;
+  }
+  __syncthreads();
+
+  const bool active = h < p.H;
+  const int cidx = lane % LPT, tl = lane / LPT;
+  const int64_t row_elems = (int64_t)p.H * D;
+  const int64_t hoff = (int64_t)h * D + cidx * EPC;
+  const char* kbase = (const char*)p.kpool;
+  const char* vbase = (const char*)p.vpool;
+  float* scw = sc[wave];
+
+  float m = -INFINITY, l = 0.f;
+  if (active) {
+    float qv[EPC];
+    {
+      const u32x4 qr =
+          *(const u32x4*)((const char*)p.q + ((int64_t)b * p.q_sb + (int64_t)h * p.q_sh + cidx * EPC) * ES);
+#pragma unroll
+      for (int i = 0; i < EPC; ++i) qv[i] = elem<DT>(qr, i) * p.c;
+    }
+    const float slope2 = p.slopes ? p.slopes[h] * kLog2e : 0.f;
+
+    // Pass 1: scores of the partition.
+    for (int t0 = p0; t0 < p1; t0 += TPI * U) {
+      u32x4 kr[U];
+      bool ok[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int tk = t0 + u * TPI + tl;
+        int blk = -1;
+        if (tk < p1) blk = btl[tk / p.bs - pg0];
+        ok[u] = blk >= 0;
+        kr[u] = ok[u] ? *(const u32x4*)(kbase + (((int64_t)blk * p.bs + tk % p.bs) * row_elems + hoff) * ES)
+                      : (u32x4){0u, 0u, 0u, 0u};
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        float dot = 0.f;
+#pragma unroll
+        for (int i = 0; i < EPC; ++i) dot = fmaf(qv[i], elem<DT>(kr[u], i), dot);
+#pragma unroll
+        for (int off = LPT / 2; off >= 1; off >>= 1) dot += __shfl_xor(dot, off, 64);
+        const int tk = t0 + u * TPI + tl;
+        if (cidx == 0 && tk < p1) scw[tk - p0] = ok[u] ? dot + slope2 * (float)(tk - ctx) : -INFINITY;
+      }
+    }
+  }
+  __syncthreads();
+
+  if (active) {
+    for (int i = lane; i < n; i += 64) m = fmaxf(m, scw[i]);
+    m = wave_max(m);
+    for (int i = lane; i < n; i += 64) {
+      const float e = m == -INFINITY ? 0.f : fast_exp2(scw[i] - m);
+      scw[i] = e;
+      l += e;
+    }
+    l = wave_sum(l);
+  }
+  __syncthreads();
+
+  if (active) {
+    // Pass 2: o = sum_t p_t v_t.
+    float acc[EPC];
+#pragma unroll
+    for (int i = 0; i < EPC; ++i) acc[i] = 0.f;
+    for (int t0 = p0; t0 < p1; t0 += TPI * U) {
+      u32x4 vr[U];
+      float pw[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int tk = t0 + u * TPI + tl;
+        int blk = -1;
+        if (tk < p1) blk = btl[tk / p.bs - pg0];
+        pw[u] = blk >= 0 ? scw[tk - p0] : 0.f;
+        vr[u] = blk >= 0 ? *(const u32x4*)(vbase + (((int64_t)blk * p.bs + tk % p.bs) * row_elems + hoff) * ES)
+                         : (u32x4){0u, 0u, 0u, 0u};
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int i = 0; i < EPC; ++i) acc[i] = fmaf(pw[u], elem<DT>(vr[u], i), acc[i]);
+    }
+#pragma unroll
+    for (int off = LPT; off < 64; off <<= 1)
+#pragma unroll
+      for (int i = 0; i < EPC; ++i) acc[i] += __shfl_xor(acc[i], off, 64);
+
+    const int64_t slot = ((int64_t)b * p.H + h) * p.max_parts + part;
+    if (tl == 0) {
+      float* wo = p.ws_o + slot * D + cidx * EPC;
+#pragma unroll
+      for (int i = 0; i < EPC; i += 4) *(f32x4*)(wo + i) = (f32x4){acc[i], acc[i + 1], acc[i + 2], acc[i + 3]};
+    }
+    if (lane == 0) {
+      p.ws_ml[2 * slot] = m;
+      p.ws_ml[2 * slot + 1] = l;
+    }
+  }
+}
+
+// Combine the partitions of one (sequence, head): the online-softmax merge
+// (mlx_primitives/attention/_online_softmax.py:42-106) over all partitions,
+// then the exact normalisation o / l of the reference's softmax.
+template <int DT>
+__global__ __launch_bounds__(64) void paged_decode_merge_kernel(DecodeParams p, int D) {
+  const int bh = blockIdx.x;
+  const int b = bh / p.H, h = bh - (bh / p.H) * p.H;
+  const int lane = threadIdx.x;
+  const int ctx = max(0, min(p.cl[b], p.max_blocks * p.bs));
+  const int nparts = (ctx + kPart - 1) / kPart;
+  const int64_t base = (int64_t)bh * p.max_parts;
+  float M = -INFINITY;
+  for (int i = 0; i < nparts; ++i) M = fmaxf(M, p.ws_ml[2 * (base + i)]);
+  for (int d = lane; d < D; d += 64) {
+    float acc = 0.f, L = 0.f;
+    for (int i = 0; i < nparts; ++i) {
+      const float w = fast_exp2(p.ws_ml[2 * (base + i)] - M);
+      L += w * p.ws_ml[2 * (base + i) + 1];
+      acc += w * p.ws_o[(base + i) * D + d];
+    }
+    const float out = acc / L;  // no valid token: 0 / 0 = NaN, as the reference
+    const int64_t off = (int64_t)b * p.o_sb + (int64_t)h * p.o_sh + d;
+    if constexpr (DT == MPX_F32) {
+      ((float*)p.o)[off] = out;
+    } else if constexpr (DT == MPX_BF16) {
+      ((__bf16*)p.o)[off] = (__bf16)out;
+    } else {
+      ((_Float16*)p.o)[off] = (_Float16)out;
+    }
+  }
+}
+
+namespace {
+
+int max_parts_for(int block_size, int max_blocks) {
+  const long tokens = (long)block_size * max_blocks;
+  return (int)((tokens + kPart - 1) / kPart);
+}
+
+template <int D, int DT>
+hipError_t launch_decode(const DecodeParams& p, hipStream_t st) {
+  const dim3 grid((p.H + kHeadsPerWG - 1) / kHeadsPerWG, p.max_parts, p.B);
+  hipLaunchKernelGGL((paged_decode_part_kernel<D, DT>), grid, dim3(256), 0, st, p);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(paged_decode_merge_kernel<DT>, dim3(p.B * p.H), dim3(64), 0, st, p, D);
+  return hipGetLastError();
+}
+
+template <int DT>
+hipError_t dispatch_decode_d(const DecodeParams& p, int D, hipStream_t st) {
+  switch (D) {
+    case 32: return launch_decode<32, DT>(p, st);
+    case 64: return launch_decode<64, DT>(p, st);
+    default: return launch_decode<128, DT>(p, st);
+  }
+}
+
+}  // namespace
+}  // namespace mpx
+
+using namespace mpx;
+
+extern "C" size_t mpx_paged_decode_workspace_bytes(int B, int H, int D, int block_size,
+                                                   int max_blocks) {
+  if (B <= 0 || H <= 0 || D <= 0 || block_size <= 0 || max_blocks <= 0) return 0;
+  return (size_t)B * H * max_parts_for(block_size, max_blocks) * (D + 2) * sizeof(float);
+}
+
+extern "C" int mpx_paged_decode(const void* q, const void* k_pool, const void* v_pool,
+                                const int32_t* block_tables, const int32_t* context_lens,
+                                const float* alibi_slopes, void* o, const int64_t* q_strides,
+                                const int64_t* o_strides, int B, int H, int D, int num_blocks,
+                                int block_size, int max_blocks, float scale, int dtype,
+                                void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  MPX_CHECK_ARG(dtype == MPX_F32 || dtype == MPX_F16 || dtype == MPX_BF16,
+                "mpx_paged_decode: unknown dtype code %d", dtype);
+  MPX_CHECK_ARG(B >= 0 && H >= 0 && num_blocks >= 0 && max_blocks >= 0,
+                "mpx_paged_decode: negative size");
+  MPX_CHECK_ARG(block_size > 0, "mpx_paged_decode: block_size must be positive");
+  if (D != 32 && D != 64 && D != 128) {
+    set_error("mpx_paged_decode: head_dim %d not supported (kernels exist for 32, 64, 128)", D);
+    return MPX_EUNSUPPORTED;
+  }
+  MPX_CHECK_ARG(std::isfinite(scale), "mpx_paged_decode: scale must be finite");
+  if ((long)B * H == 0) return MPX_OK;
+  MPX_CHECK_ARG(q && o && context_lens && q_strides && o_strides,
+                "mpx_paged_decode: null pointer argument");
+  MPX_CHECK_ARG(max_blocks == 0 || (k_pool && v_pool && block_tables) || num_blocks == 0,
+                "mpx_paged_decode: null pool/table pointer");
+  const int vec = dtype == MPX_F32 ? 4 : 8;
+  MPX_CHECK_ARG(((uintptr_t)q & 15u) == 0 && ((uintptr_t)k_pool & 15u) == 0 &&
+                    ((uintptr_t)v_pool & 15u) == 0,
+                "mpx_paged_decode: q and pools must be 16-byte aligned");
+  MPX_CHECK_ARG(q_strides[0] % vec == 0 && q_strides[1] % vec == 0,
+                "mpx_paged_decode: q strides must be multiples of %d elements", vec);
+  const long max_tokens = (long)max_blocks * block_size;
+  MPX_CHECK_ARG(max_tokens < (1L << 30), "mpx_paged_decode: block table too large");
+
+  DecodeParams p;
+  p.q = q; p.kpool = k_pool; p.vpool = v_pool; p.bt = block_tables; p.cl = context_lens;
+  p.slopes = alibi_slopes; p.o = o;
+  p.q_sb = q_strides[0]; p.q_sh = q_strides[1]; p.o_sb = o_strides[0]; p.o_sh = o_strides[1];
+  p.B = B; p.H = H; p.num_blocks = num_blocks; p.bs = block_size; p.max_blocks = max_blocks;
+  p.max_parts = std::max(1, max_parts_for(block_size, max_blocks));
+  p.c = scale * kLog2e;
+  const size_t need = (size_t)B * H * p.max_parts * (D + 2) * sizeof(float);
+  MPX_CHECK_ARG(workspace != nullptr && workspace_bytes >= need && ((uintptr_t)workspace & 15u) == 0,
+                "mpx_paged_decode: 16-byte aligned workspace of %zu bytes required, %zu given",
+                need, workspace_bytes);
+  MPX_CHECK_ARG(p.max_parts <= 65535 && B <= 65535, "mpx_paged_decode: grid too large");
+  p.ws_o = (float*)workspace;
+  p.ws_ml = (float*)workspace + (size_t)B * H * p.max_parts * D;
+  if (num_blocks == 0 || max_blocks == 0) {
+    // No page can be valid; the partition kernel has no work, the merge writes NaN.
+    p.max_blocks = 0;
+  }
+
+  hipStream_t st = (hipStream_t)stream;
+  hipError_t e;
+  if (dtype == MPX_F32)
+    e = dispatch_decode_d<MPX_F32>(p, D, st);
+  else if (dtype == MPX_BF16)
+    e = dispatch_decode_d<MPX_BF16>(p, D, st);
+  else
+    e = dispatch_decode_d<MPX_F16>(p, D, st);
+  MPX_CHECK_HIP(e);
+  return MPX_OK;
+}

@@ -1,0 +1,160 @@
+"""ctypes binding of libmpx_attn.so (the gfx950 HIP kernels and their C ABI).
+
+This is the launch layer that replaces the reference's
+``mx.fast.metal_kernel`` dispatch (mlx_primitives/attention/flash.py:410-476,
+mlx_primitives/kernels/_registry.py:36-165): the library is loaded once
+(thread-safe), tensors are passed as raw device pointers plus element strides,
+work is enqueued on torch's current HIP stream, and workspaces come from
+torch's caching allocator. There is no CPU fallback: if the library is missing
+or the tensors are not on a ROCm device, the call raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+from typing import Optional, Sequence
+
+import torch
+
+_LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libmpx_attn.so")
+
+MPX_OK = 0
+MPX_EINVAL = -1
+MPX_EUNSUPPORTED = -2
+MPX_EHIP = -3
+
+DTYPE_CODES = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
+
+_lib: Optional[ctypes.CDLL] = None
+_lock = threading.Lock()
+
+_i64p = ctypes.POINTER(ctypes.c_int64)
+
+
+def library_path() -> str:
+    return _LIB_PATH
+
+
+def load() -> ctypes.CDLL:
+    """Load libmpx_attn.so once (double-checked under a lock)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(_LIB_PATH):
+            raise RuntimeError(
+                f"libmpx_attn.so not found at {_LIB_PATH}; build it with "
+                "`python mlx-primitives_amd/build.py` (hipcc, gfx950)")
+        lib = ctypes.CDLL(_LIB_PATH)
+        lib.mpx_version.restype = ctypes.c_int
+        lib.mpx_version.argtypes = []
+        lib.mpx_last_error.restype = ctypes.c_char_p
+        lib.mpx_last_error.argtypes = []
+        lib.mpx_attn_fwd.restype = ctypes.c_int
+        lib.mpx_attn_fwd.argtypes = [
+            ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+            _i64p, _i64p, _i64p, _i64p,
+            ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+            ctypes.c_float, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+            ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
+        ]
+        lib.mpx_attn_fwd_workspace_bytes.restype = ctypes.c_size_t
+        lib.mpx_attn_fwd_workspace_bytes.argtypes = [ctypes.c_int] * 9
+        lib.mpx_paged_decode.restype = ctypes.c_int
+        lib.mpx_paged_decode.argtypes = [
+            ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+            ctypes.c_void_p, ctypes.c_void_p, _i64p, _i64p,
+            ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+            ctypes.c_float, ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
+        ]
+        lib.mpx_paged_decode_workspace_bytes.restype = ctypes.c_size_t
+        lib.mpx_paged_decode_workspace_bytes.argtypes = [ctypes.c_int] * 5
+        _lib = lib
+        return lib
+
+
+def _check(rc: int, what: str) -> None:
+    if rc == MPX_OK:
+        return
+    msg = load().mpx_last_error().decode(errors="replace") or what
+    if rc == MPX_EINVAL:
+        raise ValueError(msg)
+    if rc == MPX_EUNSUPPORTED:
+        raise NotImplementedError(msg)
+    raise RuntimeError(msg)
+
+
+def _strides(vals: Sequence[int]) -> ctypes.Array:
+    return (ctypes.c_int64 * len(vals))(*[int(x) for x in vals])
+
+
+def require_device(*tensors: torch.Tensor) -> torch.device:
+    """All tensors on one ROCm device; the kernels have no CPU path."""
+    dev = tensors[0].device
+    if dev.type != "cuda":
+        raise RuntimeError(
+            "mlx_primitives (MI355X build) runs on ROCm device tensors only; got "
+            f"{dev.type} tensors")
+    for t in tensors[1:]:
+        if t.device != dev:
+            raise ValueError(f"all tensors must be on {dev}, got {t.device}")
+    return dev
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    try:
+        return DTYPE_CODES[dtype]
+    except KeyError:
+        raise ValueError(f"unsupported dtype {dtype}; expected float32, float16 or bfloat16") from None
+
+
+def _stream_ptr(dev: torch.device) -> int:
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def attn_fwd_workspace_bytes(B: int, H: int, Sq: int, Sk: int, D: int, causal: bool,
+                             window_left: int, window_right: int, dtype: torch.dtype) -> int:
+    return int(load().mpx_attn_fwd_workspace_bytes(
+        B, H, Sq, Sk, D, int(causal), window_left, window_right, dtype_code(dtype)))
+
+
+def attn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor,
+             q_strides: Sequence[int], k_strides: Sequence[int], v_strides: Sequence[int],
+             o_strides: Sequence[int], B: int, H: int, Sq: int, Sk: int, D: int,
+             scale: float, causal: bool, window_left: int = -1, window_right: int = -1) -> None:
+    """Enqueue mpx_attn_fwd on the current stream (strides in (b, h, s) order)."""
+    lib = load()
+    dev = require_device(q, k, v, o)
+    code = dtype_code(q.dtype)
+    ws_bytes = int(lib.mpx_attn_fwd_workspace_bytes(
+        B, H, Sq, Sk, D, int(causal), window_left, window_right, code))
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
+    rc = lib.mpx_attn_fwd(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+        _strides(q_strides), _strides(k_strides), _strides(v_strides), _strides(o_strides),
+        B, H, Sq, Sk, D, float(scale), int(causal), int(window_left), int(window_right), code,
+        ws.data_ptr() if ws is not None else None, ws_bytes, _stream_ptr(dev))
+    _check(rc, "mpx_attn_fwd failed")
+
+
+def paged_decode(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
+                 block_tables: torch.Tensor, context_lens: torch.Tensor,
+                 alibi_slopes: Optional[torch.Tensor], o: torch.Tensor,
+                 q_strides: Sequence[int], o_strides: Sequence[int], B: int, H: int, D: int,
+                 num_blocks: int, block_size: int, max_blocks: int, scale: float) -> None:
+    """Enqueue mpx_paged_decode on the current stream."""
+    lib = load()
+    dev = require_device(q, k_pool, v_pool, block_tables, context_lens, o)
+    code = dtype_code(q.dtype)
+    ws_bytes = int(lib.mpx_paged_decode_workspace_bytes(B, H, D, block_size, max_blocks))
+    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=dev)
+    rc = lib.mpx_paged_decode(
+        q.data_ptr(), k_pool.data_ptr(), v_pool.data_ptr(), block_tables.data_ptr(),
+        context_lens.data_ptr(), alibi_slopes.data_ptr() if alibi_slopes is not None else None,
+        o.data_ptr(), _strides(q_strides), _strides(o_strides), B, H, D, num_blocks,
+        block_size, max_blocks, float(scale), code, ws.data_ptr(), ws.numel(), _stream_ptr(dev))
+    _check(rc, "mpx_paged_decode failed")

@@ -1,0 +1,15 @@
+"""Paged KV-cache attention (decode) over the reference's page layout."""
+
+from mlx_primitives.cache.paged_attention import (
+    create_block_table_from_lengths,
+    get_alibi_slopes,
+    paged_attention,
+    paged_attention_with_bias,
+)
+
+__all__ = [
+    "paged_attention",
+    "paged_attention_with_bias",
+    "create_block_table_from_lengths",
+    "get_alibi_slopes",
+]

@@ -1,0 +1,134 @@
+"""Host-side behaviour of the drop-in API (no GPU): argument validation with the
+reference's messages, the no-CPU-fallback rule, and the pure host helpers."""
+
+import numpy as np
+import pytest
+import torch
+
+from mlx_primitives.attention import (
+    ChunkedCrossAttention,
+    FlashAttention,
+    SlidingWindowAttention,
+    chunked_cross_attention,
+    create_sliding_window_mask,
+    estimate_memory_savings,
+    flash_attention,
+    get_optimal_flash_config,
+    sliding_window_attention,
+)
+from mlx_primitives.cache import (
+    create_block_table_from_lengths,
+    get_alibi_slopes,
+    paged_attention,
+    paged_attention_with_bias,
+)
+from mlx_primitives.constants import Layout
+from oracle import paged as op
+
+
+def t(*shape, dtype=torch.float32):
+    return torch.zeros(shape, dtype=dtype)
+
+
+def test_flash_validation_messages():
+    with pytest.raises(ValueError, match="Expected 4D tensors, got 3D"):
+        flash_attention(t(1, 2, 3), t(1, 2, 3, 4), t(1, 2, 3, 4))
+    with pytest.raises(ValueError, match="Expected K to be 4D"):
+        flash_attention(t(1, 2, 3, 4), t(2, 3, 4), t(1, 2, 3, 4))
+    with pytest.raises(ValueError, match="layout must be"):
+        flash_attention(t(1, 2, 3, 4), t(1, 2, 3, 4), t(1, 2, 3, 4), layout="SBHD")
+    with pytest.raises(ValueError, match="Batch size mismatch"):
+        flash_attention(t(1, 2, 3, 4), t(2, 2, 3, 4), t(1, 2, 3, 4))
+    with pytest.raises(ValueError, match="Number of heads mismatch"):
+        flash_attention(t(1, 2, 3, 4), t(1, 2, 5, 4), t(1, 2, 5, 4))
+    with pytest.raises(ValueError, match="Head dimension mismatch between Q and K"):
+        flash_attention(t(1, 2, 3, 4), t(1, 2, 3, 8), t(1, 2, 3, 4))
+    with pytest.raises(ValueError, match="Sequence length mismatch between K and V"):
+        flash_attention(t(1, 2, 3, 4), t(1, 5, 3, 4), t(1, 6, 3, 4))
+    with pytest.raises(ValueError, match="dtype mismatch"):
+        flash_attention(t(1, 2, 3, 4), t(1, 2, 3, 4, dtype=torch.float16), t(1, 2, 3, 4))
+    # BHSD reads heads from dim 1
+    with pytest.raises(ValueError, match="Number of heads mismatch"):
+        flash_attention(t(1, 2, 3, 4), t(1, 3, 3, 4), t(1, 3, 3, 4), layout=Layout.BHSD)
+
+
+def test_no_cpu_fallback():
+    x = t(1, 8, 2, 64)
+    with pytest.raises(RuntimeError, match="ROCm device tensors only"):
+        flash_attention(x, x, x)
+    with pytest.raises(RuntimeError, match="ROCm device tensors only"):
+        sliding_window_attention(x, x, x, window_size=2)
+    with pytest.raises(RuntimeError, match="ROCm device tensors only"):
+        chunked_cross_attention(x, x, x)
+    q = t(2, 1, 2, 64); pool = t(4, 16, 2, 64)
+    with pytest.raises(RuntimeError, match="ROCm device tensors only"):
+        paged_attention(q, pool, pool, torch.zeros(2, 1, dtype=torch.int32),
+                        torch.ones(2, dtype=torch.int32))
+
+
+def test_dropout_not_silently_dropped():
+    x = t(1, 8, 2, 64)
+    with pytest.raises(NotImplementedError):
+        flash_attention(x, x, x, dropout_p=0.1)
+    with pytest.raises(NotImplementedError):
+        sliding_window_attention(x, x, x, 2, dropout_p=0.1)
+    with pytest.raises(NotImplementedError):
+        chunked_cross_attention(x, x, x, dropout_p=0.1)
+
+
+def test_paged_validation():
+    q = t(2, 1, 2, 64); pool = t(4, 16, 2, 64)
+    tables = torch.zeros(2, 1, dtype=torch.int32); lens = torch.ones(2, dtype=torch.int32)
+    with pytest.raises(ValueError, match="block_size"):
+        paged_attention(q, pool, pool, tables, lens, block_size=8)
+    with pytest.raises(NotImplementedError, match="prefill"):
+        paged_attention(t(2, 3, 2, 64), pool, pool, tables, lens)
+    with pytest.raises(ValueError, match="Cannot specify both"):
+        paged_attention_with_bias(q, pool, pool, tables, lens, attention_bias=q,
+                                  alibi_slopes=torch.ones(2))
+    with pytest.raises(NotImplementedError):
+        paged_attention_with_bias(q, pool, pool, tables, lens, attention_bias=q)
+
+
+def test_module_defaults():
+    assert FlashAttention(8, 64).block_q == 32 and FlashAttention(8, 128).block_kv == 16
+    assert FlashAttention(8, 128, block_q=8, block_kv=8).block_q == 8
+    assert SlidingWindowAttention(8, 64, 32).scale == pytest.approx(0.125)
+    assert ChunkedCrossAttention(8, 64).chunk_size == 1024
+
+
+def test_optimal_config_kats():
+    # tests/attention/test_flash.py:315-336
+    bq, bk = get_optimal_flash_config(1024, 32, 8)
+    assert bq >= 16 and bk >= 16
+    bq, bk = get_optimal_flash_config(1024, 128, 8)
+    assert bq <= 32 and bk <= 32
+    bq, bk = get_optimal_flash_config(16, 64, 8)
+    assert bq <= 16 and bk <= 16
+
+
+def test_memory_savings():
+    dense, chunk, ratio = estimate_memory_savings(512, 65536, 16, 64, 1024)
+    assert dense == 512 * 65536 * 16 * 4 and chunk == 512 * 1024 * 16 * 4 and ratio == 64
+
+
+def test_sliding_window_mask_kats():
+    # tests/attention/test_sliding_window.py:74-103
+    causal = create_sliding_window_mask(5, 2, causal=True).int().tolist()
+    assert causal == [[1, 0, 0, 0, 0], [1, 1, 0, 0, 0], [1, 1, 1, 0, 0], [0, 1, 1, 1, 0],
+                      [0, 0, 1, 1, 1]]
+    bi = create_sliding_window_mask(5, 1, causal=False).int().tolist()
+    assert bi == [[1, 1, 0, 0, 0], [1, 1, 1, 0, 0], [0, 1, 1, 1, 0], [0, 0, 1, 1, 1],
+                  [0, 0, 0, 1, 1]]
+
+
+@pytest.mark.parametrize("lens,bs", [([16, 32, 48], 16), ([10, 25], 16), ([1, 100, 7], 8)])
+def test_block_tables_match_oracle(lens, bs):
+    got = create_block_table_from_lengths(torch.tensor(lens, dtype=torch.int32), bs)
+    np.testing.assert_array_equal(got.numpy(), op.create_block_table_from_lengths(np.array(lens), bs))
+    assert got.dtype == torch.int32
+
+
+def test_alibi_slopes_match_oracle():
+    for h in (1, 8, 12, 32):
+        np.testing.assert_allclose(get_alibi_slopes(h).numpy(), op.get_alibi_slopes(h), rtol=1e-7)

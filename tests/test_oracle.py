@@ -1,0 +1,367 @@
+"""Pins of the CPU oracle (oracle/attention.py, oracle/paged.py).
+
+Each oracle function is checked against something that does not restate it:
+  * known-answer cases from the reference's own tests (cited file:line);
+  * an independent brute-force evaluation (per-row Python loops, math.exp)
+    on tiny inputs;
+  * torch.nn.functional.scaled_dot_product_attention in float64 (the routine
+    the reference's parity suite compares with,
+    tests/parity/pytorch/test_attention_parity.py:87-105);
+  * invariants: block/chunk-size independence, merge associativity, full
+    window == causal, large/small input scales.
+The last group plants mistakes in the oracle and checks a pin catches each.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import attention as oa
+from oracle import paged as op
+
+
+def rnd(shape, seed, dtype=np.float64):
+    return np.random.default_rng(seed).standard_normal(shape).astype(dtype)
+
+
+def brute_attention(q, k, v, scale, allowed, eps=0.0):
+    """q (B,Sq,H,D), k/v (B,Sk,H,D); allowed(i, j) -> bool. Pure loops."""
+    B, Sq, H, D = q.shape
+    Sk = k.shape[1]
+    out = np.zeros((B, Sq, H, v.shape[3]))
+    for b in range(B):
+        for h in range(H):
+            for i in range(Sq):
+                js = [j for j in range(Sk) if allowed(i, j)]
+                s = [sum(float(q[b, i, h, d]) * float(k[b, j, h, d]) for d in range(D)) * scale
+                     for j in js]
+                m = max(s)
+                w = [math.exp(x - m) for x in s]
+                tot = sum(w)
+                for wi, j in zip(w, js):
+                    out[b, i, h] += wi * v[b, j, h].astype(np.float64)
+                out[b, i, h] /= (tot + eps)
+    return out
+
+
+def sdpa(q, k, v, scale, mask=None):
+    """torch SDPA in float64 on BSHD numpy arrays; mask (Sq, Sk) bool."""
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).double().transpose(1, 2)
+    m = None if mask is None else torch.from_numpy(mask)
+    out = F.scaled_dot_product_attention(t(q), t(k), t(v), attn_mask=m, scale=scale)
+    return out.transpose(1, 2).numpy()
+
+
+def causal_mask(sq, sk):
+    return np.arange(sk)[None, :] <= np.arange(sq)[:, None]
+
+
+def window_mask(s, w, causal):
+    i, j = np.arange(s)[:, None], np.arange(s)[None, :]
+    m = np.abs(i - j) <= w
+    return m & (j <= i) if causal else m
+
+
+# ---- known answers from the reference's tests ---------------------------------
+
+@pytest.mark.parametrize("block", [1, 2, 4, 32])
+def test_attention_identity_kat(block):
+    # tests/reference.py:453-468: q = k = 1, v = [1,2,3,4] -> [1, 1.5, 2, 2.5].
+    q = np.ones((1, 4, 1, 1))
+    v = np.array([1.0, 2.0, 3.0, 4.0]).reshape(1, 4, 1, 1)
+    out = oa.tiled_flash_attention(q, q.copy(), v, 1.0, True, block, block)
+    np.testing.assert_allclose(out.ravel(), [1.0, 1.5, 2.0, 2.5], rtol=1e-5)
+    dense = oa.dense_attention_bhsd(q.transpose(0, 2, 1, 3), q.transpose(0, 2, 1, 3),
+                                    v.transpose(0, 2, 1, 3), 1.0, True)
+    np.testing.assert_allclose(dense.ravel(), [1.0, 1.5, 2.0, 2.5], rtol=1e-12)
+
+
+def test_single_token_returns_v():
+    # tests/attention/test_flash.py:217-230
+    q, k, v = (rnd((2, 1, 4, 64), s) for s in (1, 2, 3))
+    out = oa.flash_attention(q, k, v, causal=True)
+    np.testing.assert_allclose(out, v, rtol=1e-5, atol=1e-6)
+
+
+def test_first_position_sees_only_self():
+    # tests/attention/test_metal_python_parity.py:159-184
+    q = np.zeros((1, 16, 2, 32)); k = np.zeros((1, 16, 2, 32)); v = np.ones((1, 16, 2, 32))
+    q[:, 0] = 1.0; k[:, 0] = 1.0
+    out = oa.flash_attention(q, k, v, causal=True)
+    np.testing.assert_allclose(out[:, 0], 1.0, rtol=1e-4, atol=1e-4)
+
+
+def test_uniform_attention_mean():
+    # tests/attention/test_metal_python_parity.py:207-232
+    seq = 64
+    q = np.ones((1, seq, 2, 32)); k = np.ones((1, seq, 2, 32))
+    v = np.broadcast_to(np.arange(seq, dtype=np.float64).reshape(1, seq, 1, 1), (1, seq, 2, 32)).copy()
+    out = oa.flash_attention(q, k, v, causal=False)
+    np.testing.assert_allclose(out.mean(), (seq - 1) / 2.0, rtol=1e-2)
+
+
+def test_window_restriction_kat():
+    # tests/attention/test_sliding_window.py:216-233
+    q = np.zeros((1, 16, 1, 8)); k = np.zeros((1, 16, 1, 8)); v = np.zeros((1, 16, 1, 8))
+    q[0, 0, 0, 0] = 1.0; k[0, 15, 0, 0] = 1.0; v[0, 15, 0, 0] = 100.0
+    out = oa.sliding_window_attention(q, k, v, window_size=4, causal=False)
+    assert abs(out[0, 0, 0, 0]) < 1.0
+
+
+def test_full_window_equals_causal():
+    # tests/attention/test_sliding_window.py:192-211
+    q, k, v = (rnd((2, 16, 2, 32), s) for s in (4, 5, 6))
+    sw = oa.sliding_window_attention(q, k, v, window_size=16, causal=True)
+    ref = sdpa(q, k, v, 1 / math.sqrt(32), causal_mask(16, 16))
+    np.testing.assert_allclose(sw, ref, rtol=1e-5, atol=1e-6)
+
+
+def test_merge_two_chunks_kat():
+    # tests/attention/test_flash.py:395-441: two chunks merged == full attention
+    q = rnd((2, 8, 4, 32), 7); k = rnd((2, 32, 4, 32), 8); v = rnd((2, 32, 4, 32), 9)
+    s = 1 / math.sqrt(32)
+    o1, m1, l1 = oa.compute_chunk_attention(q, k[:, :16], v[:, :16], s)
+    o2, m2, l2 = oa.compute_chunk_attention(q, k[:, 16:], v[:, 16:], s, kv_offset=16)
+    o, _, l = oa.online_softmax_merge(o1, m1, l1, o2, m2, l2)
+    np.testing.assert_allclose(o / l[..., None], sdpa(q, k, v, s), rtol=1e-10, atol=1e-12)
+
+
+def test_merge_large_score_difference_kat():
+    # tests/attention/test_flash.py:528-566
+    q = rnd((1, 4, 2, 16), 10)
+    k = np.concatenate([rnd((1, 8, 2, 16), 11) * 5, rnd((1, 8, 2, 16), 12) * 0.1], axis=1)
+    v = rnd((1, 16, 2, 16), 13)
+    s = 0.25
+    o1, m1, l1 = oa.compute_chunk_attention(q, k[:, :8], v[:, :8], s)
+    o2, m2, l2 = oa.compute_chunk_attention(q, k[:, 8:], v[:, 8:], s, kv_offset=8)
+    o, _, l = oa.online_softmax_merge(o1, m1, l1, o2, m2, l2)
+    np.testing.assert_allclose(o / l[..., None], sdpa(q, k, v, s), rtol=1e-10, atol=1e-12)
+
+
+# ---- brute force on tiny inputs -------------------------------------------------
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("block", [1, 2, 3, 32])
+def test_tiled_flash_vs_brute(causal, block):
+    q, k, v = (rnd((2, 7, 2, 3), s) for s in (20, 21, 22))
+    s = 0.7
+    out = oa.tiled_flash_attention(q, k, v, s, causal, block, block)
+    ref = brute_attention(q, k, v, s, (lambda i, j: j <= i) if causal else (lambda i, j: True),
+                          eps=1e-6)
+    np.testing.assert_allclose(out, ref, rtol=1e-12, atol=1e-12)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("w", [0, 1, 3, 9])
+def test_sliding_window_vs_brute(causal, w):
+    q, k, v = (rnd((1, 9, 2, 3), s) for s in (23, 24, 25))
+    s = 0.9
+    out = oa.tiled_sliding_window_attention(q, k, v, w, s, causal, block_q=4)
+    allowed = (lambda i, j: abs(i - j) <= w and j <= i) if causal else (lambda i, j: abs(i - j) <= w)
+    ref = brute_attention(q, k, v, s, allowed, eps=1e-6)
+    np.testing.assert_allclose(out, ref, rtol=1e-12, atol=1e-12)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_chunked_cross_vs_brute(causal):
+    q = rnd((1, 5, 2, 3), 26); k = rnd((1, 11, 2, 3), 27); v = rnd((1, 11, 2, 3), 28)
+    s = 0.6
+    out = oa.chunked_cross_attention(q, k, v, chunk_size=4, scale=s, causal=causal)
+    ref = brute_attention(q, k, v, s, (lambda i, j: j <= i) if causal else (lambda i, j: True),
+                          eps=1e-6)
+    np.testing.assert_allclose(out, ref, rtol=1e-12, atol=1e-12)
+
+
+def test_attention_rows_vs_brute():
+    q, k, v = (rnd((1, 12, 1, 4), s) for s in (29, 30, 31))
+    rows = np.array([0, 5, 11])
+    out = oa.attention_rows(q[0, rows, 0], k[0, :, 0], v[0, :, 0], rows, 0.5, True, window_left=4)
+    ref = brute_attention(q, k, v, 0.5, lambda i, j: j <= i and i - j <= 4, eps=1e-6)
+    np.testing.assert_allclose(out, ref[0, rows, 0], rtol=1e-12, atol=1e-12)
+
+
+def _brute_paged(q, k_pool, v_pool, tables, lens, scale, bs, slopes=None):
+    """Rebuild each sequence's contiguous K/V from its pages, then loop."""
+    B, _, H, D = q.shape
+    out = np.zeros((B, 1, H, D))
+    for b in range(B):
+        toks = []
+        for t in range(int(lens[b])):
+            blk = int(tables[b, t // bs])
+            if blk >= 0:
+                toks.append((t, blk, t % bs))
+        for h in range(H):
+            sc = []
+            for t, blk, slot in toks:
+                x = sum(float(q[b, 0, h, d]) * float(k_pool[blk, slot, h, d]) for d in range(D)) * scale
+                if slopes is not None:
+                    x += float(slopes[h]) * (t - int(lens[b]))
+                sc.append(x)
+            m = max(sc)
+            w = [math.exp(x - m) for x in sc]
+            for wi, (t, blk, slot) in zip(w, toks):
+                out[b, 0, h] += wi * v_pool[blk, slot, h]
+            out[b, 0, h] /= sum(w)
+    return out
+
+
+@pytest.mark.parametrize("alibi", [False, True])
+def test_paged_decode_kat_tables(alibi):
+    # tests/cache/test_paged_attention.py:164-197 (tables and lengths)
+    rng = np.random.default_rng(32)
+    H, D, bs = 2, 4, 16
+    q = rng.standard_normal((4, 1, H, D)); kp = rng.standard_normal((20, bs, H, D))
+    vp = rng.standard_normal((20, bs, H, D))
+    lens = np.array([16, 32, 48, 25], np.int32)
+    tables = np.array([[0, -1, -1], [1, 2, -1], [3, 4, 5], [6, 7, -1]], np.int32)
+    slopes = op.get_alibi_slopes(H) if alibi else None
+    out = op.paged_attention(q, kp, vp, tables, lens, scale=0.5, block_size=bs, alibi_slopes=slopes)
+    ref = _brute_paged(q, kp, vp, tables, lens, 0.5, bs, slopes)
+    np.testing.assert_allclose(out, ref, rtol=1e-6, atol=1e-7)
+
+
+def test_paged_decode_single_token_and_invalid_page():
+    # ctx = [1] (tests/cache/test_paged_attention.py:232-259) and a -1 page
+    # inside the context that must be masked.
+    rng = np.random.default_rng(33)
+    q = rng.standard_normal((2, 1, 2, 4)); kp = rng.standard_normal((5, 4, 2, 4))
+    vp = rng.standard_normal((5, 4, 2, 4))
+    lens = np.array([1, 10], np.int32)
+    tables = np.array([[3, -1, -1], [0, -1, 2]], np.int32)
+    out = op.paged_attention(q, kp, vp, tables, lens, scale=1.0, block_size=4)
+    np.testing.assert_allclose(out[0, 0], vp[3, 0], rtol=1e-12)
+    ref = _brute_paged(q, kp, vp, tables, lens, 1.0, 4)
+    np.testing.assert_allclose(out, ref, rtol=1e-10, atol=1e-12)
+
+
+def test_paged_decode_empty_context_is_nan():
+    q = np.ones((1, 1, 1, 4)); kp = np.ones((2, 4, 1, 4))
+    out = op.paged_attention(q, kp, kp, np.array([[0]], np.int32), np.array([0], np.int32),
+                             block_size=4)
+    assert np.isnan(out).all()
+
+
+def test_paged_prefill_vs_brute():
+    rng = np.random.default_rng(34)
+    q = rng.standard_normal((1, 3, 1, 2)); kp = rng.standard_normal((3, 2, 1, 2))
+    vp = rng.standard_normal((3, 2, 1, 2))
+    tables = np.array([[2, 0]], np.int32); lens = np.array([4], np.int32)
+    out = op.paged_attention(q, kp, vp, tables, lens, scale=1.0, block_size=2, causal=True)
+    kc = np.concatenate([kp[2], kp[0]])[None]; vc = np.concatenate([vp[2], vp[0]])[None]
+    ref = brute_attention(q, kc, vc, 1.0, lambda i, j: j <= i)
+    np.testing.assert_allclose(out, ref, rtol=1e-10, atol=1e-12)
+
+
+def test_block_table_kats():
+    # tests/cache/test_paged_attention.py:311-333
+    t = op.create_block_table_from_lengths(np.array([16, 32, 48]), 16)
+    assert t.shape == (3, 3) and t[0, 0] == 0 and t[0, 1] == -1
+    np.testing.assert_array_equal(t, [[0, -1, -1], [1, 2, -1], [3, 4, 5]])
+    t = op.create_block_table_from_lengths(np.array([10, 25]), 16)
+    assert t.shape == (2, 2) and t[0, 1] == -1
+
+
+def test_alibi_slopes_kat():
+    # docstring of mlx_primitives/cache/paged_attention.py:33-35: 8 heads -> 2^-1 .. 2^-8
+    np.testing.assert_allclose(op.get_alibi_slopes(8), [2.0 ** -(i + 1) for i in range(8)])
+
+
+# ---- torch SDPA (library routine) ------------------------------------------------
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("layout", ["BSHD", "BHSD"])
+def test_flash_vs_sdpa(causal, layout):
+    q, k, v = (rnd((2, 47, 3, 16), s) for s in (40, 41, 42))
+    mask = causal_mask(47, 47) if causal else None
+    ref = sdpa(q, k, v, 0.25, mask)
+    if layout == "BHSD":
+        t = lambda x: np.ascontiguousarray(x.transpose(0, 2, 1, 3))
+        out = oa.flash_attention(t(q), t(k), t(v), 0.25, causal, layout="BHSD").transpose(0, 2, 1, 3)
+        tol = 1e-12
+    else:
+        out = oa.flash_attention(q, k, v, 0.25, causal, block_q=16, block_kv=8)
+        tol = 2e-6  # the tiled path's 1e-6 epsilon
+    np.testing.assert_allclose(out, ref, rtol=tol, atol=tol)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_window_vs_sdpa(causal):
+    q, k, v = (rnd((1, 70, 2, 8), s) for s in (43, 44, 45))
+    out = oa.sliding_window_attention(q, k, v, 20, scale=0.3, causal=causal)
+    ref = sdpa(q, k, v, 0.3, window_mask(70, 20, causal))
+    np.testing.assert_allclose(out, ref, rtol=2e-6, atol=2e-6)
+
+
+def test_chunked_vs_sdpa():
+    q = rnd((1, 33, 2, 8), 46); k = rnd((1, 300, 2, 8), 47); v = rnd((1, 300, 2, 8), 48)
+    out = oa.chunked_cross_attention(q, k, v, chunk_size=64, scale=0.4)
+    np.testing.assert_allclose(out, sdpa(q, k, v, 0.4), rtol=2e-6, atol=2e-6)
+
+
+# ---- invariants ------------------------------------------------------------------
+
+def test_block_size_independence():
+    q, k, v = (rnd((2, 64, 2, 16), s) for s in (50, 51, 52))
+    outs = [oa.tiled_flash_attention(q, k, v, 0.25, True, b, b) for b in (8, 16, 32, 64)]
+    for o in outs[1:]:
+        np.testing.assert_allclose(o, outs[0], rtol=1e-12, atol=1e-12)
+
+
+def test_chunk_size_independence():
+    q = rnd((2, 16, 2, 8), 53); k = rnd((2, 128, 2, 8), 54); v = rnd((2, 128, 2, 8), 55)
+    outs = [oa.chunked_cross_attention_impl(q, k, v, c, 0.3, False) for c in (8, 16, 32, 64, 128)]
+    for o in outs[1:]:
+        np.testing.assert_allclose(o, outs[0], rtol=1e-12, atol=1e-12)
+
+
+def test_merge_associative_and_commutative():
+    q = rnd((1, 4, 2, 8), 56); k = rnd((1, 24, 2, 8), 57); v = rnd((1, 24, 2, 8), 58)
+    parts = [oa.compute_chunk_attention(q, k[:, i:i + 8], v[:, i:i + 8], 0.5) for i in (0, 8, 16)]
+    a = oa.online_softmax_merge(*oa.online_softmax_merge(*parts[0], *parts[1]), *parts[2])
+    b = oa.online_softmax_merge(*parts[0], *oa.online_softmax_merge(*parts[1], *parts[2]))
+    c = oa.online_softmax_merge(*parts[2], *oa.online_softmax_merge(*parts[1], *parts[0]))
+    for x in (b, c):
+        np.testing.assert_allclose(x[0] / x[2][..., None], a[0] / a[2][..., None], rtol=1e-12)
+
+
+@pytest.mark.parametrize("mult", [10.0, 0.001])
+def test_no_nan_at_extreme_scales(mult):
+    # tests/attention/test_flash.py:163-211
+    q, k = rnd((1, 32, 4, 64), 59) * mult, rnd((1, 32, 4, 64), 60) * mult
+    v = rnd((1, 32, 4, 64), 61)
+    out = oa.flash_attention(q.astype(np.float32), k.astype(np.float32), v.astype(np.float32))
+    assert np.isfinite(out).all()
+
+
+# ---- planted mistakes are caught ---------------------------------------------------
+
+def test_pin_catches_merge_without_rescale(monkeypatch):
+    def bad_merge(ao, am, al, no, nm, nl):
+        gm = np.maximum(am, nm)
+        return ao + no, gm, al + nl  # forgets the exp(m - M) corrections
+    monkeypatch.setattr(oa, "online_softmax_merge", bad_merge)
+    with pytest.raises(AssertionError):
+        test_tiled_flash_vs_brute(True, 2)
+
+
+def test_pin_catches_window_off_by_one(monkeypatch):
+    orig = oa.windowed_chunk_attention
+
+    def bad(q, k, v, scale, causal, q_off, kv_off, w):
+        return orig(q, k, v, scale, causal, q_off, kv_off, w - 1)  # W keys instead of W+1
+    monkeypatch.setattr(oa, "windowed_chunk_attention", bad)
+    with pytest.raises(AssertionError):
+        test_sliding_window_vs_brute(True, 3)
+
+
+def test_pin_catches_transposed_causal_mask(monkeypatch):
+    orig = oa.compute_chunk_attention
+
+    def bad(q, k, v, scale, causal=False, q_offset=0, kv_offset=0):
+        return orig(q, k, v, scale, causal, kv_offset, q_offset)  # swapped offsets
+    monkeypatch.setattr(oa, "compute_chunk_attention", bad)
+    with pytest.raises(AssertionError):
+        test_tiled_flash_vs_brute(True, 3)
