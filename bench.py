@@ -196,7 +196,7 @@ def main() -> int:
                    "head_dim": cfg["D"], "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": achieved / PEAK_BF16_TFLOPS, "traffic": None,
-                     "kernel": "fa_fwd16_kernel<128,64,4,bf16>",
+                     "kernel": "fa_fwd16_kernel<128,64,8,bf16>",
                      "flop_per_launch": flops, "launch_ms": ev_ms},
         "cpu_baseline": cpu,
         "paged_decode": {

@@ -47,6 +47,23 @@ struct FwdParams {
   int neg;  // scale < 0: Q is negated on load (exact) and |scale| used
 };
 
+// Tile configuration (overridable at build time for tuning builds).
+// 16-bit kernel: 8 waves x 32 rows = 256 query rows per workgroup, two waves
+// per SIMD (<= 256 registers each) so one wave's softmax overlaps the other's
+// MFMAs. fp32 kernel: 4 waves.
+#ifndef MPX_FA_NWAVES
+#define MPX_FA_NWAVES 8
+#endif
+#ifndef MPX_FA_WAVES_PER_EU
+#define MPX_FA_WAVES_PER_EU 2
+#endif
+#ifndef MPX_FA_NWAVES_F32
+#define MPX_FA_NWAVES_F32 4
+#endif
+#ifndef MPX_FA_BN16
+#define MPX_FA_BN16 64
+#endif
+
 // Rescale threshold of the lazy running max, in log2 units.
 constexpr float kRescaleThreshold = 8.0f;
 
@@ -116,7 +133,8 @@ __device__ __forceinline__ void classify_tile(const FwdParams& p, int kv0, int q
 // of the PV step over keys [16*(2nb+h), +16) with k-group g = keys +8g..+8g+7.
 // ---------------------------------------------------------------------------
 template <int D, int BN, int NW, bool BF16>
-__global__ __launch_bounds__(64 * NW) void fa_fwd16_kernel(FwdParams p) {
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(MPX_FA_WAVES_PER_EU)))
+void fa_fwd16_kernel(FwdParams p) {
   constexpr int BM = 32 * NW, NT = 64 * NW;
   constexpr int KS = D + 8;   // K row stride (elements): 16-byte pad, conflict-free b128 reads
   constexpr int VS = BN + 8;  // V^T row stride (elements)
@@ -125,9 +143,15 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd16_kernel(FwdParams p) {
   constexpr int CPR = D / 8;  // 16-byte chunks per row
   constexpr int K_CHUNKS = BN * CPR;
   constexpr int K_PER_T = (K_CHUNKS + NT - 1) / NT;
-  constexpr int V_UNITS = (BN / 4) * CPR;  // 4 keys x 8 dims per unit
+  // V is staged as V^T in units of 2 keys x 8 dims (two 16-byte row chunks,
+  // eight 4-byte transposed words).
+  constexpr int V_UNITS = (BN / 2) * CPR;
   constexpr int V_PER_T = (V_UNITS + NT - 1) / NT;
-  static_assert(D % 32 == 0 && BN % 32 == 0, "tile shape");
+  constexpr int VXM = BN / 8 - 1;  // XOR mask of the V^T layout, in 16-byte chunks
+  static_assert(D % 32 == 0 && BN % 32 == 0 && BN <= 64, "tile shape");
+  // Stay within 128 KB of LDS per workgroup (a 136 KB configuration gave wrong
+  // results on gfx950).
+  static_assert(2 * STAGE * 2 <= 131072, "LDS budget");
 
   __shared__ __align__(16) uint16_t smem[2 * STAGE];
 
@@ -140,55 +164,94 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd16_kernel(FwdParams p) {
   kv_range<BM, BN>(p, q0, wi.split, kv_lo, t_begin, t_end);
 
   const uint16_t* __restrict__ Qp = (const uint16_t*)p.q + wi.b * p.q_sb + wi.h * p.q_sh;
-  const uint16_t* __restrict__ Kp = (const uint16_t*)p.k + wi.b * p.k_sb + wi.h * p.k_sh;
-  const uint16_t* __restrict__ Vp = (const uint16_t*)p.v + wi.b * p.v_sb + wi.h * p.v_sh;
+  const char* __restrict__ Kb = (const char*)((const uint16_t*)p.k + wi.b * p.k_sb + wi.h * p.k_sh);
+  const char* __restrict__ Vb = (const char*)((const uint16_t*)p.v + wi.b * p.v_sb + wi.h * p.v_sh);
 
   // Q^T as B operand, k-group g of 16-dim step ks = dims 16*ks + 8*g .. +8.
+  // Rows past Sq read the last row (never stored).
   const int wq0 = q0 + wave * 32;
   const int myq = wq0 + j;
   u32x4 qreg[NKS];
-  if (myq < p.Sq) {
-    const u32x4* src = (const u32x4*)(Qp + (int64_t)myq * p.q_ss);
+  {
+    const u32x4* src = (const u32x4*)(Qp + (int64_t)min(myq, p.Sq - 1) * p.q_ss);
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks) qreg[ks] = src[2 * ks + g];
-  } else {
-#pragma unroll
-    for (int ks = 0; ks < NKS; ++ks) qreg[ks] = (u32x4){0u, 0u, 0u, 0u};
   }
   if (p.neg) {
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks) qreg[ks] ^= 0x80008000u;
   }
+  // Drain Q now, so that the MFMAs reading qreg never wait on the K/V
+  // prefetches issued inside the loop (vmcnt completes in order).
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+
+  // Per-thread byte offsets of the prefetch loads inside a tile (32-bit; the
+  // host guarantees BN * seq_stride * 2 < 2^31).
+  uint32_t koff[K_PER_T];
+#pragma unroll
+  for (int i = 0; i < K_PER_T; ++i) {
+    const int c = tid + i * NT;
+    const int row = c / CPR, col = c - (c / CPR) * CPR;
+    koff[i] = (uint32_t)((row * p.k_ss + col * 8) * 2);
+  }
+  // V unit u: row pair kp = u / CPR, 16-byte column chunk dq = u % CPR (a wave
+  // reads whole rows).
+  uint32_t voff[V_PER_T][2];
+#pragma unroll
+  for (int i = 0; i < V_PER_T; ++i) {
+    const int u = tid + i * NT;
+    const int kp = u / CPR, dq = u - (u / CPR) * CPR;
+    voff[i][0] = (uint32_t)(((2 * kp) * p.v_ss + dq * 8) * 2);
+    voff[i][1] = (uint32_t)(((2 * kp + 1) * p.v_ss + dq * 8) * 2);
+  }
 
   u32x4 kbuf[K_PER_T];
-  u32x4 vbuf[V_PER_T * 4];
+  u32x4 vbuf[V_PER_T][2];
 
   auto load_tile = [&](int kv0) {
+    const char* kt = Kb + (int64_t)kv0 * p.k_ss * 2;
+    const char* vt = Vb + (int64_t)kv0 * p.v_ss * 2;
+    if (kv0 + BN <= p.Sk) {
 #pragma unroll
-    for (int i = 0; i < K_PER_T; ++i) {
-      const int c = tid + i * NT;
-      if (K_CHUNKS % NT == 0 || c < K_CHUNKS) {
-        const int row = c / CPR, col = c - (c / CPR) * CPR;
-        const int kv = kv0 + row;
-        kbuf[i] = kv < p.Sk ? *(const u32x4*)(Kp + (int64_t)kv * p.k_ss + col * 8)
-                            : (u32x4){0u, 0u, 0u, 0u};
+      for (int i = 0; i < K_PER_T; ++i)
+        if (K_CHUNKS % NT == 0 || tid + i * NT < K_CHUNKS) kbuf[i] = *(const u32x4*)(kt + koff[i]);
+#pragma unroll
+      for (int i = 0; i < V_PER_T; ++i)
+        if (V_UNITS % NT == 0 || tid + i * NT < V_UNITS) {
+          vbuf[i][0] = *(const u32x4*)(vt + voff[i][0]);
+          vbuf[i][1] = *(const u32x4*)(vt + voff[i][1]);
+        }
+    } else {
+      // Tail tile: rows past Sk read the last valid row; V rows past Sk are
+      // zeroed (their weights are 0, keep 0 * v finite).
+      const int lim = p.Sk - 1 - kv0;
+#pragma unroll
+      for (int i = 0; i < K_PER_T; ++i) {
+        const int c = tid + i * NT;
+        if (K_CHUNKS % NT == 0 || c < K_CHUNKS) {
+          const int row = min(c / CPR, lim), col = c - (c / CPR) * CPR;
+          kbuf[i] = *(const u32x4*)(kt + ((int64_t)row * p.k_ss + col * 8) * 2);
+        }
       }
-    }
 #pragma unroll
-    for (int i = 0; i < V_PER_T; ++i) {
-      const int u = tid + i * NT;
-      if (V_UNITS % NT == 0 || u < V_UNITS) {
-        const int kq = u / CPR, dq = u - (u / CPR) * CPR;
+      for (int i = 0; i < V_PER_T; ++i) {
+        const int u = tid + i * NT;
+        if (V_UNITS % NT == 0 || u < V_UNITS) {
+          const int kp = u / CPR, dq = u - (u / CPR) * CPR;
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-          const int kv = kv0 + 4 * kq + rr;
-          vbuf[4 * i + rr] = kv < p.Sk ? *(const u32x4*)(Vp + (int64_t)kv * p.v_ss + dq * 8)
-                                       : (u32x4){0u, 0u, 0u, 0u};
+          for (int r = 0; r < 2; ++r) {
+            const int row = 2 * kp + r;
+            const u32x4 x = *(const u32x4*)(vt + ((int64_t)min(row, lim) * p.v_ss + dq * 8) * 2);
+            vbuf[i][r] = row <= lim ? x : (u32x4){0u, 0u, 0u, 0u};
+          }
         }
       }
     }
   };
 
+  // V^T layout: element (d, kv) sits in 4-byte word (kv/2) ^ (4 * ((d/16) & VXM))
+  // of row d. The XOR keeps 16-byte groups of 8 keys intact for the b128
+  // operand reads and spreads one store instruction over all 64 banks.
   auto store_tile = [&](int stage) {
     uint16_t* Ks = smem + stage * STAGE;
     uint16_t* Vt = Ks + K_ELEMS;
@@ -200,21 +263,18 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd16_kernel(FwdParams p) {
         *(u32x4*)(Ks + row * KS + col * 8) = kbuf[i];
       }
     }
-    // V (4 keys x 8 dims) -> V^T (8 dims x 4 keys).
 #pragma unroll
     for (int i = 0; i < V_PER_T; ++i) {
       const int u = tid + i * NT;
       if (V_UNITS % NT == 0 || u < V_UNITS) {
-        const int kq = u / CPR, dq = u - (u / CPR) * CPR;
+        const int kp = u / CPR, dq = u - (u / CPR) * CPR;
+        const int word = kp ^ (4 * ((dq >> 1) & VXM));
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
-          const u32 r0 = vbuf[4 * i + 0][jj], r1 = vbuf[4 * i + 1][jj];
-          const u32 r2 = vbuf[4 * i + 2][jj], r3 = vbuf[4 * i + 3][jj];
-          const u32x2 lo = {(r0 & 0xffffu) | (r1 << 16), (r2 & 0xffffu) | (r3 << 16)};
-          const u32x2 hi = {(r0 >> 16) | (r1 & 0xffff0000u), (r2 >> 16) | (r3 & 0xffff0000u)};
+          const u32 r0 = vbuf[i][0][jj], r1 = vbuf[i][1][jj];
           const int d = dq * 8 + 2 * jj;
-          *(u32x2*)(Vt + d * VS + 4 * kq) = lo;
-          *(u32x2*)(Vt + (d + 1) * VS + 4 * kq) = hi;
+          *(u32*)(Vt + d * VS + 2 * word) = (r0 & 0xffffu) | (r1 << 16);
+          *(u32*)(Vt + (d + 1) * VS + 2 * word) = (r0 >> 16) | (r1 & 0xffff0000u);
         }
       }
     }
@@ -229,6 +289,13 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd16_kernel(FwdParams p) {
   const float c = p.c;
 
   const int krow_perm = (j & ~12) | ((j & 4) << 1) | ((j & 8) >> 1);
+  // Visible keys of this lane's query row: [kv_first, kv_last].
+  const int kv_first = p.win_left >= 0 ? myq - p.win_left : -(1 << 30);
+  const int kv_last = min(p.win_right >= 0 ? myq + p.win_right : (1 << 30), p.Sk - 1);
+  // V^T operand rows d = 32*db + j; their XOR pattern in 16-byte units.
+  int vxor[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) vxor[db] = ((db * 32 + j) >> 4) & VXM;
 
   if (t_begin < t_end) {
     load_tile(kv_lo + t_begin * BN);
@@ -251,10 +318,13 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd16_kernel(FwdParams p) {
       f32x16 s[NB];
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) {
-        s[nb] = (f32x16){};
         const u32x4* kp = (const u32x4*)(Ks + (nb * 32 + krow_perm) * KS) + g;
+        u32x4 ka[NKS];
 #pragma unroll
-        for (int ks = 0; ks < NKS; ++ks) s[nb] = mfma32x32x16<BF16>(kp[2 * ks], qreg[ks], s[nb]);
+        for (int ks = 0; ks < NKS; ++ks) ka[ks] = kp[2 * ks];
+        s[nb] = (f32x16){};
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) s[nb] = mfma32x32x16<BF16>(ka[ks], qreg[ks], s[nb]);
       }
 
       if (!full) {
@@ -263,7 +333,7 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd16_kernel(FwdParams p) {
 #pragma unroll
           for (int e = 0; e < 16; ++e) {
             const int kv = kv0 + nb * 32 + 16 * (e >> 3) + 8 * g + (e & 7);
-            if (!kv_valid(p, myq, kv)) s[nb][e] = -INFINITY;
+            s[nb][e] = ((kv >= kv_first) & (kv <= kv_last)) ? s[nb][e] : -INFINITY;
           }
       }
 
@@ -304,9 +374,12 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd16_kernel(FwdParams p) {
 
 #pragma unroll
       for (int db = 0; db < NDB; ++db) {
-        const u32x4* vp = (const u32x4*)(Vt + (db * 32 + j) * VS) + g;
+        const u32x4* vp = (const u32x4*)(Vt + (db * 32 + j) * VS);
+        u32x4 va[NSL];
 #pragma unroll
-        for (int sl = 0; sl < NSL; ++sl) o[db] = mfma32x32x16<BF16>(vp[2 * sl], pop[sl], o[db]);
+        for (int sl = 0; sl < NSL; ++sl) va[sl] = vp[(2 * sl + g) ^ vxor[db]];
+#pragma unroll
+        for (int sl = 0; sl < NSL; ++sl) o[db] = mfma32x32x16<BF16>(va[sl], pop[sl], o[db]);
       }
     }
 
@@ -366,6 +439,7 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd32_kernel(FwdParams p) {
   constexpr int CHUNKS = BN * CPR;
   constexpr int PER_T = (CHUNKS + NT - 1) / NT;
   static_assert(D % 32 == 0 && BN % 32 == 0, "tile shape");
+  static_assert(2 * STAGE * 4 <= 131072, "LDS budget");
 
   __shared__ __align__(16) float smem[2 * STAGE];
 
@@ -598,7 +672,8 @@ __global__ __launch_bounds__(256) void fa_split_merge_kernel(const float* __rest
 // ---------------------------------------------------------------------------
 namespace {
 
-constexpr int kNumWaves = 4;          // 4 waves x 32 rows = 128 query rows per workgroup
+constexpr int kNumWaves16 = MPX_FA_NWAVES;     // waves per workgroup, 16-bit kernel
+constexpr int kNumWaves32 = MPX_FA_NWAVES_F32; // waves per workgroup, fp32 kernel
 constexpr int kTargetWorkgroups = 512; // 256 CUs x 2 resident workgroups
 
 struct Plan {
@@ -606,12 +681,15 @@ struct Plan {
   size_t ws_bytes;
 };
 
-int tile_n(int D, int dtype) { return (dtype == MPX_F32 && D > 64) ? 32 : 64; }
+int tile_n(int D, int dtype) {
+  if (dtype == MPX_F32) return D > 64 ? 32 : 64;
+  return MPX_FA_BN16;
+}
 
 Plan make_plan(int B, int H, int Sq, int Sk, int D, int causal, int window_left,
                int window_right, int dtype) {
   Plan pl;
-  pl.BM = 32 * kNumWaves;
+  pl.BM = 32 * (dtype == MPX_F32 ? kNumWaves32 : kNumWaves16);
   pl.BN = tile_n(D, dtype);
   pl.win_left = window_left < 0 ? -1 : window_left;
   pl.win_right = causal ? 0 : (window_right < 0 ? -1 : window_right);
@@ -642,11 +720,11 @@ Plan make_plan(int B, int H, int Sq, int Sk, int D, int causal, int window_left,
 template <int D, int BN, bool F32, bool BF16>
 hipError_t launch_fwd(const FwdParams& p, int grid, hipStream_t stream) {
   if constexpr (F32) {
-    hipLaunchKernelGGL((fa_fwd32_kernel<D, BN, kNumWaves>), dim3(grid), dim3(64 * kNumWaves), 0,
-                       stream, p);
+    hipLaunchKernelGGL((fa_fwd32_kernel<D, BN, kNumWaves32>), dim3(grid), dim3(64 * kNumWaves32),
+                       0, stream, p);
   } else {
-    hipLaunchKernelGGL((fa_fwd16_kernel<D, BN, kNumWaves, BF16>), dim3(grid),
-                       dim3(64 * kNumWaves), 0, stream, p);
+    hipLaunchKernelGGL((fa_fwd16_kernel<D, BN, kNumWaves16, BF16>), dim3(grid),
+                       dim3(64 * kNumWaves16), 0, stream, p);
   }
   return hipGetLastError();
 }
@@ -660,15 +738,15 @@ hipError_t dispatch_fwd(const FwdParams& p, int D, int dtype, int grid, hipStrea
     }
   } else if (dtype == MPX_BF16) {
     switch (D) {
-      case 32: return launch_fwd<32, 64, false, true>(p, grid, st);
-      case 64: return launch_fwd<64, 64, false, true>(p, grid, st);
-      default: return launch_fwd<128, 64, false, true>(p, grid, st);
+      case 32: return launch_fwd<32, MPX_FA_BN16, false, true>(p, grid, st);
+      case 64: return launch_fwd<64, MPX_FA_BN16, false, true>(p, grid, st);
+      default: return launch_fwd<128, MPX_FA_BN16, false, true>(p, grid, st);
     }
   } else {
     switch (D) {
-      case 32: return launch_fwd<32, 64, false, false>(p, grid, st);
-      case 64: return launch_fwd<64, 64, false, false>(p, grid, st);
-      default: return launch_fwd<128, 64, false, false>(p, grid, st);
+      case 32: return launch_fwd<32, MPX_FA_BN16, false, false>(p, grid, st);
+      case 64: return launch_fwd<64, MPX_FA_BN16, false, false>(p, grid, st);
+      default: return launch_fwd<128, MPX_FA_BN16, false, false>(p, grid, st);
     }
   }
 }

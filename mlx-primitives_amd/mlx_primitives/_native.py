@@ -18,7 +18,9 @@ from typing import Optional, Sequence
 
 import torch
 
-_LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libmpx_attn.so")
+# MPX_ATTN_LIB selects another build of the library (e.g. a tuning variant).
+_LIB_PATH = os.environ.get("MPX_ATTN_LIB") or os.path.join(
+    os.path.dirname(os.path.abspath(__file__)), "_lib", "libmpx_attn.so")
 
 MPX_OK = 0
 MPX_EINVAL = -1

@@ -95,9 +95,16 @@ def test_flash_explicit_scale(device, scale):
 @pytest.mark.parametrize("mult", [10.0, 0.001])
 def test_flash_extreme_input_scales(device, mult):
     # tests/attention/test_flash.py:163-211: no NaN/Inf at x10 / x0.001
+    # At x10 the logits reach ~1e2: fp32 rounding of q.k (~1e-7 * |q||k|) alone moves
+    # the weights by ~1e-4 relative, so the comparison with the float64 oracle uses a
+    # 1e-3 relative bound there; the reference checks only finiteness.
     (q, k, v), (qn, kn, vn) = inputs([(1, 64, 4, 64)] * 3, torch.float32, 8, device, mult)
     out = flash_attention(q, k, v, causal=True)
-    check(out, oa.flash_attention(qn, kn, vn, causal=True), torch.float32)
+    got = out.double().cpu().numpy()
+    assert np.isfinite(got).all()
+    rtol = 1e-3 if mult > 1 else F32_RTOL
+    np.testing.assert_allclose(got, oa.flash_attention(qn, kn, vn, causal=True), rtol=rtol,
+                               atol=F32_ATOL)
 
 
 def test_flash_non_contiguous_inputs(device):
