@@ -43,6 +43,8 @@ struct FwdParams {
   int B, H, Sq, Sk;
   int win_left, win_right;  // -1 = unbounded
   int n_qtiles, num_splits, tiles_per_split;
+  int n_slots;  // q-tile slots per (batch, head)
+  int paired;   // a slot runs q-tiles n_qtiles-1-slot and slot (causal balance)
   float c;  // |scale| * log2(e)
   int neg;  // scale < 0: Q is negated on load (exact) and |scale| used
 };
@@ -57,6 +59,12 @@ struct FwdParams {
 #ifndef MPX_FA_WAVES_PER_EU
 #define MPX_FA_WAVES_PER_EU 2
 #endif
+#ifndef MPX_FA_SCHED
+#define MPX_FA_SCHED 2
+#endif
+#ifndef MPX_FA_PRIO
+#define MPX_FA_PRIO 0
+#endif
 #ifndef MPX_FA_NWAVES_F32
 #define MPX_FA_NWAVES_F32 4
 #endif
@@ -64,29 +72,56 @@ struct FwdParams {
 #define MPX_FA_BN16 64
 #endif
 
+// Compile-time integer tag (selects a register set in the unrolled loop).
+template <int N>
+struct Const {
+  static constexpr int value = N;
+};
+
+// Raw buffer resource flags (word 3) for gfx950 buffer loads.
+constexpr int kBufferFlags = 0x00020000;
+
 // Rescale threshold of the lazy running max, in log2 units.
 constexpr float kRescaleThreshold = 8.0f;
 
-// Work item of this workgroup. Consecutive workgroup ids are dealt round-robin
-// to the 8 XCDs; the remap gives every XCD a contiguous slice of the work so
-// the q-tiles of one (batch, head) share that XCD's L2 for their K/V reads.
-// Within a (batch, head) the q-tiles run longest (most KV tiles) first.
+// Work of a workgroup: one slot (batch*head, slot, split). Consecutive
+// workgroup ids are dealt round-robin to the 8 XCDs; the remap gives every XCD
+// a contiguous slice of the work so the q-tiles of one (batch, head) share that
+// XCD's L2 for their K/V reads.
+struct WorkSlot {
+  int bh, slot, split;
+};
+
 struct WorkItem {
   int b, h, qt, split;
 };
 
-__device__ __forceinline__ WorkItem decode_work(const FwdParams& p) {
+__device__ __forceinline__ WorkSlot decode_slot(const FwdParams& p) {
   const int L = blockIdx.x, N = gridDim.x;
   const int w = (N & 7) == 0 ? (L & 7) * (N >> 3) + (L >> 3) : L;
-  const int per_bh = p.n_qtiles * p.num_splits;
-  const int bh = w / per_bh;
-  const int r = w - bh * per_bh;
-  const int qi = r / p.num_splits;
+  const int per_bh = p.n_slots * p.num_splits;
+  WorkSlot ws;
+  ws.bh = w / per_bh;
+  const int r = w - ws.bh * per_bh;
+  ws.slot = r / p.num_splits;
+  ws.split = r - ws.slot * p.num_splits;
+  return ws;
+}
+
+// A slot runs q-tile n_qtiles-1-slot (the longest KV range first) and, in a
+// paired launch, then q-tile `slot`: under a causal mask the two ranges add up
+// to the same number of KV tiles for every slot, so all workgroups finish
+// together instead of the last-dispatched long q-tiles trailing the launch.
+__device__ __forceinline__ int slot_items(const FwdParams& p, const WorkSlot& ws) {
+  return p.paired && ws.slot < p.n_qtiles - 1 - ws.slot ? 2 : 1;
+}
+
+__device__ __forceinline__ WorkItem slot_item(const FwdParams& p, const WorkSlot& ws, int item) {
   WorkItem wi;
-  wi.qt = p.n_qtiles - 1 - qi;
-  wi.split = r - qi * p.num_splits;
-  wi.b = bh / p.H;
-  wi.h = bh - wi.b * p.H;
+  wi.qt = item == 0 ? p.n_qtiles - 1 - ws.slot : ws.slot;
+  wi.split = ws.split;
+  wi.b = ws.bh / p.H;
+  wi.h = ws.bh - wi.b * p.H;
   return wi;
 }
 
@@ -132,13 +167,22 @@ __device__ __forceinline__ void classify_tile(const FwdParams& p, int kv0, int q
 // of query j, so elements 8h..8h+7 are 8 consecutive keys: exactly the B operand
 // of the PV step over keys [16*(2nb+h), +16) with k-group g = keys +8g..+8g+7.
 // ---------------------------------------------------------------------------
+// LDS stage of the 16-bit kernel: BN K rows of stride D+8 (16-byte pad,
+// conflict-free b128 reads) and D V^T rows of stride BN+8, in elements.
+template <int D, int BN>
+constexpr int fa16_stage_elems() {
+  return BN * (D + 8) + D * (BN + 8);
+}
+
+// Query rows [32*NW*wi.qt, +32*NW) of one (batch, head) against its KV range.
 template <int D, int BN, int NW, bool BF16>
-__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(MPX_FA_WAVES_PER_EU)))
-void fa_fwd16_kernel(FwdParams p) {
+__device__ __forceinline__ void fa16_rows(const FwdParams& p, const WorkItem wi,
+                                          uint16_t* __restrict__ smem) {
   constexpr int BM = 32 * NW, NT = 64 * NW;
-  constexpr int KS = D + 8;   // K row stride (elements): 16-byte pad, conflict-free b128 reads
+  constexpr int KS = D + 8;   // K row stride (elements)
   constexpr int VS = BN + 8;  // V^T row stride (elements)
   constexpr int K_ELEMS = BN * KS, V_ELEMS = D * VS, STAGE = K_ELEMS + V_ELEMS;
+  static_assert(STAGE == fa16_stage_elems<D, BN>(), "stage layout");
   constexpr int NB = BN / 32, NSL = BN / 16, NKS = D / 16, NDB = D / 32;
   constexpr int CPR = D / 8;  // 16-byte chunks per row
   constexpr int K_CHUNKS = BN * CPR;
@@ -149,23 +193,25 @@ void fa_fwd16_kernel(FwdParams p) {
   constexpr int V_PER_T = (V_UNITS + NT - 1) / NT;
   constexpr int VXM = BN / 8 - 1;  // XOR mask of the V^T layout, in 16-byte chunks
   static_assert(D % 32 == 0 && BN % 32 == 0 && BN <= 64, "tile shape");
-  // Stay within 128 KB of LDS per workgroup (a 136 KB configuration gave wrong
-  // results on gfx950).
-  static_assert(2 * STAGE * 2 <= 131072, "LDS budget");
 
-  __shared__ __align__(16) uint16_t smem[2 * STAGE];
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // The wave index is made an SGPR value so per-wave tile decisions (skip,
+  // diagonal masking) compile to scalar branches.
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int j = lane & 31, g = lane >> 5;
 
-  const WorkItem wi = decode_work(p);
   const int q0 = wi.qt * BM;
   int kv_lo, t_begin, t_end;
   kv_range<BM, BN>(p, q0, wi.split, kv_lo, t_begin, t_end);
 
   const uint16_t* __restrict__ Qp = (const uint16_t*)p.q + wi.b * p.q_sb + wi.h * p.q_sh;
-  const char* __restrict__ Kb = (const char*)((const uint16_t*)p.k + wi.b * p.k_sb + wi.h * p.k_sh);
-  const char* __restrict__ Vb = (const char*)((const uint16_t*)p.v + wi.b * p.v_sb + wi.h * p.v_sh);
+  // K/V of this (batch, head) through buffer resources: SGPR base, 32-bit
+  // offsets (the host guarantees Sk * seq_stride * 2 < 2^31), no per-load
+  // address arithmetic.
+  const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)((const uint16_t*)p.k + wi.b * p.k_sb + wi.h * p.k_sh), 0, 0x7fffffff, kBufferFlags);
+  const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)((const uint16_t*)p.v + wi.b * p.v_sb + wi.h * p.v_sh), 0, 0x7fffffff, kBufferFlags);
 
   // Q^T as B operand, k-group g of 16-dim step ks = dims 16*ks + 8*g .. +8.
   // Rows past Sq read the last row (never stored).
@@ -185,52 +231,64 @@ void fa_fwd16_kernel(FwdParams p) {
   // prefetches issued inside the loop (vmcnt completes in order).
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
 
-  // Per-thread byte offsets of the prefetch loads inside a tile (32-bit; the
-  // host guarantees BN * seq_stride * 2 < 2^31).
-  uint32_t koff[K_PER_T];
+  // Per-thread byte offsets of the prefetch loads inside a tile.
+  int koff[K_PER_T];
 #pragma unroll
   for (int i = 0; i < K_PER_T; ++i) {
     const int c = tid + i * NT;
     const int row = c / CPR, col = c - (c / CPR) * CPR;
-    koff[i] = (uint32_t)((row * p.k_ss + col * 8) * 2);
+    koff[i] = (int)((row * p.k_ss + col * 8) * 2);
   }
   // V unit u: row pair kp = u / CPR, 16-byte column chunk dq = u % CPR (a wave
   // reads whole rows).
-  uint32_t voff[V_PER_T][2];
+  int voff[V_PER_T][2];
 #pragma unroll
   for (int i = 0; i < V_PER_T; ++i) {
     const int u = tid + i * NT;
     const int kp = u / CPR, dq = u - (u / CPR) * CPR;
-    voff[i][0] = (uint32_t)(((2 * kp) * p.v_ss + dq * 8) * 2);
-    voff[i][1] = (uint32_t)(((2 * kp + 1) * p.v_ss + dq * 8) * 2);
+    voff[i][0] = (int)(((2 * kp) * p.v_ss + dq * 8) * 2);
+    voff[i][1] = (int)(((2 * kp + 1) * p.v_ss + dq * 8) * 2);
   }
 
-  u32x4 kbuf[K_PER_T];
-  u32x4 vbuf[V_PER_T][2];
+  // Prefetch registers, two sets: tile i+2 is loaded into set i%2 while tile
+  // i computes and tile i+1 (loaded one iteration earlier) is staged to LDS,
+  // so a load has two tile times to arrive.
+  u32x4 kbuf[2][K_PER_T];
+  u32x4 vbuf[2][V_PER_T][2];
+  // Rows of a staged tile at or past v_rows are zeroed when V is stored (BN
+  // except for the tail tile).
+  int v_rows[2] = {BN, BN};
 
-  auto load_tile = [&](int kv0) {
-    const char* kt = Kb + (int64_t)kv0 * p.k_ss * 2;
-    const char* vt = Vb + (int64_t)kv0 * p.v_ss * 2;
+  // The loads never depend on data (no selects): a select on a loaded value
+  // would make the compiler wait for the prefetch right after issuing it.
+  auto load_tile = [&](int kv0, auto SET) __attribute__((always_inline)) {
+    constexpr int S = decltype(SET)::value;
+    const int kso = kv0 * (int)p.k_ss * 2, vso = kv0 * (int)p.v_ss * 2;
     if (kv0 + BN <= p.Sk) {
+      v_rows[S] = BN;
 #pragma unroll
       for (int i = 0; i < K_PER_T; ++i)
-        if (K_CHUNKS % NT == 0 || tid + i * NT < K_CHUNKS) kbuf[i] = *(const u32x4*)(kt + koff[i]);
+        if (K_CHUNKS % NT == 0 || tid + i * NT < K_CHUNKS)
+          kbuf[S][i] = __builtin_amdgcn_raw_buffer_load_b128(krs, koff[i], kso, 0);
 #pragma unroll
       for (int i = 0; i < V_PER_T; ++i)
         if (V_UNITS % NT == 0 || tid + i * NT < V_UNITS) {
-          vbuf[i][0] = *(const u32x4*)(vt + voff[i][0]);
-          vbuf[i][1] = *(const u32x4*)(vt + voff[i][1]);
+          vbuf[S][i][0] = __builtin_amdgcn_raw_buffer_load_b128(vrs, voff[i][0], vso, 0);
+          vbuf[S][i][1] = __builtin_amdgcn_raw_buffer_load_b128(vrs, voff[i][1], vso, 0);
         }
     } else {
-      // Tail tile: rows past Sk read the last valid row; V rows past Sk are
-      // zeroed (their weights are 0, keep 0 * v finite).
+      // Tail tile: rows past Sk re-read the last valid row (K rows there are
+      // masked; V rows are zeroed at store time).
+      asm volatile("" ::: "memory");
+      v_rows[S] = p.Sk - kv0;
       const int lim = p.Sk - 1 - kv0;
 #pragma unroll
       for (int i = 0; i < K_PER_T; ++i) {
         const int c = tid + i * NT;
         if (K_CHUNKS % NT == 0 || c < K_CHUNKS) {
           const int row = min(c / CPR, lim), col = c - (c / CPR) * CPR;
-          kbuf[i] = *(const u32x4*)(kt + ((int64_t)row * p.k_ss + col * 8) * 2);
+          kbuf[S][i] = __builtin_amdgcn_raw_buffer_load_b128(
+              krs, (row * (int)p.k_ss + col * 8) * 2, kso, 0);
         }
       }
 #pragma unroll
@@ -239,11 +297,9 @@ void fa_fwd16_kernel(FwdParams p) {
         if (V_UNITS % NT == 0 || u < V_UNITS) {
           const int kp = u / CPR, dq = u - (u / CPR) * CPR;
 #pragma unroll
-          for (int r = 0; r < 2; ++r) {
-            const int row = 2 * kp + r;
-            const u32x4 x = *(const u32x4*)(vt + ((int64_t)min(row, lim) * p.v_ss + dq * 8) * 2);
-            vbuf[i][r] = row <= lim ? x : (u32x4){0u, 0u, 0u, 0u};
-          }
+          for (int r = 0; r < 2; ++r)
+            vbuf[S][i][r] = __builtin_amdgcn_raw_buffer_load_b128(
+                vrs, (min(2 * kp + r, lim) * (int)p.v_ss + dq * 8) * 2, vso, 0);
         }
       }
     }
@@ -252,15 +308,27 @@ void fa_fwd16_kernel(FwdParams p) {
   // V^T layout: element (d, kv) sits in 4-byte word (kv/2) ^ (4 * ((d/16) & VXM))
   // of row d. The XOR keeps 16-byte groups of 8 keys intact for the b128
   // operand reads and spreads one store instruction over all 64 banks.
-  auto store_tile = [&](int stage) {
-    uint16_t* Ks = smem + stage * STAGE;
+  // Register set S is staged into LDS stage S.
+  auto store_tile = [&](auto SET) __attribute__((always_inline)) {
+    constexpr int S = decltype(SET)::value;
+    uint16_t* Ks = smem + S * STAGE;
     uint16_t* Vt = Ks + K_ELEMS;
 #pragma unroll
     for (int i = 0; i < K_PER_T; ++i) {
       const int c = tid + i * NT;
       if (K_CHUNKS % NT == 0 || c < K_CHUNKS) {
         const int row = c / CPR, col = c - (c / CPR) * CPR;
-        *(u32x4*)(Ks + row * KS + col * 8) = kbuf[i];
+        *(u32x4*)(Ks + row * KS + col * 8) = kbuf[S][i];
+      }
+    }
+    if (v_rows[S] < BN) {
+      asm volatile("" ::: "memory");
+#pragma unroll
+      for (int i = 0; i < V_PER_T; ++i) {
+        const int kp = (tid + i * NT) / CPR;
+#pragma unroll
+        for (int r = 0; r < 2; ++r)
+          if (2 * kp + r >= v_rows[S]) vbuf[S][i][r] = (u32x4){0u, 0u, 0u, 0u};
       }
     }
 #pragma unroll
@@ -271,10 +339,10 @@ void fa_fwd16_kernel(FwdParams p) {
         const int word = kp ^ (4 * ((dq >> 1) & VXM));
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
-          const u32 r0 = vbuf[i][0][jj], r1 = vbuf[i][1][jj];
+          const u32 r0 = vbuf[S][i][0][jj], r1 = vbuf[S][i][1][jj];
           const int d = dq * 8 + 2 * jj;
-          *(u32*)(Vt + d * VS + 2 * word) = (r0 & 0xffffu) | (r1 << 16);
-          *(u32*)(Vt + (d + 1) * VS + 2 * word) = (r0 >> 16) | (r1 & 0xffff0000u);
+          *(u32*)(Vt + d * VS + 2 * word) = __builtin_amdgcn_perm(r1, r0, 0x05040100u);
+          *(u32*)(Vt + (d + 1) * VS + 2 * word) = __builtin_amdgcn_perm(r1, r0, 0x07060302u);
         }
       }
     }
@@ -292,100 +360,145 @@ void fa_fwd16_kernel(FwdParams p) {
   // Visible keys of this lane's query row: [kv_first, kv_last].
   const int kv_first = p.win_left >= 0 ? myq - p.win_left : -(1 << 30);
   const int kv_last = min(p.win_right >= 0 ? myq + p.win_right : (1 << 30), p.Sk - 1);
-  // V^T operand rows d = 32*db + j; their XOR pattern in 16-byte units.
-  int vxor[NDB];
-#pragma unroll
-  for (int db = 0; db < NDB; ++db) vxor[db] = ((db * 32 + j) >> 4) & VXM;
+  // V^T operand of lane (j, g) for dims 32*db + j and keys 16*sl + 8*g .. +8:
+  // chunk (2*sl + g) ^ ((2*db + j/16) & VXM) = 2*(sl ^ (db & VXM/2)) + (g ^ j/16),
+  // so one lane base plus compile-time offsets addresses every operand.
+  const int vlane = j * (VS / 8) + (g ^ ((j >> 4) & 1));
 
-  if (t_begin < t_end) {
-    load_tile(kv_lo + t_begin * BN);
-    store_tile(0);
-  }
-  __syncthreads();
-
-  for (int t = t_begin; t < t_end; ++t) {
-    const int stage = (t - t_begin) & 1;
-    const int kv0 = kv_lo + t * BN;
-    const bool has_next = t + 1 < t_end;
-    if (has_next) load_tile(kv0 + BN);
-
+  // Attention of this wave's rows to the tile at kv0 staged in LDS stage `stage`.
+  auto compute_tile = [&](int stage, int kv0) __attribute__((always_inline)) {
     bool skip, full;
     classify_tile<BN>(p, kv0, wq0, wq0 + 31, skip, full);
-    if (!skip) {
-      const uint16_t* Ks = smem + stage * STAGE;
-      const uint16_t* Vt = Ks + K_ELEMS;
+    if (skip) return;
+    const uint16_t* Ks = smem + stage * STAGE;
+    const uint16_t* Vt = Ks + K_ELEMS;
 
-      f32x16 s[NB];
+    f32x16 s[NB];
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb) {
-        const u32x4* kp = (const u32x4*)(Ks + (nb * 32 + krow_perm) * KS) + g;
-        u32x4 ka[NKS];
+    for (int nb = 0; nb < NB; ++nb) {
+      const u32x4* kp = (const u32x4*)(Ks + (nb * 32 + krow_perm) * KS) + g;
+      u32x4 ka[NKS];
 #pragma unroll
-        for (int ks = 0; ks < NKS; ++ks) ka[ks] = kp[2 * ks];
-        s[nb] = (f32x16){};
+      for (int ks = 0; ks < NKS; ++ks) ka[ks] = kp[2 * ks];
+      s[nb] = (f32x16){};
 #pragma unroll
-        for (int ks = 0; ks < NKS; ++ks) s[nb] = mfma32x32x16<BF16>(ka[ks], qreg[ks], s[nb]);
-      }
+      for (int ks = 0; ks < NKS; ++ks) s[nb] = mfma32x32x16<BF16>(ka[ks], qreg[ks], s[nb]);
+    }
+#if MPX_FA_SCHED >= 1
+    // Keep the K operand reads of block nb+1 in flight under the MFMAs of block nb.
+    __builtin_amdgcn_sched_group_barrier(0x100, NKS, 0);
+#pragma unroll
+    for (int i = 0; i < NKS * (NB - 1); ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, NKS, 0);
+#endif
 
-      if (!full) {
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-          for (int e = 0; e < 16; ++e) {
-            const int kv = kv0 + nb * 32 + 16 * (e >> 3) + 8 * g + (e & 7);
-            s[nb][e] = ((kv >= kv_first) & (kv <= kv_last)) ? s[nb][e] : -INFINITY;
-          }
-      }
-
-      float mt = -INFINITY;
+    if (!full) {
+      // The empty volatile asm keeps this a real (scalar) branch: without it
+      // the selects are folded into unconditional code run on every tile.
+      asm volatile("" ::: "memory");
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) mt = fmaxf(mt, s[nb][e]);
-      mt = fmaxf(mt, xor32(mt)) * c;
-      m_max = fmaxf(m_max, mt);
-
-      if (__any(mt > m_run + kRescaleThreshold)) {
-        const float m_new = fmaxf(m_run, mt);
-        const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(m_run - m_new);
-        l_run *= alpha;
-#pragma unroll
-        for (int db = 0; db < NDB; ++db)
-#pragma unroll
-          for (int e = 0; e < 16; ++e) o[db][e] *= alpha;
-        m_run = m_new;
-      }
-      const float msub = m_run == -INFINITY ? 0.f : m_run;
-
-      u32x4 pop[NSL];
-      float lsum = 0.f;
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-        for (int hh = 0; hh < 2; ++hh)
-#pragma unroll
-          for (int e2 = 0; e2 < 4; ++e2) {
-            const float x0 = fast_exp2(s[nb][8 * hh + 2 * e2] * c - msub);
-            const float x1 = fast_exp2(s[nb][8 * hh + 2 * e2 + 1] * c - msub);
-            lsum += x0 + x1;
-            pop[2 * nb + hh][e2] = pack2<BF16>(x0, x1);
-          }
-      l_run += lsum;
-
-#pragma unroll
-      for (int db = 0; db < NDB; ++db) {
-        const u32x4* vp = (const u32x4*)(Vt + (db * 32 + j) * VS);
-        u32x4 va[NSL];
-#pragma unroll
-        for (int sl = 0; sl < NSL; ++sl) va[sl] = vp[(2 * sl + g) ^ vxor[db]];
-#pragma unroll
-        for (int sl = 0; sl < NSL; ++sl) o[db] = mfma32x32x16<BF16>(va[sl], pop[sl], o[db]);
-      }
+        for (int e = 0; e < 16; ++e) {
+          const int kv = kv0 + nb * 32 + 16 * (e >> 3) + 8 * g + (e & 7);
+          s[nb][e] = ((kv >= kv_first) & (kv <= kv_last)) ? s[nb][e] : -INFINITY;
+        }
     }
 
-    if (has_next) store_tile(stage ^ 1);
-    __syncthreads();
+    float mt = -INFINITY;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) mt = fmaxf(mt, s[nb][e]);
+    mt = fmaxf(mt, xor32(mt)) * c;
+    m_max = fmaxf(m_max, mt);
+
+    if (__any(mt > m_run + kRescaleThreshold)) {
+      asm volatile("" ::: "memory");  // a real branch, not selects on all of o
+      const float m_new = fmaxf(m_run, mt);
+      const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(m_run - m_new);
+      l_run *= alpha;
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) o[db][e] *= alpha;
+      m_run = m_new;
+    }
+    const float msub = m_run == -INFINITY ? 0.f : m_run;
+
+    // P = exp2(s*c - m), packed to 16 bits; the row sum accumulates the
+    // packed (rounded) weights, the exact weights the PV product uses.
+    u32x4 pop[NSL];
+    float lsum = 0.f;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+        for (int e2 = 0; e2 < 4; ++e2) {
+          const float x0 = fast_exp2(s[nb][8 * hh + 2 * e2] * c - msub);
+          const float x1 = fast_exp2(s[nb][8 * hh + 2 * e2 + 1] * c - msub);
+          const u32 pk = pack2<BF16>(x0, x1);
+          pop[2 * nb + hh][e2] = pk;
+          lsum = dot2_sum<BF16>(pk, lsum);
+        }
+    l_run += lsum;
+
+    const u32x4* vp = (const u32x4*)Vt + vlane;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+      u32x4 va[NSL];
+#pragma unroll
+      for (int sl = 0; sl < NSL; ++sl)
+        va[sl] = vp[db * 32 * (VS / 8) + 2 * (sl ^ (db & (VXM >> 1)))];
+#pragma unroll
+      for (int sl = 0; sl < NSL; ++sl) o[db] = mfma32x32x16<BF16>(va[sl], pop[sl], o[db]);
+    }
+#if MPX_FA_SCHED >= 2
+    __builtin_amdgcn_sched_group_barrier(0x100, NSL, 1);
+#pragma unroll
+    for (int i = 0; i < NSL * (NDB - 1); ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, NSL, 1);
+#endif
+  };
+
+  const int n_tiles = t_end - t_begin;
+  if (n_tiles > 0) {
+    load_tile(kv_lo + t_begin * BN, Const<0>{});
+    store_tile(Const<0>{});
+    if (n_tiles > 1) load_tile(kv_lo + (t_begin + 1) * BN, Const<1>{});
   }
+  __syncthreads();
+#if MPX_FA_PRIO == 1
+  // Ping-pong: waves 0..NW/2-1 (one per SIMD) win issue arbitration, so the
+  // other wave on each SIMD runs its softmax while the first one's MFMAs run
+  // and vice versa, instead of both waves contending for the same unit.
+  if (wave < NW / 2) __builtin_amdgcn_s_setprio(1);
+#endif
+
+  // Tile i: computed from stage i%2; tile i+2 loaded into register set i%2;
+  // tile i+1 staged from register set (i+1)%2 into stage (i+1)%2.
+  auto step = [&](int i, auto PAR) __attribute__((always_inline)) {
+    constexpr int P = decltype(PAR)::value;
+    const int kv0 = kv_lo + (t_begin + i) * BN;
+    if (i + 2 < n_tiles) load_tile(kv0 + 2 * BN, Const<P>{});
+    compute_tile(P, kv0);
+    if (i + 1 < n_tiles) store_tile(Const<1 - P>{});
+    __syncthreads();
+  };
+  for (int i = 0; i < n_tiles; i += 2) {
+    step(i, Const<0>{});
+    if (i + 1 < n_tiles) step(i + 1, Const<1>{});
+  }
+#if MPX_FA_PRIO == 1
+  __builtin_amdgcn_s_setprio(0);
+#endif
 
   // Epilogue: move o and l to the true max, then normalise (or emit partials).
   const float l_tot = l_run + xor32(l_run);
@@ -422,6 +535,22 @@ void fa_fwd16_kernel(FwdParams p) {
   }
 }
 
+template <int D, int BN, int NW, bool BF16>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(MPX_FA_WAVES_PER_EU)))
+void fa_fwd16_kernel(FwdParams p) {
+  // Stay within 128 KB of LDS per workgroup (a 136 KB configuration gave wrong
+  // results on gfx950).
+  static_assert(2 * fa16_stage_elems<D, BN>() * 2 <= 131072, "LDS budget");
+  __shared__ __align__(16) uint16_t smem[2 * fa16_stage_elems<D, BN>()];
+  const WorkSlot ws = decode_slot(p);
+  const int n_items = slot_items(p, ws);
+  // Every item ends with a barrier after its last LDS read, so the next item
+  // may restage LDS at once.
+#pragma nounroll
+  for (int item = 0; item < n_items; ++item)
+    fa16_rows<D, BN, NW, BF16>(p, slot_item(p, ws, item), smem);
+}
+
 // ---------------------------------------------------------------------------
 // fp32 kernel: 32x32x2 f32 MFMA (true fp32 products, for fp32 parity).
 // S^T = K Q^T with k index (4-dim run) dims 8*(ks/4) + 4*g + ks%4; C element e
@@ -446,7 +575,7 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd32_kernel(FwdParams p) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int j = lane & 31, g = lane >> 5;
 
-  const WorkItem wi = decode_work(p);
+  const WorkItem wi = slot_item(p, decode_slot(p), 0);
   const int q0 = wi.qt * BM;
   int kv_lo, t_begin, t_end;
   kv_range<BM, BN>(p, q0, wi.split, kv_lo, t_begin, t_end);
@@ -471,17 +600,20 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd32_kernel(FwdParams p) {
     for (int jj = 0; jj < NQ4; ++jj) qf[jj] = -qf[jj];
   }
 
+  // Rows past Sk re-read the last valid row (no data-dependent selects at
+  // load time); their V values are zeroed when stored.
   f32x4 kbuf[PER_T], vbuf[PER_T];
+  int v_rows = BN;
   auto load_tile = [&](int kv0) {
+    v_rows = min(BN, p.Sk - kv0);
 #pragma unroll
     for (int i = 0; i < PER_T; ++i) {
       const int cc = tid + i * NT;
       if (CHUNKS % NT == 0 || cc < CHUNKS) {
         const int row = cc / CPR, col = cc - (cc / CPR) * CPR;
-        const int kv = kv0 + row;
-        const bool ok = kv < p.Sk;
-        kbuf[i] = ok ? *(const f32x4*)(Kp + (int64_t)kv * p.k_ss + col * 4) : (f32x4){};
-        vbuf[i] = ok ? *(const f32x4*)(Vp + (int64_t)kv * p.v_ss + col * 4) : (f32x4){};
+        const int kv = min(kv0 + row, p.Sk - 1);
+        kbuf[i] = *(const f32x4*)(Kp + (int64_t)kv * p.k_ss + col * 4);
+        vbuf[i] = *(const f32x4*)(Vp + (int64_t)kv * p.v_ss + col * 4);
       }
     }
   };
@@ -494,7 +626,7 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd32_kernel(FwdParams p) {
       if (CHUNKS % NT == 0 || cc < CHUNKS) {
         const int row = cc / CPR, col = cc - (cc / CPR) * CPR;
         *(f32x4*)(Ks + row * KS + col * 4) = kbuf[i];
-        *(f32x4*)(Vs + row * VS + col * 4) = vbuf[i];
+        *(f32x4*)(Vs + row * VS + col * 4) = row < v_rows ? vbuf[i] : (f32x4){};
       }
     }
   };
@@ -555,6 +687,7 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd32_kernel(FwdParams p) {
       m_max = fmaxf(m_max, mt);
 
       if (__any(mt > m_run + kRescaleThreshold)) {
+        asm volatile("" ::: "memory");  // a real branch, not selects on all of o
         const float m_new = fmaxf(m_run, mt);
         const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(m_run - m_new);
         l_run *= alpha;
@@ -675,9 +808,11 @@ namespace {
 constexpr int kNumWaves16 = MPX_FA_NWAVES;     // waves per workgroup, 16-bit kernel
 constexpr int kNumWaves32 = MPX_FA_NWAVES_F32; // waves per workgroup, fp32 kernel
 constexpr int kTargetWorkgroups = 512; // 256 CUs x 2 resident workgroups
+constexpr int kNumCUs = 256;
 
 struct Plan {
   int BM, BN, n_qtiles, splits, tiles_per_split, win_left, win_right;
+  int n_slots, paired;
   size_t ws_bytes;
 };
 
@@ -714,6 +849,13 @@ Plan make_plan(int B, int H, int Sq, int Sk, int D, int causal, int window_left,
   if (splits > 1) splits = (max_tiles + pl.tiles_per_split - 1) / pl.tiles_per_split;
   pl.splits = splits;
   pl.ws_bytes = splits > 1 ? (size_t)splits * B * H * Sq * (D + 2) * sizeof(float) : 0;
+  // Causal-shaped launches (KV range growing with the q-tile) of the 16-bit
+  // kernel pair q-tiles into equal-work slots while that still leaves a full
+  // wave of workgroups for the CUs.
+  const int half = (pl.n_qtiles + 1) / 2;
+  pl.paired = dtype != MPX_F32 && splits == 1 && pl.win_left < 0 && pl.win_right >= 0 &&
+              pl.n_qtiles >= 2 && (long)B * H * half >= kNumCUs;
+  pl.n_slots = pl.paired ? half : pl.n_qtiles;
   return pl;
 }
 
@@ -798,8 +940,17 @@ extern "C" int mpx_attn_fwd(const void* q, const void* k, const void* v, void* o
                   workspace_bytes);
     MPX_CHECK_ARG(aligned16(workspace), "mpx_attn_fwd: workspace must be 16-byte aligned");
   }
-  const long grid_l = (long)B * H * pl.n_qtiles * pl.splits;
+  const long grid_l = (long)B * H * pl.n_slots * pl.splits;
   MPX_CHECK_ARG(grid_l < (1L << 31), "mpx_attn_fwd: problem too large");
+  if (dtype != MPX_F32) {
+    // The 16-bit kernel addresses one (batch, head) of K/V with 32-bit byte offsets.
+    const int64_t span_k = ((int64_t)Sk + 64) * k_strides[2] * 2 + (int64_t)D * 2;
+    const int64_t span_v = ((int64_t)Sk + 64) * v_strides[2] * 2 + (int64_t)D * 2;
+    if (span_k >= (1LL << 31) || span_v >= (1LL << 31)) {
+      set_error("mpx_attn_fwd: Sk * seq_stride exceeds the 2 GiB addressing range of one head");
+      return MPX_EUNSUPPORTED;
+    }
+  }
 
   FwdParams p;
   p.q = q; p.k = k; p.v = v; p.o = o;
@@ -812,6 +963,7 @@ extern "C" int mpx_attn_fwd(const void* q, const void* k, const void* v, void* o
   p.B = B; p.H = H; p.Sq = Sq; p.Sk = Sk;
   p.win_left = pl.win_left; p.win_right = pl.win_right;
   p.n_qtiles = pl.n_qtiles; p.num_splits = pl.splits; p.tiles_per_split = pl.tiles_per_split;
+  p.n_slots = pl.n_slots; p.paired = pl.paired;
   p.c = std::fabs(scale) * kLog2e;
   p.neg = scale < 0.f ? 1 : 0;
 

@@ -78,6 +78,18 @@ __device__ __forceinline__ u32 pack2(float a, float b) {
   }
 }
 
+// acc + lo(x) + hi(x) for a packed pair of 16-bit values (one v_dot2c).
+template <bool BF16>
+__device__ __forceinline__ float dot2_sum(u32 x, float acc) {
+  if constexpr (BF16) {
+    const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, x), one, acc, false);
+  } else {
+    const f16x2 one = {(_Float16)1.0f, (_Float16)1.0f};
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, x), one, acc, false);
+  }
+}
+
 // 32x32x16 MFMA on 8 packed 16-bit values per lane.
 template <bool BF16>
 __device__ __forceinline__ f32x16 mfma32x32x16(u32x4 a, u32x4 b, f32x16 c) {

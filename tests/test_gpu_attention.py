@@ -72,6 +72,18 @@ def test_flash_ragged_lengths(device, S, dtype):
     check(flash_attention(q, k, v, causal=True), oa.flash_attention(qn, kn, vn, causal=True), dtype)
 
 
+@pytest.mark.parametrize("S,D", [(1100, 64), (1100, 128), (1536, 64), (1280, 32)])
+def test_flash_paired_causal_slots(device, S, D):
+    # 96 (batch, head) pairs x >= 3 q-tile slots: the causal launch pairs q-tile i
+    # with q-tile n-1-i in one workgroup. S=1100 / 1280 give 5 q-tiles (the middle
+    # slot runs a single q-tile; 1100 also has a ragged last tile), 1536 gives 6.
+    (q, k, v), (qn, kn, vn) = inputs([(2, 48, S, D)] * 3, torch.bfloat16, S + D, device)
+    out = flash_attention(q, k, v, causal=True, layout="BHSD")
+    sel = [0, 13, 47]
+    ref = oa.flash_attention(qn[:, sel], kn[:, sel], vn[:, sel], causal=True, layout="BHSD")
+    check(out[:, sel], ref, torch.bfloat16)
+
+
 @pytest.mark.parametrize("D", [1, 8, 16, 40, 80, 96])
 def test_flash_padded_head_dims(device, D):
     (q, k, v), (qn, kn, vn) = inputs([(2, 70, 2, D)] * 3, torch.float32, D, device)
