@@ -7,6 +7,12 @@ context ~ U{512..8192}, 16-token pages) and reports it under "paged_decode".
 Inputs are synthetic (seeded N(0,1)) and resident in HBM before timing.
 
 Prints ONE JSON line. Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+
+`--only flash|paged|copy` runs a single leg (no CPU baseline) for profiler
+passes; `copy` streams a 1 GiB float32 buffer through an elementwise kernel,
+the known-size reference for scaling the HBM byte counters. The HBM traffic
+per launch measured by those passes (rocprofv3 FETCH_SIZE / WRITE_SIZE) is read
+from profiles/hbm_traffic.json when present.
 """
 
 from __future__ import annotations
@@ -28,6 +34,18 @@ import workloads as wl  # noqa: E402
 
 PEAK_BF16_TFLOPS = 2516.6   # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+TRAFFIC_FILE = os.path.join(REPO, "profiles", "hbm_traffic.json")
+FLASH_KERNEL = "fa_fwd16_kernel<128,64,8,bf16>"
+PAGED_KERNELS = "paged_decode_part_kernel + paged_decode_merge_kernel"
+
+
+def measured_traffic(key: str):
+    """HBM bytes per launch recorded by the counter passes, or None."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            return json.load(f)[key]["bytes_per_launch"]
+    except (OSError, KeyError, ValueError):
+        return None
 
 
 def log(msg: str) -> None:
@@ -35,7 +53,8 @@ def log(msg: str) -> None:
 
 
 def time_steps(fn, steps: int, warmup: int):
-    """Warmup, then `steps` timed calls; returns (wall ms/step, mean event ms/call).
+    """Warmup, then `steps` timed calls; returns (wall ms/step, mean, min and
+    median event ms/call).
 
     Events are recorded on torch's current stream, the stream the kernels are
     launched on, around every call."""
@@ -52,8 +71,8 @@ def time_steps(fn, steps: int, warmup: int):
         ends[i].record()
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3 / steps
-    ev = [s.elapsed_time(e) for s, e in zip(starts, ends)]
-    return wall_ms, sum(ev) / len(ev), min(ev)
+    ev = sorted(s.elapsed_time(e) for s, e in zip(starts, ends))
+    return wall_ms, sum(ev) / len(ev), ev[0], ev[len(ev) // 2]
 
 
 def blas_threads() -> int:
@@ -126,19 +145,54 @@ def cpu_baseline_paged(inp, cfg: dict, budget_s: float) -> dict:
                       f"decode in float32 numpy, {t_total:.1f} s"}
 
 
+def run_one_leg(args) -> int:
+    """One leg for a profiler pass: warmup + steps calls, timing on stderr/stdout."""
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    if args.only == "copy":
+        n = 1 << 28  # 2^28 float32 = 1 GiB read + 1 GiB written per launch
+        src = torch.ones(n, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        fn = lambda: torch.mul(src, 1.0, out=dst)
+        work, unit = 2.0 * n * 4, "bytes"
+    elif args.only == "flash":
+        from mlx_primitives.attention import flash_attention
+
+        cfg = wl.CONFIGS["flash_bf16_bhsd"]
+        q, k, v = wl.make_qkv(cfg, device=dev)
+        fn = lambda: flash_attention(q, k, v, causal=True, layout="BHSD")
+        work, unit = wl.config_work("flash_bf16_bhsd"), "flop"
+    else:
+        from mlx_primitives.cache import paged_attention
+
+        pin = wl.make_paged(wl.CONFIGS["paged_decode_fp16"], device=dev)
+        fn = lambda: paged_attention(pin.q, pin.k_pool, pin.v_pool, pin.block_tables,
+                                     pin.context_lens, block_size=pin.block_size)
+        work, unit = wl.config_work("paged_decode_fp16", pin), "bytes"
+    wall_ms, ev_ms, ev_min, _ = time_steps(fn, args.steps, args.warmup)
+    print(json.dumps({"leg": args.only, "steps": args.steps, "warmup": args.warmup,
+                      "ms_per_call": ev_ms, "min_ms": ev_min, "work_per_call": work,
+                      "work_unit": unit}), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--cpu-budget", type=float, default=10.0,
                     help="seconds of CPU work per baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--only", choices=["flash", "paged", "copy"], default=None,
+                    help="run one leg only (profiler passes); prints that leg's timing")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
               "(this build has no multi-GPU path)", file=sys.stderr)
         return 2
+    if args.only is not None:
+        return run_one_leg(args)
 
     from mlx_primitives.attention import flash_attention
     from mlx_primitives.cache import paged_attention
@@ -153,7 +207,7 @@ def main() -> int:
     flops = wl.config_work(name)
     step = lambda: flash_attention(q, k, v, causal=True, layout="BHSD")
     log(f"[bench] {name}: warmup {args.warmup}, steps {args.steps}")
-    wall_ms, ev_ms, ev_min = time_steps(step, args.steps, args.warmup)
+    wall_ms, ev_ms, ev_min, ev_med = time_steps(step, args.steps, args.warmup)
     achieved = flops / (ev_ms * 1e-3) / 1e12
     log(f"[bench] {name}: {wall_ms:.3f} ms/step wall, kernel {ev_ms:.3f} ms "
         f"(min {ev_min:.3f}) -> {achieved:.1f} TFLOP/s")
@@ -166,7 +220,7 @@ def main() -> int:
     pstep = lambda: paged_attention(pin.q, pin.k_pool, pin.v_pool, pin.block_tables,
                                     pin.context_lens, block_size=pin.block_size)
     log(f"[bench] {pname}: warmup {args.warmup}, steps {args.steps}")
-    p_wall, p_ev, p_min = time_steps(pstep, args.steps, args.warmup)
+    p_wall, p_ev, p_min, p_med = time_steps(pstep, args.steps, args.warmup)
     p_gbs = pbytes / (p_ev * 1e-3) / 1e9
     log(f"[bench] {pname}: {p_wall:.3f} ms/step wall, kernels {p_ev:.3f} ms -> {p_gbs:.1f} GB/s")
 
@@ -195,17 +249,22 @@ def main() -> int:
                    "global_batch": cfg["B"], "seq_len": cfg["S"], "heads": cfg["H"],
                    "head_dim": cfg["D"], "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS,
-                     "unit": "TFLOP/s", "frac": achieved / PEAK_BF16_TFLOPS, "traffic": None,
-                     "kernel": "fa_fwd16_kernel<128,64,8,bf16>",
-                     "flop_per_launch": flops, "launch_ms": ev_ms},
+                     "unit": "TFLOP/s", "frac": achieved / PEAK_BF16_TFLOPS,
+                     "traffic": measured_traffic("flash_bf16_bhsd"),
+                     "kernel": FLASH_KERNEL, "traffic_unit": "bytes per launch",
+                     "flop_per_launch": flops, "launch_ms": ev_ms, "launch_ms_median": ev_med,
+                     "launch_ms_min": ev_min},
         "cpu_baseline": cpu,
         "paged_decode": {
             "workload": "paged_attention decode fp16, 64 seqs, H=32, D=128, ctx~U{512..8192}, "
                         "16-token pages, permuted block table",
             "value": p_gbs, "unit": "GB/s", "ms_per_step": p_wall, "kernel_ms": p_ev,
+            "kernel_ms_median": p_med, "kernel_ms_min": p_min,
             "bytes_per_step": pbytes,
             "roofline": {"bound": "hbm", "achieved": p_gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                         "frac": p_gbs / PEAK_HBM_GBS, "traffic": None},
+                         "frac": p_gbs / PEAK_HBM_GBS,
+                         "traffic": measured_traffic("paged_decode_fp16"),
+                         "kernel": PAGED_KERNELS, "traffic_unit": "bytes per launch"},
             "cpu_baseline": pcpu,
         },
     }

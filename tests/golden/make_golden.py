@@ -1,0 +1,185 @@
+"""Writes the golden fixtures of tests/golden/*.npz.
+
+Each fixture holds seeded inputs (values already rounded to the case's dtype,
+stored as float32, which represents bf16/fp16 exactly), the expected output in
+float64 and a JSON `meta` string (no pickled objects: np.load with
+allow_pickle=False reads them).
+
+The expected output is the float64 oracle (oracle/attention.py,
+oracle/paged.py). Before a fixture is written it is checked against an
+independent evaluation: torch.nn.functional.scaled_dot_product_attention in
+float64 with an explicit boolean mask, the library routine the reference's own
+parity suite compares with (tests/parity/pytorch/test_attention_parity.py:87-105,
+288-337). The reference ships no golden files (its generator recipes are
+scripts/validation/generators/attention/sdpa.py:93-141 and efficient.py:276-339);
+these fixtures follow the same idea at small sizes. Windows follow the
+production convention |i - j| <= W (W+1 keys including self with causal,
+attention/sliding_window.py:151-157), not the generator's W-key variant.
+
+Run from the repository root:  python tests/golden/make_golden.py
+"""
+
+from __future__ import annotations
+
+import json
+import math
+import os
+import sys
+
+import numpy as np
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(os.path.dirname(HERE))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+from oracle import attention as oa  # noqa: E402
+from oracle import paged as op  # noqa: E402
+
+DTYPES = {"float32": torch.float32, "float16": torch.float16, "bfloat16": torch.bfloat16}
+# Oracle vs torch SDPA, both float64. The tiled paths normalise by l + 1e-6
+# (attention/flash.py:312, sliding_window.py:115, chunked.py:169) where SDPA is
+# exact; with l >= 1 that moves outputs by <= 1e-6 relative. Paged decode is
+# exact in both.
+AGREE_TILED = 1e-5
+AGREE_EXACT = 1e-9
+
+
+def rounded(shape, dtype, gen, mult=1.0):
+    x = torch.randn(shape, generator=gen, dtype=torch.float32) * mult
+    return x.to(DTYPES[dtype]).to(torch.float32).numpy()
+
+
+def sdpa_rows(q, k, v, scale, keep):
+    """softmax(q k^T * scale, masked by keep) v per (b, h); q/k/v (B, H, S, D)."""
+    qt, kt, vt = (torch.from_numpy(np.ascontiguousarray(x)).double() for x in (q, k, v))
+    out = torch.nn.functional.scaled_dot_product_attention(
+        qt, kt, vt, attn_mask=torch.from_numpy(keep), scale=scale)
+    return out.numpy()
+
+
+def window_keep(Sq, Sk, causal, left, right):
+    i = np.arange(Sq)[:, None]
+    j = np.arange(Sk)[None, :]
+    keep = np.ones((Sq, Sk), dtype=bool)
+    if causal:
+        keep &= j <= i
+    if left >= 0:
+        keep &= j >= i - left
+    if right >= 0:
+        keep &= j <= i + right
+    return keep
+
+
+def to_bhsd(x, layout):
+    return x if layout == "BHSD" else np.transpose(x, (0, 2, 1, 3))
+
+
+def save(name, meta, **arrays):
+    path = os.path.join(HERE, f"{name}.npz")
+    np.savez_compressed(path, meta=np.array(json.dumps(meta, sort_keys=True)), **arrays)
+    print(f"{name}: {', '.join(f'{k}{tuple(v.shape)}' for k, v in arrays.items())}")
+
+
+def agree(name, a, b, tol=AGREE_TILED):
+    err = float(np.nanmax(np.abs(a - b)))
+    assert err <= tol, f"{name}: oracle and SDPA disagree by {err}"
+
+
+def flash_case(name, shape, dtype, layout, causal, seed, scale=None):
+    g = torch.Generator().manual_seed(seed)
+    q, k, v = (rounded(shape, dtype, g) for _ in range(3))
+    D = shape[-1]
+    s = 1.0 / math.sqrt(D) if scale is None else scale
+    exp = oa.flash_attention(q.astype(np.float64), k.astype(np.float64), v.astype(np.float64),
+                             scale=scale, causal=causal, layout=layout)
+    Sq = shape[2] if layout == "BHSD" else shape[1]
+    keep = window_keep(Sq, Sq, causal, -1, -1)
+    ref = sdpa_rows(to_bhsd(q, layout), to_bhsd(k, layout), to_bhsd(v, layout), s, keep)
+    agree(name, to_bhsd(exp, layout), ref)
+    save(name, {"kind": "flash", "dtype": dtype, "layout": layout, "causal": causal,
+                "scale": scale}, q=q, k=k, v=v, expected=exp)
+
+
+def window_case(name, shape, dtype, W, causal, seed):
+    g = torch.Generator().manual_seed(seed)
+    q, k, v = (rounded(shape, dtype, g) for _ in range(3))
+    exp = oa.sliding_window_attention(q.astype(np.float64), k.astype(np.float64),
+                                      v.astype(np.float64), W, causal=causal)
+    S = shape[1]
+    keep = window_keep(S, S, causal, W, -1 if causal else W)
+    ref = sdpa_rows(to_bhsd(q, "BSHD"), to_bhsd(k, "BSHD"), to_bhsd(v, "BSHD"),
+                    1.0 / math.sqrt(shape[-1]), keep)
+    agree(name, to_bhsd(exp, "BSHD"), ref)
+    save(name, {"kind": "window", "dtype": dtype, "window": W, "causal": causal},
+         q=q, k=k, v=v, expected=exp)
+
+
+def chunked_case(name, qshape, kvlen, dtype, chunk, causal, seed):
+    g = torch.Generator().manual_seed(seed)
+    B, Sq, H, D = qshape
+    q = rounded(qshape, dtype, g)
+    k = rounded((B, kvlen, H, D), dtype, g)
+    v = rounded((B, kvlen, H, D), dtype, g)
+    exp = oa.chunked_cross_attention(q.astype(np.float64), k.astype(np.float64),
+                                     v.astype(np.float64), chunk_size=chunk, causal=causal)
+    keep = window_keep(Sq, kvlen, causal, -1, -1)
+    ref = sdpa_rows(to_bhsd(q, "BSHD"), to_bhsd(k, "BSHD"), to_bhsd(v, "BSHD"),
+                    1.0 / math.sqrt(D), keep)
+    agree(name, to_bhsd(exp, "BSHD"), ref)
+    save(name, {"kind": "chunked", "dtype": dtype, "chunk_size": chunk, "causal": causal},
+         q=q, k=k, v=v, expected=exp)
+
+
+def paged_case(name, lens, tables, num_blocks, bs, H, D, dtype, seed, alibi=False):
+    g = torch.Generator().manual_seed(seed)
+    B = len(lens)
+    q = rounded((B, 1, H, D), dtype, g)
+    kp = rounded((num_blocks, bs, H, D), dtype, g)
+    vp = rounded((num_blocks, bs, H, D), dtype, g)
+    tables = np.asarray(tables, dtype=np.int32)
+    lens = np.asarray(lens, dtype=np.int32)
+    slopes = op.get_alibi_slopes(H) if alibi else None
+    scale = 1.0 / math.sqrt(D)
+    exp = op.paged_attention_decode(q.astype(np.float64), kp.astype(np.float64),
+                                    vp.astype(np.float64), tables, lens, scale, bs,
+                                    alibi_slopes=slopes)
+    # Independent check: gather each sequence's valid tokens, then SDPA with the
+    # ALiBi bias slope_h * (pos - ctx) (cache/paged_attention.py:163-178).
+    for b in range(B):
+        pos = np.arange(int(lens[b]))
+        pages = tables[b, pos // bs]
+        ok = pages >= 0
+        kk = kp[pages[ok], (pos % bs)[ok]].transpose(1, 0, 2)[None].astype(np.float64)
+        vv = vp[pages[ok], (pos % bs)[ok]].transpose(1, 0, 2)[None].astype(np.float64)
+        qq = q[b:b + 1].transpose(0, 2, 1, 3).astype(np.float64)
+        bias = np.zeros((1, H, 1, kk.shape[2]))
+        if alibi:
+            bias = (slopes[:, None] * (pos[ok] - int(lens[b]))[None, :])[None, :, None, :]
+        ref = torch.nn.functional.scaled_dot_product_attention(
+            torch.from_numpy(qq), torch.from_numpy(kk), torch.from_numpy(vv),
+            attn_mask=torch.from_numpy(bias), scale=scale).numpy()
+        agree(f"{name}[{b}]", exp[b:b + 1].transpose(0, 2, 1, 3), ref, AGREE_EXACT)
+    save(name, {"kind": "paged", "dtype": dtype, "block_size": bs, "alibi": alibi},
+         q=q, k_pool=kp, v_pool=vp, block_tables=tables, context_lens=lens, expected=exp)
+
+
+def main():
+    flash_case("flash_causal_f32_bshd", (1, 37, 2, 32), "float32", "BSHD", True, 101)
+    flash_case("flash_full_bf16_bhsd", (2, 3, 70, 64), "bfloat16", "BHSD", False, 102)
+    flash_case("flash_causal_f16_bshd_d128", (1, 129, 2, 128), "float16", "BSHD", True, 103)
+    flash_case("flash_full_f32_negscale", (1, 20, 1, 64), "float32", "BSHD", False, 104, scale=-0.3)
+    window_case("window_causal_f32_w7", (1, 100, 2, 64), "float32", 7, True, 105)
+    window_case("window_full_bf16_w16", (1, 90, 2, 32), "bfloat16", 16, False, 106)
+    chunked_case("chunked_full_f32", (1, 16, 2, 64), 300, "float32", 64, False, 107)
+    chunked_case("chunked_causal_bf16", (1, 40, 2, 64), 200, "bfloat16", 64, True, 108)
+    # tests/cache/test_paged_attention.py:164-197 (hand-built tables, page 8 unused)
+    paged_case("paged_ref_tables_f32", [16, 32, 48, 25], [[0, -1, -1], [1, 2, -1], [3, 4, 5],
+                                                          [6, 7, -1]], 9, 16, 2, 32, "float32", 109)
+    paged_case("paged_alibi_f16", [5, 40, 17], [[3, -1, -1], [0, 4, 1], [2, 5, -1]], 6, 16, 4,
+               64, "float16", 110, alibi=True)
+
+
+if __name__ == "__main__":
+    main()
