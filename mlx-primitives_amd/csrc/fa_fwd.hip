@@ -71,6 +71,23 @@ struct FwdParams {
 #ifndef MPX_FA_BN16
 #define MPX_FA_BN16 64
 #endif
+// 1: the two waves sharing a SIMD run half a tile apart (see fa16_rows).
+#ifndef MPX_FA_PINGPONG
+#define MPX_FA_PINGPONG 0
+#endif
+// 1: fully visible tiles overlap the softmax with the MFMAs of the same wave
+// (see spec_tile in fa16_rows).
+#ifndef MPX_FA_SPEC
+#define MPX_FA_SPEC 0
+#endif
+// K/V tiles held in registers ahead of their LDS staging: 2 (tile i+2 is
+// loaded while tile i computes) or 1 (tile i+1).
+#ifndef MPX_FA_DEPTH
+#define MPX_FA_DEPTH 2
+#endif
+// LDS stages of the 16-bit kernel: the offset schedule keeps tile i-1
+// readable while tile i+1 is staged.
+constexpr int kFa16Stages = MPX_FA_PINGPONG ? 3 : 2;
 
 // Compile-time integer tag (selects a register set in the unrolled loop).
 template <int N>
@@ -231,33 +248,27 @@ __device__ __forceinline__ void fa16_rows(const FwdParams& p, const WorkItem wi,
   // prefetches issued inside the loop (vmcnt completes in order).
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
 
-  // Per-thread byte offsets of the prefetch loads inside a tile.
-  int koff[K_PER_T];
-#pragma unroll
-  for (int i = 0; i < K_PER_T; ++i) {
-    const int c = tid + i * NT;
-    const int row = c / CPR, col = c - (c / CPR) * CPR;
-    koff[i] = (int)((row * p.k_ss + col * 8) * 2);
-  }
+  // Per-thread byte offsets of the prefetch loads inside a tile: one lane
+  // offset each for K and V; load i of a thread sits NT/CPR rows further (a
+  // wave-uniform step, passed as the scalar offset of the buffer load).
+  static_assert(NT % CPR == 0, "whole rows per load round");
+  constexpr int ROWS_PER_ROUND = NT / CPR;
+  const int koff = (int)(((tid / CPR) * p.k_ss + (tid % CPR) * 8) * 2);
+  const int kstep = ROWS_PER_ROUND * (int)p.k_ss * 2;
   // V unit u: row pair kp = u / CPR, 16-byte column chunk dq = u % CPR (a wave
-  // reads whole rows).
-  int voff[V_PER_T][2];
-#pragma unroll
-  for (int i = 0; i < V_PER_T; ++i) {
-    const int u = tid + i * NT;
-    const int kp = u / CPR, dq = u - (u / CPR) * CPR;
-    voff[i][0] = (int)(((2 * kp) * p.v_ss + dq * 8) * 2);
-    voff[i][1] = (int)(((2 * kp + 1) * p.v_ss + dq * 8) * 2);
-  }
+  // reads whole rows); the second row of the pair is one seq stride further.
+  const int voff = (int)(((2 * (tid / CPR)) * p.v_ss + (tid % CPR) * 8) * 2);
+  const int vstep = 2 * ROWS_PER_ROUND * (int)p.v_ss * 2, vrow = (int)p.v_ss * 2;
 
   // Prefetch registers, two sets: tile i+2 is loaded into set i%2 while tile
   // i computes and tile i+1 (loaded one iteration earlier) is staged to LDS,
   // so a load has two tile times to arrive.
-  u32x4 kbuf[2][K_PER_T];
-  u32x4 vbuf[2][V_PER_T][2];
+  constexpr int NSET = MPX_FA_DEPTH;
+  u32x4 kbuf[NSET][K_PER_T];
+  u32x4 vbuf[NSET][V_PER_T][2];
   // Rows of a staged tile at or past v_rows are zeroed when V is stored (BN
   // except for the tail tile).
-  int v_rows[2] = {BN, BN};
+  int v_rows[NSET];
 
   // The loads never depend on data (no selects): a select on a loaded value
   // would make the compiler wait for the prefetch right after issuing it.
@@ -269,12 +280,13 @@ __device__ __forceinline__ void fa16_rows(const FwdParams& p, const WorkItem wi,
 #pragma unroll
       for (int i = 0; i < K_PER_T; ++i)
         if (K_CHUNKS % NT == 0 || tid + i * NT < K_CHUNKS)
-          kbuf[S][i] = __builtin_amdgcn_raw_buffer_load_b128(krs, koff[i], kso, 0);
+          kbuf[S][i] = __builtin_amdgcn_raw_buffer_load_b128(krs, koff, kso + i * kstep, 0);
 #pragma unroll
       for (int i = 0; i < V_PER_T; ++i)
         if (V_UNITS % NT == 0 || tid + i * NT < V_UNITS) {
-          vbuf[S][i][0] = __builtin_amdgcn_raw_buffer_load_b128(vrs, voff[i][0], vso, 0);
-          vbuf[S][i][1] = __builtin_amdgcn_raw_buffer_load_b128(vrs, voff[i][1], vso, 0);
+          vbuf[S][i][0] = __builtin_amdgcn_raw_buffer_load_b128(vrs, voff, vso + i * vstep, 0);
+          vbuf[S][i][1] =
+              __builtin_amdgcn_raw_buffer_load_b128(vrs, voff, vso + i * vstep + vrow, 0);
         }
     } else {
       // Tail tile: rows past Sk re-read the last valid row (K rows there are
@@ -308,10 +320,10 @@ __device__ __forceinline__ void fa16_rows(const FwdParams& p, const WorkItem wi,
   // V^T layout: element (d, kv) sits in 4-byte word (kv/2) ^ (4 * ((d/16) & VXM))
   // of row d. The XOR keeps 16-byte groups of 8 keys intact for the b128
   // operand reads and spreads one store instruction over all 64 banks.
-  // Register set S is staged into LDS stage S.
-  auto store_tile = [&](auto SET) __attribute__((always_inline)) {
+  // Register set S is staged into LDS stage `stage`.
+  auto store_tile = [&](auto SET, int stage) __attribute__((always_inline)) {
     constexpr int S = decltype(SET)::value;
-    uint16_t* Ks = smem + S * STAGE;
+    uint16_t* Ks = smem + stage * STAGE;
     uint16_t* Vt = Ks + K_ELEMS;
 #pragma unroll
     for (int i = 0; i < K_PER_T; ++i) {
@@ -365,15 +377,8 @@ __device__ __forceinline__ void fa16_rows(const FwdParams& p, const WorkItem wi,
   // so one lane base plus compile-time offsets addresses every operand.
   const int vlane = j * (VS / 8) + (g ^ ((j >> 4) & 1));
 
-  // Attention of this wave's rows to the tile at kv0 staged in LDS stage `stage`.
-  auto compute_tile = [&](int stage, int kv0) __attribute__((always_inline)) {
-    bool skip, full;
-    classify_tile<BN>(p, kv0, wq0, wq0 + 31, skip, full);
-    if (skip) return;
-    const uint16_t* Ks = smem + stage * STAGE;
-    const uint16_t* Vt = Ks + K_ELEMS;
-
-    f32x16 s[NB];
+  // Scores S^T of this wave's rows against the K tile staged at Ks.
+  auto qk_tile = [&](const uint16_t* Ks, f32x16 (&s)[NB]) __attribute__((always_inline)) {
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
       const u32x4* kp = (const u32x4*)(Ks + (nb * 32 + krow_perm) * KS) + g;
@@ -394,7 +399,11 @@ __device__ __forceinline__ void fa16_rows(const FwdParams& p, const WorkItem wi,
     }
     __builtin_amdgcn_sched_group_barrier(0x008, NKS, 0);
 #endif
+  };
 
+  // Masks and online softmax of the tile at kv0: P^T (packed 16-bit) in pop.
+  auto softmax_p = [&](int kv0, bool full, f32x16 (&s)[NB], u32x4 (&pop)[NSL])
+      __attribute__((always_inline)) {
     if (!full) {
       // The empty volatile asm keeps this a real (scalar) branch: without it
       // the selects are folded into unconditional code run on every tile.
@@ -431,7 +440,6 @@ __device__ __forceinline__ void fa16_rows(const FwdParams& p, const WorkItem wi,
 
     // P = exp2(s*c - m), packed to 16 bits; the row sum accumulates the
     // packed (rounded) weights, the exact weights the PV product uses.
-    u32x4 pop[NSL];
     float lsum = 0.f;
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb)
@@ -446,7 +454,10 @@ __device__ __forceinline__ void fa16_rows(const FwdParams& p, const WorkItem wi,
           lsum = dot2_sum<BF16>(pk, lsum);
         }
     l_run += lsum;
+  };
 
+  // O += P V for the V^T tile staged at Vt.
+  auto pv_tile = [&](const uint16_t* Vt, const u32x4 (&pop)[NSL]) __attribute__((always_inline)) {
     const u32x4* vp = (const u32x4*)Vt + vlane;
 #pragma unroll
     for (int db = 0; db < NDB; ++db) {
@@ -468,11 +479,154 @@ __device__ __forceinline__ void fa16_rows(const FwdParams& p, const WorkItem wi,
 #endif
   };
 
+  auto softmax_pv = [&](const uint16_t* Vt, int kv0, bool full, f32x16 (&s)[NB])
+      __attribute__((always_inline)) {
+    u32x4 pop[NSL];
+    softmax_p(kv0, full, s, pop);
+    pv_tile(Vt, pop);
+  };
+
+#if MPX_FA_SPEC
+  // exp2(s*c - msub) of one 32-key block, packed into two PV B operands; the
+  // row sum accumulates the packed weights.
+  auto exp_block = [&](const f32x16& sb, float msub, u32x4& p_lo, u32x4& p_hi, float& lsum)
+      __attribute__((always_inline)) {
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+      for (int e2 = 0; e2 < 4; ++e2) {
+        const float x0 = fast_exp2(sb[8 * hh + 2 * e2] * c - msub);
+        const float x1 = fast_exp2(sb[8 * hh + 2 * e2 + 1] * c - msub);
+        const u32 pk = pack2<BF16>(x0, x1);
+        if (hh == 0) p_lo[e2] = pk; else p_hi[e2] = pk;
+        lsum = dot2_sum<BF16>(pk, lsum);
+      }
+  };
+
+  // A fully visible tile with the softmax interleaved into the same wave's
+  // MFMAs: the weights of keys 0..31 are computed against the running max
+  // m_run while the scores of keys 32..63 are still in the MFMA pipe, and the
+  // weights of keys 32..63 while the PV MFMAs of keys 0..31 run. Exact: if
+  // the tile's max exceeds m_run by more than the rescale threshold, O and l
+  // are rescaled and the weights of keys 0..31 recomputed before any PV
+  // MFMA uses them.
+  auto spec_tile = [&](const uint16_t* Ks, const uint16_t* Vt) __attribute__((always_inline)) {
+    static_assert(NB == 2, "two 32-key blocks per tile");
+    f32x16 s0, s1;
+    {
+      const u32x4* kp0 = (const u32x4*)(Ks + krow_perm * KS) + g;
+      const u32x4* kp1 = (const u32x4*)(Ks + (32 + krow_perm) * KS) + g;
+      u32x4 ka[NKS], kb[NKS];
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) ka[ks] = kp0[2 * ks];
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) kb[ks] = kp1[2 * ks];
+      s0 = (f32x16){};
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) s0 = mfma32x32x16<BF16>(ka[ks], qreg[ks], s0);
+      s1 = (f32x16){};
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) s1 = mfma32x32x16<BF16>(kb[ks], qreg[ks], s1);
+    }
+    float mt0 = s0[0];
+#pragma unroll
+    for (int e = 1; e < 16; ++e) mt0 = fmaxf(mt0, s0[e]);
+    const float msub0 = m_run == -INFINITY ? 0.f : m_run;
+    u32x4 pop[NSL];
+    float lsum0 = 0.f;
+    exp_block(s0, msub0, pop[0], pop[1], lsum0);
+    // K reads, then block 0's MFMAs under block 1's K reads, then block 1's
+    // MFMAs with block 0's max / exp / pack between them.
+    __builtin_amdgcn_sched_group_barrier(0x100, NKS, 0);
+#pragma unroll
+    for (int i = 0; i < NKS; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < NKS; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x402, 7, 0);
+    }
+
+    float mt = mt0;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) mt = fmaxf(mt, s1[e]);
+    mt = fmaxf(mt, xor32(mt)) * c;
+    m_max = fmaxf(m_max, mt);
+    if (__any(mt > m_run + kRescaleThreshold)) {
+      asm volatile("" ::: "memory");  // a real branch, not selects on all of o
+      const float m_new = fmaxf(m_run, mt);
+      const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(m_run - m_new);
+      l_run *= alpha;
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) o[db][e] *= alpha;
+      m_run = m_new;
+      lsum0 = 0.f;
+      exp_block(s0, m_run == -INFINITY ? 0.f : m_run, pop[0], pop[1], lsum0);
+    }
+    const float msub = m_run == -INFINITY ? 0.f : m_run;
+    float lsum1 = 0.f;
+    exp_block(s1, msub, pop[2], pop[3], lsum1);
+    l_run += lsum0 + lsum1;
+
+    // PV in (key half, dim block) pairs: two MFMAs per pair, the V operands
+    // of the next pair read under them; block 1's exp / pack runs under the
+    // MFMAs of keys 0..31.
+    const u32x4* vp = (const u32x4*)Vt + vlane;
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) {
+        const u32x4 v0 = vp[db * 32 * (VS / 8) + 2 * ((2 * h) ^ (db & (VXM >> 1)))];
+        const u32x4 v1 = vp[db * 32 * (VS / 8) + 2 * ((2 * h + 1) ^ (db & (VXM >> 1)))];
+        o[db] = mfma32x32x16<BF16>(v0, pop[2 * h], o[db]);
+        o[db] = mfma32x32x16<BF16>(v1, pop[2 * h + 1], o[db]);
+      }
+    __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
+#pragma unroll
+    for (int i = 0; i < NDB; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+      __builtin_amdgcn_sched_group_barrier(0x402, 6, 1);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+      __builtin_amdgcn_sched_group_barrier(0x402, 6, 1);
+    }
+#pragma unroll
+    for (int i = 0; i < NDB - 1; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 2, 1);
+  };
+#endif
+
+  // Attention of this wave's rows to the tile at kv0 staged in LDS stage `stage`.
+  auto compute_tile = [&](int stage, int kv0) __attribute__((always_inline)) {
+    bool skip, full;
+    classify_tile<BN>(p, kv0, wq0, wq0 + 31, skip, full);
+    if (skip) return;
+    const uint16_t* Ks = smem + stage * STAGE;
+#if MPX_FA_SPEC
+    if (full) {
+      spec_tile(Ks, Ks + K_ELEMS);
+      return;
+    }
+    asm volatile("" ::: "memory");
+#endif
+    f32x16 s[NB];
+    qk_tile(Ks, s);
+    softmax_pv(Ks + K_ELEMS, kv0, full, s);
+  };
+
   const int n_tiles = t_end - t_begin;
   if (n_tiles > 0) {
     load_tile(kv_lo + t_begin * BN, Const<0>{});
-    store_tile(Const<0>{});
-    if (n_tiles > 1) load_tile(kv_lo + (t_begin + 1) * BN, Const<1>{});
+    store_tile(Const<0>{}, 0);
+    if (NSET == 2 && n_tiles > 1) load_tile(kv_lo + (t_begin + 1) * BN, Const<NSET - 1>{});
   }
   __syncthreads();
 #if MPX_FA_PRIO == 1
@@ -482,20 +636,66 @@ __device__ __forceinline__ void fa16_rows(const FwdParams& p, const WorkItem wi,
   if (wave < NW / 2) __builtin_amdgcn_s_setprio(1);
 #endif
 
-  // Tile i: computed from stage i%2; tile i+2 loaded into register set i%2;
-  // tile i+1 staged from register set (i+1)%2 into stage (i+1)%2.
+#if MPX_FA_PINGPONG
+  // Offset schedule: on every SIMD one wave (wave < NW/2) computes tile i
+  // (QK -> softmax -> PV) while its partner (wave + NW/2) runs PV of tile i-1
+  // and then QK and softmax of tile i, so each wave's softmax runs under the
+  // other's MFMAs instead of both waves contending for the same unit. Tile i
+  // sits in stage i%3; tile i+1 is staged into stage (i+1)%3 while stage
+  // (i-1)%3 still holds tile i-1 for the trailing waves.
+  // Both groups run QK and softmax of tile i in the same place; a lead wave
+  // then runs PV of tile i, a trailing wave runs PV of tile i-1 first (its
+  // P^T carried over the barrier in pp).
+  const bool lead = wave < NW / 2;
+  auto stage_of = [](int i) { return i - (i / 3) * 3; };
+  f32x16 sp[NB];
+  u32x4 pp[NSL];
+  bool pp_valid = false;
   auto step = [&](int i, auto PAR) __attribute__((always_inline)) {
     constexpr int P = decltype(PAR)::value;
     const int kv0 = kv_lo + (t_begin + i) * BN;
+    const int stage = stage_of(i);
     if (i + 2 < n_tiles) load_tile(kv0 + 2 * BN, Const<P>{});
-    compute_tile(P, kv0);
-    if (i + 1 < n_tiles) store_tile(Const<1 - P>{});
+    if (!lead && pp_valid) pv_tile(smem + stage_of(i + 2) * STAGE + K_ELEMS, pp);
+    bool skip, full;
+    classify_tile<BN>(p, kv0, wq0, wq0 + 31, skip, full);
+    pp_valid = !skip;
+    if (!skip) {
+      qk_tile(smem + stage * STAGE, sp);
+      softmax_p(kv0, full, sp, pp);
+      if (lead) pv_tile(smem + stage * STAGE + K_ELEMS, pp);
+    }
+    if (i + 1 < n_tiles) store_tile(Const<1 - P>{}, stage_of(i + 1));
     __syncthreads();
   };
   for (int i = 0; i < n_tiles; i += 2) {
     step(i, Const<0>{});
     if (i + 1 < n_tiles) step(i + 1, Const<1>{});
   }
+  if (!lead && pp_valid) pv_tile(smem + stage_of(n_tiles - 1) * STAGE + K_ELEMS, pp);
+  // The trailing waves read LDS after the last barrier of the loop; the next
+  // item restages it.
+  __syncthreads();
+#else
+  // Tile i: computed from stage i%2; tile i+2 loaded into register set i%2;
+  // tile i+1 staged from register set (i+1)%2 into stage (i+1)%2.
+  auto step = [&](int i, auto PAR) __attribute__((always_inline)) {
+    constexpr int P = decltype(PAR)::value;
+    const int kv0 = kv_lo + (t_begin + i) * BN;
+    if constexpr (NSET == 2) {
+      if (i + 2 < n_tiles) load_tile(kv0 + 2 * BN, Const<P>{});
+    } else {
+      if (i + 1 < n_tiles) load_tile(kv0 + BN, Const<0>{});
+    }
+    compute_tile(P, kv0);
+    if (i + 1 < n_tiles) store_tile(Const<NSET == 2 ? 1 - P : 0>{}, 1 - P);
+    __syncthreads();
+  };
+  for (int i = 0; i < n_tiles; i += 2) {
+    step(i, Const<0>{});
+    if (i + 1 < n_tiles) step(i + 1, Const<1>{});
+  }
+#endif
 #if MPX_FA_PRIO == 1
   __builtin_amdgcn_s_setprio(0);
 #endif
@@ -540,8 +740,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(MPX_FA_
 void fa_fwd16_kernel(FwdParams p) {
   // Stay within 128 KB of LDS per workgroup (a 136 KB configuration gave wrong
   // results on gfx950).
-  static_assert(2 * fa16_stage_elems<D, BN>() * 2 <= 131072, "LDS budget");
-  __shared__ __align__(16) uint16_t smem[2 * fa16_stage_elems<D, BN>()];
+  static_assert(kFa16Stages * fa16_stage_elems<D, BN>() * 2 <= 131072, "LDS budget");
+  __shared__ __align__(16) uint16_t smem[kFa16Stages * fa16_stage_elems<D, BN>()];
   const WorkSlot ws = decode_slot(p);
   const int n_items = slot_items(p, ws);
   // Every item ends with a barrier after its last LDS read, so the next item

@@ -10,11 +10,11 @@
 //   * split-K: each sequence's tokens are cut into partitions of PART tokens;
 //     a workgroup = 4 waves = 4 consecutive heads of one (sequence, partition),
 //     so the four waves stream adjacent 256-byte head rows of the same pages;
-//   * pass 1 streams K: a token row of one head is read by LPT lanes with
-//     16-byte loads (U loads in flight per lane), partial dot products are
-//     reduced across the LPT lanes, scores land in LDS;
-//   * partition max / exp2 / sum over the LDS scores, then pass 2 streams V
-//     and accumulates p * v in fp32;
+//   * one pass over the partition: a token row of one head is read by LPT
+//     lanes with 16-byte loads; the K and V rows of U tokens per lane are
+//     requested together, partial dot products are reduced across the LPT
+//     lanes, and every token group keeps its own running max and fp32
+//     accumulator (online softmax), merged across the wave at the end;
 //   * per-partition (o, m, l) go to the workspace; paged_decode_merge_kernel
 //     combines them (online-softmax merge) and normalises by the exact sum.
 // The page ids of a partition are staged once in LDS, invalid ids (< 0 or
@@ -41,7 +41,15 @@ struct DecodeParams {
   float c;  // scale * log2(e)
 };
 
-constexpr int kPart = 512;   // tokens per partition
+// Tokens per partition and 16-byte loads in flight per lane (overridable at
+// build time for tuning builds).
+#ifndef MPX_PD_PART
+#define MPX_PD_PART 512
+#endif
+#ifndef MPX_PD_U
+#define MPX_PD_U 16
+#endif
+constexpr int kPart = MPX_PD_PART;
 constexpr int kHeadsPerWG = 4;
 
 template <int DT>
@@ -73,10 +81,9 @@ __global__ __launch_bounds__(256) void paged_decode_part_kernel(DecodeParams p) 
   constexpr int EPC = 16 / ES;               // elements per 16-byte chunk
   constexpr int LPT = D / EPC;               // lanes per token row
   constexpr int TPI = 64 / LPT;              // tokens per wave-wide load
-  constexpr int U = 8;                       // loads in flight per lane
+  constexpr int U = MPX_PD_U;                // tokens per lane per batch
   static_assert(LPT >= 1 && LPT <= 64 && 64 % LPT == 0, "head_dim");
 
-  __shared__ float sc[kHeadsPerWG][kPart];
   __shared__ int btl[kPart + 1];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -86,7 +93,6 @@ __global__ __launch_bounds__(256) void paged_decode_part_kernel(DecodeParams p) 
   const int p0 = part * kPart;
   if (p0 >= ctx) return;  // uniform over the workgroup
   const int p1 = min(p0 + kPart, ctx);
-  const int n = p1 - p0;
   const int pg0 = p0 / p.bs;
   const int npg = (p1 - 1) / p.bs - pg0 + 1;
   for (int i = tid; i < npg; i += 256) {
@@ -94,102 +100,97 @@ __global__ __launch_bounds__(256) void paged_decode_part_kernel(DecodeParams p) 
     btl[i] = (blk >= 0 && blk < p.num_blocks) ? blk : -1;
   }
   __syncthreads();
+  if (h >= p.H) return;
 
-  const bool active = h < p.H;
+  // Lane (tl, cidx): 16-byte chunk cidx of the head row of tokens tl, tl+TPI, ...
   const int cidx = lane % LPT, tl = lane / LPT;
   const int64_t row_elems = (int64_t)p.H * D;
   const int64_t hoff = (int64_t)h * D + cidx * EPC;
   const char* kbase = (const char*)p.kpool;
   const char* vbase = (const char*)p.vpool;
-  float* scw = sc[wave];
 
+  float qv[EPC];
+  {
+    const u32x4 qr = *(const u32x4*)((const char*)p.q +
+                                     ((int64_t)b * p.q_sb + (int64_t)h * p.q_sh + cidx * EPC) * ES);
+#pragma unroll
+    for (int i = 0; i < EPC; ++i) qv[i] = elem<DT>(qr, i) * p.c;
+  }
+  const float slope2 = p.slopes ? p.slopes[h] * kLog2e : 0.f;
+
+  // One pass over the partition: the K and V rows of a batch of U tokens per
+  // lane are requested together; every token group (the LPT lanes of one
+  // token slot) keeps its own running max m, so no cross-lane exchange is
+  // needed until the end.
+  float acc[EPC];
+#pragma unroll
+  for (int i = 0; i < EPC; ++i) acc[i] = 0.f;
   float m = -INFINITY, l = 0.f;
-  if (active) {
-    float qv[EPC];
-    {
-      const u32x4 qr =
-          *(const u32x4*)((const char*)p.q + ((int64_t)b * p.q_sb + (int64_t)h * p.q_sh + cidx * EPC) * ES);
+  for (int t0 = p0; t0 < p1; t0 += TPI * U) {
+    u32x4 kr[U], vr[U];
+    bool ok[U];
 #pragma unroll
-      for (int i = 0; i < EPC; ++i) qv[i] = elem<DT>(qr, i) * p.c;
+    for (int u = 0; u < U; ++u) {
+      const int tk = t0 + u * TPI + tl;
+      int blk = -1;
+      if (tk < p1) blk = btl[tk / p.bs - pg0];
+      ok[u] = blk >= 0;
+      const int64_t off = (((int64_t)blk * p.bs + tk % p.bs) * row_elems + hoff) * ES;
+      kr[u] = ok[u] ? *(const u32x4*)(kbase + off) : (u32x4){0u, 0u, 0u, 0u};
+      vr[u] = ok[u] ? *(const u32x4*)(vbase + off) : (u32x4){0u, 0u, 0u, 0u};
     }
-    const float slope2 = p.slopes ? p.slopes[h] * kLog2e : 0.f;
-
-    // Pass 1: scores of the partition.
-    for (int t0 = p0; t0 < p1; t0 += TPI * U) {
-      u32x4 kr[U];
-      bool ok[U];
+    float sc[U];
+    float mb = m;
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int tk = t0 + u * TPI + tl;
-        int blk = -1;
-        if (tk < p1) blk = btl[tk / p.bs - pg0];
-        ok[u] = blk >= 0;
-        kr[u] = ok[u] ? *(const u32x4*)(kbase + (((int64_t)blk * p.bs + tk % p.bs) * row_elems + hoff) * ES)
-                      : (u32x4){0u, 0u, 0u, 0u};
-      }
+    for (int u = 0; u < U; ++u) {
+      float dot = 0.f;
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        float dot = 0.f;
+      for (int i = 0; i < EPC; ++i) dot = fmaf(qv[i], elem<DT>(kr[u], i), dot);
 #pragma unroll
-        for (int i = 0; i < EPC; ++i) dot = fmaf(qv[i], elem<DT>(kr[u], i), dot);
+      for (int off = LPT / 2; off >= 1; off >>= 1) dot += __shfl_xor(dot, off, 64);
+      const int tk = t0 + u * TPI + tl;
+      sc[u] = ok[u] ? dot + slope2 * (float)(tk - ctx) : -INFINITY;
+      mb = fmaxf(mb, sc[u]);
+    }
+    if (mb > m) {
+      const float alpha = m == -INFINITY ? 0.f : fast_exp2(m - mb);
+      l *= alpha;
 #pragma unroll
-        for (int off = LPT / 2; off >= 1; off >>= 1) dot += __shfl_xor(dot, off, 64);
-        const int tk = t0 + u * TPI + tl;
-        if (cidx == 0 && tk < p1) scw[tk - p0] = ok[u] ? dot + slope2 * (float)(tk - ctx) : -INFINITY;
-      }
+      for (int i = 0; i < EPC; ++i) acc[i] *= alpha;
+      m = mb;
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const float w = sc[u] == -INFINITY ? 0.f : fast_exp2(sc[u] - m);
+      l += w;
+#pragma unroll
+      for (int i = 0; i < EPC; ++i) acc[i] = fmaf(w, elem<DT>(vr[u], i), acc[i]);
     }
   }
-  __syncthreads();
 
-  if (active) {
-    for (int i = lane; i < n; i += 64) m = fmaxf(m, scw[i]);
-    m = wave_max(m);
-    for (int i = lane; i < n; i += 64) {
-      const float e = m == -INFINITY ? 0.f : fast_exp2(scw[i] - m);
-      scw[i] = e;
-      l += e;
-    }
-    l = wave_sum(l);
+  // Merge the token groups of the wave: rescale to the wave max, then sum
+  // over the lanes holding the same dims.
+  const float M = wave_max(m);
+  const float f = m == -INFINITY ? 0.f : fast_exp2(m - M);
+  l *= f;
+#pragma unroll
+  for (int i = 0; i < EPC; ++i) acc[i] *= f;
+#pragma unroll
+  for (int off = LPT; off < 64; off <<= 1) {
+    l += __shfl_xor(l, off, 64);
+#pragma unroll
+    for (int i = 0; i < EPC; ++i) acc[i] += __shfl_xor(acc[i], off, 64);
   }
-  __syncthreads();
 
-  if (active) {
-    // Pass 2: o = sum_t p_t v_t.
-    float acc[EPC];
+  const int64_t slot = ((int64_t)b * p.H + h) * p.max_parts + part;
+  if (tl == 0) {
+    float* wo = p.ws_o + slot * D + cidx * EPC;
 #pragma unroll
-    for (int i = 0; i < EPC; ++i) acc[i] = 0.f;
-    for (int t0 = p0; t0 < p1; t0 += TPI * U) {
-      u32x4 vr[U];
-      float pw[U];
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int tk = t0 + u * TPI + tl;
-        int blk = -1;
-        if (tk < p1) blk = btl[tk / p.bs - pg0];
-        pw[u] = blk >= 0 ? scw[tk - p0] : 0.f;
-        vr[u] = blk >= 0 ? *(const u32x4*)(vbase + (((int64_t)blk * p.bs + tk % p.bs) * row_elems + hoff) * ES)
-                         : (u32x4){0u, 0u, 0u, 0u};
-      }
-#pragma unroll
-      for (int u = 0; u < U; ++u)
-#pragma unroll
-        for (int i = 0; i < EPC; ++i) acc[i] = fmaf(pw[u], elem<DT>(vr[u], i), acc[i]);
-    }
-#pragma unroll
-    for (int off = LPT; off < 64; off <<= 1)
-#pragma unroll
-      for (int i = 0; i < EPC; ++i) acc[i] += __shfl_xor(acc[i], off, 64);
-
-    const int64_t slot = ((int64_t)b * p.H + h) * p.max_parts + part;
-    if (tl == 0) {
-      float* wo = p.ws_o + slot * D + cidx * EPC;
-#pragma unroll
-      for (int i = 0; i < EPC; i += 4) *(f32x4*)(wo + i) = (f32x4){acc[i], acc[i + 1], acc[i + 2], acc[i + 3]};
-    }
-    if (lane == 0) {
-      p.ws_ml[2 * slot] = m;
-      p.ws_ml[2 * slot + 1] = l;
-    }
+    for (int i = 0; i < EPC; i += 4) *(f32x4*)(wo + i) = (f32x4){acc[i], acc[i + 1], acc[i + 2], acc[i + 3]};
+  }
+  if (lane == 0) {
+    p.ws_ml[2 * slot] = M;
+    p.ws_ml[2 * slot + 1] = l;
   }
 }
 
@@ -208,7 +209,20 @@ __global__ __launch_bounds__(64) void paged_decode_merge_kernel(DecodeParams p, 
   for (int i = 0; i < nparts; ++i) M = fmaxf(M, p.ws_ml[2 * (base + i)]);
   for (int d = lane; d < D; d += 64) {
     float acc = 0.f, L = 0.f;
-    for (int i = 0; i < nparts; ++i) {
+    int i = 0;
+    // Eight partials per round, their loads issued together.
+    for (; i + 8 <= nparts; i += 8) {
+      float ov[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) ov[k] = p.ws_o[(base + i + k) * D + d];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const float w = fast_exp2(p.ws_ml[2 * (base + i + k)] - M);
+        L += w * p.ws_ml[2 * (base + i + k) + 1];
+        acc += w * ov[k];
+      }
+    }
+    for (; i < nparts; ++i) {
       const float w = fast_exp2(p.ws_ml[2 * (base + i)] - M);
       L += w * p.ws_ml[2 * (base + i) + 1];
       acc += w * p.ws_o[(base + i) * D + d];
