@@ -62,32 +62,28 @@ struct FwdParams {
 #ifndef MPX_FA_SCHED
 #define MPX_FA_SCHED 2
 #endif
-#ifndef MPX_FA_PRIO
-#define MPX_FA_PRIO 0
-#endif
 #ifndef MPX_FA_NWAVES_F32
 #define MPX_FA_NWAVES_F32 4
 #endif
 #ifndef MPX_FA_BN16
 #define MPX_FA_BN16 64
 #endif
-// 1: the two waves sharing a SIMD run half a tile apart (see fa16_rows).
-#ifndef MPX_FA_PINGPONG
-#define MPX_FA_PINGPONG 0
-#endif
-// 1: fully visible tiles overlap the softmax with the MFMAs of the same wave
-// (see spec_tile in fa16_rows).
-#ifndef MPX_FA_SPEC
-#define MPX_FA_SPEC 0
-#endif
 // K/V tiles held in registers ahead of their LDS staging: 2 (tile i+2 is
 // loaded while tile i computes) or 1 (tile i+1).
 #ifndef MPX_FA_DEPTH
 #define MPX_FA_DEPTH 2
 #endif
-// LDS stages of the 16-bit kernel: the offset schedule keeps tile i-1
-// readable while tile i+1 is staged.
-constexpr int kFa16Stages = MPX_FA_PINGPONG ? 3 : 2;
+// 1: D = 128 tiles are staged by direct global->LDS loads (see fa16_rows_direct).
+#ifndef MPX_FA_DIRECT
+#define MPX_FA_DIRECT 1
+#endif
+// LDS stages of the direct path (3: tile i+2 in flight while tile i
+// computes; 4: tile i+3, 128 KB of LDS).
+#ifndef MPX_FA_DSTAGES
+#define MPX_FA_DSTAGES 4
+#endif
+// LDS stages of the register-staged 16-bit kernel.
+constexpr int kFa16Stages = 2;
 
 // Compile-time integer tag (selects a register set in the unrolled loop).
 template <int N>
@@ -486,123 +482,6 @@ __device__ __forceinline__ void fa16_rows(const FwdParams& p, const WorkItem wi,
     pv_tile(Vt, pop);
   };
 
-#if MPX_FA_SPEC
-  // exp2(s*c - msub) of one 32-key block, packed into two PV B operands; the
-  // row sum accumulates the packed weights.
-  auto exp_block = [&](const f32x16& sb, float msub, u32x4& p_lo, u32x4& p_hi, float& lsum)
-      __attribute__((always_inline)) {
-#pragma unroll
-    for (int hh = 0; hh < 2; ++hh)
-#pragma unroll
-      for (int e2 = 0; e2 < 4; ++e2) {
-        const float x0 = fast_exp2(sb[8 * hh + 2 * e2] * c - msub);
-        const float x1 = fast_exp2(sb[8 * hh + 2 * e2 + 1] * c - msub);
-        const u32 pk = pack2<BF16>(x0, x1);
-        if (hh == 0) p_lo[e2] = pk; else p_hi[e2] = pk;
-        lsum = dot2_sum<BF16>(pk, lsum);
-      }
-  };
-
-  // A fully visible tile with the softmax interleaved into the same wave's
-  // MFMAs: the weights of keys 0..31 are computed against the running max
-  // m_run while the scores of keys 32..63 are still in the MFMA pipe, and the
-  // weights of keys 32..63 while the PV MFMAs of keys 0..31 run. Exact: if
-  // the tile's max exceeds m_run by more than the rescale threshold, O and l
-  // are rescaled and the weights of keys 0..31 recomputed before any PV
-  // MFMA uses them.
-  auto spec_tile = [&](const uint16_t* Ks, const uint16_t* Vt) __attribute__((always_inline)) {
-    static_assert(NB == 2, "two 32-key blocks per tile");
-    f32x16 s0, s1;
-    {
-      const u32x4* kp0 = (const u32x4*)(Ks + krow_perm * KS) + g;
-      const u32x4* kp1 = (const u32x4*)(Ks + (32 + krow_perm) * KS) + g;
-      u32x4 ka[NKS], kb[NKS];
-#pragma unroll
-      for (int ks = 0; ks < NKS; ++ks) ka[ks] = kp0[2 * ks];
-#pragma unroll
-      for (int ks = 0; ks < NKS; ++ks) kb[ks] = kp1[2 * ks];
-      s0 = (f32x16){};
-#pragma unroll
-      for (int ks = 0; ks < NKS; ++ks) s0 = mfma32x32x16<BF16>(ka[ks], qreg[ks], s0);
-      s1 = (f32x16){};
-#pragma unroll
-      for (int ks = 0; ks < NKS; ++ks) s1 = mfma32x32x16<BF16>(kb[ks], qreg[ks], s1);
-    }
-    float mt0 = s0[0];
-#pragma unroll
-    for (int e = 1; e < 16; ++e) mt0 = fmaxf(mt0, s0[e]);
-    const float msub0 = m_run == -INFINITY ? 0.f : m_run;
-    u32x4 pop[NSL];
-    float lsum0 = 0.f;
-    exp_block(s0, msub0, pop[0], pop[1], lsum0);
-    // K reads, then block 0's MFMAs under block 1's K reads, then block 1's
-    // MFMAs with block 0's max / exp / pack between them.
-    __builtin_amdgcn_sched_group_barrier(0x100, NKS, 0);
-#pragma unroll
-    for (int i = 0; i < NKS; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-    }
-#pragma unroll
-    for (int i = 0; i < NKS; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x402, 7, 0);
-    }
-
-    float mt = mt0;
-#pragma unroll
-    for (int e = 0; e < 16; ++e) mt = fmaxf(mt, s1[e]);
-    mt = fmaxf(mt, xor32(mt)) * c;
-    m_max = fmaxf(m_max, mt);
-    if (__any(mt > m_run + kRescaleThreshold)) {
-      asm volatile("" ::: "memory");  // a real branch, not selects on all of o
-      const float m_new = fmaxf(m_run, mt);
-      const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(m_run - m_new);
-      l_run *= alpha;
-#pragma unroll
-      for (int db = 0; db < NDB; ++db)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) o[db][e] *= alpha;
-      m_run = m_new;
-      lsum0 = 0.f;
-      exp_block(s0, m_run == -INFINITY ? 0.f : m_run, pop[0], pop[1], lsum0);
-    }
-    const float msub = m_run == -INFINITY ? 0.f : m_run;
-    float lsum1 = 0.f;
-    exp_block(s1, msub, pop[2], pop[3], lsum1);
-    l_run += lsum0 + lsum1;
-
-    // PV in (key half, dim block) pairs: two MFMAs per pair, the V operands
-    // of the next pair read under them; block 1's exp / pack runs under the
-    // MFMAs of keys 0..31.
-    const u32x4* vp = (const u32x4*)Vt + vlane;
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-      for (int db = 0; db < NDB; ++db) {
-        const u32x4 v0 = vp[db * 32 * (VS / 8) + 2 * ((2 * h) ^ (db & (VXM >> 1)))];
-        const u32x4 v1 = vp[db * 32 * (VS / 8) + 2 * ((2 * h + 1) ^ (db & (VXM >> 1)))];
-        o[db] = mfma32x32x16<BF16>(v0, pop[2 * h], o[db]);
-        o[db] = mfma32x32x16<BF16>(v1, pop[2 * h + 1], o[db]);
-      }
-    __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
-#pragma unroll
-    for (int i = 0; i < NDB; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
-      __builtin_amdgcn_sched_group_barrier(0x402, 6, 1);
-      __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
-      __builtin_amdgcn_sched_group_barrier(0x402, 6, 1);
-    }
-#pragma unroll
-    for (int i = 0; i < NDB - 1; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
-      __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
-    }
-    __builtin_amdgcn_sched_group_barrier(0x008, 2, 1);
-  };
-#endif
 
   // Attention of this wave's rows to the tile at kv0 staged in LDS stage `stage`.
   auto compute_tile = [&](int stage, int kv0) __attribute__((always_inline)) {
@@ -610,13 +489,6 @@ __device__ __forceinline__ void fa16_rows(const FwdParams& p, const WorkItem wi,
     classify_tile<BN>(p, kv0, wq0, wq0 + 31, skip, full);
     if (skip) return;
     const uint16_t* Ks = smem + stage * STAGE;
-#if MPX_FA_SPEC
-    if (full) {
-      spec_tile(Ks, Ks + K_ELEMS);
-      return;
-    }
-    asm volatile("" ::: "memory");
-#endif
     f32x16 s[NB];
     qk_tile(Ks, s);
     softmax_pv(Ks + K_ELEMS, kv0, full, s);
@@ -629,54 +501,7 @@ __device__ __forceinline__ void fa16_rows(const FwdParams& p, const WorkItem wi,
     if (NSET == 2 && n_tiles > 1) load_tile(kv_lo + (t_begin + 1) * BN, Const<NSET - 1>{});
   }
   __syncthreads();
-#if MPX_FA_PRIO == 1
-  // Ping-pong: waves 0..NW/2-1 (one per SIMD) win issue arbitration, so the
-  // other wave on each SIMD runs its softmax while the first one's MFMAs run
-  // and vice versa, instead of both waves contending for the same unit.
-  if (wave < NW / 2) __builtin_amdgcn_s_setprio(1);
-#endif
 
-#if MPX_FA_PINGPONG
-  // Offset schedule: on every SIMD one wave (wave < NW/2) computes tile i
-  // (QK -> softmax -> PV) while its partner (wave + NW/2) runs PV of tile i-1
-  // and then QK and softmax of tile i, so each wave's softmax runs under the
-  // other's MFMAs instead of both waves contending for the same unit. Tile i
-  // sits in stage i%3; tile i+1 is staged into stage (i+1)%3 while stage
-  // (i-1)%3 still holds tile i-1 for the trailing waves.
-  // Both groups run QK and softmax of tile i in the same place; a lead wave
-  // then runs PV of tile i, a trailing wave runs PV of tile i-1 first (its
-  // P^T carried over the barrier in pp).
-  const bool lead = wave < NW / 2;
-  auto stage_of = [](int i) { return i - (i / 3) * 3; };
-  f32x16 sp[NB];
-  u32x4 pp[NSL];
-  bool pp_valid = false;
-  auto step = [&](int i, auto PAR) __attribute__((always_inline)) {
-    constexpr int P = decltype(PAR)::value;
-    const int kv0 = kv_lo + (t_begin + i) * BN;
-    const int stage = stage_of(i);
-    if (i + 2 < n_tiles) load_tile(kv0 + 2 * BN, Const<P>{});
-    if (!lead && pp_valid) pv_tile(smem + stage_of(i + 2) * STAGE + K_ELEMS, pp);
-    bool skip, full;
-    classify_tile<BN>(p, kv0, wq0, wq0 + 31, skip, full);
-    pp_valid = !skip;
-    if (!skip) {
-      qk_tile(smem + stage * STAGE, sp);
-      softmax_p(kv0, full, sp, pp);
-      if (lead) pv_tile(smem + stage * STAGE + K_ELEMS, pp);
-    }
-    if (i + 1 < n_tiles) store_tile(Const<1 - P>{}, stage_of(i + 1));
-    __syncthreads();
-  };
-  for (int i = 0; i < n_tiles; i += 2) {
-    step(i, Const<0>{});
-    if (i + 1 < n_tiles) step(i + 1, Const<1>{});
-  }
-  if (!lead && pp_valid) pv_tile(smem + stage_of(n_tiles - 1) * STAGE + K_ELEMS, pp);
-  // The trailing waves read LDS after the last barrier of the loop; the next
-  // item restages it.
-  __syncthreads();
-#else
   // Tile i: computed from stage i%2; tile i+2 loaded into register set i%2;
   // tile i+1 staged from register set (i+1)%2 into stage (i+1)%2.
   auto step = [&](int i, auto PAR) __attribute__((always_inline)) {
@@ -695,12 +520,326 @@ __device__ __forceinline__ void fa16_rows(const FwdParams& p, const WorkItem wi,
     step(i, Const<0>{});
     if (i + 1 < n_tiles) step(i + 1, Const<1>{});
   }
-#endif
-#if MPX_FA_PRIO == 1
-  __builtin_amdgcn_s_setprio(0);
-#endif
 
   // Epilogue: move o and l to the true max, then normalise (or emit partials).
+  const float l_tot = l_run + xor32(l_run);
+  const float f = m_max == -INFINITY ? 0.f : fast_exp2(m_run - m_max);
+  if (p.num_splits == 1) {
+    if (myq < p.Sq) {
+      const float inv = m_max == -INFINITY ? 0.f : f / (l_tot * f + kSoftmaxEps);
+      uint16_t* Op = (uint16_t*)p.o + wi.b * p.o_sb + wi.h * p.o_sh + (int64_t)myq * p.o_ss;
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int e4 = 0; e4 < 4; ++e4) {
+          const int d = db * 32 + 8 * e4 + 4 * g;
+          const u32x2 val = {pack2<BF16>(o[db][4 * e4] * inv, o[db][4 * e4 + 1] * inv),
+                             pack2<BF16>(o[db][4 * e4 + 2] * inv, o[db][4 * e4 + 3] * inv)};
+          *(u32x2*)(Op + d) = val;
+        }
+    }
+  } else if (myq < p.Sq) {
+    const int64_t row = (((int64_t)wi.split * p.B + wi.b) * p.H + wi.h) * p.Sq + myq;
+    float* wo = p.ws_o + row * D;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int e4 = 0; e4 < 4; ++e4) {
+        const int d = db * 32 + 8 * e4 + 4 * g;
+        *(f32x4*)(wo + d) = (f32x4){o[db][4 * e4] * f, o[db][4 * e4 + 1] * f,
+                                    o[db][4 * e4 + 2] * f, o[db][4 * e4 + 3] * f};
+      }
+    if (g == 0) {
+      p.ws_ml[2 * row] = m_max;
+      p.ws_ml[2 * row + 1] = l_tot * f;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// D = 128 with direct global->LDS staging (gfx950 LDS DMA): the K and V tiles
+// go from HBM/L2 straight into LDS with buffer_load ... lds, without passing
+// through registers; three LDS stages hold tiles i (computing), i+1 (landed)
+// and i+2 (in flight).
+//
+// LDS rows are 256 bytes, unpadded (a DMA instruction writes 64 consecutive
+// 16-byte slots), so bank conflicts are avoided by XOR-swizzling 16-byte
+// chunks instead:
+//   K row r: chunk c stored at slot c ^ (r & 15)      (QK operand reads:
+//            16 lanes read 16 different rows at one logical chunk);
+//   V row r: chunk c stored at slot c ^ (4 * (r & 3)) (PV operand reads:
+//            ds_read_b64_tr_b16 takes 4 rows x 64 bytes per 32 lanes).
+// V stays row-major: the transposing LDS read delivers V^T operands. For a
+// group of 16 lanes whose lane s addresses row base + s/4, columns
+// c0 + 4*(s%4) .. +3, lane s receives column c0 + s of rows base .. base + 3.
+// ---------------------------------------------------------------------------
+// Workgroup barrier without the memory fence of __syncthreads (which would wait
+// for every outstanding load, including the DMA of the tile two steps ahead);
+// the caller has already waited for the loads the other waves need. The empty
+// asm statements keep the compiler from moving LDS accesses across it.
+__device__ __forceinline__ void stage_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// One 16-byte-per-lane DMA: lane l's bytes land at LDS address lds_addr +
+// 16*l. Issued as inline assembly so the compiler does not track it: its
+// waitcnt pass would otherwise make LDS reads after the loop back-edge wait
+// for every DMA in flight (it cannot tell their target stages apart there).
+// The caller waits for completion with explicit s_waitcnt vmcnt. M0 carries
+// the LDS address; nothing else in these kernels uses M0.
+__device__ __forceinline__ void dma16(u32x4 rsrc, unsigned lds_addr, int voff, int soff) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :
+               : "s"(lds_addr), "v"(voff), "s"(rsrc), "s"(soff)
+               : "memory", "m0");
+}
+
+// Raw buffer descriptor words (base, stride 0, num_records, gfx950 flags).
+__device__ __forceinline__ u32x4 buffer_desc(const void* base) {
+  const unsigned long long a = (unsigned long long)base;
+  return (u32x4){(u32)a, (u32)(a >> 32) & 0xffffu, 0x7fffffffu, (u32)kBufferFlags};
+}
+
+__device__ __forceinline__ u32 lds_addr(const void* p) {
+  return (u32)(unsigned long long)(__attribute__((address_space(3))) const void*)p;
+}
+
+__device__ __forceinline__ u32x2 lds_read_tr16(const unsigned char* p) {
+  typedef __attribute__((ext_vector_type(4))) short s16x4;
+  const s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s16x4*)(p));
+  return __builtin_bit_cast(u32x2, r);
+}
+
+template <int NW, bool BF16, int NST>
+__device__ __forceinline__ void fa16_rows_direct(const FwdParams& p, const WorkItem wi,
+                                                 unsigned char* __restrict__ st0,
+                                                 unsigned char* __restrict__ st1,
+                                                 unsigned char* __restrict__ st2,
+                                                 unsigned char* __restrict__ st3) {
+  constexpr int D = 128, BN = 64, BM = 32 * NW;
+  constexpr int NB = BN / 32, NSL = BN / 16, NKS = D / 16, NDB = D / 32;
+  constexpr int ROWB = 2 * D;          // bytes per K or V row
+  constexpr int KBYTES = BN * ROWB;    // one K (or V) tile
+  constexpr int STAGEB = 2 * KBYTES;   // K then V
+  static_assert(NW == 8, "each wave stages rows 4*wave .. +3 and +32 .. +35");
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int j = lane & 31, g = lane >> 5;
+
+  const int q0 = wi.qt * BM;
+  int kv_lo, t_begin, t_end;
+  kv_range<BM, BN>(p, q0, wi.split, kv_lo, t_begin, t_end);
+
+  const uint16_t* __restrict__ Qp = (const uint16_t*)p.q + wi.b * p.q_sb + wi.h * p.q_sh;
+  const u32x4 krs = buffer_desc((const uint16_t*)p.k + wi.b * p.k_sb + wi.h * p.k_sh);
+  const u32x4 vrs = buffer_desc((const uint16_t*)p.v + wi.b * p.v_sb + wi.h * p.v_sh);
+
+  const int wq0 = q0 + wave * 32;
+  const int myq = wq0 + j;
+  u32x4 qreg[NKS];
+  {
+    const u32x4* src = (const u32x4*)(Qp + (int64_t)min(myq, p.Sq - 1) * p.q_ss);
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) qreg[ks] = src[2 * ks + g];
+  }
+  if (p.neg) {
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) qreg[ks] ^= 0x80008000u;
+  }
+  // Q has landed (and the previous item's stores retired) before any tile
+  // DMA, so the explicit vmcnt waits below count tile loads only.
+  __builtin_amdgcn_s_waitcnt(0x0F70);
+
+  // DMA lane mapping: this wave's first instruction fills LDS rows
+  // 4*wave .. +3 (lane -> row lr, slot lane%16), the second rows lr + 32.
+  const int lr = 4 * wave + (lane >> 4);
+  const int kchunk = (lane & 15) ^ (lr & 15);
+  const int vchunk = (lane & 15) ^ (4 * (lr & 3));
+  const int kgo = (lr * (int)p.k_ss + kchunk * 8) * 2;
+  const int vgo = (lr * (int)p.v_ss + vchunk * 8) * 2;
+  const int k32 = 32 * (int)p.k_ss * 2, v32 = 32 * (int)p.v_ss * 2;
+  auto stage_ptr = [&](auto ST) __attribute__((always_inline)) -> unsigned char* {
+    constexpr int S = decltype(ST)::value;
+    return S == 0 ? st0 : (S == 1 ? st1 : (S == 2 ? st2 : st3));
+  };
+  auto load_tile = [&](int kv0, unsigned char* stbase) __attribute__((always_inline)) {
+    const u32 kdst = lds_addr(stbase + wave * 4 * ROWB);
+    const u32 vdst = kdst + KBYTES;
+    const int kso = kv0 * (int)p.k_ss * 2, vso = kv0 * (int)p.v_ss * 2;
+    if (kv0 + BN <= p.Sk) {
+      dma16(krs, kdst, kgo, kso);
+      dma16(krs, kdst + 32 * ROWB, kgo, kso + k32);
+      dma16(vrs, vdst, vgo, vso);
+      dma16(vrs, vdst + 32 * ROWB, vgo, vso + v32);
+    } else {
+      // Tail tile: rows past Sk re-read the last valid row (their scores are
+      // masked, so their weights are exactly 0).
+      const int lim = p.Sk - 1 - kv0;
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const int row = min(lr + 32 * r, lim);
+        dma16(krs, kdst + r * 32 * ROWB, (row * (int)p.k_ss + kchunk * 8) * 2, kso);
+        dma16(vrs, vdst + r * 32 * ROWB, (row * (int)p.v_ss + vchunk * 8) * 2, vso);
+      }
+    }
+  };
+
+  // QK operand (A = K rows) of lane (j, g): row nb*32 + krow_perm, logical
+  // chunk 2*ks + g, stored at slot (2*ks + g) ^ (row & 15).
+  const int krow_perm = (j & ~12) | ((j & 4) << 1) | ((j & 8) >> 1);
+  const int ky = krow_perm & 15;
+  int kaddr[NKS];
+#pragma unroll
+  for (int ks = 0; ks < NKS; ++ks)
+    kaddr[ks] = krow_perm * ROWB + 32 * (ks ^ (ky >> 1)) + 16 * (g ^ (ky & 1));
+  // PV operand (A = V^T) of lane L = j + 32g: rows 16*sl + 8g + 4h + s/4,
+  // columns 32*db + 16*(L/16 % 2) + 4*(s%4) of the transposing read, s = L%16.
+  const int s16 = lane & 15;
+  int vaddr[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db)
+    vaddr[db] = (8 * g + (s16 >> 2)) * ROWB + 64 * (db ^ (s16 >> 2)) + 32 * ((lane >> 4) & 1) +
+                8 * (s16 & 3);
+
+  f32x16 o[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) o[db] = (f32x16){};
+  float m_run = -INFINITY, m_max = -INFINITY, l_run = 0.f;
+  const float c = p.c;
+  const int kv_first = p.win_left >= 0 ? myq - p.win_left : -(1 << 30);
+  const int kv_last = min(p.win_right >= 0 ? myq + p.win_right : (1 << 30), p.Sk - 1);
+
+  auto compute_tile = [&](const unsigned char* Kb, int kv0) __attribute__((always_inline)) {
+    bool skip, full;
+    classify_tile<BN>(p, kv0, wq0, wq0 + 31, skip, full);
+    if (skip) return;
+    const unsigned char* Vb = Kb + KBYTES;
+
+    f32x16 s[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      u32x4 ka[NKS];
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) ka[ks] = *(const u32x4*)(Kb + kaddr[ks] + nb * 32 * ROWB);
+      s[nb] = (f32x16){};
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) s[nb] = mfma32x32x16<BF16>(ka[ks], qreg[ks], s[nb]);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x100, NKS, 0);
+#pragma unroll
+    for (int i = 0; i < NKS * (NB - 1); ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, NKS, 0);
+
+    if (!full) {
+      asm volatile("" ::: "memory");
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int kv = kv0 + nb * 32 + 16 * (e >> 3) + 8 * g + (e & 7);
+          s[nb][e] = ((kv >= kv_first) & (kv <= kv_last)) ? s[nb][e] : -INFINITY;
+        }
+    }
+    float mt = -INFINITY;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) mt = fmaxf(mt, s[nb][e]);
+    mt = fmaxf(mt, xor32(mt)) * c;
+    m_max = fmaxf(m_max, mt);
+    if (__any(mt > m_run + kRescaleThreshold)) {
+      asm volatile("" ::: "memory");
+      const float m_new = fmaxf(m_run, mt);
+      const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(m_run - m_new);
+      l_run *= alpha;
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) o[db][e] *= alpha;
+      m_run = m_new;
+    }
+    const float msub = m_run == -INFINITY ? 0.f : m_run;
+    u32x4 pop[NSL];
+    float lsum = 0.f;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+        for (int e2 = 0; e2 < 4; ++e2) {
+          const float x0 = fast_exp2(s[nb][8 * hh + 2 * e2] * c - msub);
+          const float x1 = fast_exp2(s[nb][8 * hh + 2 * e2 + 1] * c - msub);
+          const u32 pk = pack2<BF16>(x0, x1);
+          pop[2 * nb + hh][e2] = pk;
+          lsum = dot2_sum<BF16>(pk, lsum);
+        }
+    l_run += lsum;
+
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+      u32x4 va[NSL];
+#pragma unroll
+      for (int sl = 0; sl < NSL; ++sl) {
+        const u32x2 lo = lds_read_tr16(Vb + vaddr[db] + (16 * sl) * ROWB);
+        const u32x2 hi = lds_read_tr16(Vb + vaddr[db] + (16 * sl + 4) * ROWB);
+        va[sl] = (u32x4){lo[0], lo[1], hi[0], hi[1]};
+      }
+#pragma unroll
+      for (int sl = 0; sl < NSL; ++sl) o[db] = mfma32x32x16<BF16>(va[sl], pop[sl], o[db]);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x100, 2 * NSL, 1);
+#pragma unroll
+    for (int i = 0; i < NSL * (NDB - 1); ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, NSL, 1);
+  };
+
+  // Every tile is 4 DMA instructions per wave; after issuing tiles up to
+  // `last`, tile t has landed once at most 4 * (last - t) loads are pending.
+  auto wait_tiles_after = [&](int pending_tiles) __attribute__((always_inline)) {
+    if (pending_tiles >= 2) {
+      __builtin_amdgcn_s_waitcnt(0x0F78);  // vmcnt(8)
+    } else if (pending_tiles == 1) {
+      __builtin_amdgcn_s_waitcnt(0x0F74);  // vmcnt(4)
+    } else {
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    }
+  };
+  const int n_tiles = t_end - t_begin;
+  if (n_tiles > 0) load_tile(kv_lo + t_begin * BN, st0);
+  if (n_tiles > 1) load_tile(kv_lo + (t_begin + 1) * BN, st1);
+  if (NST == 4 && n_tiles > 2) load_tile(kv_lo + (t_begin + 2) * BN, st2);
+  wait_tiles_after(min(n_tiles, NST - 1) - 1);  // tile 0 landed
+  stage_barrier();
+  // Tile i computes from stage i%NST; tile i+NST-1 goes to the stage tile
+  // i-1 used (every wave finished reading it before the last barrier).
+  auto step = [&](int i, auto ST) __attribute__((always_inline)) {
+    constexpr int S = decltype(ST)::value;
+    const int kv0 = kv_lo + (t_begin + i) * BN;
+    if (i + NST - 1 < n_tiles)
+      load_tile(kv0 + (NST - 1) * BN, stage_ptr(Const<(S + NST - 1) % NST>{}));
+    compute_tile(stage_ptr(Const<S>{}), kv0);
+    // Tile i+1 must have landed before the barrier that hands it to every
+    // wave; the tiles issued after it may stay in flight.
+    wait_tiles_after(min(n_tiles - 1, i + NST - 1) - (i + 1));
+    stage_barrier();
+  };
+  for (int i = 0; i < n_tiles; i += NST) {
+    step(i, Const<0>{});
+    if (i + 1 < n_tiles) step(i + 1, Const<1>{});
+    if (i + 2 < n_tiles) step(i + 2, Const<2 % NST>{});
+    if (NST == 4 && i + 3 < n_tiles) step(i + 3, Const<3 % NST>{});
+  }
+
   const float l_tot = l_run + xor32(l_run);
   const float f = m_max == -INFINITY ? 0.f : fast_exp2(m_run - m_max);
   if (p.num_splits == 1) {
@@ -740,15 +879,31 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(MPX_FA_
 void fa_fwd16_kernel(FwdParams p) {
   // Stay within 128 KB of LDS per workgroup (a 136 KB configuration gave wrong
   // results on gfx950).
-  static_assert(kFa16Stages * fa16_stage_elems<D, BN>() * 2 <= 131072, "LDS budget");
-  __shared__ __align__(16) uint16_t smem[kFa16Stages * fa16_stage_elems<D, BN>()];
+  constexpr bool kDirect = MPX_FA_DIRECT && D == 128 && BN == 64 && NW == 8;
+  constexpr int kDStages = MPX_FA_DSTAGES;
+  constexpr int kLdsBytes =
+      kDirect ? kDStages * 2 * BN * 2 * D : kFa16Stages * fa16_stage_elems<D, BN>() * 2;
+  static_assert(kLdsBytes <= 131072, "LDS budget");
+  // Direct staging uses three separate stage arrays (so alias analysis can
+  // tell a stage being read from the stage a DMA is writing); smem is used by
+  // the register-staged path.
+  constexpr int kStageB = kDirect ? 2 * BN * 2 * D : 16;
+  __shared__ __align__(16) uint16_t smem[kDirect ? 8 : kLdsBytes / 2];
+  __shared__ __align__(16) unsigned char dst0[kStageB];
+  __shared__ __align__(16) unsigned char dst1[kStageB];
+  __shared__ __align__(16) unsigned char dst2[kStageB];
+  __shared__ __align__(16) unsigned char dst3[kDStages == 4 ? kStageB : 16];
   const WorkSlot ws = decode_slot(p);
   const int n_items = slot_items(p, ws);
   // Every item ends with a barrier after its last LDS read, so the next item
   // may restage LDS at once.
 #pragma nounroll
-  for (int item = 0; item < n_items; ++item)
-    fa16_rows<D, BN, NW, BF16>(p, slot_item(p, ws, item), smem);
+  for (int item = 0; item < n_items; ++item) {
+    if constexpr (kDirect)
+      fa16_rows_direct<NW, BF16, kDStages>(p, slot_item(p, ws, item), dst0, dst1, dst2, dst3);
+    else
+      fa16_rows<D, BN, NW, BF16>(p, slot_item(p, ws, item), smem);
+  }
 }
 
 // ---------------------------------------------------------------------------
