@@ -713,13 +713,9 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& p, const WorkI
   const int kv_first = p.win_left >= 0 ? myq - p.win_left : -(1 << 30);
   const int kv_last = min(p.win_right >= 0 ? myq + p.win_right : (1 << 30), p.Sk - 1);
 
-  auto compute_tile = [&](const unsigned char* Kb, int kv0) __attribute__((always_inline)) {
-    bool skip, full;
-    classify_tile<BN>(p, kv0, wq0, wq0 + 31, skip, full);
-    if (skip) return;
-    const unsigned char* Vb = Kb + KBYTES;
-
-    f32x16 s[NB];
+  // S^T of this wave's rows against the K tile at Kb (MFMAs only; the
+  // caller orders them against other work).
+  auto qk_mfma = [&](const unsigned char* Kb, f32x16 (&s)[NB]) __attribute__((always_inline)) {
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
       u32x4 ka[NKS];
@@ -729,6 +725,9 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& p, const WorkI
 #pragma unroll
       for (int ks = 0; ks < NKS; ++ks) s[nb] = mfma32x32x16<BF16>(ka[ks], qreg[ks], s[nb]);
     }
+  };
+  // K reads of block nb+1 in flight under the MFMAs of block nb.
+  auto qk_sched = [&]() __attribute__((always_inline)) {
     __builtin_amdgcn_sched_group_barrier(0x100, NKS, 0);
 #pragma unroll
     for (int i = 0; i < NKS * (NB - 1); ++i) {
@@ -736,7 +735,9 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& p, const WorkI
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     }
     __builtin_amdgcn_sched_group_barrier(0x008, NKS, 0);
-
+  };
+  // Masks, row max and (rare) rescale of O for the tile at kv0.
+  auto max_rescale = [&](f32x16 (&s)[NB], int kv0, bool full) __attribute__((always_inline)) {
     if (!full) {
       asm volatile("" ::: "memory");
 #pragma unroll
@@ -765,8 +766,11 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& p, const WorkI
         for (int e = 0; e < 16; ++e) o[db][e] *= alpha;
       m_run = m_new;
     }
+  };
+  // P^T = exp2(s*c - m) packed to 16 bits; the row sum accumulates the packed
+  // (rounded) weights, the exact weights the PV product uses.
+  auto exp_p = [&](const f32x16 (&s)[NB], u32x4 (&pop)[NSL]) __attribute__((always_inline)) {
     const float msub = m_run == -INFINITY ? 0.f : m_run;
-    u32x4 pop[NSL];
     float lsum = 0.f;
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb)
@@ -781,7 +785,9 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& p, const WorkI
           lsum = dot2_sum<BF16>(pk, lsum);
         }
     l_run += lsum;
-
+  };
+  // O += P V for the V tile at Vb (operands through the transposing read).
+  auto pv_mfma = [&](const unsigned char* Vb, const u32x4 (&pop)[NSL]) __attribute__((always_inline)) {
 #pragma unroll
     for (int db = 0; db < NDB; ++db) {
       u32x4 va[NSL];
@@ -794,6 +800,8 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& p, const WorkI
 #pragma unroll
       for (int sl = 0; sl < NSL; ++sl) o[db] = mfma32x32x16<BF16>(va[sl], pop[sl], o[db]);
     }
+  };
+  auto pv_sched = [&]() __attribute__((always_inline)) {
     __builtin_amdgcn_sched_group_barrier(0x100, 2 * NSL, 1);
 #pragma unroll
     for (int i = 0; i < NSL * (NDB - 1); ++i) {
@@ -801,6 +809,20 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& p, const WorkI
       __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
     }
     __builtin_amdgcn_sched_group_barrier(0x008, NSL, 1);
+  };
+
+  auto compute_tile = [&](const unsigned char* Kb, int kv0) __attribute__((always_inline)) {
+    bool skip, full;
+    classify_tile<BN>(p, kv0, wq0, wq0 + 31, skip, full);
+    if (skip) return;
+    f32x16 s[NB];
+    qk_mfma(Kb, s);
+    qk_sched();
+    max_rescale(s, kv0, full);
+    u32x4 pop[NSL];
+    exp_p(s, pop);
+    pv_mfma(Kb + KBYTES, pop);
+    pv_sched();
   };
 
   // Every tile is 4 DMA instructions per wave; after issuing tiles up to
