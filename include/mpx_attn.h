@@ -114,6 +114,67 @@ int mpx_paged_decode(const void* q, const void* k_pool, const void* v_pool,
 /* Workspace needed by mpx_paged_decode (per-partition (o, m, l) partials). */
 size_t mpx_paged_decode_workspace_bytes(int B, int H, int D, int block_size, int max_blocks);
 
+/*
+ * Paged-KV prefill attention: Sq query tokens per sequence against the
+ * sequence's cached tokens, gathered through a block table inside the
+ * attention kernel (no dense copy of the pages is made).
+ *
+ * Replaces paged_attention(...) with seq_q > 1
+ * (mlx_primitives/cache/paged_attention.py:44-105 -> prefill path 211-320).
+ *
+ *   q             (B, H, Sq, D) via q_strides = {batch, head, seq}, D contiguous
+ *   k_pool/v_pool (num_blocks, block_size, H, D), contiguous
+ *   block_tables  int32 (B, max_blocks), row-major, -1 = no page
+ *   context_lens  int32 (B,)
+ *   alibi_slopes  float32 (H,) or NULL; bias = slope_h * (kv_pos - q_pos)
+ *   o             (B, H, Sq, D) via o_strides
+ *
+ * Query i sits at position i (top-left alignment, as in the reference): with
+ * causal != 0 it sees kv_pos <= i. Token t of sequence b is valid iff
+ * t < context_lens[b] and 0 <= block_tables[b, t / block_size] < num_blocks.
+ * Exact softmax over the valid, unmasked tokens; a query row with none gets
+ * NaN (the reference's softmax over an all -inf row). D in {32, 64, 128};
+ * 16-bit pools must be below 4 GiB each (MPX_EUNSUPPORTED otherwise).
+ */
+int mpx_paged_prefill(const void* q, const void* k_pool, const void* v_pool,
+                      const int32_t* block_tables, const int32_t* context_lens,
+                      const float* alibi_slopes, void* o,
+                      const int64_t* q_strides, const int64_t* o_strides,
+                      int B, int Sq, int H, int D, int num_blocks, int block_size,
+                      int max_blocks, float scale, int causal, int dtype,
+                      void* workspace, size_t workspace_bytes, void* stream);
+
+/* Workspace needed by mpx_paged_prefill (split-KV partials when few query tiles). */
+size_t mpx_paged_prefill_workspace_bytes(int B, int Sq, int H, int D, int block_size,
+                                         int max_blocks, int causal, int dtype);
+
+/*
+ * KV-cache append: write T new key/value token rows per sequence into their
+ * pages. Token t (< n_tokens[b]) of sequence b goes to position
+ * pos = start_pos[b] + t, i.e. page block_tables[b, pos / block_size], slot
+ * pos % block_size of both pools.
+ *
+ * Replaces KVCache._store_kv (mlx_primitives/cache/kv_cache.py:194-264) and the
+ * BlockAllocator.set_block_data writes it issues
+ * (mlx_primitives/cache/block_allocator.py:299-331), batched over sequences.
+ *
+ *   k, v          (B, T, H, D) via k_strides / v_strides = {batch, token, head}
+ *   k_pool/v_pool (num_blocks, block_size, H, D), contiguous, updated in place
+ *   block_tables  int32 (B, max_blocks); start_pos, n_tokens int32 (B,)
+ *   errors        int32[3] device words, cleared to 0 by the caller; the kernel
+ *                 sets [0] = 1 for a negative position, [1] = 1 for a block
+ *                 index >= max_blocks, [2] = 1 for a page id outside
+ *                 [0, num_blocks). Such tokens are skipped; all others are
+ *                 written. Two tokens aimed at the same slot race.
+ *
+ * D * element size must be a multiple of 16 bytes.
+ */
+int mpx_kv_append(const void* k, const void* v, void* k_pool, void* v_pool,
+                  const int32_t* block_tables, const int32_t* start_pos,
+                  const int32_t* n_tokens, const int64_t* k_strides, const int64_t* v_strides,
+                  int B, int T, int H, int D, int num_blocks, int block_size, int max_blocks,
+                  int dtype, int32_t* errors, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

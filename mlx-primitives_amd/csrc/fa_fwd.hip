@@ -47,7 +47,25 @@ struct FwdParams {
   int paired;   // a slot runs q-tiles n_qtiles-1-slot and slot (causal balance)
   float c;  // |scale| * log2(e)
   int neg;  // scale < 0: Q is negated on load (exact) and |scale| used
+  float eps;      // normaliser epsilon: O / (l + eps)
+  int nan_empty;  // rows that see no key give NaN (exact softmax) instead of 0
+  // Paged K/V (prefill over a block-table cache; the PAGED kernels only): k
+  // and v are the pools (num_blocks, bs, H, D), k_ss / v_ss their token row
+  // stride H*D; the rows of batch b come through bt[b, pos / bs].
+  const int32_t* bt;    // (B, max_blocks) page ids, < 0 or >= num_blocks = none
+  const int32_t* ctx;   // (B,) context lengths: keys [0, ctx[b]) exist
+  const float* slopes;  // (H,) ALiBi slopes (bias slope * (kv - q)) or null
+  int bs, bs_log2;      // page size in tokens; log2(bs) or -1 if not a power of 2
+  int max_blocks, num_blocks;
+  uint32_t pool_bytes;  // bytes of one pool from its base (bounds of the buffer loads)
 };
+
+// Page-table slice of one work item staged in LDS (entries).
+constexpr int kMaxItemPages = 2048;
+
+__device__ __forceinline__ int page_of(const FwdParams& p, int pos) {
+  return p.bs_log2 >= 0 ? pos >> p.bs_log2 : pos / p.bs;
+}
 
 // Tile configuration (overridable at build time for tuning builds).
 // 16-bit kernel: 8 waves x 32 rows = 256 query rows per workgroup, two waves
@@ -188,9 +206,13 @@ constexpr int fa16_stage_elems() {
 }
 
 // Query rows [32*NW*wi.qt, +32*NW) of one (batch, head) against its KV range.
-template <int D, int BN, int NW, bool BF16>
-__device__ __forceinline__ void fa16_rows(const FwdParams& p, const WorkItem wi,
-                                          uint16_t* __restrict__ smem) {
+// PAGED: K/V rows come from pools through the page table (prefill over a
+// paged cache); invalid rows load as zeros and are masked.
+template <int D, int BN, int NW, bool BF16, bool PAGED>
+__device__ __forceinline__ void fa16_rows(const FwdParams& pin, const WorkItem wi,
+                                          uint16_t* __restrict__ smem, int* __restrict__ pages) {
+  FwdParams p = pin;
+  if constexpr (PAGED) p.Sk = max(0, min(pin.ctx[wi.b], pin.max_blocks * pin.bs));
   constexpr int BM = 32 * NW, NT = 64 * NW;
   constexpr int KS = D + 8;   // K row stride (elements)
   constexpr int VS = BN + 8;  // V^T row stride (elements)
@@ -219,12 +241,44 @@ __device__ __forceinline__ void fa16_rows(const FwdParams& p, const WorkItem wi,
 
   const uint16_t* __restrict__ Qp = (const uint16_t*)p.q + wi.b * p.q_sb + wi.h * p.q_sh;
   // K/V of this (batch, head) through buffer resources: SGPR base, 32-bit
-  // offsets (the host guarantees Sk * seq_stride * 2 < 2^31), no per-load
-  // address arithmetic.
+  // offsets (the host guarantees Sk * seq_stride * 2 < 2^31, or for pools
+  // pool_bytes < 2^32), no per-load address arithmetic. Paged: the record
+  // count is the pool's extent, so an offset past it loads zeros.
+  const int krec = PAGED ? (int)(p.pool_bytes - (uint32_t)(wi.h * p.k_sh * 2)) : 0x7fffffff;
+  const int vrec = PAGED ? (int)(p.pool_bytes - (uint32_t)(wi.h * p.v_sh * 2)) : 0x7fffffff;
   const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)((const uint16_t*)p.k + wi.b * p.k_sb + wi.h * p.k_sh), 0, 0x7fffffff, kBufferFlags);
+      (void*)((const uint16_t*)p.k + wi.b * p.k_sb + wi.h * p.k_sh), 0, krec, kBufferFlags);
   const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)((const uint16_t*)p.v + wi.b * p.v_sb + wi.h * p.v_sh), 0, 0x7fffffff, kBufferFlags);
+      (void*)((const uint16_t*)p.v + wi.b * p.v_sb + wi.h * p.v_sh), 0, vrec, kBufferFlags);
+  constexpr int kNoRow = (int)0xFFFFFFF0u;  // beyond any pool: loads zeros
+
+  // Paged: this item's slice of the page table, validated, in LDS.
+  int pg_first = 0;
+  if constexpr (PAGED) {
+    const int kv_a = kv_lo + t_begin * BN, kv_b = min(kv_lo + t_end * BN, p.Sk);
+    pg_first = page_of(p, kv_a);
+    const int npg = kv_b > kv_a ? page_of(p, kv_b - 1) - pg_first + 1 : 0;
+    const int32_t* row = p.bt + (int64_t)wi.b * p.max_blocks + pg_first;
+    for (int i = tid; i < npg; i += NT) {
+      const int blk = row[i];
+      pages[i] = (blk >= 0 && blk < p.num_blocks) ? blk : -1;
+    }
+    __syncthreads();
+  }
+  // Byte offset of the 16-byte chunk `col` of key row `pos` (paged: through
+  // the page table; missing rows -> kNoRow).
+  // (32-bit arithmetic: the host guarantees pool_bytes < 2^32.)
+  auto paged_off = [&](int pos, int col, uint32_t row_bytes) __attribute__((always_inline)) {
+    uint32_t off = (uint32_t)kNoRow;
+    if (pos < p.Sk) {
+      const int pg = page_of(p, pos);
+      const int page = pages[pg - pg_first];
+      if (page >= 0)
+        off = ((uint32_t)page * (uint32_t)p.bs + (uint32_t)(pos - pg * p.bs)) * row_bytes +
+              (uint32_t)col * 16u;
+    }
+    return (int)off;
+  };
 
   // Q^T as B operand, k-group g of 16-dim step ks = dims 16*ks + 8*g .. +8.
   // Rows past Sq read the last row (never stored).
@@ -259,7 +313,9 @@ __device__ __forceinline__ void fa16_rows(const FwdParams& p, const WorkItem wi,
   // Prefetch registers, two sets: tile i+2 is loaded into set i%2 while tile
   // i computes and tile i+1 (loaded one iteration earlier) is staged to LDS,
   // so a load has two tile times to arrive.
-  constexpr int NSET = MPX_FA_DEPTH;
+  // (The paged variant prefetches one tile ahead: its page lookups need the
+  // registers of the second set.)
+  constexpr int NSET = PAGED ? 1 : MPX_FA_DEPTH;
   u32x4 kbuf[NSET][K_PER_T];
   u32x4 vbuf[NSET][V_PER_T][2];
   // Rows of a staged tile at or past v_rows are zeroed when V is stored (BN
@@ -270,6 +326,28 @@ __device__ __forceinline__ void fa16_rows(const FwdParams& p, const WorkItem wi,
   // would make the compiler wait for the prefetch right after issuing it.
   auto load_tile = [&](int kv0, auto SET) __attribute__((always_inline)) {
     constexpr int S = decltype(SET)::value;
+    if constexpr (PAGED) {
+      v_rows[S] = BN;  // missing rows already load as zeros
+#pragma unroll
+      for (int i = 0; i < K_PER_T; ++i) {
+        const int c = tid + i * NT;
+        if (K_CHUNKS % NT == 0 || c < K_CHUNKS)
+          kbuf[S][i] = __builtin_amdgcn_raw_buffer_load_b128(
+              krs, paged_off(kv0 + c / CPR, c % CPR, (uint32_t)p.k_ss * 2u), 0, 0);
+      }
+#pragma unroll
+      for (int i = 0; i < V_PER_T; ++i) {
+        const int u = tid + i * NT;
+        if (V_UNITS % NT == 0 || u < V_UNITS) {
+          const int kp = u / CPR, dq = u % CPR;
+#pragma unroll
+          for (int r = 0; r < 2; ++r)
+            vbuf[S][i][r] = __builtin_amdgcn_raw_buffer_load_b128(
+                vrs, paged_off(kv0 + 2 * kp + r, dq, (uint32_t)p.v_ss * 2u), 0, 0);
+        }
+      }
+      return;
+    }
     const int kso = kv0 * (int)p.k_ss * 2, vso = kv0 * (int)p.v_ss * 2;
     if (kv0 + BN <= p.Sk) {
       v_rows[S] = BN;
@@ -372,6 +450,14 @@ __device__ __forceinline__ void fa16_rows(const FwdParams& p, const WorkItem wi,
   // chunk (2*sl + g) ^ ((2*db + j/16) & VXM) = 2*(sl ^ (db & VXM/2)) + (g ^ j/16),
   // so one lane base plus compile-time offsets addresses every operand.
   const int vlane = j * (VS / 8) + (g ^ ((j >> 4) & 1));
+  // Paged: validity of the tile's keys (bit r = key kv0 + r) and the ALiBi
+  // slope divided by |scale| (the bias is added to raw scores). The bias
+  // slope * (kv - q) is applied as slope * (kv - kv_last): the two differ by a
+  // per-row constant, which softmax ignores, and the second is small for the
+  // keys that carry the weight, so its float32 rounding stays small when the
+  // context is much longer than the query range.
+  uint64_t vmask = ~0ull;
+  const float alibi = (PAGED && p.slopes) ? p.slopes[wi.h] * kLog2e / p.c : 0.f;
 
   // Scores S^T of this wave's rows against the K tile staged at Ks.
   auto qk_tile = [&](const uint16_t* Ks, f32x16 (&s)[NB]) __attribute__((always_inline)) {
@@ -404,12 +490,22 @@ __device__ __forceinline__ void fa16_rows(const FwdParams& p, const WorkItem wi,
       // The empty volatile asm keeps this a real (scalar) branch: without it
       // the selects are folded into unconditional code run on every tile.
       asm volatile("" ::: "memory");
+      // Paged: this lane's keys are kv0 + 8g + (compile-time offset).
+      const uint64_t vm = PAGED ? vmask >> (8 * g) : 0;
+      const float dq0 = PAGED ? (float)(kv0 + 8 * g - kv_last) : 0.f;
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
-          const int kv = kv0 + nb * 32 + 16 * (e >> 3) + 8 * g + (e & 7);
-          s[nb][e] = ((kv >= kv_first) & (kv <= kv_last)) ? s[nb][e] : -INFINITY;
+          const int kc = nb * 32 + 16 * (e >> 3) + (e & 7);
+          const int kv = kv0 + kc + 8 * g;
+          bool ok = (kv >= kv_first) & (kv <= kv_last);
+          float sv = s[nb][e];
+          if constexpr (PAGED) {
+            ok = ok & (((vm >> kc) & 1ull) != 0);
+            sv += alibi * (dq0 + (float)kc);
+          }
+          s[nb][e] = ok ? sv : -INFINITY;
         }
     }
 
@@ -488,6 +584,14 @@ __device__ __forceinline__ void fa16_rows(const FwdParams& p, const WorkItem wi,
     bool skip, full;
     classify_tile<BN>(p, kv0, wq0, wq0 + 31, skip, full);
     if (skip) return;
+    if constexpr (PAGED) {
+      const int key = kv0 + (lane % BN);
+      bool ok = key < p.Sk;
+      if (ok) ok = pages[page_of(p, key) - pg_first] >= 0;
+      vmask = __ballot(ok);
+      if (BN < 64) vmask &= (1ull << BN) - 1;
+      if (vmask != (BN < 64 ? (1ull << BN) - 1 : ~0ull) || alibi != 0.f) full = false;
+    }
     const uint16_t* Ks = smem + stage * STAGE;
     f32x16 s[NB];
     qk_tile(Ks, s);
@@ -526,7 +630,8 @@ __device__ __forceinline__ void fa16_rows(const FwdParams& p, const WorkItem wi,
   const float f = m_max == -INFINITY ? 0.f : fast_exp2(m_run - m_max);
   if (p.num_splits == 1) {
     if (myq < p.Sq) {
-      const float inv = m_max == -INFINITY ? 0.f : f / (l_tot * f + kSoftmaxEps);
+      const float inv = m_max == -INFINITY ? (p.nan_empty ? __builtin_nanf("") : 0.f)
+                                           : f / (l_tot * f + p.eps);
       uint16_t* Op = (uint16_t*)p.o + wi.b * p.o_sb + wi.h * p.o_sh + (int64_t)myq * p.o_ss;
 #pragma unroll
       for (int db = 0; db < NDB; ++db)
@@ -866,7 +971,8 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& p, const WorkI
   const float f = m_max == -INFINITY ? 0.f : fast_exp2(m_run - m_max);
   if (p.num_splits == 1) {
     if (myq < p.Sq) {
-      const float inv = m_max == -INFINITY ? 0.f : f / (l_tot * f + kSoftmaxEps);
+      const float inv = m_max == -INFINITY ? (p.nan_empty ? __builtin_nanf("") : 0.f)
+                                           : f / (l_tot * f + p.eps);
       uint16_t* Op = (uint16_t*)p.o + wi.b * p.o_sb + wi.h * p.o_sh + (int64_t)myq * p.o_ss;
 #pragma unroll
       for (int db = 0; db < NDB; ++db)
@@ -896,12 +1002,12 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& p, const WorkI
   }
 }
 
-template <int D, int BN, int NW, bool BF16>
+template <int D, int BN, int NW, bool BF16, bool PAGED>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(MPX_FA_WAVES_PER_EU)))
 void fa_fwd16_kernel(FwdParams p) {
   // Stay within 128 KB of LDS per workgroup (a 136 KB configuration gave wrong
   // results on gfx950).
-  constexpr bool kDirect = MPX_FA_DIRECT && D == 128 && BN == 64 && NW == 8;
+  constexpr bool kDirect = MPX_FA_DIRECT && D == 128 && BN == 64 && NW == 8 && !PAGED;
   constexpr int kDStages = MPX_FA_DSTAGES;
   constexpr int kLdsBytes =
       kDirect ? kDStages * 2 * BN * 2 * D : kFa16Stages * fa16_stage_elems<D, BN>() * 2;
@@ -915,6 +1021,7 @@ void fa_fwd16_kernel(FwdParams p) {
   __shared__ __align__(16) unsigned char dst1[kStageB];
   __shared__ __align__(16) unsigned char dst2[kStageB];
   __shared__ __align__(16) unsigned char dst3[kDStages == 4 ? kStageB : 16];
+  __shared__ int pages[PAGED ? kMaxItemPages : 1];
   const WorkSlot ws = decode_slot(p);
   const int n_items = slot_items(p, ws);
   // Every item ends with a barrier after its last LDS read, so the next item
@@ -924,7 +1031,7 @@ void fa_fwd16_kernel(FwdParams p) {
     if constexpr (kDirect)
       fa16_rows_direct<NW, BF16, kDStages>(p, slot_item(p, ws, item), dst0, dst1, dst2, dst3);
     else
-      fa16_rows<D, BN, NW, BF16>(p, slot_item(p, ws, item), smem);
+      fa16_rows<D, BN, NW, BF16, PAGED>(p, slot_item(p, ws, item), smem, pages);
   }
 }
 
@@ -934,8 +1041,8 @@ void fa_fwd16_kernel(FwdParams p) {
 // of lane (j, g) holds key 32*nb + 8*(e/4) + 4*g + e%4. PV step (nb, e) has
 // k = g <-> that key, so P^T needs no repacking and V stays row-major in LDS.
 // ---------------------------------------------------------------------------
-template <int D, int BN, int NW>
-__global__ __launch_bounds__(64 * NW) void fa_fwd32_kernel(FwdParams p) {
+template <int D, int BN, int NW, bool PAGED>
+__global__ __launch_bounds__(64 * NW) void fa_fwd32_kernel(FwdParams pin) {
   constexpr int BM = 32 * NW, NT = 64 * NW;
   constexpr int KS = D + 4;  // conflict-free 16-byte reads along rows
   constexpr int VS = D + 8;  // rows kv and kv+4 land on opposite bank halves
@@ -948,11 +1055,14 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd32_kernel(FwdParams p) {
   static_assert(2 * STAGE * 4 <= 131072, "LDS budget");
 
   __shared__ __align__(16) float smem[2 * STAGE];
+  __shared__ int pages[PAGED ? kMaxItemPages : 1];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int j = lane & 31, g = lane >> 5;
 
-  const WorkItem wi = slot_item(p, decode_slot(p), 0);
+  const WorkItem wi = slot_item(pin, decode_slot(pin), 0);
+  FwdParams p = pin;
+  if constexpr (PAGED) p.Sk = max(0, min(pin.ctx[wi.b], pin.max_blocks * pin.bs));
   const int q0 = wi.qt * BM;
   int kv_lo, t_begin, t_end;
   kv_range<BM, BN>(p, q0, wi.split, kv_lo, t_begin, t_end);
@@ -977,9 +1087,25 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd32_kernel(FwdParams p) {
     for (int jj = 0; jj < NQ4; ++jj) qf[jj] = -qf[jj];
   }
 
+  // Paged: this item's slice of the page table, validated, in LDS.
+  int pg_first = 0;
+  if constexpr (PAGED) {
+    const int kv_a = kv_lo + t_begin * BN, kv_b = min(kv_lo + t_end * BN, p.Sk);
+    pg_first = page_of(p, kv_a);
+    const int npg = kv_b > kv_a ? page_of(p, kv_b - 1) - pg_first + 1 : 0;
+    const int32_t* row = p.bt + (int64_t)wi.b * p.max_blocks + pg_first;
+    for (int i = tid; i < npg; i += NT) {
+      const int blk = row[i];
+      pages[i] = (blk >= 0 && blk < p.num_blocks) ? blk : -1;
+    }
+    __syncthreads();
+  }
+
   // Rows past Sk re-read the last valid row (no data-dependent selects at
-  // load time); their V values are zeroed when stored.
+  // load time); their V values are zeroed when stored. Paged: missing rows
+  // read row 0 of the pool and are zeroed / masked the same way.
   f32x4 kbuf[PER_T], vbuf[PER_T];
+  bool vok[PER_T];
   int v_rows = BN;
   auto load_tile = [&](int kv0) {
     v_rows = min(BN, p.Sk - kv0);
@@ -988,9 +1114,24 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd32_kernel(FwdParams p) {
       const int cc = tid + i * NT;
       if (CHUNKS % NT == 0 || cc < CHUNKS) {
         const int row = cc / CPR, col = cc - (cc / CPR) * CPR;
-        const int kv = min(kv0 + row, p.Sk - 1);
-        kbuf[i] = *(const f32x4*)(Kp + (int64_t)kv * p.k_ss + col * 4);
-        vbuf[i] = *(const f32x4*)(Vp + (int64_t)kv * p.v_ss + col * 4);
+        int64_t kr, vr;
+        if constexpr (PAGED) {
+          const int pos = kv0 + row;
+          int64_t prow = -1;
+          if (pos < p.Sk) {
+            const int pg = page_of(p, pos);
+            const int page = pages[pg - pg_first];
+            if (page >= 0) prow = (int64_t)page * p.bs + (pos - pg * p.bs);
+          }
+          vok[i] = prow >= 0;
+          kr = max(prow, (int64_t)0);
+          vr = kr;
+        } else {
+          vok[i] = true;
+          kr = vr = min(kv0 + row, p.Sk - 1);
+        }
+        kbuf[i] = *(const f32x4*)(Kp + kr * p.k_ss + col * 4);
+        vbuf[i] = *(const f32x4*)(Vp + vr * p.v_ss + col * 4);
       }
     }
   };
@@ -1003,7 +1144,7 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd32_kernel(FwdParams p) {
       if (CHUNKS % NT == 0 || cc < CHUNKS) {
         const int row = cc / CPR, col = cc - (cc / CPR) * CPR;
         *(f32x4*)(Ks + row * KS + col * 4) = kbuf[i];
-        *(f32x4*)(Vs + row * VS + col * 4) = row < v_rows ? vbuf[i] : (f32x4){};
+        *(f32x4*)(Vs + row * VS + col * 4) = (row < v_rows && vok[i]) ? vbuf[i] : (f32x4){};
       }
     }
   };
@@ -1013,6 +1154,10 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd32_kernel(FwdParams p) {
   for (int db = 0; db < NDB; ++db) o[db] = (f32x16){};
   float m_run = -INFINITY, m_max = -INFINITY, l_run = 0.f;
   const float c = p.c;
+  // ALiBi as in the 16-bit kernel: slope / |scale| on raw scores, measured
+  // from the row's last visible key.
+  const float alibi = (PAGED && p.slopes) ? p.slopes[wi.h] * kLog2e / p.c : 0.f;
+  const int kv_anchor = min(p.win_right >= 0 ? myq + p.win_right : (1 << 30), p.Sk - 1);
 
   if (t_begin < t_end) {
     load_tile(kv_lo + t_begin * BN);
@@ -1028,6 +1173,17 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd32_kernel(FwdParams p) {
 
     bool skip, full;
     classify_tile<BN>(p, kv0, wq0, wq0 + 31, skip, full);
+    uint64_t vmask = ~0ull;
+    if constexpr (PAGED) {
+      if (!skip) {
+        const int key = kv0 + (lane % BN);
+        bool ok = key < p.Sk;
+        if (ok) ok = pages[page_of(p, key) - pg_first] >= 0;
+        vmask = __ballot(ok);
+        if (BN < 64) vmask &= (1ull << BN) - 1;
+        if (vmask != (BN < 64 ? (1ull << BN) - 1 : ~0ull) || alibi != 0.f) full = false;
+      }
+    }
     if (!skip) {
       const float* Ks = smem + stage * STAGE;
       const float* Vs = Ks + K_ELEMS;
@@ -1050,8 +1206,14 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd32_kernel(FwdParams p) {
         for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
           for (int e = 0; e < 16; ++e) {
-            const int kv = kv0 + nb * 32 + 8 * (e >> 2) + 4 * g + (e & 3);
-            if (!kv_valid(p, myq, kv)) s[nb][e] = -INFINITY;
+            const int kr = nb * 32 + 8 * (e >> 2) + 4 * g + (e & 3);
+            const int kv = kv0 + kr;
+            bool ok = kv_valid(p, myq, kv);
+            if constexpr (PAGED) {
+              ok = ok && ((vmask >> kr) & 1ull) != 0;
+              s[nb][e] += alibi * (float)(kv - kv_anchor);
+            }
+            if (!ok) s[nb][e] = -INFINITY;
           }
       }
 
@@ -1106,7 +1268,8 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd32_kernel(FwdParams p) {
   const float f = m_max == -INFINITY ? 0.f : fast_exp2(m_run - m_max);
   if (p.num_splits == 1) {
     if (myq < p.Sq) {
-      const float inv = m_max == -INFINITY ? 0.f : f / (l_tot * f + kSoftmaxEps);
+      const float inv = m_max == -INFINITY ? (p.nan_empty ? __builtin_nanf("") : 0.f)
+                                           : f / (l_tot * f + p.eps);
       float* Op = (float*)p.o + wi.b * p.o_sb + wi.h * p.o_sh + (int64_t)myq * p.o_ss;
 #pragma unroll
       for (int db = 0; db < NDB; ++db)
@@ -1138,14 +1301,16 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd32_kernel(FwdParams p) {
 // ---------------------------------------------------------------------------
 // Split-KV merge: the reference's online_softmax_merge
 // (mlx_primitives/attention/_online_softmax.py:42-106) folded over all splits,
-// then O / (l + 1e-6). One thread per (row, 4 dims).
+// then O / (l + eps) (rows that saw no key: 0, or NaN for the exact softmax).
+// One thread per (row, 4 dims).
 // ---------------------------------------------------------------------------
 template <int DT>
 __global__ __launch_bounds__(256) void fa_split_merge_kernel(const float* __restrict__ ws_o,
                                                              const float* __restrict__ ws_ml,
                                                              void* o, int64_t o_sb, int64_t o_sh,
                                                              int64_t o_ss, int B, int H, int Sq,
-                                                             int D, int splits) {
+                                                             int D, int splits, float eps,
+                                                             int nan_empty) {
   const int chunks = D / 4;
   const int64_t rows = (int64_t)B * H * Sq;
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -1163,7 +1328,9 @@ __global__ __launch_bounds__(256) void fa_split_merge_kernel(const float* __rest
       L += wgt * ws_ml[2 * r + 1];
       acc += wgt * *(const f32x4*)(ws_o + r * D + 4 * c4);
     }
-    acc = acc / (L + kSoftmaxEps);
+    acc = acc / (L + eps);
+  } else if (nan_empty) {
+    acc = (f32x4){} + __builtin_nanf("");
   }
   const int q = (int)(row % Sq);
   const int bh = (int)(row / Sq);
@@ -1199,7 +1366,7 @@ int tile_n(int D, int dtype) {
 }
 
 Plan make_plan(int B, int H, int Sq, int Sk, int D, int causal, int window_left,
-               int window_right, int dtype) {
+               int window_right, int dtype, int max_tiles_per_split = 1 << 30) {
   Plan pl;
   pl.BM = 32 * (dtype == MPX_F32 ? kNumWaves32 : kNumWaves16);
   pl.BN = tile_n(D, dtype);
@@ -1223,7 +1390,8 @@ Plan make_plan(int B, int H, int Sq, int Sk, int D, int causal, int window_left,
     splits = std::max(splits, 1);
   }
   pl.tiles_per_split = splits > 1 ? (max_tiles + splits - 1) / splits : std::max(max_tiles, 1);
-  if (splits > 1) splits = (max_tiles + pl.tiles_per_split - 1) / pl.tiles_per_split;
+  pl.tiles_per_split = std::min(pl.tiles_per_split, std::max(max_tiles_per_split, 1));
+  splits = std::max(1, (max_tiles + pl.tiles_per_split - 1) / pl.tiles_per_split);
   pl.splits = splits;
   pl.ws_bytes = splits > 1 ? (size_t)splits * B * H * Sq * (D + 2) * sizeof(float) : 0;
   // Causal-shaped launches (KV range growing with the q-tile) of the 16-bit
@@ -1236,38 +1404,96 @@ Plan make_plan(int B, int H, int Sq, int Sk, int D, int causal, int window_left,
   return pl;
 }
 
-template <int D, int BN, bool F32, bool BF16>
+template <int D, int BN, bool F32, bool BF16, bool PAGED>
 hipError_t launch_fwd(const FwdParams& p, int grid, hipStream_t stream) {
   if constexpr (F32) {
-    hipLaunchKernelGGL((fa_fwd32_kernel<D, BN, kNumWaves32>), dim3(grid), dim3(64 * kNumWaves32),
-                       0, stream, p);
+    hipLaunchKernelGGL((fa_fwd32_kernel<D, BN, kNumWaves32, PAGED>), dim3(grid),
+                       dim3(64 * kNumWaves32), 0, stream, p);
   } else {
-    hipLaunchKernelGGL((fa_fwd16_kernel<D, BN, kNumWaves16, BF16>), dim3(grid),
+    hipLaunchKernelGGL((fa_fwd16_kernel<D, BN, kNumWaves16, BF16, PAGED>), dim3(grid),
                        dim3(64 * kNumWaves16), 0, stream, p);
   }
   return hipGetLastError();
 }
 
+template <bool PAGED>
 hipError_t dispatch_fwd(const FwdParams& p, int D, int dtype, int grid, hipStream_t st) {
   if (dtype == MPX_F32) {
     switch (D) {
-      case 32: return launch_fwd<32, 64, true, false>(p, grid, st);
-      case 64: return launch_fwd<64, 64, true, false>(p, grid, st);
-      default: return launch_fwd<128, 32, true, false>(p, grid, st);
+      case 32: return launch_fwd<32, 64, true, false, PAGED>(p, grid, st);
+      case 64: return launch_fwd<64, 64, true, false, PAGED>(p, grid, st);
+      default: return launch_fwd<128, 32, true, false, PAGED>(p, grid, st);
     }
   } else if (dtype == MPX_BF16) {
     switch (D) {
-      case 32: return launch_fwd<32, MPX_FA_BN16, false, true>(p, grid, st);
-      case 64: return launch_fwd<64, MPX_FA_BN16, false, true>(p, grid, st);
-      default: return launch_fwd<128, MPX_FA_BN16, false, true>(p, grid, st);
+      case 32: return launch_fwd<32, MPX_FA_BN16, false, true, PAGED>(p, grid, st);
+      case 64: return launch_fwd<64, MPX_FA_BN16, false, true, PAGED>(p, grid, st);
+      default: return launch_fwd<128, MPX_FA_BN16, false, true, PAGED>(p, grid, st);
     }
   } else {
     switch (D) {
-      case 32: return launch_fwd<32, MPX_FA_BN16, false, false>(p, grid, st);
-      case 64: return launch_fwd<64, MPX_FA_BN16, false, false>(p, grid, st);
-      default: return launch_fwd<128, MPX_FA_BN16, false, false>(p, grid, st);
+      case 32: return launch_fwd<32, MPX_FA_BN16, false, false, PAGED>(p, grid, st);
+      case 64: return launch_fwd<64, MPX_FA_BN16, false, false, PAGED>(p, grid, st);
+      default: return launch_fwd<128, MPX_FA_BN16, false, false, PAGED>(p, grid, st);
     }
   }
+}
+
+// Attention kernel(s) for a prepared FwdParams: the forward launch, then the
+// split merge when the plan splits the KV range.
+template <bool PAGED>
+int run_fwd(FwdParams& p, const Plan& pl, int D, int dtype, void* workspace, hipStream_t st) {
+  p.ws_o = pl.splits > 1 ? (float*)workspace : nullptr;
+  p.ws_ml = pl.splits > 1 ? (float*)workspace + (size_t)pl.splits * p.B * p.H * p.Sq * D : nullptr;
+  p.win_left = pl.win_left; p.win_right = pl.win_right;
+  p.n_qtiles = pl.n_qtiles; p.num_splits = pl.splits; p.tiles_per_split = pl.tiles_per_split;
+  p.n_slots = pl.n_slots; p.paired = pl.paired;
+  const long grid_l = (long)p.B * p.H * pl.n_slots * pl.splits;
+  MPX_CHECK_ARG(grid_l < (1L << 31), "attention: problem too large");
+  MPX_CHECK_HIP(dispatch_fwd<PAGED>(p, D, dtype, (int)grid_l, st));
+  if (pl.splits > 1) {
+    const long threads = (long)p.B * p.H * p.Sq * (D / 4);
+    const int blocks = (int)((threads + 255) / 256);
+#define MPX_MERGE(DT)                                                                         \
+  hipLaunchKernelGGL(fa_split_merge_kernel<DT>, dim3(blocks), dim3(256), 0, st, p.ws_o, p.ws_ml, \
+                     p.o, p.o_sb, p.o_sh, p.o_ss, p.B, p.H, p.Sq, D, pl.splits, p.eps,         \
+                     p.nan_empty)
+    if (dtype == MPX_F32)
+      MPX_MERGE(MPX_F32);
+    else if (dtype == MPX_BF16)
+      MPX_MERGE(MPX_BF16);
+    else
+      MPX_MERGE(MPX_F16);
+#undef MPX_MERGE
+    MPX_CHECK_HIP(hipGetLastError());
+  }
+  return MPX_OK;
+}
+
+// Output rows of a query that can see no key at all (empty pool): NaN, as the
+// reference's softmax over an all -inf row.
+template <int DT>
+__global__ void fill_nan_kernel(void* o, int64_t o_sb, int64_t o_sh, int64_t o_ss, int B, int H,
+                                int Sq, int D) {
+  const int64_t n = (int64_t)B * H * Sq * D;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int d = (int)(i % D);
+    const int64_t r = i / D;
+    const int q = (int)(r % Sq);
+    const int64_t bh = r / Sq;
+    const int b = (int)(bh / H), h = (int)(bh % H);
+    const int64_t off = b * o_sb + h * o_sh + q * o_ss + d;
+    if constexpr (DT == MPX_F32)
+      ((float*)o)[off] = __builtin_nanf("");
+    else
+      ((uint16_t*)o)[off] = DT == MPX_BF16 ? 0x7FC0 : 0x7E00;
+  }
+}
+
+// Tiles per split so that one work item's pages fit the LDS page table.
+int paged_tile_cap(int block_size, int BN) {
+  return std::max(1, (int)std::min<long>(1L << 30, (long)(kMaxItemPages - 2) * block_size / BN));
 }
 
 bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
@@ -1317,8 +1543,6 @@ extern "C" int mpx_attn_fwd(const void* q, const void* k, const void* v, void* o
                   workspace_bytes);
     MPX_CHECK_ARG(aligned16(workspace), "mpx_attn_fwd: workspace must be 16-byte aligned");
   }
-  const long grid_l = (long)B * H * pl.n_slots * pl.splits;
-  MPX_CHECK_ARG(grid_l < (1L << 31), "mpx_attn_fwd: problem too large");
   if (dtype != MPX_F32) {
     // The 16-bit kernel addresses one (batch, head) of K/V with 32-bit byte offsets.
     const int64_t span_k = ((int64_t)Sk + 64) * k_strides[2] * 2 + (int64_t)D * 2;
@@ -1329,36 +1553,109 @@ extern "C" int mpx_attn_fwd(const void* q, const void* k, const void* v, void* o
     }
   }
 
-  FwdParams p;
+  FwdParams p = {};
   p.q = q; p.k = k; p.v = v; p.o = o;
   p.q_sb = q_strides[0]; p.q_sh = q_strides[1]; p.q_ss = q_strides[2];
   p.k_sb = k_strides[0]; p.k_sh = k_strides[1]; p.k_ss = k_strides[2];
   p.v_sb = v_strides[0]; p.v_sh = v_strides[1]; p.v_ss = v_strides[2];
   p.o_sb = o_strides[0]; p.o_sh = o_strides[1]; p.o_ss = o_strides[2];
-  p.ws_o = pl.splits > 1 ? (float*)workspace : nullptr;
-  p.ws_ml = pl.splits > 1 ? (float*)workspace + (size_t)pl.splits * B * H * Sq * D : nullptr;
   p.B = B; p.H = H; p.Sq = Sq; p.Sk = Sk;
-  p.win_left = pl.win_left; p.win_right = pl.win_right;
-  p.n_qtiles = pl.n_qtiles; p.num_splits = pl.splits; p.tiles_per_split = pl.tiles_per_split;
-  p.n_slots = pl.n_slots; p.paired = pl.paired;
   p.c = std::fabs(scale) * kLog2e;
   p.neg = scale < 0.f ? 1 : 0;
+  p.eps = kSoftmaxEps;
+  p.nan_empty = 0;
+  return run_fwd<false>(p, pl, D, dtype, workspace, (hipStream_t)stream);
+}
 
-  hipStream_t st = (hipStream_t)stream;
-  MPX_CHECK_HIP(dispatch_fwd(p, D, dtype, (int)grid_l, st));
-  if (pl.splits > 1) {
-    const long threads = (long)B * H * Sq * (D / 4);
-    const int blocks = (int)((threads + 255) / 256);
-    if (dtype == MPX_F32)
-      hipLaunchKernelGGL(fa_split_merge_kernel<MPX_F32>, dim3(blocks), dim3(256), 0, st, p.ws_o,
-                         p.ws_ml, o, p.o_sb, p.o_sh, p.o_ss, B, H, Sq, D, pl.splits);
-    else if (dtype == MPX_BF16)
-      hipLaunchKernelGGL(fa_split_merge_kernel<MPX_BF16>, dim3(blocks), dim3(256), 0, st, p.ws_o,
-                         p.ws_ml, o, p.o_sb, p.o_sh, p.o_ss, B, H, Sq, D, pl.splits);
-    else
-      hipLaunchKernelGGL(fa_split_merge_kernel<MPX_F16>, dim3(blocks), dim3(256), 0, st, p.ws_o,
-                         p.ws_ml, o, p.o_sb, p.o_sh, p.o_ss, B, H, Sq, D, pl.splits);
-    MPX_CHECK_HIP(hipGetLastError());
+extern "C" size_t mpx_paged_prefill_workspace_bytes(int B, int Sq, int H, int D, int block_size,
+                                                    int max_blocks, int causal, int dtype) {
+  if (B <= 0 || H <= 0 || Sq <= 0 || D <= 0 || block_size <= 0 || max_blocks <= 0) return 0;
+  const int BN = tile_n(D, dtype);
+  return make_plan(B, H, Sq, max_blocks * block_size, D, causal, -1, -1, dtype,
+                   paged_tile_cap(block_size, BN))
+      .ws_bytes;
+}
+
+extern "C" int mpx_paged_prefill(const void* q, const void* k_pool, const void* v_pool,
+                                 const int32_t* block_tables, const int32_t* context_lens,
+                                 const float* alibi_slopes, void* o, const int64_t* q_strides,
+                                 const int64_t* o_strides, int B, int Sq, int H, int D,
+                                 int num_blocks, int block_size, int max_blocks, float scale,
+                                 int causal, int dtype, void* workspace, size_t workspace_bytes,
+                                 void* stream) {
+  clear_error();
+  MPX_CHECK_ARG(dtype == MPX_F32 || dtype == MPX_F16 || dtype == MPX_BF16,
+                "mpx_paged_prefill: unknown dtype code %d", dtype);
+  MPX_CHECK_ARG(B >= 0 && Sq >= 0 && H >= 0 && num_blocks >= 0 && max_blocks >= 0,
+                "mpx_paged_prefill: negative size");
+  MPX_CHECK_ARG(block_size > 0, "mpx_paged_prefill: block_size must be positive");
+  if (D != 32 && D != 64 && D != 128) {
+    set_error("mpx_paged_prefill: head_dim %d not supported (kernels exist for 32, 64, 128)", D);
+    return MPX_EUNSUPPORTED;
   }
-  return MPX_OK;
+  MPX_CHECK_ARG(std::isfinite(scale), "mpx_paged_prefill: scale must be finite");
+  if ((long)B * H * Sq == 0) return MPX_OK;
+  MPX_CHECK_ARG(q && o && context_lens && q_strides && o_strides,
+                "mpx_paged_prefill: null pointer argument");
+  MPX_CHECK_ARG(max_blocks == 0 || num_blocks == 0 || (k_pool && v_pool && block_tables),
+                "mpx_paged_prefill: null pool/table pointer");
+  MPX_CHECK_ARG(aligned16(q) && aligned16(o) && aligned16(k_pool) && aligned16(v_pool),
+                "mpx_paged_prefill: tensors must be 16-byte aligned");
+  const int vec = dtype == MPX_F32 ? 4 : 8;
+  for (int i = 0; i < 3; ++i)
+    MPX_CHECK_ARG(q_strides[i] >= 0 && q_strides[i] % vec == 0 && o_strides[i] >= 0 &&
+                      o_strides[i] % vec == 0,
+                  "mpx_paged_prefill: strides must be non-negative multiples of %d elements", vec);
+  const long max_tokens = (long)max_blocks * block_size;
+  MPX_CHECK_ARG(max_tokens < (1L << 30), "mpx_paged_prefill: block table too large");
+  const int es = dtype == MPX_F32 ? 4 : 2;
+  const uint64_t pool_bytes = (uint64_t)num_blocks * block_size * H * D * es;
+  if (dtype != MPX_F32 && pool_bytes >= 0xFFFFFF00ull) {
+    set_error("mpx_paged_prefill: 16-bit pools above 4 GiB are not supported");
+    return MPX_EUNSUPPORTED;
+  }
+  hipStream_t st = (hipStream_t)stream;
+  if (num_blocks == 0 || max_blocks == 0) {
+    // No key exists for any query: every output row is NaN.
+    const long n = (long)B * H * Sq * D;
+    const int blocks = (int)std::min<long>((n + 255) / 256, 4096);
+    if (dtype == MPX_F32)
+      hipLaunchKernelGGL(fill_nan_kernel<MPX_F32>, dim3(blocks), dim3(256), 0, st, o,
+                         o_strides[0], o_strides[1], o_strides[2], B, H, Sq, D);
+    else if (dtype == MPX_BF16)
+      hipLaunchKernelGGL(fill_nan_kernel<MPX_BF16>, dim3(blocks), dim3(256), 0, st, o,
+                         o_strides[0], o_strides[1], o_strides[2], B, H, Sq, D);
+    else
+      hipLaunchKernelGGL(fill_nan_kernel<MPX_F16>, dim3(blocks), dim3(256), 0, st, o,
+                         o_strides[0], o_strides[1], o_strides[2], B, H, Sq, D);
+    MPX_CHECK_HIP(hipGetLastError());
+    return MPX_OK;
+  }
+  const int BN = tile_n(D, dtype);
+  const Plan pl = make_plan(B, H, Sq, (int)max_tokens, D, causal, -1, -1, dtype,
+                            paged_tile_cap(block_size, BN));
+  if (pl.splits > 1) {
+    MPX_CHECK_ARG(workspace != nullptr && workspace_bytes >= pl.ws_bytes,
+                  "mpx_paged_prefill: workspace of %zu bytes required, %zu given", pl.ws_bytes,
+                  workspace_bytes);
+    MPX_CHECK_ARG(aligned16(workspace), "mpx_paged_prefill: workspace must be 16-byte aligned");
+  }
+
+  FwdParams p = {};
+  p.q = q; p.k = k_pool; p.v = v_pool; p.o = o;
+  p.q_sb = q_strides[0]; p.q_sh = q_strides[1]; p.q_ss = q_strides[2];
+  p.k_sb = 0; p.k_sh = D; p.k_ss = (int64_t)H * D;
+  p.v_sb = 0; p.v_sh = D; p.v_ss = (int64_t)H * D;
+  p.o_sb = o_strides[0]; p.o_sh = o_strides[1]; p.o_ss = o_strides[2];
+  p.B = B; p.H = H; p.Sq = Sq; p.Sk = (int)max_tokens;
+  p.c = std::fabs(scale) * kLog2e;
+  p.neg = scale < 0.f ? 1 : 0;
+  p.eps = 0.f;
+  p.nan_empty = 1;
+  p.bt = block_tables; p.ctx = context_lens; p.slopes = alibi_slopes;
+  p.bs = block_size;
+  p.bs_log2 = (block_size & (block_size - 1)) == 0 ? __builtin_ctz((unsigned)block_size) : -1;
+  p.max_blocks = max_blocks; p.num_blocks = num_blocks;
+  p.pool_bytes = (uint32_t)std::min<uint64_t>(pool_bytes, 0xFFFFFFFFull);
+  return run_fwd<true>(p, pl, D, dtype, workspace, st);
 }

@@ -75,6 +75,23 @@ def load() -> ctypes.CDLL:
         ]
         lib.mpx_paged_decode_workspace_bytes.restype = ctypes.c_size_t
         lib.mpx_paged_decode_workspace_bytes.argtypes = [ctypes.c_int] * 5
+        lib.mpx_paged_prefill.restype = ctypes.c_int
+        lib.mpx_paged_prefill.argtypes = [
+            ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+            ctypes.c_void_p, ctypes.c_void_p, _i64p, _i64p,
+            ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+            ctypes.c_int, ctypes.c_float, ctypes.c_int, ctypes.c_int,
+            ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
+        ]
+        lib.mpx_paged_prefill_workspace_bytes.restype = ctypes.c_size_t
+        lib.mpx_paged_prefill_workspace_bytes.argtypes = [ctypes.c_int] * 8
+        lib.mpx_kv_append.restype = ctypes.c_int
+        lib.mpx_kv_append.argtypes = [
+            ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+            ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, _i64p, _i64p,
+            ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+            ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p,
+        ]
         _lib = lib
         return lib
 
@@ -160,3 +177,40 @@ def paged_decode(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
         o.data_ptr(), _strides(q_strides), _strides(o_strides), B, H, D, num_blocks,
         block_size, max_blocks, float(scale), code, ws.data_ptr(), ws.numel(), _stream_ptr(dev))
     _check(rc, "mpx_paged_decode failed")
+
+
+def paged_prefill(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
+                  block_tables: torch.Tensor, context_lens: torch.Tensor,
+                  alibi_slopes: Optional[torch.Tensor], o: torch.Tensor,
+                  q_strides: Sequence[int], o_strides: Sequence[int], B: int, Sq: int, H: int,
+                  D: int, num_blocks: int, block_size: int, max_blocks: int, scale: float,
+                  causal: bool) -> None:
+    """Enqueue mpx_paged_prefill on the current stream (strides in (b, h, s) order)."""
+    lib = load()
+    dev = require_device(q, k_pool, v_pool, block_tables, context_lens, o)
+    code = dtype_code(q.dtype)
+    ws_bytes = int(lib.mpx_paged_prefill_workspace_bytes(B, Sq, H, D, block_size, max_blocks,
+                                                          int(causal), code))
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
+    rc = lib.mpx_paged_prefill(
+        q.data_ptr(), k_pool.data_ptr(), v_pool.data_ptr(), block_tables.data_ptr(),
+        context_lens.data_ptr(), alibi_slopes.data_ptr() if alibi_slopes is not None else None,
+        o.data_ptr(), _strides(q_strides), _strides(o_strides), B, Sq, H, D, num_blocks,
+        block_size, max_blocks, float(scale), int(causal), code,
+        ws.data_ptr() if ws is not None else None, ws_bytes, _stream_ptr(dev))
+    _check(rc, "mpx_paged_prefill failed")
+
+
+def kv_append(k: torch.Tensor, v: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
+              block_tables: torch.Tensor, start_pos: torch.Tensor, n_tokens: torch.Tensor,
+              errors: torch.Tensor, k_strides: Sequence[int], v_strides: Sequence[int], B: int,
+              T: int, H: int, D: int, num_blocks: int, block_size: int, max_blocks: int) -> None:
+    """Enqueue mpx_kv_append on the current stream (strides in (b, t, h) order)."""
+    lib = load()
+    dev = require_device(k, v, k_pool, v_pool, block_tables, start_pos, n_tokens, errors)
+    rc = lib.mpx_kv_append(
+        k.data_ptr(), v.data_ptr(), k_pool.data_ptr(), v_pool.data_ptr(),
+        block_tables.data_ptr(), start_pos.data_ptr(), n_tokens.data_ptr(),
+        _strides(k_strides), _strides(v_strides), B, T, H, D, num_blocks, block_size, max_blocks,
+        dtype_code(k_pool.dtype), errors.data_ptr(), _stream_ptr(dev))
+    _check(rc, "mpx_kv_append failed")

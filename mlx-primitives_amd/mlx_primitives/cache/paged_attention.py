@@ -5,7 +5,8 @@ paged_attention 44-105, paged_attention_with_bias 323-384,
 create_block_table_from_lengths 387-440) over the same KV layout: pools
 (num_blocks, block_size, H, D), int32 block tables (B, max_blocks) padded
 with -1, int32 context lengths (B,). Decode (seq_q == 1) runs the gfx950
-split-K paged-decode kernel; nothing is gathered into a dense tensor.
+split-K paged-decode kernel and prefill (seq_q > 1) the flash kernel with
+block-table indirection; nothing is gathered into a dense tensor.
 """
 
 from __future__ import annotations
@@ -48,12 +49,16 @@ def paged_attention(
     q: (batch, seq_q, heads, dim); k_pool, v_pool: (num_blocks, block_size,
     heads, dim); block_tables: (batch, max_blocks) page ids, -1 = none;
     context_lens: (batch,) cached tokens per sequence; alibi_slopes: optional
-    (heads,), bias slope * (kv_pos - q_pos) with q_pos = context_len in decode.
+    (heads,), bias slope * (kv_pos - q_pos) with q_pos = context_len in decode
+    and q_pos = 0..seq_q-1 in prefill.
 
     Decode (seq_q == 1) ignores ``causal`` like the reference
-    (paged_attention.py:108-208). Returns (batch, seq_q, heads, dim) in q's
-    dtype. A sequence with no valid cached token yields NaN (the reference's
-    softmax over an all -inf row).
+    (paged_attention.py:108-208). Prefill (seq_q > 1, paged_attention.py:
+    211-320) places query i at position i: with ``causal`` it sees cached
+    positions <= i. Both run gfx950 kernels that read the pages through the
+    block table. Returns (batch, seq_q, heads, dim) in q's dtype. A query row
+    with no valid cached token yields NaN (the reference's softmax over an all
+    -inf row).
     """
     if q.ndim != 4:
         raise ValueError(f"Expected q of shape (batch, seq_q, heads, dim), got {q.ndim}D")
@@ -78,9 +83,6 @@ def paged_attention(
     if q.dtype != k_pool.dtype or q.dtype != v_pool.dtype:
         raise ValueError(
             f"q/k_pool/v_pool dtype mismatch: {q.dtype}, {k_pool.dtype}, {v_pool.dtype}")
-    if seq_q != 1:
-        raise NotImplementedError(
-            "paged_attention prefill (seq_q > 1) is not implemented by the MI355X kernels yet")
 
     _native.require_device(q, k_pool, v_pool, block_tables, context_lens)
     if alibi_slopes is not None:
@@ -96,15 +98,24 @@ def paged_attention(
     k_pool = k_pool.contiguous()
     v_pool = v_pool.contiguous()
     vec = 4 if q.dtype == torch.float32 else 8
-    if q.stride(-1) != 1 or q.stride(0) % vec or q.stride(2) % vec or q.data_ptr() % 16:
+    if (q.stride(-1) != 1 or q.stride(0) % vec or q.stride(1) % vec or q.stride(2) % vec
+            or q.data_ptr() % 16):
         q = q.contiguous()
     tables = _as_i32(block_tables)
     lens = _as_i32(context_lens)
-    out = torch.empty((batch, 1, heads, dk), dtype=q.dtype, device=q.device)
-    _native.paged_decode(
-        q, k_pool, v_pool, tables, lens, alibi_slopes, out,
-        (q.stride(0), q.stride(2)), (out.stride(0), out.stride(2)),
-        batch, heads, dk, k_pool.shape[0], block_size, tables.shape[1], scale)
+    out = torch.empty((batch, seq_q, heads, dk), dtype=q.dtype, device=q.device)
+    if seq_q == 1:
+        _native.paged_decode(
+            q, k_pool, v_pool, tables, lens, alibi_slopes, out,
+            (q.stride(0), q.stride(2)), (out.stride(0), out.stride(2)),
+            batch, heads, dk, k_pool.shape[0], block_size, tables.shape[1], scale)
+    else:
+        _native.paged_prefill(
+            q, k_pool, v_pool, tables, lens, alibi_slopes, out,
+            (q.stride(0), q.stride(2), q.stride(1)),
+            (out.stride(0), out.stride(2), out.stride(1)),
+            batch, seq_q, heads, dk, k_pool.shape[0], block_size, tables.shape[1], scale,
+            causal)
     if dk != dim:
         out = out[..., :dim].contiguous()
     return out

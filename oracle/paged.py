@@ -104,7 +104,9 @@ def paged_attention_prefill(
         safe = np.maximum(tbl, 0)
         kb = k_pool[safe].reshape(max_ctx, heads, dim)
         vb = v_pool[safe].reshape(max_ctx, heads, v_pool.shape[-1])
-        scores = np.einsum("qhd,thd->hqt", q[b], kb) * q.dtype.type(scale)
+        # (H, Sq, T) = per-head q k^T (batched matmul over heads)
+        scores = np.matmul(np.transpose(q[b], (1, 0, 2)), np.transpose(kb, (1, 2, 0)))
+        scores = scores * q.dtype.type(scale)
         if alibi_slopes is not None:
             diff = (pos[None, :] - qpos[:, None]).astype(np.float32)
             scores = scores + (np.asarray(alibi_slopes, np.float32)[:, None, None] * diff[None]).astype(q.dtype)
@@ -116,7 +118,7 @@ def paged_attention_prefill(
             m = np.max(scores, axis=-1, keepdims=True)
             e = np.exp(scores - m)
             w = e / np.sum(e, axis=-1, keepdims=True)
-        out[b] = np.einsum("hqt,thd->qhd", w, vb)
+        out[b] = np.transpose(np.matmul(w, np.transpose(vb, (1, 0, 2))), (1, 0, 2))
     return out
 
 

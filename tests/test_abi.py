@@ -30,7 +30,8 @@ def lib():
 def test_header_declares_expected_entry_points():
     assert declared_functions() == sorted([
         "mpx_version", "mpx_last_error", "mpx_attn_fwd", "mpx_attn_fwd_workspace_bytes",
-        "mpx_paged_decode", "mpx_paged_decode_workspace_bytes"])
+        "mpx_paged_decode", "mpx_paged_decode_workspace_bytes", "mpx_paged_prefill",
+        "mpx_paged_prefill_workspace_bytes", "mpx_kv_append"])
 
 
 def test_library_exports_every_declared_symbol(lib):
@@ -91,3 +92,41 @@ def test_paged_workspace_and_validation(lib):
     rc = lib.mpx_paged_decode(16, 16, 16, 16, 16, None, 16, st, st, 1, 32, 128, 4, 16, 1, 0.1, 1,
                               16, 8, None)
     assert rc == _native.MPX_EINVAL and b"workspace" in lib.mpx_last_error()
+
+
+def _prefill(lib, dtype=1, D=128, bs=16, ws=None, ws_bytes=0, B=1, Sq=64, scale=0.1):
+    st = (ctypes.c_int64 * 3)(64 * 32 * 128, 128, 32 * 128)
+    return lib.mpx_paged_prefill(16, 16, 16, 16, 16, None, 16, st, st, B, Sq, 32, D, 64, bs, 8,
+                                 scale, 1, dtype, ws, ws_bytes, None)
+
+
+def test_paged_prefill_validation(lib):
+    assert _prefill(lib, dtype=5) == _native.MPX_EINVAL and b"dtype" in lib.mpx_last_error()
+    assert _prefill(lib, D=96) == _native.MPX_EUNSUPPORTED
+    assert b"head_dim" in lib.mpx_last_error()
+    assert _prefill(lib, bs=0) == _native.MPX_EINVAL and b"block_size" in lib.mpx_last_error()
+    assert _prefill(lib, scale=float("inf")) == _native.MPX_EINVAL
+    assert _prefill(lib, B=0) == _native.MPX_OK and lib.mpx_last_error() == b""
+    # one sequence, 64 queries over 8 pages of 16: no split, no workspace
+    assert lib.mpx_paged_prefill_workspace_bytes(1, 64, 32, 128, 16, 8, 1, 1) == 0
+    # few queries over a long table: split-KV partials are needed
+    need = lib.mpx_paged_prefill_workspace_bytes(1, 64, 8, 128, 16, 4096, 0, 1)
+    assert need > 0
+    st = (ctypes.c_int64 * 3)(64 * 8 * 128, 128, 8 * 128)
+    rc = lib.mpx_paged_prefill(16, 16, 16, 16, 16, None, 16, st, st, 1, 64, 8, 128, 4096, 16,
+                               4096, 0.1, 0, 1, 16, need - 1, None)
+    assert rc == _native.MPX_EINVAL and b"workspace" in lib.mpx_last_error()
+
+
+def _append(lib, dtype=2, D=128, B=2, T=4, bs=16, errors=16):
+    st = (ctypes.c_int64 * 3)(T * 8 * D, 8 * D, D)
+    return lib.mpx_kv_append(16, 16, 16, 16, 16, 16, 16, st, st, B, T, 8, D, 32, bs, 4, dtype,
+                             errors, None)
+
+
+def test_kv_append_validation(lib):
+    assert _append(lib, dtype=9) == _native.MPX_EINVAL and b"dtype" in lib.mpx_last_error()
+    assert _append(lib, D=4) == _native.MPX_EINVAL and b"16 bytes" in lib.mpx_last_error()
+    assert _append(lib, bs=0) == _native.MPX_EINVAL
+    assert _append(lib, errors=None) == _native.MPX_EINVAL and b"null" in lib.mpx_last_error()
+    assert _append(lib, B=0) == _native.MPX_OK and lib.mpx_last_error() == b""

@@ -21,6 +21,8 @@ from mlx_primitives.cache import (
     get_alibi_slopes,
     paged_attention,
     paged_attention_with_bias,
+    set_block_data,
+    store_kv,
 )
 from mlx_primitives.constants import Layout
 from oracle import paged as op
@@ -81,8 +83,8 @@ def test_paged_validation():
     tables = torch.zeros(2, 1, dtype=torch.int32); lens = torch.ones(2, dtype=torch.int32)
     with pytest.raises(ValueError, match="block_size"):
         paged_attention(q, pool, pool, tables, lens, block_size=8)
-    with pytest.raises(NotImplementedError, match="prefill"):
-        paged_attention(t(2, 3, 2, 64), pool, pool, tables, lens)
+    with pytest.raises(RuntimeError, match="ROCm device tensors only"):
+        paged_attention(t(2, 3, 2, 64), pool, pool, tables, lens)  # prefill: no CPU path
     with pytest.raises(ValueError, match="Cannot specify both"):
         paged_attention_with_bias(q, pool, pool, tables, lens, attention_bias=q,
                                   alibi_slopes=torch.ones(2))
@@ -132,3 +134,21 @@ def test_block_tables_match_oracle(lens, bs):
 def test_alibi_slopes_match_oracle():
     for h in (1, 8, 12, 32):
         np.testing.assert_allclose(get_alibi_slopes(h).numpy(), op.get_alibi_slopes(h), rtol=1e-7)
+
+
+def test_store_kv_validation():
+    pool = t(8, 16, 2, 64); x = t(2, 3, 2, 64); tables = torch.zeros(2, 1, dtype=torch.int32)
+    with pytest.raises(ValueError, match="k and v"):
+        store_kv(pool, pool, tables, x, t(2, 3, 2, 32), 0)
+    with pytest.raises(ValueError, match="heads/dim"):
+        store_kv(pool, pool, tables, t(2, 3, 4, 64), t(2, 3, 4, 64), 0)
+    with pytest.raises(ValueError, match="dtype"):
+        store_kv(pool, pool, tables, x.half(), x.half(), 0)
+    with pytest.raises(ValueError, match="block_tables"):
+        store_kv(pool, pool, tables[:1], x, x, 0)
+    with pytest.raises(RuntimeError, match="ROCm device tensors only"):
+        store_kv(pool, pool, tables, x, x, 0)
+    with pytest.raises(ValueError, match="block_id"):
+        set_block_data(pool, pool, 8, x[0], x[0])
+    with pytest.raises(ValueError, match="fit"):
+        set_block_data(pool, pool, 0, t(4, 2, 64), t(4, 2, 64), start_pos=14)

@@ -1,4 +1,4 @@
-"""Pins of the CPU oracle (oracle/attention.py, oracle/paged.py).
+"""Pins of the CPU oracle (oracle/attention.py, oracle/paged.py, oracle/kv_cache.py).
 
 Each oracle function is checked against something that does not restate it:
   * known-answer cases from the reference's own tests (cited file:line);
@@ -8,7 +8,8 @@ Each oracle function is checked against something that does not restate it:
     the reference's parity suite compares with,
     tests/parity/pytorch/test_attention_parity.py:87-105);
   * invariants: block/chunk-size independence, merge associativity, full
-    window == causal, large/small input scales.
+    window == causal, large/small input scales, KV append write-then-gather
+    round trips.
 The last group plants mistakes in the oracle and checks a pin catches each.
 """
 
@@ -20,6 +21,7 @@ import torch
 import torch.nn.functional as F
 
 from oracle import attention as oa
+from oracle import kv_cache as ok
 from oracle import paged as op
 
 
@@ -255,6 +257,153 @@ def test_paged_prefill_vs_brute():
     np.testing.assert_allclose(out, ref, rtol=1e-10, atol=1e-12)
 
 
+def _brute_paged_prefill(q, k_pool, v_pool, tables, lens, scale, bs, causal, slopes=None):
+    """Per (b, h, i) loops over the tokens rebuilt page by page."""
+    B, Sq, H, D = q.shape
+    out = np.full((B, Sq, H, D), np.nan)
+    for b in range(B):
+        toks = [(t, int(tables[b, t // bs]), t % bs) for t in range(int(lens[b]))
+                if int(tables[b, t // bs]) >= 0]
+        for h in range(H):
+            for i in range(Sq):
+                sel = [x for x in toks if not causal or x[0] <= i]
+                if not sel:
+                    continue
+                sc = []
+                for t, blk, slot in sel:
+                    x = sum(float(q[b, i, h, d]) * float(k_pool[blk, slot, h, d])
+                            for d in range(D)) * scale
+                    if slopes is not None:
+                        x += float(slopes[h]) * (t - i)
+                    sc.append(x)
+                m = max(sc)
+                w = [math.exp(x - m) for x in sc]
+                acc = np.zeros(D)
+                for wi, (t, blk, slot) in zip(w, sel):
+                    acc += wi * v_pool[blk, slot, h]
+                out[b, i, h] = acc / sum(w)
+    return out
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("alibi", [False, True])
+def test_paged_prefill_general_vs_brute(causal, alibi):
+    # ragged contexts, a -1 page inside the context, ctx < Sq and ctx > Sq,
+    # an empty context (NaN rows)
+    rng = np.random.default_rng(35)
+    H, D, bs = 2, 3, 4
+    q = rng.standard_normal((3, 6, H, D)); kp = rng.standard_normal((7, bs, H, D))
+    vp = rng.standard_normal((7, bs, H, D))
+    tables = np.array([[4, -1, 1], [6, 0, 2], [3, -1, -1]], np.int32)
+    lens = np.array([11, 5, 0], np.int32)
+    slopes = op.get_alibi_slopes(H) if alibi else None
+    out = op.paged_attention(q, kp, vp, tables, lens, scale=0.7, block_size=bs, causal=causal,
+                             alibi_slopes=slopes)
+    ref = _brute_paged_prefill(q, kp, vp, tables, lens, 0.7, bs, causal, slopes)
+    np.testing.assert_allclose(out, ref, rtol=1e-10, atol=1e-12)
+    assert np.isnan(out[2]).all()
+
+
+def test_paged_prefill_vs_sdpa():
+    # gathered contiguous K/V + additive float mask (ALiBi, validity, causal)
+    rng = np.random.default_rng(36)
+    B, Sq, H, D, bs = 2, 9, 3, 8, 4
+    q = rng.standard_normal((B, Sq, H, D)); kp = rng.standard_normal((8, bs, H, D))
+    vp = rng.standard_normal((8, bs, H, D))
+    tables = np.array([[5, 2, -1, 7], [0, 1, 3, 4]], np.int32)
+    lens = np.array([14, 9], np.int32)
+    slopes = op.get_alibi_slopes(H)
+    out = op.paged_attention(q, kp, vp, tables, lens, scale=0.3, block_size=bs, causal=True,
+                             alibi_slopes=slopes)
+    for b in range(B):
+        idx = [(int(tables[b, t // bs]), t % bs, t) for t in range(tables.shape[1] * bs)]
+        kc = np.stack([kp[max(p, 0), s] for p, s, _ in idx])[None]
+        vc = np.stack([vp[max(p, 0), s] for p, s, _ in idx])[None]
+        T = len(idx)
+        mask = np.zeros((H, Sq, T))
+        for i in range(Sq):
+            for j, (p, s, t) in enumerate(idx):
+                if p < 0 or t >= lens[b] or t > i:
+                    mask[:, i, j] = -np.inf
+                else:
+                    mask[:, i, j] = slopes * (t - i)
+        ref = F.scaled_dot_product_attention(
+            torch.from_numpy(q[b:b + 1]).transpose(1, 2), torch.from_numpy(kc).transpose(1, 2),
+            torch.from_numpy(vc).transpose(1, 2), attn_mask=torch.from_numpy(mask)[None],
+            scale=0.3).transpose(1, 2).numpy()
+        np.testing.assert_allclose(out[b:b + 1], ref, rtol=1e-10, atol=1e-12)
+
+
+# ---- KV append (oracle/kv_cache.py) ------------------------------------------------
+
+def gather_tokens(pool, table, bs, start, n):
+    """Read positions start..start+n-1 back through one block table."""
+    return np.stack([pool[table[p // bs], p % bs] for p in range(start, start + n)])
+
+
+def test_set_get_block_data_kat():
+    # tests/cache/test_block_allocator.py:97-119: write 8 tokens at slot 0 of a
+    # page, read the page back, the first 8 slots equal the input
+    rng = np.random.default_rng(40)
+    kp = np.zeros((10, 16, 8, 64), np.float32); vp = np.zeros_like(kp)
+    k = rng.standard_normal((8, 8, 64)).astype(np.float32); v = -k
+    ok.set_block_data(kp, vp, 3, k, v, start_pos=0, length=8)
+    np.testing.assert_array_equal(kp[3, :8], k)
+    np.testing.assert_array_equal(vp[3, :8], v)
+    assert not kp[3, 8:].any() and not np.delete(kp, 3, axis=0).any()
+
+
+@pytest.mark.parametrize("start,n", [(0, 1), (0, 16), (5, 3), (13, 22), (31, 1), (7, 41)])
+def test_kv_append_round_trip(start, n):
+    rng = np.random.default_rng(start * 100 + n)
+    bs, H, D = 8, 2, 4
+    kp = rng.standard_normal((12, bs, H, D)); vp = rng.standard_normal((12, bs, H, D))
+    kp0, vp0 = kp.copy(), vp.copy()
+    table = np.array([9, 2, 11, 0, 5, 7, 1], np.int32)  # scattered pages
+    k = rng.standard_normal((1, n, H, D)); v = rng.standard_normal((1, n, H, D))
+    ok.kv_append(kp, vp, table[None], k, v, [start])
+    np.testing.assert_array_equal(gather_tokens(kp, table, bs, start, n), k[0])
+    np.testing.assert_array_equal(gather_tokens(vp, table, bs, start, n), v[0])
+    # every slot outside the written positions is untouched
+    touched = np.zeros(kp.shape[:2], bool)
+    for p in range(start, start + n):
+        touched[table[p // bs], p % bs] = True
+    np.testing.assert_array_equal(kp[~touched], kp0[~touched])
+    np.testing.assert_array_equal(vp[~touched], vp0[~touched])
+
+
+def test_kv_append_batched_ragged():
+    rng = np.random.default_rng(41)
+    bs, H, D = 4, 3, 2
+    kp = np.zeros((10, bs, H, D)); vp = np.zeros((10, bs, H, D))
+    tables = np.array([[1, 4, 7], [0, 2, -1], [9, 8, 6]], np.int32)
+    k = rng.standard_normal((3, 5, H, D)); v = rng.standard_normal((3, 5, H, D))
+    starts, counts = [2, 0, 7], [5, 3, 5]
+    ok.kv_append(kp, vp, tables, k, v, starts, counts)
+    for b in range(3):
+        got = gather_tokens(kp, tables[b], bs, starts[b], counts[b])
+        np.testing.assert_array_equal(got, k[b, :counts[b]])
+    # sequence 1 appends 3 of its 5 rows (positions 0..2 -> page 0, slots 0..2):
+    # its slot 3 and its second page stay empty
+    assert not kp[2].any() and not kp[0, 3].any()
+
+
+def test_kv_append_errors():
+    kp = np.zeros((4, 4, 1, 2)); vp = np.zeros_like(kp)
+    x = np.ones((1, 3, 1, 2))
+    with pytest.raises(ValueError):
+        ok.kv_append(kp, vp, np.array([[0, 1]], np.int32), x, x, [-1])
+    with pytest.raises(RuntimeError):
+        ok.kv_append(kp, vp, np.array([[0, 1]], np.int32), x, x, [6])  # positions 6..8
+    with pytest.raises(ValueError):
+        ok.kv_append(kp, vp, np.array([[0, 9]], np.int32), x, x, [3])  # page 9 of 4
+    # the reference writes the chunk before the failing block
+    kp[:] = 0
+    with pytest.raises(RuntimeError):
+        ok.kv_append(kp, vp, np.array([[2, 1]], np.int32), np.ones((1, 3, 1, 2)), x, [6])
+    assert kp[1, 2:].all() and not kp[2].any()
+
+
 def test_block_table_kats():
     # tests/cache/test_paged_attention.py:311-333
     t = op.create_block_table_from_lengths(np.array([16, 32, 48]), 16)
@@ -365,3 +514,26 @@ def test_pin_catches_transposed_causal_mask(monkeypatch):
     monkeypatch.setattr(oa, "compute_chunk_attention", bad)
     with pytest.raises(AssertionError):
         test_tiled_flash_vs_brute(True, 3)
+
+
+def test_pin_catches_append_slot_off_by_one(monkeypatch):
+    orig = ok.set_block_data
+
+    def bad(k_pool, v_pool, block_id, k, v, start_pos=0, length=None):
+        return orig(k_pool, v_pool, block_id, k, v, max(start_pos - 1, 0), length)
+    monkeypatch.setattr(ok, "set_block_data", bad)
+    with pytest.raises(AssertionError):
+        test_kv_append_round_trip(5, 3)
+
+
+def test_pin_catches_prefill_alibi_sign(monkeypatch):
+    orig = op.paged_attention_prefill
+
+    def bad(q, k_pool, v_pool, tables, lens, scale, bs, causal, alibi_slopes=None):
+        flipped = None if alibi_slopes is None else -alibi_slopes  # q_pos - kv_pos
+        return orig(q, k_pool, v_pool, tables, lens, scale, bs, causal, flipped)
+    monkeypatch.setattr(op, "paged_attention_prefill", bad)
+    with pytest.raises(AssertionError):
+        test_paged_prefill_vs_sdpa()
+    with pytest.raises(AssertionError):
+        test_paged_prefill_general_vs_brute(True, True)
