@@ -3,12 +3,14 @@
 A step is one forward pass of the headline workload, flash_attention bf16
 BHSD B=4 H=32 S=4096 D=128 causal (the configuration the metric is quoted
 on). The same run also times paged-KV decode fp16 (64 sequences, H=32, D=128,
-context ~ U{512..8192}, 16-token pages) and reports it under "paged_decode".
+context ~ U{512..8192}, 16-token pages) under "paged_decode", paged prefill of
+the headline shape over 16-token pages under "paged_prefill", and the KV append
+that writes those prompts into pages under "kv_append".
 Inputs are synthetic (seeded N(0,1)) and resident in HBM before timing.
 
 Prints ONE JSON line. Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 
-`--only flash|paged|copy` runs a single leg (no CPU baseline) for profiler
+`--only flash|paged|prefill|append|copy` runs a single leg (no CPU baseline) for profiler
 passes; `copy` streams a 1 GiB float32 buffer through an elementwise kernel,
 the known-size reference for scaling the HBM byte counters. The HBM traffic
 per launch measured by those passes (rocprofv3 FETCH_SIZE / WRITE_SIZE) is read
@@ -37,6 +39,8 @@ PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 TRAFFIC_FILE = os.path.join(REPO, "profiles", "hbm_traffic.json")
 FLASH_KERNEL = "fa_fwd16_kernel<128,64,8,bf16>"
 PAGED_KERNELS = "paged_decode_part_kernel + paged_decode_merge_kernel"
+PREFILL_KERNEL = "fa_fwd16_kernel<128,64,8,bf16,paged>"
+APPEND_KERNEL = "kv_append_kernel"
 
 
 def measured_traffic(key: str):
@@ -145,6 +149,79 @@ def cpu_baseline_paged(inp, cfg: dict, budget_s: float) -> dict:
                       f"decode in float32 numpy, {t_total:.1f} s"}
 
 
+def cpu_baseline_prefill(inp, cfg: dict, budget_s: float) -> dict:
+    """The oracle's paged prefill (gather + dense masked softmax,
+    paged_attention.py:211-320) in float32, one whole sequence at a time."""
+    from oracle import paged as op
+
+    B = inp.q.shape[0]
+    per_seq = wl.flash_flops(1, cfg["H"], cfg["S"], cfg["D"], True)
+    t_total, done = 0.0, 0
+    for b in range(B):
+        row = inp.block_tables[b:b + 1]
+        kp = inp.k_pool[row[0].long()].float().cpu().numpy()
+        vp = inp.v_pool[row[0].long()].float().cpu().numpy()
+        local = torch.arange(row.shape[1], dtype=torch.int32)[None].numpy()
+        q = inp.q[b:b + 1].float().cpu().numpy()
+        t0 = time.perf_counter()
+        op.paged_attention_prefill(q, kp, vp, local, inp.context_lens[b:b + 1].cpu().numpy(),
+                                   wl.default_scale(cfg["D"]), inp.block_size, True)
+        t_total += time.perf_counter() - t0
+        done += 1
+        if t_total >= budget_s:
+            break
+    return {"value": done * per_seq / t_total / 1e12, "unit": "TFLOP/s", "cores": blas_threads(),
+            "kind": "port",
+            "sample": f"{done} of {B} sequences of the same workload, oracle paged prefill in "
+                      f"float32 numpy, {t_total:.1f} s"}
+
+
+def cpu_baseline_append(inp, cfg: dict, budget_s: float) -> dict:
+    """The oracle's KVCache._store_kv page-chunk loop (kv_cache.py:219-264) on
+    host arrays, whole sequences, repeated until about budget_s / 4 seconds."""
+    from oracle import kv_cache as ok
+
+    B, T, H, D = inp.k.shape
+    k = inp.k.view(torch.int16).cpu().numpy(); v = inp.v.view(torch.int16).cpu().numpy()
+    kp = torch.zeros(inp.k_pool.shape, dtype=torch.int16).numpy(); vp = kp.copy()
+    tables = inp.block_tables.cpu().numpy()
+    per_seq = 4.0 * T * H * D * 2
+    t_total, done = 0.0, 0
+    while t_total < budget_s / 4:
+        b = done % B
+        t0 = time.perf_counter()
+        ok.store_kv(kp, vp, tables[b], k[b], v[b], 0, cfg["block_size"])
+        t_total += time.perf_counter() - t0
+        done += 1
+    return {"value": done * per_seq / t_total / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"{done} sequence appends of {T} tokens (the workload's sequences in turn), "
+                      f"oracle page-chunk loop in numpy, {t_total:.1f} s"}
+
+
+def prefill_step(dev):
+    from mlx_primitives.cache import paged_attention
+
+    inp = wl.make_paged_prefill(wl.CONFIGS["paged_prefill_bf16"], device=dev)
+    fn = lambda: paged_attention(inp.q, inp.k_pool, inp.v_pool, inp.block_tables,
+                                 inp.context_lens, block_size=inp.block_size, causal=True)
+    return inp, fn
+
+
+def append_step(dev):
+    """The C-ABI append over the whole workload, error words preallocated."""
+    from mlx_primitives import _native
+
+    inp = wl.make_append(wl.CONFIGS["kv_append_bf16"], device=dev)
+    B, T, H, D = inp.k.shape
+    errors = torch.zeros(3, dtype=torch.int32, device=dev)
+    counts = torch.full((B,), T, dtype=torch.int32, device=dev)
+    fn = lambda: _native.kv_append(inp.k, inp.v, inp.k_pool, inp.v_pool, inp.block_tables,
+                                   inp.start_pos, counts, errors, inp.k.stride()[:3],
+                                   inp.v.stride()[:3], B, T, H, D, inp.k_pool.shape[0],
+                                   inp.k_pool.shape[1], inp.block_tables.shape[1])
+    return inp, fn, errors
+
+
 def run_one_leg(args) -> int:
     """One leg for a profiler pass: warmup + steps calls, timing on stderr/stdout."""
     dev = torch.device("cuda:0")
@@ -162,6 +239,12 @@ def run_one_leg(args) -> int:
         q, k, v = wl.make_qkv(cfg, device=dev)
         fn = lambda: flash_attention(q, k, v, causal=True, layout="BHSD")
         work, unit = wl.config_work("flash_bf16_bhsd"), "flop"
+    elif args.only == "prefill":
+        _, fn = prefill_step(dev)
+        work, unit = wl.config_work("paged_prefill_bf16"), "flop"
+    elif args.only == "append":
+        _, fn, _ = append_step(dev)
+        work, unit = wl.config_work("kv_append_bf16"), "bytes"
     else:
         from mlx_primitives.cache import paged_attention
 
@@ -184,7 +267,8 @@ def main() -> int:
     ap.add_argument("--cpu-budget", type=float, default=10.0,
                     help="seconds of CPU work per baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=["flash", "paged", "copy"], default=None,
+    ap.add_argument("--only", choices=["flash", "paged", "prefill", "append", "copy"],
+                    default=None,
                     help="run one leg only (profiler passes); prints that leg's timing")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -224,12 +308,33 @@ def main() -> int:
     p_gbs = pbytes / (p_ev * 1e-3) / 1e9
     log(f"[bench] {pname}: {p_wall:.3f} ms/step wall, kernels {p_ev:.3f} ms -> {p_gbs:.1f} GB/s")
 
-    cpu = None
-    pcpu = None
+    # ---- paged prefill, bf16 (prompt processing over pages) ------------------------
+    fname = "paged_prefill_bf16"
+    finp, fstep = prefill_step(dev)
+    fflops = wl.config_work(fname)
+    log(f"[bench] {fname}: warmup {args.warmup}, steps {args.steps}")
+    f_wall, f_ev, f_min, f_med = time_steps(fstep, args.steps, args.warmup)
+    f_tf = fflops / (f_ev * 1e-3) / 1e12
+    log(f"[bench] {fname}: {f_wall:.3f} ms/step wall, kernel {f_ev:.3f} ms -> {f_tf:.1f} TFLOP/s")
+
+    # ---- KV append, bf16 (write the prompts into their pages) ------------------------
+    aname = "kv_append_bf16"
+    ainp, astep, aerr = append_step(dev)
+    abytes = wl.config_work(aname)
+    log(f"[bench] {aname}: warmup {args.warmup}, steps {args.steps}")
+    a_wall, a_ev, a_min, a_med = time_steps(astep, args.steps, args.warmup)
+    a_gbs = abytes / (a_ev * 1e-3) / 1e9
+    if aerr.tolist() != [0, 0, 0]:
+        raise RuntimeError(f"kv append reported errors {aerr.tolist()}")
+    log(f"[bench] {aname}: {a_wall:.3f} ms/step wall, kernel {a_ev:.3f} ms -> {a_gbs:.1f} GB/s")
+
+    cpu = pcpu = fcpu = acpu = None
     if not args.no_cpu_baseline:
         log("[bench] cpu baselines (oracle restatement on host cores)")
         cpu = cpu_baseline_flash(cfg, q, k, v, args.cpu_budget)
         pcpu = cpu_baseline_paged(pin, pcfg, args.cpu_budget)
+        fcpu = cpu_baseline_prefill(finp, wl.CONFIGS[fname], args.cpu_budget)
+        acpu = cpu_baseline_append(ainp, wl.CONFIGS[aname], args.cpu_budget)
 
     result = {
         "metric": "causal fwd TFLOP/s @S=4096,D=128 + paged-decode HBM GB/s, % of roofline",
@@ -266,6 +371,27 @@ def main() -> int:
                          "traffic": measured_traffic("paged_decode_fp16"),
                          "kernel": PAGED_KERNELS, "traffic_unit": "bytes per launch"},
             "cpu_baseline": pcpu,
+        },
+        "paged_prefill": {
+            "workload": "paged_attention prefill bf16, 4 prompts x 4096 tokens, H=32, D=128, "
+                        "causal, context = prompt in 16-token pages of a permuted pool",
+            "value": f_tf, "unit": "TFLOP/s", "ms_per_step": f_wall, "kernel_ms": f_ev,
+            "kernel_ms_median": f_med, "kernel_ms_min": f_min, "flop_per_step": fflops,
+            "roofline": {"bound": "mfma", "achieved": f_tf, "peak": PEAK_BF16_TFLOPS,
+                         "unit": "TFLOP/s", "frac": f_tf / PEAK_BF16_TFLOPS,
+                         "traffic": measured_traffic(fname), "kernel": PREFILL_KERNEL,
+                         "traffic_unit": "bytes per launch"},
+            "cpu_baseline": fcpu,
+        },
+        "kv_append": {
+            "workload": "KV append bf16 through the C ABI: 4 sequences x 4096 new tokens, H=32, "
+                        "D=128, into 16-token pages of a permuted pool",
+            "value": a_gbs, "unit": "GB/s", "ms_per_step": a_wall, "kernel_ms": a_ev,
+            "kernel_ms_median": a_med, "kernel_ms_min": a_min, "bytes_per_step": abytes,
+            "roofline": {"bound": "hbm", "achieved": a_gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                         "frac": a_gbs / PEAK_HBM_GBS, "traffic": measured_traffic(aname),
+                         "kernel": APPEND_KERNEL, "traffic_unit": "bytes per launch"},
+            "cpu_baseline": acpu,
         },
     }
     print(json.dumps(result), flush=True)

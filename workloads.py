@@ -1,5 +1,6 @@
-"""Seeded synthetic workloads of the five BASELINE configurations, and the
-algorithmic FLOP / byte counts used for throughput and roofline figures.
+"""Seeded synthetic workloads of the five BASELINE configurations and of the
+paged prefill / KV append rows, and the algorithmic FLOP / byte counts used
+for throughput and roofline figures.
 
 Inputs are drawn N(0, 1) in float32 from one torch.Generator seeded with 42
 (the reference benchmarks' seed, benchmarks/config.py:29) in the order q, k, v
@@ -30,6 +31,13 @@ CONFIGS: Dict[str, dict] = {
                               ctx_lo=512, ctx_hi=8192, block_size=16),
     "chunked_bf16": dict(kind="chunked", dtype=torch.bfloat16, B=1, H=16, D=64,
                          Sq=512, Skv=65536, chunk_size=1024, causal=False),
+    # Prompt processing over a paged cache: the headline shape (4 x 4096 tokens,
+    # 32 heads of 128, causal) with its K/V in 16-token pages of a permuted pool,
+    # and the append that writes those prompts into the pages.
+    "paged_prefill_bf16": dict(kind="paged_prefill", dtype=torch.bfloat16, B=4, S=4096, H=32,
+                               D=128, block_size=16, causal=True),
+    "kv_append_bf16": dict(kind="append", dtype=torch.bfloat16, B=4, S=4096, H=32, D=128,
+                           block_size=16),
 }
 
 
@@ -96,6 +104,61 @@ def make_paged(cfg: dict, device="cpu", seed: int = SEED) -> PagedInputs:
     return PagedInputs(q, k_pool, v_pool, tables.to(device), ctx.to(torch.int32).to(device), bs)
 
 
+@dataclass
+class PrefillInputs:
+    q: torch.Tensor             # (B, S, H, D)
+    k_pool: torch.Tensor        # (B * S / bs, bs, H, D)
+    v_pool: torch.Tensor
+    block_tables: torch.Tensor  # int32 (B, S / bs), a permutation of the pool
+    context_lens: torch.Tensor  # int32 (B,) = S
+    block_size: int
+
+
+def _permuted_tables(gen: torch.Generator, B: int, pages: int) -> torch.Tensor:
+    return torch.randperm(B * pages, generator=gen).to(torch.int32).reshape(B, pages)
+
+
+def make_paged_prefill(cfg: dict, device="cpu", seed: int = SEED) -> PrefillInputs:
+    """Prefill inputs: every sequence's context is its own S-token prompt, stored
+    in S / bs pages drawn from a random permutation of the pool."""
+    gen = torch.Generator(device="cpu").manual_seed(seed)
+    B, S, H, D, bs = cfg["B"], cfg["S"], cfg["H"], cfg["D"], cfg["block_size"]
+    pages = (S + bs - 1) // bs
+    tables = _permuted_tables(gen, B, pages)
+    dgen = gen if device == "cpu" else torch.Generator(device=device).manual_seed(seed + 1)
+    dt = cfg["dtype"]
+    q = _randn(dgen, (B, S, H, D), device).to(dt)
+    k_pool = _randn(dgen, (B * pages, bs, H, D), device).to(dt)
+    v_pool = _randn(dgen, (B * pages, bs, H, D), device).to(dt)
+    ctx = torch.full((B,), S, dtype=torch.int32)
+    return PrefillInputs(q, k_pool, v_pool, tables.to(device), ctx.to(device), bs)
+
+
+@dataclass
+class AppendInputs:
+    k: torch.Tensor             # (B, S, H, D) new tokens
+    v: torch.Tensor
+    k_pool: torch.Tensor        # (B * S / bs, bs, H, D), written in place
+    v_pool: torch.Tensor
+    block_tables: torch.Tensor  # int32 (B, S / bs), a permutation of the pool
+    start_pos: torch.Tensor     # int32 (B,) zeros
+
+
+def make_append(cfg: dict, device="cpu", seed: int = SEED) -> AppendInputs:
+    gen = torch.Generator(device="cpu").manual_seed(seed)
+    B, S, H, D, bs = cfg["B"], cfg["S"], cfg["H"], cfg["D"], cfg["block_size"]
+    pages = (S + bs - 1) // bs
+    tables = _permuted_tables(gen, B, pages)
+    dgen = gen if device == "cpu" else torch.Generator(device=device).manual_seed(seed + 1)
+    dt = cfg["dtype"]
+    k = _randn(dgen, (B, S, H, D), device).to(dt)
+    v = _randn(dgen, (B, S, H, D), device).to(dt)
+    k_pool = torch.zeros((B * pages, bs, H, D), dtype=dt, device=device)
+    v_pool = torch.zeros_like(k_pool)
+    return AppendInputs(k, v, k_pool, v_pool, tables.to(device),
+                        torch.zeros(B, dtype=torch.int32, device=device))
+
+
 # ---- algorithmic work -------------------------------------------------------
 
 def flash_flops(B: int, H: int, S: int, D: int, causal: bool) -> float:
@@ -123,10 +186,20 @@ def paged_bytes(ctx: torch.Tensor, H: int, D: int, elem_bytes: int, max_blocks: 
     return kv + qo + B * max_blocks * 4 + B * 4
 
 
+def append_bytes(B: int, T: int, H: int, D: int, elem_bytes: int, max_blocks: int) -> float:
+    """K and V rows read once and written once, + tables, starts and counts."""
+    return 4.0 * B * T * H * D * elem_bytes + B * max_blocks * 4 + 2 * B * 4
+
+
 def config_work(name: str, paged: Optional[PagedInputs] = None) -> float:
     cfg = CONFIGS[name]
-    if cfg["kind"] == "flash":
-        return flash_flops(cfg["B"], cfg["H"], cfg["S"], cfg["D"], cfg["causal"])
+    if cfg["kind"] in ("flash", "paged_prefill"):
+        # prefill with context == prompt is the causal square of flash
+        return flash_flops(cfg["B"], cfg["H"], cfg["S"], cfg["D"], cfg.get("causal", True))
+    if cfg["kind"] == "append":
+        pages = (cfg["S"] + cfg["block_size"] - 1) // cfg["block_size"]
+        return append_bytes(cfg["B"], cfg["S"], cfg["H"], cfg["D"],
+                            torch.finfo(cfg["dtype"]).bits // 8, pages)
     if cfg["kind"] == "window":
         return window_flops(cfg["B"], cfg["H"], cfg["S"], cfg["D"], cfg["window"])
     if cfg["kind"] == "chunked":
