@@ -6,9 +6,10 @@ float64 and a JSON `meta` string (no pickled objects: np.load with
 allow_pickle=False reads them).
 
 The expected output is the float64 oracle (oracle/attention.py,
-oracle/paged.py). Before a fixture is written it is checked against an
-independent evaluation: torch.nn.functional.scaled_dot_product_attention in
-float64 with an explicit boolean mask, the library routine the reference's own
+oracle/paged.py, oracle/kv_cache.py). Before a fixture is written it is checked
+against an independent evaluation: for attention,
+torch.nn.functional.scaled_dot_product_attention in float64 with an explicit
+mask, the library routine the reference's own
 parity suite compares with (tests/parity/pytorch/test_attention_parity.py:87-105,
 288-337). The reference ships no golden files (its generator recipes are
 scripts/validation/generators/attention/sdpa.py:93-141 and efficient.py:276-339);
@@ -35,6 +36,7 @@ if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
 from oracle import attention as oa  # noqa: E402
+from oracle import kv_cache as ok  # noqa: E402
 from oracle import paged as op  # noqa: E402
 
 DTYPES = {"float32": torch.float32, "float16": torch.float16, "bfloat16": torch.bfloat16}
@@ -165,6 +167,72 @@ def paged_case(name, lens, tables, num_blocks, bs, H, D, dtype, seed, alibi=Fals
          q=q, k_pool=kp, v_pool=vp, block_tables=tables, context_lens=lens, expected=exp)
 
 
+def paged_prefill_case(name, Sq, lens, tables, num_blocks, bs, H, D, dtype, causal, seed,
+                       alibi=False):
+    g = torch.Generator().manual_seed(seed)
+    B = len(lens)
+    q = rounded((B, Sq, H, D), dtype, g)
+    kp = rounded((num_blocks, bs, H, D), dtype, g)
+    vp = rounded((num_blocks, bs, H, D), dtype, g)
+    tables = np.asarray(tables, dtype=np.int32)
+    lens = np.asarray(lens, dtype=np.int32)
+    slopes = op.get_alibi_slopes(H) if alibi else None
+    scale = 1.0 / math.sqrt(D)
+    exp = op.paged_attention_prefill(q.astype(np.float64), kp.astype(np.float64),
+                                     vp.astype(np.float64), tables, lens, scale, bs, causal,
+                                     alibi_slopes=slopes)
+    # Independent check: the valid tokens of each sequence gathered in order,
+    # SDPA with an additive mask = ALiBi slope_h * (kv - q) (paged_attention.py:
+    # 266-285), -inf where kv > q under the causal flag (300-309).
+    for b in range(B):
+        pos = np.arange(int(lens[b]))
+        pages = tables[b, pos // bs]
+        ok_ = pages >= 0
+        pos = pos[ok_]
+        kk = kp[pages[ok_], pos % bs].transpose(1, 0, 2)[None].astype(np.float64)
+        vv = vp[pages[ok_], pos % bs].transpose(1, 0, 2)[None].astype(np.float64)
+        qq = q[b:b + 1].transpose(0, 2, 1, 3).astype(np.float64)
+        diff = (pos[None, :] - np.arange(Sq)[:, None]).astype(np.float64)
+        mask = np.zeros((1, H, Sq, len(pos)))
+        if alibi:
+            mask = mask + slopes[None, :, None, None] * diff[None, None]
+        if causal:
+            mask = np.where(diff[None, None] > 0, -np.inf, mask)
+        ref = torch.nn.functional.scaled_dot_product_attention(
+            torch.from_numpy(qq), torch.from_numpy(kk), torch.from_numpy(vv),
+            attn_mask=torch.from_numpy(mask), scale=scale).numpy()
+        agree(f"{name}[{b}]", exp[b:b + 1].transpose(0, 2, 1, 3), ref, AGREE_EXACT)
+    save(name, {"kind": "paged_prefill", "dtype": dtype, "block_size": bs, "alibi": alibi,
+                "causal": causal},
+         q=q, k_pool=kp, v_pool=vp, block_tables=tables, context_lens=lens, expected=exp)
+
+
+def kv_append_case(name, T, starts, counts, tables, num_blocks, bs, H, D, dtype, seed):
+    g = torch.Generator().manual_seed(seed)
+    B = len(starts)
+    k = rounded((B, T, H, D), dtype, g)
+    v = rounded((B, T, H, D), dtype, g)
+    kp = rounded((num_blocks, bs, H, D), dtype, g)
+    vp = rounded((num_blocks, bs, H, D), dtype, g)
+    tables = np.asarray(tables, dtype=np.int32)
+    starts = np.asarray(starts, dtype=np.int32)
+    counts = np.asarray(counts, dtype=np.int32)
+    ek, ev = kp.copy(), vp.copy()
+    ok.kv_append(ek, ev, tables, k, v, starts, counts, bs)
+    # Independent check: token by token, position -> (page, slot) directly.
+    ik, iv = kp.copy(), vp.copy()
+    for b in range(B):
+        for t in range(int(counts[b])):
+            p = int(starts[b]) + t
+            ik[tables[b, p // bs], p % bs] = k[b, t]
+            iv[tables[b, p // bs], p % bs] = v[b, t]
+    if not (np.array_equal(ek, ik) and np.array_equal(ev, iv)):
+        raise SystemExit(f"{name}: oracle append disagrees with the per-token placement")
+    save(name, {"kind": "kv_append", "dtype": dtype, "block_size": bs},
+         k=k, v=v, k_pool=kp, v_pool=vp, block_tables=tables, start_pos=starts,
+         n_tokens=counts, expected=np.stack([ek, ev]))
+
+
 def main():
     flash_case("flash_causal_f32_bshd", (1, 37, 2, 32), "float32", "BSHD", True, 101)
     flash_case("flash_full_bf16_bhsd", (2, 3, 70, 64), "bfloat16", "BHSD", False, 102)
@@ -179,6 +247,14 @@ def main():
                                                           [6, 7, -1]], 9, 16, 2, 32, "float32", 109)
     paged_case("paged_alibi_f16", [5, 40, 17], [[3, -1, -1], [0, 4, 1], [2, 5, -1]], 6, 16, 4,
                64, "float16", 110, alibi=True)
+    # prefill: ragged contexts (longer / shorter than the queries), a missing page
+    paged_prefill_case("paged_prefill_alibi_bf16", 24, [40, 13], [[4, -1, 1], [0, 3, -1]], 5,
+                       16, 2, 64, "bfloat16", True, 111, alibi=True)
+    paged_prefill_case("paged_prefill_full_f32", 12, [30, 20], [[2, 0], [3, 1]], 4, 16, 2, 32,
+                       "float32", False, 112)
+    # append: starts inside a page, spans over pages, a decode-style single token, nothing
+    kv_append_case("kv_append_ragged_bf16", 20, [3, 16, 0], [20, 1, 0],
+                   [[5, 0, 7], [2, 6, 1], [3, 4, 8]], 9, 8, 2, 64, "bfloat16", 113)
 
 
 if __name__ == "__main__":

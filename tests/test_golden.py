@@ -17,6 +17,7 @@ import pytest
 import torch
 
 from oracle import attention as oa
+from oracle import kv_cache as ok
 from oracle import paged as op
 
 HERE = os.path.dirname(os.path.abspath(__file__))
@@ -47,15 +48,25 @@ def oracle_output(meta, a):
     if kind == "chunked":
         return oa.chunked_cross_attention(f64["q"], f64["k"], f64["v"],
                                           chunk_size=meta["chunk_size"], causal=meta["causal"])
+    if kind == "kv_append":
+        kp, vp = f64["k_pool"].copy(), f64["v_pool"].copy()
+        ok.kv_append(kp, vp, a["block_tables"], f64["k"], f64["v"], a["start_pos"],
+                     a["n_tokens"], meta["block_size"])
+        return np.stack([kp, vp])
     H, D = a["q"].shape[2], a["q"].shape[3]
     slopes = op.get_alibi_slopes(H) if meta["alibi"] else None
+    if kind == "paged_prefill":
+        return op.paged_attention_prefill(f64["q"], f64["k_pool"], f64["v_pool"],
+                                          a["block_tables"], a["context_lens"],
+                                          1.0 / math.sqrt(D), meta["block_size"], meta["causal"],
+                                          alibi_slopes=slopes)
     return op.paged_attention_decode(f64["q"], f64["k_pool"], f64["v_pool"], a["block_tables"],
                                      a["context_lens"], 1.0 / math.sqrt(D), meta["block_size"],
                                      alibi_slopes=slopes)
 
 
 def test_fixtures_present():
-    assert len(FIXTURES) >= 10
+    assert len(FIXTURES) >= 13
 
 
 @pytest.mark.parametrize("path", FIXTURES, ids=fixture_id)
@@ -68,7 +79,7 @@ def test_oracle_matches_golden(path):
 @pytest.mark.parametrize("path", FIXTURES, ids=fixture_id)
 def test_kernel_matches_golden(device, path):
     from mlx_primitives.attention import chunked_cross_attention, flash_attention, sliding_window_attention
-    from mlx_primitives.cache import get_alibi_slopes, paged_attention
+    from mlx_primitives.cache import get_alibi_slopes, paged_attention, store_kv
 
     meta, a = load(path)
     dt = TORCH_DTYPES[meta["dtype"]]
@@ -83,11 +94,19 @@ def test_kernel_matches_golden(device, path):
     elif kind == "chunked":
         out = chunked_cross_attention(t["q"], t["k"], t["v"], chunk_size=meta["chunk_size"],
                                       causal=meta["causal"])
+    elif kind == "kv_append":
+        store_kv(t["k_pool"], t["v_pool"], t["block_tables"], t["k"], t["v"], t["start_pos"],
+                 t["n_tokens"])
+        # a copy: the pools must equal the expected ones exactly
+        got = torch.stack([t["k_pool"], t["v_pool"]]).double().cpu().numpy()
+        np.testing.assert_array_equal(got, a["expected"])
+        return
     else:
         H = a["q"].shape[2]
         slopes = get_alibi_slopes(H).to(device) if meta["alibi"] else None
         out = paged_attention(t["q"], t["k_pool"], t["v_pool"], t["block_tables"],
-                              t["context_lens"], block_size=meta["block_size"], alibi_slopes=slopes)
+                              t["context_lens"], block_size=meta["block_size"],
+                              causal=meta.get("causal", True), alibi_slopes=slopes)
     assert out.dtype == dt
     got = out.double().cpu().numpy()
     exp = a["expected"]

@@ -33,6 +33,9 @@ def test_stub_loads_and_binds():
     assert ns["_lib"].mpx_version() > 0
     with pytest.raises(ValueError):
         ns["_raise"](-1)
+    for fn in ("flash_attention_fwd", "paged_attention_decode", "paged_attention_prefill",
+               "store_kv"):
+        assert callable(ns[fn]), fn
 
 
 @pytest.mark.gpu
@@ -88,3 +91,59 @@ def test_stub_paged_matches_api(device):
     ref = paged_attention(q, kp, vp, tables, lens, block_size=bs, alibi_slopes=slopes)
     torch.cuda.synchronize()
     assert torch.equal(o, ref)
+
+
+@pytest.mark.gpu
+def test_stub_paged_prefill_matches_api(device):
+    from mlx_primitives.cache import get_alibi_slopes, paged_attention
+
+    ns = stub_namespace()
+    g = torch.Generator().manual_seed(7)
+    B, Sq, H, D, bs, nb = 2, 40, 4, 64, 16, 10
+    q = torch.randn(B, Sq, H, D, generator=g).to(torch.bfloat16).to(device)
+    kp = torch.randn(nb, bs, H, D, generator=g).to(torch.bfloat16).to(device)
+    vp = torch.randn(nb, bs, H, D, generator=g).to(torch.bfloat16).to(device)
+    tables = torch.tensor([[3, 7, 1, -1], [0, 2, 9, 4]], dtype=torch.int32, device=device)
+    lens = torch.tensor([45, 60], dtype=torch.int32, device=device)
+    slopes = get_alibi_slopes(H).to(device)
+    o = torch.empty_like(q)
+    bufs = []
+
+    def alloc(n):
+        bufs.append(torch.empty(n, dtype=torch.uint8, device=device))
+        return bufs[-1].data_ptr()
+
+    ns["paged_attention_prefill"](q.data_ptr(), kp.data_ptr(), vp.data_ptr(), tables.data_ptr(),
+                                  lens.data_ptr(), o.data_ptr(), B, Sq, H, D, nb, bs, 4,
+                                  ns["BF16"], 1 / math.sqrt(D), causal=1,
+                                  alibi_slopes=slopes.data_ptr(), alloc=alloc,
+                                  stream=torch.cuda.current_stream().cuda_stream)
+    ref = paged_attention(q, kp, vp, tables, lens, block_size=bs, causal=True,
+                          alibi_slopes=slopes)
+    torch.cuda.synchronize()
+    assert torch.equal(o, ref)
+
+
+@pytest.mark.gpu
+def test_stub_store_kv_matches_api(device):
+    from mlx_primitives.cache import store_kv
+
+    ns = stub_namespace()
+    g = torch.Generator().manual_seed(8)
+    B, T, H, D, bs, nb = 2, 21, 4, 128, 16, 8
+    k = torch.randn(B, T, H, D, generator=g).half().to(device)
+    v = torch.randn(B, T, H, D, generator=g).half().to(device)
+    tables = torch.tensor([[6, 1, 3], [0, 5, 7]], dtype=torch.int32, device=device)
+    starts = torch.tensor([5, 16], dtype=torch.int32, device=device)
+    counts = torch.tensor([21, 9], dtype=torch.int32, device=device)
+    pools = [torch.zeros(nb, bs, H, D, dtype=torch.float16, device=device) for _ in range(4)]
+    errors = torch.zeros(3, dtype=torch.int32, device=device)
+    ns["store_kv"](k.data_ptr(), v.data_ptr(), pools[0].data_ptr(), pools[1].data_ptr(),
+                   tables.data_ptr(), starts.data_ptr(), counts.data_ptr(), errors.data_ptr(),
+                   B, T, H, D, nb, bs, 3, ns["F16"],
+                   stream=torch.cuda.current_stream().cuda_stream)
+    store_kv(pools[2], pools[3], tables, k, v, starts, counts)
+    torch.cuda.synchronize()
+    assert errors.tolist() == [0, 0, 0]
+    assert torch.equal(pools[0], pools[2]) and torch.equal(pools[1], pools[3])
+    assert pools[0].any()
