@@ -701,10 +701,14 @@ __device__ __forceinline__ void dma16(u32x4 rsrc, unsigned lds_addr, int voff, i
                : "memory", "m0");
 }
 
+// Offset of a key row without a page: past any pool the host accepts, so its
+// buffer loads return zeros.
+constexpr u32 kNoRowDirect = 0xFFFFFF00u;
+
 // Raw buffer descriptor words (base, stride 0, num_records, gfx950 flags).
-__device__ __forceinline__ u32x4 buffer_desc(const void* base) {
+__device__ __forceinline__ u32x4 buffer_desc(const void* base, u32 records = 0x7fffffffu) {
   const unsigned long long a = (unsigned long long)base;
-  return (u32x4){(u32)a, (u32)(a >> 32) & 0xffffu, 0x7fffffffu, (u32)kBufferFlags};
+  return (u32x4){(u32)a, (u32)(a >> 32) & 0xffffu, records, (u32)kBufferFlags};
 }
 
 __device__ __forceinline__ u32 lds_addr(const void* p) {
@@ -718,18 +722,26 @@ __device__ __forceinline__ u32x2 lds_read_tr16(const unsigned char* p) {
   return __builtin_bit_cast(u32x2, r);
 }
 
-template <int NW, bool BF16, int NST>
-__device__ __forceinline__ void fa16_rows_direct(const FwdParams& p, const WorkItem wi,
+// PAGED: K/V rows come from the pools through this item's page-table slice,
+// staged in LDS (pages); each lane's DMA offset is its row's (page, slot), and
+// a row without a page gets an offset past the pool, which the buffer range
+// check turns into zeros; those keys are masked.
+template <int NW, bool BF16, int NST, bool PAGED>
+__device__ __forceinline__ void fa16_rows_direct(const FwdParams& pin, const WorkItem wi,
                                                  unsigned char* __restrict__ st0,
                                                  unsigned char* __restrict__ st1,
                                                  unsigned char* __restrict__ st2,
-                                                 unsigned char* __restrict__ st3) {
+                                                 unsigned char* __restrict__ st3,
+                                                 int* __restrict__ pages) {
   constexpr int D = 128, BN = 64, BM = 32 * NW;
   constexpr int NB = BN / 32, NSL = BN / 16, NKS = D / 16, NDB = D / 32;
   constexpr int ROWB = 2 * D;          // bytes per K or V row
   constexpr int KBYTES = BN * ROWB;    // one K (or V) tile
   constexpr int STAGEB = 2 * KBYTES;   // K then V
   static_assert(NW == 8, "each wave stages rows 4*wave .. +3 and +32 .. +35");
+  // Paged: keys exist up to this sequence's context length.
+  FwdParams p = pin;
+  if constexpr (PAGED) p.Sk = max(0, min(pin.ctx[wi.b], pin.max_blocks * pin.bs));
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -740,8 +752,25 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& p, const WorkI
   kv_range<BM, BN>(p, q0, wi.split, kv_lo, t_begin, t_end);
 
   const uint16_t* __restrict__ Qp = (const uint16_t*)p.q + wi.b * p.q_sb + wi.h * p.q_sh;
-  const u32x4 krs = buffer_desc((const uint16_t*)p.k + wi.b * p.k_sb + wi.h * p.k_sh);
-  const u32x4 vrs = buffer_desc((const uint16_t*)p.v + wi.b * p.v_sb + wi.h * p.v_sh);
+  // Paged: the record count is the pool's extent past this head's offset.
+  const u32 krec = PAGED ? p.pool_bytes - (u32)(wi.h * p.k_sh * 2) : 0x7fffffffu;
+  const u32 vrec = PAGED ? p.pool_bytes - (u32)(wi.h * p.v_sh * 2) : 0x7fffffffu;
+  const u32x4 krs = buffer_desc((const uint16_t*)p.k + wi.b * p.k_sb + wi.h * p.k_sh, krec);
+  const u32x4 vrs = buffer_desc((const uint16_t*)p.v + wi.b * p.v_sb + wi.h * p.v_sh, vrec);
+
+  // Paged: this item's slice of the page table, validated, in LDS.
+  int pg_first = 0;
+  if constexpr (PAGED) {
+    const int kv_a = kv_lo + t_begin * BN, kv_b = min(kv_lo + t_end * BN, p.Sk);
+    pg_first = page_of(p, kv_a);
+    const int npg = kv_b > kv_a ? page_of(p, kv_b - 1) - pg_first + 1 : 0;
+    const int32_t* row = p.bt + (int64_t)wi.b * p.max_blocks + pg_first;
+    for (int i = tid; i < npg; i += 64 * NW) {
+      const int blk = row[i];
+      pages[i] = (blk >= 0 && blk < p.num_blocks) ? blk : -1;
+    }
+    __syncthreads();
+  }
 
   const int wq0 = q0 + wave * 32;
   const int myq = wq0 + j;
@@ -774,6 +803,28 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& p, const WorkI
   auto load_tile = [&](int kv0, unsigned char* stbase) __attribute__((always_inline)) {
     const u32 kdst = lds_addr(stbase + wave * 4 * ROWB);
     const u32 vdst = kdst + KBYTES;
+    if constexpr (PAGED) {
+      // Rows lr and lr + 32 through the page table (32-bit offsets: the
+      // host keeps each pool below 4 GiB - 256 bytes).
+      const u32 row_bytes = (u32)p.k_ss * 2u;
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const int pos = kv0 + lr + 32 * r;
+        u32 koff = kNoRowDirect, voff = kNoRowDirect;
+        if (pos < p.Sk) {
+          const int pg = page_of(p, pos);
+          const int page = pages[pg - pg_first];
+          if (page >= 0) {
+            const u32 base = ((u32)page * (u32)p.bs + (u32)(pos - pg * p.bs)) * row_bytes;
+            koff = base + (u32)kchunk * 16u;
+            voff = base + (u32)vchunk * 16u;
+          }
+        }
+        dma16(krs, kdst + r * 32 * ROWB, (int)koff, 0);
+        dma16(vrs, vdst + r * 32 * ROWB, (int)voff, 0);
+      }
+      return;
+    }
     const int kso = kv0 * (int)p.k_ss * 2, vso = kv0 * (int)p.v_ss * 2;
     if (kv0 + BN <= p.Sk) {
       dma16(krs, kdst, kgo, kso);
@@ -817,6 +868,13 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& p, const WorkI
   const float c = p.c;
   const int kv_first = p.win_left >= 0 ? myq - p.win_left : -(1 << 30);
   const int kv_last = min(p.win_right >= 0 ? myq + p.win_right : (1 << 30), p.Sk - 1);
+  // Paged: validity of the tile's keys (bit r = key kv0 + r) and the ALiBi
+  // slope divided by |scale| (added to raw scores), applied as
+  // slope * (kv - kv_last): it differs from slope * (kv - q) by a per-row
+  // constant, which softmax ignores, and stays small for the keys that carry
+  // the weight.
+  uint64_t vmask = ~0ull;
+  const float alibi = (PAGED && p.slopes) ? p.slopes[wi.h] * kLog2e / p.c : 0.f;
 
   // S^T of this wave's rows against the K tile at Kb (MFMAs only; the
   // caller orders them against other work).
@@ -845,12 +903,21 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& p, const WorkI
   auto max_rescale = [&](f32x16 (&s)[NB], int kv0, bool full) __attribute__((always_inline)) {
     if (!full) {
       asm volatile("" ::: "memory");
+      const uint64_t vm = PAGED ? vmask >> (8 * g) : 0;
+      const float dq0 = PAGED ? (float)(kv0 + 8 * g - kv_last) : 0.f;
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
-          const int kv = kv0 + nb * 32 + 16 * (e >> 3) + 8 * g + (e & 7);
-          s[nb][e] = ((kv >= kv_first) & (kv <= kv_last)) ? s[nb][e] : -INFINITY;
+          const int kc = nb * 32 + 16 * (e >> 3) + (e & 7);
+          const int kv = kv0 + kc + 8 * g;
+          bool ok = (kv >= kv_first) & (kv <= kv_last);
+          float sv = s[nb][e];
+          if constexpr (PAGED) {
+            ok = ok & (((vm >> kc) & 1ull) != 0);
+            sv += alibi * (dq0 + (float)kc);
+          }
+          s[nb][e] = ok ? sv : -INFINITY;
         }
     }
     float mt = -INFINITY;
@@ -920,6 +987,14 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& p, const WorkI
     bool skip, full;
     classify_tile<BN>(p, kv0, wq0, wq0 + 31, skip, full);
     if (skip) return;
+    if constexpr (PAGED) {
+      // Lane l checks key kv0 + l (one 64-bit ballot per tile).
+      const int key = kv0 + lane;
+      bool ok = key < p.Sk;
+      if (ok) ok = pages[page_of(p, key) - pg_first] >= 0;
+      vmask = __ballot(ok);
+      if (vmask != ~0ull || alibi != 0.f) full = false;
+    }
     f32x16 s[NB];
     qk_mfma(Kb, s);
     qk_sched();
@@ -1007,11 +1082,12 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(MPX_FA_
 void fa_fwd16_kernel(FwdParams p) {
   // Stay within 128 KB of LDS per workgroup (a 136 KB configuration gave wrong
   // results on gfx950).
-  constexpr bool kDirect = MPX_FA_DIRECT && D == 128 && BN == 64 && NW == 8 && !PAGED;
-  constexpr int kDStages = MPX_FA_DSTAGES;
+  constexpr bool kDirect = MPX_FA_DIRECT && D == 128 && BN == 64 && NW == 8;
+  // Paged: three stages, which leaves room for the page-table slice.
+  constexpr int kDStages = PAGED ? 3 : MPX_FA_DSTAGES;
   constexpr int kLdsBytes =
       kDirect ? kDStages * 2 * BN * 2 * D : kFa16Stages * fa16_stage_elems<D, BN>() * 2;
-  static_assert(kLdsBytes <= 131072, "LDS budget");
+  static_assert(kLdsBytes + (PAGED ? kMaxItemPages * 4 : 0) <= 131072, "LDS budget");
   // Direct staging uses three separate stage arrays (so alias analysis can
   // tell a stage being read from the stage a DMA is writing); smem is used by
   // the register-staged path.
@@ -1029,7 +1105,8 @@ void fa_fwd16_kernel(FwdParams p) {
 #pragma nounroll
   for (int item = 0; item < n_items; ++item) {
     if constexpr (kDirect)
-      fa16_rows_direct<NW, BF16, kDStages>(p, slot_item(p, ws, item), dst0, dst1, dst2, dst3);
+      fa16_rows_direct<NW, BF16, kDStages, PAGED>(p, slot_item(p, ws, item), dst0, dst1, dst2,
+                                                 dst3, pages);
     else
       fa16_rows<D, BN, NW, BF16, PAGED>(p, slot_item(p, ws, item), smem, pages);
   }
