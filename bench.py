@@ -4,13 +4,14 @@ A step is one forward pass of the headline workload, flash_attention bf16
 BHSD B=4 H=32 S=4096 D=128 causal (the configuration the metric is quoted
 on). The same run also times paged-KV decode fp16 (64 sequences, H=32, D=128,
 context ~ U{512..8192}, 16-token pages) under "paged_decode", paged prefill of
-the headline shape over 16-token pages under "paged_prefill", and the KV append
-that writes those prompts into pages under "kv_append".
+the headline shape over 16-token pages under "paged_prefill", the KV append
+that writes those prompts into pages under "kv_append", and fused RoPE + flash
+attention at the headline shape (BSHD) under "rope_attention".
 Inputs are synthetic (seeded N(0,1)) and resident in HBM before timing.
 
 Prints ONE JSON line. Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 
-`--only flash|paged|prefill|append|copy` runs a single leg (no CPU baseline) for profiler
+`--only flash|paged|prefill|append|rope|copy` runs a single leg (no CPU baseline) for profiler
 passes; `copy` streams a 1 GiB float32 buffer through an elementwise kernel,
 the known-size reference for scaling the HBM byte counters. The HBM traffic
 per launch measured by those passes (rocprofv3 FETCH_SIZE / WRITE_SIZE) is read
@@ -235,6 +236,18 @@ def append_step(dev):
     return inp, fn, errors
 
 
+def rope_attention_step(dev):
+    """fused_rope_attention at the headline shape in BSHD, caches precomputed."""
+    from mlx_primitives.kernels import fused_rope_attention, precompute_rope_cache
+
+    cfg = wl.CONFIGS["flash_bf16_bhsd"]
+    B, S, H, D = cfg["B"], cfg["S"], cfg["H"], cfg["D"]
+    q, k, v = wl.make_qkv(dict(cfg, layout="BSHD"), device=dev)
+    cos, sin = precompute_rope_cache(S, D, dtype=q.dtype, device=dev)
+    fn = lambda: fused_rope_attention(q, k, v, cos_cache=cos, sin_cache=sin, causal=True)
+    return fn
+
+
 def run_one_leg(args) -> int:
     """One leg for a profiler pass: warmup + steps calls, timing on stderr/stdout."""
     dev = torch.device("cuda:0")
@@ -258,6 +271,9 @@ def run_one_leg(args) -> int:
     elif args.only == "append":
         _, fn, _ = append_step(dev)
         work, unit = wl.config_work("kv_append_bf16"), "bytes"
+    elif args.only == "rope":
+        fn = rope_attention_step(dev)
+        work, unit = wl.config_work("flash_bf16_bhsd"), "flop"
     else:
         from mlx_primitives.cache import paged_attention
 
@@ -281,7 +297,7 @@ def main() -> int:
     ap.add_argument("--cpu-budget", type=float, default=10.0,
                     help="seconds of CPU work per baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=["flash", "paged", "prefill", "append", "copy"],
+    ap.add_argument("--only", choices=["flash", "paged", "prefill", "append", "rope", "copy"],
                     default=None,
                     help="run one leg only (profiler passes); prints that leg's timing")
     args = ap.parse_args()
@@ -350,6 +366,14 @@ def main() -> int:
     del kdst, vdst
     log(f"[bench] {aname}: device-to-device copy of the same bytes {c_gbs:.1f} GB/s")
 
+    # ---- fused RoPE + flash, bf16 BSHD (rotation kernels + attention) ----------------
+    rstep = rope_attention_step(dev)
+    log(f"[bench] rope_attention: warmup {args.warmup}, steps {args.steps}")
+    r_wall, r_ev, r_min, r_med = time_steps(rstep, args.steps, args.warmup)
+    r_tf = flops / (r_ev * 1e-3) / 1e12
+    log(f"[bench] rope_attention: {r_wall:.3f} ms/step wall, kernels {r_ev:.3f} ms -> "
+        f"{r_tf:.1f} TFLOP/s")
+
     cpu = pcpu = fcpu = acpu = None
     if not args.no_cpu_baseline:
         log("[bench] cpu baselines (oracle restatement on host cores)")
@@ -404,6 +428,15 @@ def main() -> int:
                          "traffic": measured_traffic(fname), "kernel": PREFILL_KERNEL,
                          "traffic_unit": "bytes per launch"},
             "cpu_baseline": fcpu,
+        },
+        "rope_attention": {
+            "workload": "fused_rope_attention bf16 BSHD B=4 S=4096 H=32 D=128 causal, cos/sin "
+                        "caches precomputed (rotation of Q and K + the flash kernel)",
+            "value": r_tf, "unit": "TFLOP/s", "ms_per_step": r_wall, "kernel_ms": r_ev,
+            "kernel_ms_median": r_med, "kernel_ms_min": r_min, "flop_per_step": flops,
+            "roofline": {"bound": "mfma", "achieved": r_tf, "peak": PEAK_BF16_TFLOPS,
+                         "unit": "TFLOP/s", "frac": r_tf / PEAK_BF16_TFLOPS,
+                         "kernel": "rope_kernel x2 + fa_fwd16_kernel<128,64,8,bf16>"},
         },
         "kv_append": {
             "workload": "KV append bf16 through the C ABI: 4 sequences x 4096 new tokens, H=32, "

@@ -175,6 +175,26 @@ int mpx_kv_append(const void* k, const void* v, void* k_pool, void* v_pool,
                   int B, int T, int H, int D, int num_blocks, int block_size, int max_blocks,
                   int dtype, int32_t* errors, void* stream);
 
+/*
+ * Rotary position embedding, half-split form: for a row at position
+ * p = offset + s and i < D/2, with c = cos_cache[p, i], s_ = sin_cache[p, i],
+ *   out[i] = x[i] * c - x[i + D/2] * s_,   out[i + D/2] = x[i] * s_ + x[i + D/2] * c
+ * in float32, rounded once to dtype.
+ *
+ * Replaces rope(x, cos_cache, sin_cache, offset) (mlx_primitives/kernels/rope.py:451-497)
+ * as applied to Q and K by fast_fused_rope_attention / fused_rope_attention
+ * (mlx_primitives/kernels/fused_rope_attention.py:711-714, 939-985).
+ *
+ *   x, out      (B, S, H, D) via {batch, seq, head} element strides, D contiguous,
+ *               16-byte aligned rows; out may not alias x
+ *   cos/sin     contiguous (n_pos, D/2) tables of cache_dtype; offset + S <= n_pos
+ *
+ * D must be a multiple of 16.
+ */
+int mpx_rope(const void* x, void* out, const void* cos_cache, const void* sin_cache,
+             const int64_t* x_strides, const int64_t* out_strides, int B, int S, int H, int D,
+             int offset, int n_pos, int dtype, int cache_dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,179 @@
+// Rotary position embedding (RoPE) for gfx950, half-split ("NeoX") form.
+//
+// Restates mlx_primitives/kernels/rope.py:451-497 (rope) over the cos/sin
+// cache of rope.py:223-255 (precompute_rope_cache): for a row at position p
+// and i < D/2, with c = cos[p, i], s = sin[p, i]:
+//   out[i]       = x[i] * c - x[i + D/2] * s
+//   out[i + D/2] = x[i] * s + x[i + D/2] * c
+// computed in float32 and rounded once to the element type. This is the
+// rotation fused_rope_attention applies to Q and K before attention
+// (kernels/fused_rope_attention.py:711-714). Memory bound: one thread per 8
+// dimension pairs, 16-byte loads and stores for 16-bit types. The caches are
+// contiguous (n_pos, D/2) arrays of any of the three element types.
+#include "mpx_common.h"
+
+#include <algorithm>
+
+namespace mpx {
+
+struct RopeParams {
+  const void* x;
+  void* out;
+  const void* cos;
+  const void* sin;
+  int64_t x_sb, x_ss, x_sh;  // element strides of x (batch, seq, head)
+  int64_t o_sb, o_ss, o_sh;  // element strides of out
+  int B, S, H, D;
+  int offset;   // position of sequence index 0
+  int n_pos;    // rows of the cos / sin caches
+  int64_t rows; // B * S * H
+};
+
+template <int DT>
+struct Elem;
+template <>
+struct Elem<MPX_F32> {
+  typedef float T;
+};
+template <>
+struct Elem<MPX_F16> {
+  typedef _Float16 T;
+};
+template <>
+struct Elem<MPX_BF16> {
+  typedef __bf16 T;
+};
+
+template <typename T>
+__device__ __forceinline__ float to_f(T v) {
+  return (float)v;
+}
+template <typename T>
+__device__ __forceinline__ T from_f(float v) {
+  return (T)v;
+}
+
+// Eight consecutive elements (one 16-byte load for 16-bit types, two for f32).
+template <typename T>
+struct V8 {
+  T v[8];
+};
+
+template <typename T>
+__device__ __forceinline__ V8<T> load8(const T* p) {
+  V8<T> r;
+  if constexpr (sizeof(T) == 2) {
+    *(u32x4*)r.v = *(const u32x4*)p;
+  } else {
+    *(u32x4*)r.v = *(const u32x4*)p;
+    *(u32x4*)(r.v + 4) = *(const u32x4*)(p + 4);
+  }
+  return r;
+}
+
+template <typename T>
+__device__ __forceinline__ void store8(T* p, const V8<T>& r) {
+  if constexpr (sizeof(T) == 2) {
+    *(u32x4*)p = *(const u32x4*)r.v;
+  } else {
+    *(u32x4*)p = *(const u32x4*)r.v;
+    *(u32x4*)(p + 4) = *(const u32x4*)(r.v + 4);
+  }
+}
+
+template <int XT, int CT>
+__global__ __launch_bounds__(256) void rope_kernel(RopeParams p) {
+  typedef typename Elem<XT>::T T;
+  typedef typename Elem<CT>::T C;
+  const int half = p.D / 2, cpr = half / 8;  // 8-pair chunks per row
+  const int64_t n = p.rows * cpr;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t row = i / cpr;
+    const int d = (int)(i - row * cpr) * 8;
+    const int h = (int)(row % p.H);
+    const int64_t bs = row / p.H;
+    const int s = (int)(bs % p.S);
+    const int b = (int)(bs / p.S);
+    const T* x = (const T*)p.x + b * p.x_sb + s * p.x_ss + h * p.x_sh;
+    T* o = (T*)p.out + b * p.o_sb + s * p.o_ss + h * p.o_sh;
+    const int64_t cbase = (int64_t)(p.offset + s) * half + d;
+    const V8<T> x1 = load8(x + d), x2 = load8(x + half + d);
+    const V8<C> cs = load8((const C*)p.cos + cbase), sn = load8((const C*)p.sin + cbase);
+    V8<T> y1, y2;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float a = to_f(x1.v[e]), bb = to_f(x2.v[e]);
+      const float c = to_f(cs.v[e]), sv = to_f(sn.v[e]);
+      y1.v[e] = from_f<T>(a * c - bb * sv);
+      y2.v[e] = from_f<T>(a * sv + bb * c);
+    }
+    store8(o + d, y1);
+    store8(o + half + d, y2);
+  }
+}
+
+template <int XT>
+hipError_t launch_rope(const RopeParams& p, int cache_dtype, int blocks, hipStream_t st) {
+  switch (cache_dtype) {
+    case MPX_F32:
+      hipLaunchKernelGGL((rope_kernel<XT, MPX_F32>), dim3(blocks), dim3(256), 0, st, p);
+      break;
+    case MPX_F16:
+      hipLaunchKernelGGL((rope_kernel<XT, MPX_F16>), dim3(blocks), dim3(256), 0, st, p);
+      break;
+    default:
+      hipLaunchKernelGGL((rope_kernel<XT, MPX_BF16>), dim3(blocks), dim3(256), 0, st, p);
+      break;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace mpx
+
+using namespace mpx;
+
+extern "C" int mpx_rope(const void* x, void* out, const void* cos_cache, const void* sin_cache,
+                        const int64_t* x_strides, const int64_t* out_strides, int B, int S, int H,
+                        int D, int offset, int n_pos, int dtype, int cache_dtype, void* stream) {
+  clear_error();
+  MPX_CHECK_ARG(dtype == MPX_F32 || dtype == MPX_F16 || dtype == MPX_BF16,
+                "mpx_rope: unknown dtype code %d", dtype);
+  MPX_CHECK_ARG(cache_dtype == MPX_F32 || cache_dtype == MPX_F16 || cache_dtype == MPX_BF16,
+                "mpx_rope: unknown cache dtype code %d", cache_dtype);
+  MPX_CHECK_ARG(B >= 0 && S >= 0 && H >= 0 && n_pos >= 0, "mpx_rope: negative size");
+  MPX_CHECK_ARG(D > 0 && D % 16 == 0, "mpx_rope: head_dim must be a positive multiple of 16");
+  MPX_CHECK_ARG(offset >= 0, "mpx_rope: negative position offset");
+  if ((long)B * S * H == 0) return MPX_OK;
+  MPX_CHECK_ARG((long)offset + S <= n_pos,
+                "mpx_rope: positions %d..%d exceed the cache's %d rows", offset, offset + S - 1,
+                n_pos);
+  MPX_CHECK_ARG(x && out && cos_cache && sin_cache && x_strides && out_strides,
+                "mpx_rope: null pointer argument");
+  const int es = dtype == MPX_F32 ? 4 : 2;
+  MPX_CHECK_ARG(((uintptr_t)x & 15u) == 0 && ((uintptr_t)out & 15u) == 0 &&
+                    ((uintptr_t)cos_cache & 15u) == 0 && ((uintptr_t)sin_cache & 15u) == 0,
+                "mpx_rope: tensors must be 16-byte aligned");
+  for (int i = 0; i < 3; ++i)
+    MPX_CHECK_ARG(x_strides[i] >= 0 && (x_strides[i] * es) % 16 == 0 && out_strides[i] >= 0 &&
+                      (out_strides[i] * es) % 16 == 0,
+                  "mpx_rope: strides must be non-negative multiples of 16 bytes");
+  RopeParams p;
+  p.x = x; p.out = out; p.cos = cos_cache; p.sin = sin_cache;
+  p.x_sb = x_strides[0]; p.x_ss = x_strides[1]; p.x_sh = x_strides[2];
+  p.o_sb = out_strides[0]; p.o_ss = out_strides[1]; p.o_sh = out_strides[2];
+  p.B = B; p.S = S; p.H = H; p.D = D; p.offset = offset; p.n_pos = n_pos;
+  p.rows = (int64_t)B * S * H;
+  const int64_t n = p.rows * (D / 16);
+  const int blocks = (int)std::min<int64_t>((n + 255) / 256, 65536);
+  hipStream_t st = (hipStream_t)stream;
+  hipError_t e;
+  if (dtype == MPX_F32)
+    e = launch_rope<MPX_F32>(p, cache_dtype, blocks, st);
+  else if (dtype == MPX_F16)
+    e = launch_rope<MPX_F16>(p, cache_dtype, blocks, st);
+  else
+    e = launch_rope<MPX_BF16>(p, cache_dtype, blocks, st);
+  MPX_CHECK_HIP(e);
+  return MPX_OK;
+}

@@ -85,6 +85,12 @@ def load() -> ctypes.CDLL:
         ]
         lib.mpx_paged_prefill_workspace_bytes.restype = ctypes.c_size_t
         lib.mpx_paged_prefill_workspace_bytes.argtypes = [ctypes.c_int] * 8
+        lib.mpx_rope.restype = ctypes.c_int
+        lib.mpx_rope.argtypes = [
+            ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, _i64p, _i64p,
+            ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+            ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
+        ]
         lib.mpx_kv_append.restype = ctypes.c_int
         lib.mpx_kv_append.argtypes = [
             ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
@@ -122,6 +128,15 @@ def require_device(*tensors: torch.Tensor) -> torch.device:
         if t.device != dev:
             raise ValueError(f"all tensors must be on {dev}, got {t.device}")
     return dev
+
+
+def require_no_grad(*tensors: Optional[torch.Tensor]) -> None:
+    """The kernels are forward-only: refuse inputs that autograd would track,
+    instead of returning outputs silently cut off from the graph."""
+    if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in tensors):
+        raise NotImplementedError(
+            "mlx_primitives (MI355X build) implements the forward pass only; call it under "
+            "torch.no_grad() or torch.inference_mode(), or pass detached tensors")
 
 
 def dtype_code(dtype: torch.dtype) -> int:
@@ -214,3 +229,18 @@ def kv_append(k: torch.Tensor, v: torch.Tensor, k_pool: torch.Tensor, v_pool: to
         _strides(k_strides), _strides(v_strides), B, T, H, D, num_blocks, block_size, max_blocks,
         dtype_code(k_pool.dtype), errors.data_ptr(), _stream_ptr(dev))
     _check(rc, "mpx_kv_append failed")
+
+
+def rope(x: torch.Tensor, out: torch.Tensor, cos_cache: torch.Tensor, sin_cache: torch.Tensor,
+         offset: int) -> None:
+    """Enqueue mpx_rope on the current stream: x, out (B, S, H, D), D contiguous."""
+    lib = load()
+    dev = require_device(x, out, cos_cache, sin_cache)
+    B, S, H, D = x.shape
+    rc = lib.mpx_rope(
+        x.data_ptr(), out.data_ptr(), cos_cache.data_ptr(), sin_cache.data_ptr(),
+        _strides((x.stride(0), x.stride(1), x.stride(2))),
+        _strides((out.stride(0), out.stride(1), out.stride(2))),
+        B, S, H, D, int(offset), cos_cache.shape[0], dtype_code(x.dtype),
+        dtype_code(cos_cache.dtype), _stream_ptr(dev))
+    _check(rc, "mpx_rope failed")

@@ -44,6 +44,7 @@ def run_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, layout: Lay
                   window_right: int = -1) -> torch.Tensor:
     """Attention forward on the GPU kernel; returns a new tensor shaped like q."""
     _native.require_device(q, k, v)
+    _native.require_no_grad(q, k, v)
     if layout == Layout.BSHD:
         B, Sq, H, D = q.shape
         Sk = k.shape[1]

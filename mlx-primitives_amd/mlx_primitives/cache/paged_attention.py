@@ -85,6 +85,7 @@ def paged_attention(
             f"q/k_pool/v_pool dtype mismatch: {q.dtype}, {k_pool.dtype}, {v_pool.dtype}")
 
     _native.require_device(q, k_pool, v_pool, block_tables, context_lens)
+    _native.require_no_grad(q, k_pool, v_pool, alibi_slopes)
     if alibi_slopes is not None:
         alibi_slopes = alibi_slopes.to(device=q.device, dtype=torch.float32).contiguous()
         if alibi_slopes.numel() != heads:

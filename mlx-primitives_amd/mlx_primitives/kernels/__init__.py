@@ -1,0 +1,16 @@
+"""RoPE and fused RoPE + flash attention over the gfx950 kernels."""
+
+from mlx_primitives.kernels.fused_rope_attention import (
+    FusedRoPEFlashAttention,
+    fast_fused_rope_attention,
+    fused_rope_attention,
+)
+from mlx_primitives.kernels.rope import precompute_rope_cache, rope
+
+__all__ = [
+    "precompute_rope_cache",
+    "rope",
+    "fused_rope_attention",
+    "fast_fused_rope_attention",
+    "FusedRoPEFlashAttention",
+]

@@ -31,7 +31,7 @@ def test_header_declares_expected_entry_points():
     assert declared_functions() == sorted([
         "mpx_version", "mpx_last_error", "mpx_attn_fwd", "mpx_attn_fwd_workspace_bytes",
         "mpx_paged_decode", "mpx_paged_decode_workspace_bytes", "mpx_paged_prefill",
-        "mpx_paged_prefill_workspace_bytes", "mpx_kv_append"])
+        "mpx_paged_prefill_workspace_bytes", "mpx_kv_append", "mpx_rope"])
 
 
 def test_library_exports_every_declared_symbol(lib):
@@ -130,3 +130,17 @@ def test_kv_append_validation(lib):
     assert _append(lib, bs=0) == _native.MPX_EINVAL
     assert _append(lib, errors=None) == _native.MPX_EINVAL and b"null" in lib.mpx_last_error()
     assert _append(lib, B=0) == _native.MPX_OK and lib.mpx_last_error() == b""
+
+
+def _rope(lib, dtype=2, cdt=2, D=128, S=8, offset=0, n_pos=8, ptr=16):
+    st = (ctypes.c_int64 * 3)(S * 4 * D, 4 * D, D)
+    return lib.mpx_rope(ptr, ptr, ptr, ptr, st, st, 1, S, 4, D, offset, n_pos, dtype, cdt, None)
+
+
+def test_rope_validation(lib):
+    assert _rope(lib, dtype=4) == _native.MPX_EINVAL and b"dtype" in lib.mpx_last_error()
+    assert _rope(lib, cdt=-1) == _native.MPX_EINVAL and b"cache" in lib.mpx_last_error()
+    assert _rope(lib, D=72) == _native.MPX_EINVAL and b"multiple of 16" in lib.mpx_last_error()
+    assert _rope(lib, offset=3) == _native.MPX_EINVAL and b"exceed" in lib.mpx_last_error()
+    assert _rope(lib, ptr=24) == _native.MPX_EINVAL and b"aligned" in lib.mpx_last_error()
+    assert _rope(lib, S=0) == _native.MPX_OK and lib.mpx_last_error() == b""

@@ -152,3 +152,38 @@ def test_store_kv_validation():
         set_block_data(pool, pool, 8, x[0], x[0])
     with pytest.raises(ValueError, match="fit"):
         set_block_data(pool, pool, 0, t(4, 2, 64), t(4, 2, 64), start_pos=14)
+
+
+def test_rope_host_validation():
+    from mlx_primitives.kernels import fused_rope_attention, precompute_rope_cache, rope
+    from oracle import rope as orope
+
+    x = t(1, 4, 2, 64)
+    cos, sin = precompute_rope_cache(4, 64)
+    c64, s64 = orope.precompute_rope_cache(4, 64)
+    # same float32 formula (torch's and numpy's float32 cos/sin differ by an ulp)
+    np.testing.assert_allclose(cos.numpy(), c64, rtol=0, atol=1e-6)
+    np.testing.assert_allclose(sin.numpy(), s64, rtol=0, atol=1e-6)
+    with pytest.raises(ValueError, match="even"):
+        precompute_rope_cache(4, 7)
+    with pytest.raises(ValueError, match="exceed"):
+        rope(x, cos, sin, offset=1)
+    with pytest.raises(NotImplementedError, match="multiple of 16"):
+        rope(t(1, 4, 2, 40), *precompute_rope_cache(4, 40))
+    with pytest.raises(RuntimeError, match="ROCm device tensors only"):
+        rope(x, cos, sin)
+    with pytest.raises(ValueError, match="Q must be 4D"):
+        fused_rope_attention(x[0], x, x)
+    with pytest.raises(ValueError, match="even"):
+        fused_rope_attention(t(1, 4, 2, 63), t(1, 4, 2, 63), t(1, 4, 2, 63))
+
+
+def test_forward_only_guard():
+    from mlx_primitives import _native
+
+    x = t(1, 4, 2, 64).requires_grad_()
+    with pytest.raises(NotImplementedError, match="forward pass only"):
+        _native.require_no_grad(x)
+    with torch.no_grad():
+        _native.require_no_grad(x)
+    _native.require_no_grad(x.detach(), None)

@@ -1,4 +1,5 @@
-"""Pins of the CPU oracle (oracle/attention.py, oracle/paged.py, oracle/kv_cache.py).
+"""Pins of the CPU oracle (oracle/attention.py, oracle/paged.py, oracle/kv_cache.py,
+oracle/rope.py).
 
 Each oracle function is checked against something that does not restate it:
   * known-answer cases from the reference's own tests (cited file:line);
@@ -23,6 +24,7 @@ import torch.nn.functional as F
 from oracle import attention as oa
 from oracle import kv_cache as ok
 from oracle import paged as op
+from oracle import rope as orope
 
 
 def rnd(shape, seed, dtype=np.float64):
@@ -404,6 +406,94 @@ def test_kv_append_errors():
     assert kp[1, 2:].all() and not kp[2].any()
 
 
+# ---- RoPE (oracle/rope.py) ---------------------------------------------------------
+
+def test_rope_cache_kats():
+    # position 0: cos 1, sin 0; dim 0 rotates at 1 rad per position; the last
+    # pair at base**(-(half-1)/half)
+    cos, sin = orope.precompute_rope_cache(5, 8, base=10000.0)
+    assert cos.shape == (5, 4) and sin.shape == (5, 4)
+    np.testing.assert_allclose(cos[0], 1.0) and np.testing.assert_allclose(sin[0], 0.0)
+    np.testing.assert_allclose(cos[3, 0], math.cos(3.0), rtol=1e-6)
+    np.testing.assert_allclose(sin[2, 3], math.sin(2 * 10000.0 ** (-3 / 4)), rtol=1e-5)
+
+
+def test_rope_identity_norm_and_relative_position():
+    rng = np.random.default_rng(50)
+    D, half = 16, 8
+    cos, sin = orope.precompute_rope_cache(64, D, dtype=np.float64)
+    x = rng.standard_normal((1, 3, 2, D))
+    np.testing.assert_allclose(orope.rope(x, cos, sin, 0)[:, :1], x[:, :1], rtol=0, atol=1e-15)
+    r = orope.rope(x, cos, sin, 7)
+    n_in = x[..., :half] ** 2 + x[..., half:] ** 2
+    n_out = r[..., :half] ** 2 + r[..., half:] ** 2
+    # (the cache is float32, as the reference's: cos^2 + sin^2 = 1 to ~1e-7)
+    np.testing.assert_allclose(n_out, n_in, rtol=1e-6)
+    # rope(q, m) . rope(k, n) depends only on m - n
+    q = rng.standard_normal((1, 1, 1, D)); k = rng.standard_normal((1, 1, 1, D))
+    dots = []
+    for m, n in [(5, 2), (13, 10), (40, 37)]:
+        dots.append(float(np.sum(orope.rope(q, cos, sin, m) * orope.rope(k, cos, sin, n))))
+    np.testing.assert_allclose(dots, dots[0], rtol=1e-5, atol=1e-5)
+    assert abs(dots[0] - float(np.sum(orope.rope(q, cos, sin, 6) * orope.rope(k, cos, sin, 2)))) > 1e-2
+
+
+def _brute_rope_attention(q, k, v, scale, base, q_off, kv_off, causal):
+    B, Sq, H, D = q.shape
+    Sk = k.shape[1]
+    half = D // 2
+
+    def rot(x, pos):
+        out = np.empty(D)
+        for i in range(half):
+            ang = pos * base ** (-i / half)
+            out[i] = x[i] * math.cos(ang) - x[i + half] * math.sin(ang)
+            out[i + half] = x[i] * math.sin(ang) + x[i + half] * math.cos(ang)
+        return out
+    o = np.zeros((B, Sq, H, D))
+    for b in range(B):
+        for h in range(H):
+            ks = [rot(k[b, j, h], kv_off + j) for j in range(Sk)]
+            for i in range(Sq):
+                qi = rot(q[b, i, h], q_off + i)
+                js = [j for j in range(Sk) if not causal or kv_off + j <= q_off + i]
+                sc = [scale * float(np.dot(qi, ks[j])) for j in js]
+                m = max(sc)
+                w = [math.exp(x - m) for x in sc]
+                for wj, j in zip(w, js):
+                    o[b, i, h] += wj * v[b, j, h]
+                o[b, i, h] /= sum(w)
+    return o
+
+
+@pytest.mark.parametrize("q_off,kv_off,causal,sq,sk", [
+    (0, 0, True, 5, 5), (0, 0, False, 4, 6), (3, 0, True, 2, 5), (4, 4, True, 3, 3)])
+def test_fused_rope_attention_vs_brute(q_off, kv_off, causal, sq, sk):
+    rng = np.random.default_rng(51 + q_off + sk)
+    q = rng.standard_normal((1, sq, 2, 8)); k = rng.standard_normal((1, sk, 2, 8))
+    v = rng.standard_normal((1, sk, 2, 8))
+    out = orope.fused_rope_attention(q, k, v, scale=0.4, rope_base=100.0, q_offset=q_off,
+                                     kv_offset=kv_off, causal=causal)
+    ref = _brute_rope_attention(q, k, v, 0.4, 100.0, q_off, kv_off, causal)
+    # the oracle's angles are float32 (as the reference's cache): ~1e-6 agreement
+    np.testing.assert_allclose(out, ref, rtol=2e-5, atol=2e-6)
+
+
+def test_fused_rope_attention_vs_sdpa():
+    rng = np.random.default_rng(52)
+    q = rng.standard_normal((2, 6, 3, 16)); k = rng.standard_normal((2, 9, 3, 16))
+    v = rng.standard_normal((2, 9, 3, 16))
+    cos, sin = orope.precompute_rope_cache(20, 16, dtype=np.float64)
+    out = orope.fused_rope_attention(q, k, v, scale=0.25, cos_cache=cos, sin_cache=sin,
+                                     q_offset=5, kv_offset=2, causal=True)
+    qr = torch.from_numpy(orope.rope(q, cos, sin, 5)).transpose(1, 2)
+    kr = torch.from_numpy(orope.rope(k, cos, sin, 2)).transpose(1, 2)
+    mask = torch.tensor([[2 + j <= 5 + i for j in range(9)] for i in range(6)])
+    ref = F.scaled_dot_product_attention(qr, kr, torch.from_numpy(v).transpose(1, 2),
+                                         attn_mask=mask, scale=0.25).transpose(1, 2).numpy()
+    np.testing.assert_allclose(out, ref, rtol=1e-12, atol=1e-12)
+
+
 def test_block_table_kats():
     # tests/cache/test_paged_attention.py:311-333
     t = op.create_block_table_from_lengths(np.array([16, 32, 48]), 16)
@@ -537,3 +627,13 @@ def test_pin_catches_prefill_alibi_sign(monkeypatch):
         test_paged_prefill_vs_sdpa()
     with pytest.raises(AssertionError):
         test_paged_prefill_general_vs_brute(True, True)
+
+
+def test_pin_catches_rope_sine_sign(monkeypatch):
+    orig = orope.rope
+
+    def bad(x, cos, sin, offset=0):
+        return orig(x, cos, -sin, offset)  # rotates by -angle
+    monkeypatch.setattr(orope, "rope", bad)
+    with pytest.raises(AssertionError):
+        test_fused_rope_attention_vs_brute(3, 0, True, 2, 5)
