@@ -34,7 +34,7 @@ def test_stub_loads_and_binds():
     with pytest.raises(ValueError):
         ns["_raise"](-1)
     for fn in ("flash_attention_fwd", "paged_attention_decode", "paged_attention_prefill",
-               "store_kv"):
+               "store_kv", "rope"):
         assert callable(ns[fn]), fn
 
 
@@ -147,3 +147,20 @@ def test_stub_store_kv_matches_api(device):
     assert errors.tolist() == [0, 0, 0]
     assert torch.equal(pools[0], pools[2]) and torch.equal(pools[1], pools[3])
     assert pools[0].any()
+
+
+@pytest.mark.gpu
+def test_stub_rope_matches_api(device):
+    from mlx_primitives.kernels import precompute_rope_cache, rope
+
+    ns = stub_namespace()
+    g = torch.Generator().manual_seed(9)
+    B, S, H, D = 2, 30, 4, 64
+    x = torch.randn(B, S, H, D, generator=g).to(torch.bfloat16).to(device)
+    cos, sin = precompute_rope_cache(40, D, dtype=torch.bfloat16, device=device)
+    out = torch.empty_like(x)
+    ns["rope"](x.data_ptr(), out.data_ptr(), cos.data_ptr(), sin.data_ptr(), B, S, H, D, 5, 40,
+               ns["BF16"], ns["BF16"], stream=torch.cuda.current_stream().cuda_stream)
+    ref = rope(x, cos, sin, 5)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
