@@ -176,6 +176,39 @@ int mpx_kv_append(const void* k, const void* v, void* k_pool, void* v_pool,
                   int dtype, int32_t* errors, void* stream);
 
 /*
+ * Grouped-query variants (no counterpart in the reference, whose flash_attention
+ * rejects Hq != Hk at mlx_primitives/attention/flash.py:151-154 and whose paged
+ * pools carry the query heads; an extension behind the Python flag enable_gqa):
+ * the same entries with K/V carrying H_kv heads, H a multiple of H_kv, query head h
+ * reading K/V head h / (H / H_kv). mpx_attn_fwd, mpx_paged_decode and
+ * mpx_paged_prefill are these with H_kv = H. K/V strides (and the pools'
+ * (num_blocks, block_size, H_kv, D) layout) describe the H_kv heads; workspace
+ * sizes are those of the plain entries.
+ */
+int mpx_attn_fwd_gqa(const void* q, const void* k, const void* v, void* o,
+                     const int64_t* q_strides, const int64_t* k_strides,
+                     const int64_t* v_strides, const int64_t* o_strides,
+                     int B, int H, int H_kv, int Sq, int Sk, int D, float scale, int causal,
+                     int window_left, int window_right, int dtype,
+                     void* workspace, size_t workspace_bytes, void* stream);
+
+int mpx_paged_decode_gqa(const void* q, const void* k_pool, const void* v_pool,
+                         const int32_t* block_tables, const int32_t* context_lens,
+                         const float* alibi_slopes, void* o,
+                         const int64_t* q_strides, const int64_t* o_strides,
+                         int B, int H, int H_kv, int D, int num_blocks, int block_size,
+                         int max_blocks, float scale, int dtype, void* workspace,
+                         size_t workspace_bytes, void* stream);
+
+int mpx_paged_prefill_gqa(const void* q, const void* k_pool, const void* v_pool,
+                          const int32_t* block_tables, const int32_t* context_lens,
+                          const float* alibi_slopes, void* o,
+                          const int64_t* q_strides, const int64_t* o_strides,
+                          int B, int Sq, int H, int H_kv, int D, int num_blocks, int block_size,
+                          int max_blocks, float scale, int causal, int dtype,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Rotary position embedding, half-split form: for a row at position
  * p = offset + s and i < D/2, with c = cos_cache[p, i], s_ = sin_cache[p, i],
  *   out[i] = x[i] * c - x[i + D/2] * s_,   out[i + D/2] = x[i] * s_ + x[i + D/2] * c

@@ -41,6 +41,7 @@ struct FwdParams {
   float* ws_o;   // split partials O: (splits, B, H, Sq, D) fp32, unnormalised
   float* ws_ml;  // split partials (m, l): (splits, B, H, Sq, 2) fp32, m in log2 units
   int B, H, Sq, Sk;
+  int kv_group;  // query heads per K/V head (grouped-query attention; 1 = one each)
   int win_left, win_right;  // -1 = unbounded
   int n_qtiles, num_splits, tiles_per_split;
   int n_slots;  // q-tile slots per (batch, head)
@@ -244,12 +245,13 @@ __device__ __forceinline__ void fa16_rows(const FwdParams& pin, const WorkItem w
   // offsets (the host guarantees Sk * seq_stride * 2 < 2^31, or for pools
   // pool_bytes < 2^32), no per-load address arithmetic. Paged: the record
   // count is the pool's extent, so an offset past it loads zeros.
-  const int krec = PAGED ? (int)(p.pool_bytes - (uint32_t)(wi.h * p.k_sh * 2)) : 0x7fffffff;
-  const int vrec = PAGED ? (int)(p.pool_bytes - (uint32_t)(wi.h * p.v_sh * 2)) : 0x7fffffff;
+  const int kvh = wi.h / p.kv_group;  // K/V head of this query head
+  const int krec = PAGED ? (int)(p.pool_bytes - (uint32_t)(kvh * p.k_sh * 2)) : 0x7fffffff;
+  const int vrec = PAGED ? (int)(p.pool_bytes - (uint32_t)(kvh * p.v_sh * 2)) : 0x7fffffff;
   const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)((const uint16_t*)p.k + wi.b * p.k_sb + wi.h * p.k_sh), 0, krec, kBufferFlags);
+      (void*)((const uint16_t*)p.k + wi.b * p.k_sb + kvh * p.k_sh), 0, krec, kBufferFlags);
   const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)((const uint16_t*)p.v + wi.b * p.v_sb + wi.h * p.v_sh), 0, vrec, kBufferFlags);
+      (void*)((const uint16_t*)p.v + wi.b * p.v_sb + kvh * p.v_sh), 0, vrec, kBufferFlags);
   constexpr int kNoRow = (int)0xFFFFFFF0u;  // beyond any pool: loads zeros
 
   // Paged: this item's slice of the page table, validated, in LDS.
@@ -753,10 +755,11 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& pin, const Wor
 
   const uint16_t* __restrict__ Qp = (const uint16_t*)p.q + wi.b * p.q_sb + wi.h * p.q_sh;
   // Paged: the record count is the pool's extent past this head's offset.
-  const u32 krec = PAGED ? p.pool_bytes - (u32)(wi.h * p.k_sh * 2) : 0x7fffffffu;
-  const u32 vrec = PAGED ? p.pool_bytes - (u32)(wi.h * p.v_sh * 2) : 0x7fffffffu;
-  const u32x4 krs = buffer_desc((const uint16_t*)p.k + wi.b * p.k_sb + wi.h * p.k_sh, krec);
-  const u32x4 vrs = buffer_desc((const uint16_t*)p.v + wi.b * p.v_sb + wi.h * p.v_sh, vrec);
+  const int kvh = wi.h / p.kv_group;  // K/V head of this query head
+  const u32 krec = PAGED ? p.pool_bytes - (u32)(kvh * p.k_sh * 2) : 0x7fffffffu;
+  const u32 vrec = PAGED ? p.pool_bytes - (u32)(kvh * p.v_sh * 2) : 0x7fffffffu;
+  const u32x4 krs = buffer_desc((const uint16_t*)p.k + wi.b * p.k_sb + kvh * p.k_sh, krec);
+  const u32x4 vrs = buffer_desc((const uint16_t*)p.v + wi.b * p.v_sb + kvh * p.v_sh, vrec);
 
   // Paged: this item's slice of the page table, validated, in LDS.
   int pg_first = 0;
@@ -1145,8 +1148,9 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd32_kernel(FwdParams pin) {
   kv_range<BM, BN>(p, q0, wi.split, kv_lo, t_begin, t_end);
 
   const float* __restrict__ Qp = (const float*)p.q + wi.b * p.q_sb + wi.h * p.q_sh;
-  const float* __restrict__ Kp = (const float*)p.k + wi.b * p.k_sb + wi.h * p.k_sh;
-  const float* __restrict__ Vp = (const float*)p.v + wi.b * p.v_sb + wi.h * p.v_sh;
+  const int kvh = wi.h / p.kv_group;  // K/V head of this query head
+  const float* __restrict__ Kp = (const float*)p.k + wi.b * p.k_sb + kvh * p.k_sh;
+  const float* __restrict__ Vp = (const float*)p.v + wi.b * p.v_sb + kvh * p.v_sh;
 
   const int wq0 = q0 + wave * 32;
   const int myq = wq0 + j;
@@ -1586,16 +1590,18 @@ extern "C" size_t mpx_attn_fwd_workspace_bytes(int B, int H, int Sq, int Sk, int
   return make_plan(B, H, Sq, Sk, D, causal, window_left, window_right, dtype).ws_bytes;
 }
 
-extern "C" int mpx_attn_fwd(const void* q, const void* k, const void* v, void* o,
-                            const int64_t* q_strides, const int64_t* k_strides,
-                            const int64_t* v_strides, const int64_t* o_strides, int B, int H,
-                            int Sq, int Sk, int D, float scale, int causal, int window_left,
-                            int window_right, int dtype, void* workspace, size_t workspace_bytes,
-                            void* stream) {
+extern "C" int mpx_attn_fwd_gqa(const void* q, const void* k, const void* v, void* o,
+                                const int64_t* q_strides, const int64_t* k_strides,
+                                const int64_t* v_strides, const int64_t* o_strides, int B, int H,
+                                int H_kv, int Sq, int Sk, int D, float scale, int causal,
+                                int window_left, int window_right, int dtype, void* workspace,
+                                size_t workspace_bytes, void* stream) {
   clear_error();
   MPX_CHECK_ARG(dtype == MPX_F32 || dtype == MPX_F16 || dtype == MPX_BF16,
                 "mpx_attn_fwd: unknown dtype code %d", dtype);
   MPX_CHECK_ARG(B >= 0 && H >= 0 && Sq >= 0 && Sk >= 0, "mpx_attn_fwd: negative size");
+  MPX_CHECK_ARG(H_kv > 0 ? H % H_kv == 0 : H == 0,
+                "mpx_attn_fwd: %d query heads are not a multiple of %d K/V heads", H, H_kv);
   if (D != 32 && D != 64 && D != 128) {
     set_error("mpx_attn_fwd: head_dim %d not supported (kernels exist for 32, 64, 128)", D);
     return MPX_EUNSUPPORTED;
@@ -1637,11 +1643,23 @@ extern "C" int mpx_attn_fwd(const void* q, const void* k, const void* v, void* o
   p.v_sb = v_strides[0]; p.v_sh = v_strides[1]; p.v_ss = v_strides[2];
   p.o_sb = o_strides[0]; p.o_sh = o_strides[1]; p.o_ss = o_strides[2];
   p.B = B; p.H = H; p.Sq = Sq; p.Sk = Sk;
+  p.kv_group = H / H_kv;
   p.c = std::fabs(scale) * kLog2e;
   p.neg = scale < 0.f ? 1 : 0;
   p.eps = kSoftmaxEps;
   p.nan_empty = 0;
   return run_fwd<false>(p, pl, D, dtype, workspace, (hipStream_t)stream);
+}
+
+extern "C" int mpx_attn_fwd(const void* q, const void* k, const void* v, void* o,
+                            const int64_t* q_strides, const int64_t* k_strides,
+                            const int64_t* v_strides, const int64_t* o_strides, int B, int H,
+                            int Sq, int Sk, int D, float scale, int causal, int window_left,
+                            int window_right, int dtype, void* workspace, size_t workspace_bytes,
+                            void* stream) {
+  return mpx_attn_fwd_gqa(q, k, v, o, q_strides, k_strides, v_strides, o_strides, B, H,
+                          H > 0 ? H : 1, Sq, Sk, D, scale, causal, window_left, window_right,
+                          dtype, workspace, workspace_bytes, stream);
 }
 
 extern "C" size_t mpx_paged_prefill_workspace_bytes(int B, int Sq, int H, int D, int block_size,
@@ -1653,19 +1671,22 @@ extern "C" size_t mpx_paged_prefill_workspace_bytes(int B, int Sq, int H, int D,
       .ws_bytes;
 }
 
-extern "C" int mpx_paged_prefill(const void* q, const void* k_pool, const void* v_pool,
-                                 const int32_t* block_tables, const int32_t* context_lens,
-                                 const float* alibi_slopes, void* o, const int64_t* q_strides,
-                                 const int64_t* o_strides, int B, int Sq, int H, int D,
-                                 int num_blocks, int block_size, int max_blocks, float scale,
-                                 int causal, int dtype, void* workspace, size_t workspace_bytes,
-                                 void* stream) {
+extern "C" int mpx_paged_prefill_gqa(const void* q, const void* k_pool, const void* v_pool,
+                                     const int32_t* block_tables, const int32_t* context_lens,
+                                     const float* alibi_slopes, void* o,
+                                     const int64_t* q_strides, const int64_t* o_strides, int B,
+                                     int Sq, int H, int H_kv, int D, int num_blocks,
+                                     int block_size, int max_blocks, float scale, int causal,
+                                     int dtype, void* workspace, size_t workspace_bytes,
+                                     void* stream) {
   clear_error();
   MPX_CHECK_ARG(dtype == MPX_F32 || dtype == MPX_F16 || dtype == MPX_BF16,
                 "mpx_paged_prefill: unknown dtype code %d", dtype);
   MPX_CHECK_ARG(B >= 0 && Sq >= 0 && H >= 0 && num_blocks >= 0 && max_blocks >= 0,
                 "mpx_paged_prefill: negative size");
   MPX_CHECK_ARG(block_size > 0, "mpx_paged_prefill: block_size must be positive");
+  MPX_CHECK_ARG(H_kv > 0 ? H % H_kv == 0 : H == 0,
+                "mpx_paged_prefill: %d query heads are not a multiple of %d K/V heads", H, H_kv);
   if (D != 32 && D != 64 && D != 128) {
     set_error("mpx_paged_prefill: head_dim %d not supported (kernels exist for 32, 64, 128)", D);
     return MPX_EUNSUPPORTED;
@@ -1686,7 +1707,7 @@ extern "C" int mpx_paged_prefill(const void* q, const void* k_pool, const void* 
   const long max_tokens = (long)max_blocks * block_size;
   MPX_CHECK_ARG(max_tokens < (1L << 30), "mpx_paged_prefill: block table too large");
   const int es = dtype == MPX_F32 ? 4 : 2;
-  const uint64_t pool_bytes = (uint64_t)num_blocks * block_size * H * D * es;
+  const uint64_t pool_bytes = (uint64_t)num_blocks * block_size * H_kv * D * es;
   if (dtype != MPX_F32 && pool_bytes >= 0xFFFFFF00ull) {
     set_error("mpx_paged_prefill: 16-bit pools above 4 GiB are not supported");
     return MPX_EUNSUPPORTED;
@@ -1721,10 +1742,11 @@ extern "C" int mpx_paged_prefill(const void* q, const void* k_pool, const void* 
   FwdParams p = {};
   p.q = q; p.k = k_pool; p.v = v_pool; p.o = o;
   p.q_sb = q_strides[0]; p.q_sh = q_strides[1]; p.q_ss = q_strides[2];
-  p.k_sb = 0; p.k_sh = D; p.k_ss = (int64_t)H * D;
-  p.v_sb = 0; p.v_sh = D; p.v_ss = (int64_t)H * D;
+  p.k_sb = 0; p.k_sh = D; p.k_ss = (int64_t)H_kv * D;
+  p.v_sb = 0; p.v_sh = D; p.v_ss = (int64_t)H_kv * D;
   p.o_sb = o_strides[0]; p.o_sh = o_strides[1]; p.o_ss = o_strides[2];
   p.B = B; p.H = H; p.Sq = Sq; p.Sk = (int)max_tokens;
+  p.kv_group = H / H_kv;
   p.c = std::fabs(scale) * kLog2e;
   p.neg = scale < 0.f ? 1 : 0;
   p.eps = 0.f;
@@ -1735,4 +1757,17 @@ extern "C" int mpx_paged_prefill(const void* q, const void* k_pool, const void* 
   p.max_blocks = max_blocks; p.num_blocks = num_blocks;
   p.pool_bytes = (uint32_t)std::min<uint64_t>(pool_bytes, 0xFFFFFFFFull);
   return run_fwd<true>(p, pl, D, dtype, workspace, st);
+}
+
+extern "C" int mpx_paged_prefill(const void* q, const void* k_pool, const void* v_pool,
+                                 const int32_t* block_tables, const int32_t* context_lens,
+                                 const float* alibi_slopes, void* o, const int64_t* q_strides,
+                                 const int64_t* o_strides, int B, int Sq, int H, int D,
+                                 int num_blocks, int block_size, int max_blocks, float scale,
+                                 int causal, int dtype, void* workspace, size_t workspace_bytes,
+                                 void* stream) {
+  return mpx_paged_prefill_gqa(q, k_pool, v_pool, block_tables, context_lens, alibi_slopes, o,
+                               q_strides, o_strides, B, Sq, H, H > 0 ? H : 1, D, num_blocks,
+                               block_size, max_blocks, scale, causal, dtype, workspace,
+                               workspace_bytes, stream);
 }

@@ -38,6 +38,7 @@ struct DecodeParams {
   float* ws_o;   // (B, H, max_parts, D)
   float* ws_ml;  // (B, H, max_parts, 2), m in log2 units
   int B, H, num_blocks, bs, max_blocks, max_parts;
+  int H_kv, kv_group;  // K/V heads of the pools; query heads per K/V head
   float c;  // scale * log2(e)
 };
 
@@ -104,8 +105,9 @@ __global__ __launch_bounds__(256) void paged_decode_part_kernel(DecodeParams p) 
 
   // Lane (tl, cidx): 16-byte chunk cidx of the head row of tokens tl, tl+TPI, ...
   const int cidx = lane % LPT, tl = lane / LPT;
-  const int64_t row_elems = (int64_t)p.H * D;
-  const int64_t hoff = (int64_t)h * D + cidx * EPC;
+  // Pool token rows hold H_kv heads; query head h reads K/V head h / kv_group.
+  const int64_t row_elems = (int64_t)p.H_kv * D;
+  const int64_t hoff = (int64_t)(h / p.kv_group) * D + cidx * EPC;
   const char* kbase = (const char*)p.kpool;
   const char* vbase = (const char*)p.vpool;
 
@@ -276,17 +278,20 @@ extern "C" size_t mpx_paged_decode_workspace_bytes(int B, int H, int D, int bloc
   return (size_t)B * H * max_parts_for(block_size, max_blocks) * (D + 2) * sizeof(float);
 }
 
-extern "C" int mpx_paged_decode(const void* q, const void* k_pool, const void* v_pool,
-                                const int32_t* block_tables, const int32_t* context_lens,
-                                const float* alibi_slopes, void* o, const int64_t* q_strides,
-                                const int64_t* o_strides, int B, int H, int D, int num_blocks,
-                                int block_size, int max_blocks, float scale, int dtype,
-                                void* workspace, size_t workspace_bytes, void* stream) {
+extern "C" int mpx_paged_decode_gqa(const void* q, const void* k_pool, const void* v_pool,
+                                    const int32_t* block_tables, const int32_t* context_lens,
+                                    const float* alibi_slopes, void* o,
+                                    const int64_t* q_strides, const int64_t* o_strides, int B,
+                                    int H, int H_kv, int D, int num_blocks, int block_size,
+                                    int max_blocks, float scale, int dtype, void* workspace,
+                                    size_t workspace_bytes, void* stream) {
   clear_error();
   MPX_CHECK_ARG(dtype == MPX_F32 || dtype == MPX_F16 || dtype == MPX_BF16,
                 "mpx_paged_decode: unknown dtype code %d", dtype);
   MPX_CHECK_ARG(B >= 0 && H >= 0 && num_blocks >= 0 && max_blocks >= 0,
                 "mpx_paged_decode: negative size");
+  MPX_CHECK_ARG(H_kv > 0 ? H % H_kv == 0 : H == 0,
+                "mpx_paged_decode: %d query heads are not a multiple of %d K/V heads", H, H_kv);
   MPX_CHECK_ARG(block_size > 0, "mpx_paged_decode: block_size must be positive");
   if (D != 32 && D != 64 && D != 128) {
     set_error("mpx_paged_decode: head_dim %d not supported (kernels exist for 32, 64, 128)", D);
@@ -312,6 +317,7 @@ extern "C" int mpx_paged_decode(const void* q, const void* k_pool, const void* v
   p.slopes = alibi_slopes; p.o = o;
   p.q_sb = q_strides[0]; p.q_sh = q_strides[1]; p.o_sb = o_strides[0]; p.o_sh = o_strides[1];
   p.B = B; p.H = H; p.num_blocks = num_blocks; p.bs = block_size; p.max_blocks = max_blocks;
+  p.H_kv = H_kv; p.kv_group = H / H_kv;
   p.max_parts = std::max(1, max_parts_for(block_size, max_blocks));
   p.c = scale * kLog2e;
   const size_t need = (size_t)B * H * p.max_parts * (D + 2) * sizeof(float);
@@ -336,4 +342,16 @@ extern "C" int mpx_paged_decode(const void* q, const void* k_pool, const void* v
     e = dispatch_decode_d<MPX_F16>(p, D, st);
   MPX_CHECK_HIP(e);
   return MPX_OK;
+}
+
+extern "C" int mpx_paged_decode(const void* q, const void* k_pool, const void* v_pool,
+                                const int32_t* block_tables, const int32_t* context_lens,
+                                const float* alibi_slopes, void* o, const int64_t* q_strides,
+                                const int64_t* o_strides, int B, int H, int D, int num_blocks,
+                                int block_size, int max_blocks, float scale, int dtype,
+                                void* workspace, size_t workspace_bytes, void* stream) {
+  return mpx_paged_decode_gqa(q, k_pool, v_pool, block_tables, context_lens, alibi_slopes, o,
+                              q_strides, o_strides, B, H, H > 0 ? H : 1, D, num_blocks,
+                              block_size, max_blocks, scale, dtype, workspace, workspace_bytes,
+                              stream);
 }

@@ -64,6 +64,14 @@ def load() -> ctypes.CDLL:
             ctypes.c_float, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
             ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
         ]
+        lib.mpx_attn_fwd_gqa.restype = ctypes.c_int
+        lib.mpx_attn_fwd_gqa.argtypes = [
+            ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+            _i64p, _i64p, _i64p, _i64p,
+            ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+            ctypes.c_float, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+            ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
+        ]
         lib.mpx_attn_fwd_workspace_bytes.restype = ctypes.c_size_t
         lib.mpx_attn_fwd_workspace_bytes.argtypes = [ctypes.c_int] * 9
         lib.mpx_paged_decode.restype = ctypes.c_int
@@ -73,6 +81,14 @@ def load() -> ctypes.CDLL:
             ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
             ctypes.c_float, ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
         ]
+        lib.mpx_paged_decode_gqa.restype = ctypes.c_int
+        lib.mpx_paged_decode_gqa.argtypes = [
+            ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+            ctypes.c_void_p, ctypes.c_void_p, _i64p, _i64p,
+            ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+            ctypes.c_int, ctypes.c_float, ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t,
+            ctypes.c_void_p,
+        ]
         lib.mpx_paged_decode_workspace_bytes.restype = ctypes.c_size_t
         lib.mpx_paged_decode_workspace_bytes.argtypes = [ctypes.c_int] * 5
         lib.mpx_paged_prefill.restype = ctypes.c_int
@@ -81,6 +97,14 @@ def load() -> ctypes.CDLL:
             ctypes.c_void_p, ctypes.c_void_p, _i64p, _i64p,
             ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
             ctypes.c_int, ctypes.c_float, ctypes.c_int, ctypes.c_int,
+            ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
+        ]
+        lib.mpx_paged_prefill_gqa.restype = ctypes.c_int
+        lib.mpx_paged_prefill_gqa.argtypes = [
+            ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+            ctypes.c_void_p, ctypes.c_void_p, _i64p, _i64p,
+            ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+            ctypes.c_int, ctypes.c_int, ctypes.c_float, ctypes.c_int, ctypes.c_int,
             ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
         ]
         lib.mpx_paged_prefill_workspace_bytes.restype = ctypes.c_size_t
@@ -159,18 +183,21 @@ def attn_fwd_workspace_bytes(B: int, H: int, Sq: int, Sk: int, D: int, causal: b
 def attn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor,
              q_strides: Sequence[int], k_strides: Sequence[int], v_strides: Sequence[int],
              o_strides: Sequence[int], B: int, H: int, Sq: int, Sk: int, D: int,
-             scale: float, causal: bool, window_left: int = -1, window_right: int = -1) -> None:
-    """Enqueue mpx_attn_fwd on the current stream (strides in (b, h, s) order)."""
+             scale: float, causal: bool, window_left: int = -1, window_right: int = -1,
+             H_kv: Optional[int] = None) -> None:
+    """Enqueue mpx_attn_fwd_gqa on the current stream (strides in (b, h, s) order;
+    K/V carry H_kv heads, default H)."""
     lib = load()
     dev = require_device(q, k, v, o)
     code = dtype_code(q.dtype)
     ws_bytes = int(lib.mpx_attn_fwd_workspace_bytes(
         B, H, Sq, Sk, D, int(causal), window_left, window_right, code))
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
-    rc = lib.mpx_attn_fwd(
+    rc = lib.mpx_attn_fwd_gqa(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
         _strides(q_strides), _strides(k_strides), _strides(v_strides), _strides(o_strides),
-        B, H, Sq, Sk, D, float(scale), int(causal), int(window_left), int(window_right), code,
+        B, H, H if H_kv is None else H_kv, Sq, Sk, D, float(scale), int(causal),
+        int(window_left), int(window_right), code,
         ws.data_ptr() if ws is not None else None, ws_bytes, _stream_ptr(dev))
     _check(rc, "mpx_attn_fwd failed")
 
@@ -179,18 +206,20 @@ def paged_decode(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
                  block_tables: torch.Tensor, context_lens: torch.Tensor,
                  alibi_slopes: Optional[torch.Tensor], o: torch.Tensor,
                  q_strides: Sequence[int], o_strides: Sequence[int], B: int, H: int, D: int,
-                 num_blocks: int, block_size: int, max_blocks: int, scale: float) -> None:
-    """Enqueue mpx_paged_decode on the current stream."""
+                 num_blocks: int, block_size: int, max_blocks: int, scale: float,
+                 H_kv: Optional[int] = None) -> None:
+    """Enqueue mpx_paged_decode_gqa on the current stream (pools carry H_kv heads)."""
     lib = load()
     dev = require_device(q, k_pool, v_pool, block_tables, context_lens, o)
     code = dtype_code(q.dtype)
     ws_bytes = int(lib.mpx_paged_decode_workspace_bytes(B, H, D, block_size, max_blocks))
     ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=dev)
-    rc = lib.mpx_paged_decode(
+    rc = lib.mpx_paged_decode_gqa(
         q.data_ptr(), k_pool.data_ptr(), v_pool.data_ptr(), block_tables.data_ptr(),
         context_lens.data_ptr(), alibi_slopes.data_ptr() if alibi_slopes is not None else None,
-        o.data_ptr(), _strides(q_strides), _strides(o_strides), B, H, D, num_blocks,
-        block_size, max_blocks, float(scale), code, ws.data_ptr(), ws.numel(), _stream_ptr(dev))
+        o.data_ptr(), _strides(q_strides), _strides(o_strides), B, H,
+        H if H_kv is None else H_kv, D, num_blocks, block_size, max_blocks, float(scale), code,
+        ws.data_ptr(), ws.numel(), _stream_ptr(dev))
     _check(rc, "mpx_paged_decode failed")
 
 
@@ -199,19 +228,21 @@ def paged_prefill(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
                   alibi_slopes: Optional[torch.Tensor], o: torch.Tensor,
                   q_strides: Sequence[int], o_strides: Sequence[int], B: int, Sq: int, H: int,
                   D: int, num_blocks: int, block_size: int, max_blocks: int, scale: float,
-                  causal: bool) -> None:
-    """Enqueue mpx_paged_prefill on the current stream (strides in (b, h, s) order)."""
+                  causal: bool, H_kv: Optional[int] = None) -> None:
+    """Enqueue mpx_paged_prefill_gqa on the current stream (strides in (b, h, s)
+    order; pools carry H_kv heads)."""
     lib = load()
     dev = require_device(q, k_pool, v_pool, block_tables, context_lens, o)
     code = dtype_code(q.dtype)
     ws_bytes = int(lib.mpx_paged_prefill_workspace_bytes(B, Sq, H, D, block_size, max_blocks,
                                                           int(causal), code))
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
-    rc = lib.mpx_paged_prefill(
+    rc = lib.mpx_paged_prefill_gqa(
         q.data_ptr(), k_pool.data_ptr(), v_pool.data_ptr(), block_tables.data_ptr(),
         context_lens.data_ptr(), alibi_slopes.data_ptr() if alibi_slopes is not None else None,
-        o.data_ptr(), _strides(q_strides), _strides(o_strides), B, Sq, H, D, num_blocks,
-        block_size, max_blocks, float(scale), int(causal), code,
+        o.data_ptr(), _strides(q_strides), _strides(o_strides), B, Sq, H,
+        H if H_kv is None else H_kv, D, num_blocks, block_size, max_blocks, float(scale),
+        int(causal), code,
         ws.data_ptr() if ws is not None else None, ws_bytes, _stream_ptr(dev))
     _check(rc, "mpx_paged_prefill failed")
 

@@ -47,10 +47,10 @@ def run_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, layout: Lay
     _native.require_no_grad(q, k, v)
     if layout == Layout.BSHD:
         B, Sq, H, D = q.shape
-        Sk = k.shape[1]
+        Sk, H_kv = k.shape[1], k.shape[2]
     else:
         B, H, Sq, D = q.shape
-        Sk = k.shape[2]
+        Sk, H_kv = k.shape[2], k.shape[1]
     if q.numel() == 0:
         return torch.empty(q.shape, dtype=q.dtype, device=q.device)
     dk = kernel_head_dim(D)
@@ -60,7 +60,7 @@ def run_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, layout: Lay
     o = torch.empty(out_shape, dtype=q.dtype, device=q.device)
     _native.attn_fwd(qk, kk, vk, o, _bhs(qk, layout), _bhs(kk, layout), _bhs(vk, layout),
                      _bhs(o, layout), B, H, Sq, Sk, dk, scale, causal, window_left,
-                     window_right)
+                     window_right, H_kv=H_kv)
     if dk != D:
         o = o[..., :D].contiguous()
     return o

@@ -23,7 +23,8 @@ from mlx_primitives.attention._launch import run_attention
 from mlx_primitives.constants import Layout
 
 
-def _validate(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, layout) -> Layout:
+def _validate(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, layout,
+              enable_gqa: bool = False) -> Layout:
     # Mirrors mlx_primitives/attention/flash.py:123-169 (messages included).
     if q.ndim != 4:
         raise ValueError(f"Expected 4D tensors, got {q.ndim}D")
@@ -45,7 +46,12 @@ def _validate(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, layout) -> Layo
         vb, vh, vs, vd = v.shape
     if qb != kb or qb != vb:
         raise ValueError(f"Batch size mismatch: Q={qb}, K={kb}, V={vb}")
-    if qh != kh or qh != vh:
+    if enable_gqa:
+        if kh != vh or kh == 0 or qh % kh != 0:
+            raise ValueError(
+                f"enable_gqa needs K and V with equal head counts dividing Q's: Q={qh}, "
+                f"K={kh}, V={vh}")
+    elif qh != kh or qh != vh:
         raise ValueError(f"Number of heads mismatch: Q={qh}, K={kh}, V={vh}")
     if qd != kd:
         raise ValueError(f"Head dimension mismatch between Q and K: Q={qd}, K={kd}")
@@ -74,6 +80,8 @@ def flash_attention(
     dropout_p: float = 0.0,
     training: bool = True,
     layout: Union[str, Layout] = Layout.BSHD,
+    *,
+    enable_gqa: bool = False,
 ) -> torch.Tensor:
     """Exact attention, softmax(q k^T * scale [+ causal mask]) v, tiled on MFMA.
 
@@ -89,11 +97,14 @@ def flash_attention(
         dropout_p > 0 and training, BSHD; BHSD ignores dropout like the
         reference's BHSD branch).
       layout: "BSHD" / "BHSD" or Layout.
+      enable_gqa: keyword-only extension (the reference requires equal head
+        counts, flash.py:151-154): K and V may carry H_kv heads, H a multiple
+        of H_kv; query head h attends with K/V head h // (H // H_kv).
 
     Returns a new tensor shaped like q, in q's dtype. Rows are normalised as
     o / (l + 1e-6), the reference tiled path's normaliser.
     """
-    layout = _validate(q, k, v, layout)
+    layout = _validate(q, k, v, layout, enable_gqa)
     head_dim = q.shape[-1]
     if scale is None:
         scale = 1.0 / math.sqrt(head_dim)

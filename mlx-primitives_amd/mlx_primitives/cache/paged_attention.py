@@ -43,6 +43,8 @@ def paged_attention(
     block_size: int = 16,
     causal: bool = True,
     alibi_slopes: Optional[torch.Tensor] = None,
+    *,
+    enable_gqa: bool = False,
 ) -> torch.Tensor:
     """Attention of q against a paged KV cache.
 
@@ -59,6 +61,9 @@ def paged_attention(
     block table. Returns (batch, seq_q, heads, dim) in q's dtype. A query row
     with no valid cached token yields NaN (the reference's softmax over an all
     -inf row).
+
+    enable_gqa (keyword-only extension): the pools may carry H_kv heads, heads
+    a multiple of H_kv; query head h reads K/V head h // (heads // H_kv).
     """
     if q.ndim != 4:
         raise ValueError(f"Expected q of shape (batch, seq_q, heads, dim), got {q.ndim}D")
@@ -73,9 +78,12 @@ def paged_attention(
         raise ValueError(
             f"block_size={block_size} does not match the pool's block dimension "
             f"{k_pool.shape[1]}")
-    if k_pool.shape[2] != heads or k_pool.shape[3] != dim:
+    h_kv = k_pool.shape[2]
+    heads_ok = (h_kv > 0 and heads % h_kv == 0) if enable_gqa else h_kv == heads
+    if not heads_ok or k_pool.shape[3] != dim:
         raise ValueError(
-            f"pool heads/dim {tuple(k_pool.shape[2:])} do not match q ({heads}, {dim})")
+            f"pool heads/dim {tuple(k_pool.shape[2:])} do not match q ({heads}, {dim})"
+            + (" (enable_gqa: pool heads must divide q heads)" if enable_gqa else ""))
     if block_tables.ndim != 2 or block_tables.shape[0] != batch:
         raise ValueError(f"block_tables must be (batch, max_blocks), got {tuple(block_tables.shape)}")
     if context_lens.ndim != 1 or context_lens.shape[0] != batch:
@@ -109,14 +117,14 @@ def paged_attention(
         _native.paged_decode(
             q, k_pool, v_pool, tables, lens, alibi_slopes, out,
             (q.stride(0), q.stride(2)), (out.stride(0), out.stride(2)),
-            batch, heads, dk, k_pool.shape[0], block_size, tables.shape[1], scale)
+            batch, heads, dk, k_pool.shape[0], block_size, tables.shape[1], scale, H_kv=h_kv)
     else:
         _native.paged_prefill(
             q, k_pool, v_pool, tables, lens, alibi_slopes, out,
             (q.stride(0), q.stride(2), q.stride(1)),
             (out.stride(0), out.stride(2), out.stride(1)),
             batch, seq_q, heads, dk, k_pool.shape[0], block_size, tables.shape[1], scale,
-            causal)
+            causal, H_kv=h_kv)
     if dk != dim:
         out = out[..., :dim].contiguous()
     return out

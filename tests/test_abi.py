@@ -31,7 +31,8 @@ def test_header_declares_expected_entry_points():
     assert declared_functions() == sorted([
         "mpx_version", "mpx_last_error", "mpx_attn_fwd", "mpx_attn_fwd_workspace_bytes",
         "mpx_paged_decode", "mpx_paged_decode_workspace_bytes", "mpx_paged_prefill",
-        "mpx_paged_prefill_workspace_bytes", "mpx_kv_append", "mpx_rope"])
+        "mpx_paged_prefill_workspace_bytes", "mpx_kv_append", "mpx_rope", "mpx_attn_fwd_gqa",
+        "mpx_paged_decode_gqa", "mpx_paged_prefill_gqa"])
 
 
 def test_library_exports_every_declared_symbol(lib):
@@ -144,3 +145,18 @@ def test_rope_validation(lib):
     assert _rope(lib, offset=3) == _native.MPX_EINVAL and b"exceed" in lib.mpx_last_error()
     assert _rope(lib, ptr=24) == _native.MPX_EINVAL and b"aligned" in lib.mpx_last_error()
     assert _rope(lib, S=0) == _native.MPX_OK and lib.mpx_last_error() == b""
+
+
+def test_gqa_head_counts_validated(lib):
+    st = (ctypes.c_int64 * 3)(8 * 64, 8 * 64, 64)
+    rc = lib.mpx_attn_fwd_gqa(16, 16, 16, 16, st, st, st, st, 1, 6, 4, 8, 8, 64, 0.1, 1, -1, -1,
+                              2, None, 0, None)
+    assert rc == _native.MPX_EINVAL and b"multiple" in lib.mpx_last_error()
+    st2 = (ctypes.c_int64 * 2)(4096, 128)
+    rc = lib.mpx_paged_decode_gqa(16, 16, 16, 16, 16, None, 16, st2, st2, 1, 32, 5, 128, 4, 16,
+                                  1, 0.1, 1, 16, 1 << 20, None)
+    assert rc == _native.MPX_EINVAL and b"multiple" in lib.mpx_last_error()
+    st3 = (ctypes.c_int64 * 3)(64 * 32 * 128, 128, 32 * 128)
+    rc = lib.mpx_paged_prefill_gqa(16, 16, 16, 16, 16, None, 16, st3, st3, 1, 64, 32, 0, 128, 64,
+                                   16, 8, 0.1, 1, 1, None, 0, None)
+    assert rc == _native.MPX_EINVAL and b"multiple" in lib.mpx_last_error()

@@ -187,3 +187,21 @@ def test_forward_only_guard():
     with torch.no_grad():
         _native.require_no_grad(x)
     _native.require_no_grad(x.detach(), None)
+
+
+def test_gqa_flag_validation():
+    q, k = t(1, 8, 6, 64), t(1, 8, 2, 64)
+    with pytest.raises(ValueError, match="Number of heads mismatch"):
+        flash_attention(q, k, k)
+    with pytest.raises(ValueError, match="enable_gqa"):
+        flash_attention(q, t(1, 8, 4, 64), t(1, 8, 4, 64), enable_gqa=True)
+    with pytest.raises(RuntimeError, match="ROCm device tensors only"):
+        flash_attention(q, k, k, enable_gqa=True)  # validation passes, no CPU path
+    qd = t(2, 1, 8, 64); pool = t(4, 16, 2, 64)
+    tables = torch.zeros(2, 1, dtype=torch.int32); lens = torch.ones(2, dtype=torch.int32)
+    with pytest.raises(ValueError, match="pool heads"):
+        paged_attention(qd, pool, pool, tables, lens)
+    with pytest.raises(ValueError, match="divide"):
+        paged_attention(qd, t(4, 16, 3, 64), t(4, 16, 3, 64), tables, lens, enable_gqa=True)
+    with pytest.raises(RuntimeError, match="ROCm device tensors only"):
+        paged_attention(qd, pool, pool, tables, lens, enable_gqa=True)
