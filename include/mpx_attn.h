@@ -228,6 +228,47 @@ int mpx_rope(const void* x, void* out, const void* cos_cache, const void* sin_ca
              const int64_t* x_strides, const int64_t* out_strides, int B, int S, int H, int D,
              int offset, int n_pos, int dtype, int cache_dtype, void* stream);
 
+/*
+ * Backward pass of the flash attention forward.
+ *
+ * The reference differentiates flash_attention (and sliding_window_attention,
+ * chunked_cross_attention) with mx.grad through its tiled online-softmax path
+ * (mlx_primitives/attention/flash.py:257-316; tests/attention/test_flash.py:338-362,
+ * tests/parity/pytorch/test_attention_parity.py:107-163). Here the forward
+ * saves each row's log-sum-exp and the backward recomputes the probabilities.
+ *
+ * mpx_attn_fwd_lse is mpx_attn_fwd_gqa plus lse: a (B, H, Sq) contiguous
+ * float32 array that receives m + log2(l + 1e-6) per query row (base-2 units
+ * of the scaled scores, m the row max of scale * log2(e) * q.k), +inf for rows
+ * that see no key; lse may be NULL.
+ *
+ * mpx_attn_bwd: given q, k, v, the forward output o, its lse, and dout
+ * (= dL/do), writes dq, dk, dv (dk, dv carry H_kv heads; a K/V head's gradient
+ * sums over its group of query heads). All tensors use {batch, head, seq}
+ * element strides like mpx_attn_fwd, D contiguous; dq, dk, dv must not
+ * overlap the inputs. Masks (causal, windows) are those of the forward call.
+ * Scope: dtype float16 / bfloat16 (float32: MPX_EUNSUPPORTED), D in {64, 128},
+ * scale > 0. Workspace: mpx_attn_bwd_workspace_bytes(B, H, Sq) bytes, 16-byte
+ * aligned (per-row rowsum(dout * o)).
+ */
+int mpx_attn_fwd_lse(const void* q, const void* k, const void* v, void* o, float* lse,
+                     const int64_t* q_strides, const int64_t* k_strides,
+                     const int64_t* v_strides, const int64_t* o_strides,
+                     int B, int H, int H_kv, int Sq, int Sk, int D, float scale, int causal,
+                     int window_left, int window_right, int dtype,
+                     void* workspace, size_t workspace_bytes, void* stream);
+
+size_t mpx_attn_bwd_workspace_bytes(int B, int H, int Sq);
+
+int mpx_attn_bwd(const void* q, const void* k, const void* v, const void* o, const void* dout,
+                 const float* lse, void* dq, void* dk, void* dv,
+                 const int64_t* q_strides, const int64_t* k_strides, const int64_t* v_strides,
+                 const int64_t* o_strides, const int64_t* do_strides, const int64_t* dq_strides,
+                 const int64_t* dk_strides, const int64_t* dv_strides,
+                 int B, int H, int H_kv, int Sq, int Sk, int D, float scale, int causal,
+                 int window_left, int window_right, int dtype,
+                 void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

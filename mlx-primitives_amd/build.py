@@ -23,7 +23,7 @@ INCLUDE = os.path.join(REPO, "include")
 LIB_DIR = os.path.join(HERE, "mlx_primitives", "_lib")
 LIB_PATH = os.path.join(LIB_DIR, "libmpx_attn.so")
 
-SOURCES = ["abi.hip", "fa_fwd.hip", "paged_decode.hip", "kv_cache.hip", "rope.hip"]
+SOURCES = ["abi.hip", "fa_fwd.hip", "fa_bwd.hip", "paged_decode.hip", "kv_cache.hip", "rope.hip"]
 ARCH = "gfx950"
 
 

@@ -1,0 +1,559 @@
+// Attention backward for gfx950 (MI355X), bf16 / f16, head_dim 64 or 128.
+//
+// Gradients of O = softmax(scale * Q K^T + mask) V (with the forward's
+// O / (l + eps) normaliser) for mlx_primitives' flash_attention
+// (attention/flash.py:52-254; the reference differentiates its tiled path with
+// mx.grad, tests/attention/test_flash.py:338-362). With the forward's row
+// log-sum-exp lse (log2 units), P = exp2(s * c - lse), c = scale * log2(e):
+//   Dvec_i = sum_d dO[i, d] * O[i, d]                 (fa_bwd_dvec_kernel)
+//   dP = dO V^T,  dS = P * (dP - Dvec_i)
+//   dQ = scale * dS K                                 (fa_bwd_dq_kernel)
+//   dV = P^T dO,  dK = scale * dS^T Q                 (fa_bwd_dkdv_kernel)
+// Two MFMA kernels, no atomics: dQ is query-parallel (each workgroup owns 128
+// query rows and streams K and V), dK/dV key-parallel (each workgroup owns 128
+// keys and streams Q and dO). Both recompute S and dP; tiles of 64 rows stream
+// through LDS, double buffered, loaded one tile ahead into registers.
+//
+// MFMA 32x32x16 layouts (lane = j + 32*g, j in [0,32)): A (32 x 16) lane holds
+// row j, k-group g (8 values); B (16 x 32) column j, k-group g; C (32 x 32)
+// element e of lane holds row 8*(e/4) + 4*g + e%4, column j. Streamed row
+// operands are read with rows permuted (bits 2 and 3 of the row index
+// exchanged) so that C elements 8h..8h+7 of a lane are 8 consecutive rows:
+// packed, they are directly the B operand of the next product over those rows.
+// Transposed operands come from the row-major tiles through ds_read_b64_tr_b16.
+#include "mpx_common.h"
+
+#include <algorithm>
+#include <cmath>
+
+namespace mpx {
+
+struct BwdParams {
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* o;
+  const void* dout;
+  const float* lse;   // (B, H, Sq) log2 units, +inf for rows without keys
+  float* dvec;        // (B, H, Sq) workspace
+  void* dq;
+  void* dk;
+  void* dv;
+  int64_t q_sb, q_sh, q_ss, k_sb, k_sh, k_ss, v_sb, v_sh, v_ss, o_sb, o_sh, o_ss;
+  int64_t do_sb, do_sh, do_ss, dq_sb, dq_sh, dq_ss, dk_sb, dk_sh, dk_ss, dv_sb, dv_sh, dv_ss;
+  int B, H, H_kv, kv_group, Sq, Sk;  // K/V (and dK/dV) carry H_kv = H / kv_group heads
+  int win_left, win_right;  // -1 = unbounded (causal: win_right = 0)
+  float scale, c;           // c = scale * log2(e)
+};
+
+constexpr int kBwdWaves = 4;    // waves per workgroup (one per SIMD)
+constexpr int kBwdOwn = 32 * kBwdWaves;  // rows (or keys) a workgroup owns
+constexpr int kBwdTile = 64;    // streamed rows per step
+
+__device__ __forceinline__ u32x2 tr_read16(const uint16_t* lds) {
+  typedef __attribute__((ext_vector_type(4))) short s16x4;
+  const s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s16x4*)(lds));
+  return __builtin_bit_cast(u32x2, r);
+}
+
+// LDS tiles are (64, D) row-major without padding; the 16-byte chunk c of row
+// r sits at slot c ^ swz(r). Each tile is read two ways, and the swizzle keeps
+// both conflict-free: 16 lanes reading one chunk of 16 consecutive rows (row
+// operands) hit 16 distinct bank groups, and 32 lanes of a transposing read (4
+// consecutive rows x 4 consecutive chunks) hit all 64 banks once.
+template <int D>
+__device__ __forceinline__ int swz(int r) {
+  if constexpr (D == 128) {
+    return ((r & 3) << 2) | ((r >> 2) & 3);
+  } else {
+    return (((r >> 1) & 1) << 2) | ((r >> 2) & 3);
+  }
+}
+
+// Rows of a 16-bit (rows, D) tensor slice through 256 threads: global ->
+// registers (rows past `rows` re-read the last one) -> swizzled LDS tile.
+template <int D>
+struct TileStage {
+  static constexpr int CPR = D / 8;                   // 16-byte chunks per row
+  static constexpr int PER_T = kBwdTile * CPR / 256;  // chunks per thread
+  u32x4 r[PER_T];
+  __device__ __forceinline__ void load(const uint16_t* base, int64_t row_stride, int row0,
+                                       int rows) {
+#pragma unroll
+    for (int i = 0; i < PER_T; ++i) {
+      const int c = threadIdx.x + 256 * i;
+      const int row = min(row0 + c / CPR, rows - 1);
+      r[i] = *(const u32x4*)(base + (int64_t)row * row_stride + (c % CPR) * 8);
+    }
+  }
+  __device__ __forceinline__ void store(uint16_t* lds) const {
+#pragma unroll
+    for (int i = 0; i < PER_T; ++i) {
+      const int c = threadIdx.x + 256 * i;
+      const int row = c / CPR;
+      *(u32x4*)(lds + row * D + 8 * ((c % CPR) ^ swz<D>(row))) = r[i];
+    }
+  }
+};
+
+// Dvec = rowsum(dO * O) in float32: D / 8 lanes per row, 8 elements each.
+template <int D, bool BF16>
+__global__ __launch_bounds__(256) void fa_bwd_dvec_kernel(BwdParams p) {
+  constexpr int LPR = D / 8;  // lanes per row
+  const int64_t rows = (int64_t)p.B * p.H * p.Sq;
+  const int64_t row = ((int64_t)blockIdx.x * 256 + threadIdx.x) / LPR;
+  const int l = threadIdx.x % LPR;
+  float acc = 0.f;
+  if (row < rows) {
+    const int i = (int)(row % p.Sq);
+    const int64_t bh = row / p.Sq;
+    const int b = (int)(bh / p.H), h = (int)(bh % p.H);
+    const uint16_t* o = (const uint16_t*)p.o + b * p.o_sb + h * p.o_sh + (int64_t)i * p.o_ss;
+    const uint16_t* d = (const uint16_t*)p.dout + b * p.do_sb + h * p.do_sh + (int64_t)i * p.do_ss;
+    const u32x4 ov = *(const u32x4*)(o + 8 * l);
+    const u32x4 dv = *(const u32x4*)(d + 8 * l);
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      acc += h2f<BF16>((uint16_t)(ov[w] & 0xffffu)) * h2f<BF16>((uint16_t)(dv[w] & 0xffffu));
+      acc += h2f<BF16>((uint16_t)(ov[w] >> 16)) * h2f<BF16>((uint16_t)(dv[w] >> 16));
+    }
+  }
+#pragma unroll
+  for (int off = LPR / 2; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 64);
+  if (row < rows && l == 0) p.dvec[row] = acc;
+}
+
+// Per-lane LDS element offsets into a swizzled (64, D) tile. row[ks]: A
+// operand rows 32*nb + perm(j), k-step ks (add nb * 32 * D). tr[db][hf]: the
+// transposing read for A = X^T over rows 16*sl + 8g + 4hf + s/4, columns
+// 32*db + 16*((lane/16) % 2) + 4*(s % 4), s = lane % 16 (add 16 * sl * D); for a
+// group of 16 lanes it returns to lane s column 32*db + 16*((lane/16) % 2) + s
+// of the 4 rows, i.e. row j = dim of the A operand, k-group g = 8 rows.
+template <int D>
+struct Addr {
+  static constexpr int NKS = D / 16, NDB = D / 32;
+  int row[NKS];
+  int tr[NDB][2];
+  __device__ __forceinline__ void init(int lane) {
+    const int j = lane & 31, g = lane >> 5;
+    const int perm = (j & ~12) | ((j & 4) << 1) | ((j & 8) >> 1);
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) row[ks] = perm * D + 8 * ((2 * ks + g) ^ swz<D>(perm));
+    const int s = lane & 15, half = (lane >> 4) & 1;
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      const int r = 8 * g + 4 * hf + (s >> 2);
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+        tr[db][hf] = r * D + 8 * ((4 * db + 2 * half + ((s & 3) >> 1)) ^ swz<D>(r)) + 4 * (s & 1);
+    }
+  }
+};
+
+// 16-bit row of a tensor as MFMA B-operand fragments (column j = this row,
+// k-group g): NKS fragments of 8 values.
+template <int NKS>
+__device__ __forceinline__ void load_row_frags(const uint16_t* row, int g, u32x4 (&f)[NKS]) {
+#pragma unroll
+  for (int ks = 0; ks < NKS; ++ks) f[ks] = *(const u32x4*)(row + 16 * ks + 8 * g);
+}
+
+// Store an accumulator set (NDB C blocks, lane = output row, elements = dims)
+// times `mul` as one 16-bit row.
+template <int NDB, bool BF16>
+__device__ __forceinline__ void store_row(uint16_t* row, int g, const f32x16 (&acc)[NDB],
+                                          float mul) {
+#pragma unroll
+  for (int db = 0; db < NDB; ++db)
+#pragma unroll
+    for (int e4 = 0; e4 < 4; ++e4) {
+      const int d = db * 32 + 8 * e4 + 4 * g;
+      const u32x2 val = {pack2<BF16>(acc[db][4 * e4] * mul, acc[db][4 * e4 + 1] * mul),
+                         pack2<BF16>(acc[db][4 * e4 + 2] * mul, acc[db][4 * e4 + 3] * mul)};
+      *(u32x2*)(row + d) = val;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// dQ: a workgroup owns query rows [128 * qt, +128) of one (batch, head); wave
+// w rows +32w. Per KV tile: S^T = K Q^T and dP^T = V dO^T (K, V rows from LDS,
+// Q, dO in registers), dS^T = P^T * (dP^T - Dvec), dQ^T += K^T dS^T.
+// ---------------------------------------------------------------------------
+template <int D, bool BF16>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void fa_bwd_dq_kernel(BwdParams p) {
+  constexpr int NB = kBwdTile / 32, NKS = D / 16, NDB = D / 32, NSL = kBwdTile / 16;
+  __shared__ __align__(16) uint16_t ks_lds[2][kBwdTile * D];
+  __shared__ __align__(16) uint16_t vs_lds[2][kBwdTile * D];
+
+  const int n_qt = (p.Sq + kBwdOwn - 1) / kBwdOwn;
+  const int qt = blockIdx.x % n_qt;
+  const int bh = blockIdx.x / n_qt;
+  const int b = bh / p.H, h = bh % p.H;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int j = lane & 31, g = lane >> 5;
+  const int q0 = qt * kBwdOwn, wq0 = q0 + wave * 32, myq = wq0 + j;
+  const int qrow = min(myq, p.Sq - 1);
+
+  const int kvh = h / p.kv_group;
+  const uint16_t* Q = (const uint16_t*)p.q + b * p.q_sb + h * p.q_sh;
+  const uint16_t* K = (const uint16_t*)p.k + b * p.k_sb + kvh * p.k_sh;
+  const uint16_t* V = (const uint16_t*)p.v + b * p.v_sb + kvh * p.v_sh;
+  const uint16_t* dO = (const uint16_t*)p.dout + b * p.do_sb + h * p.do_sh;
+  u32x4 qf[NKS], df[NKS];
+  load_row_frags<NKS>(Q + (int64_t)qrow * p.q_ss, g, qf);
+  load_row_frags<NKS>(dO + (int64_t)qrow * p.do_ss, g, df);
+  const int64_t rix = (int64_t)bh * p.Sq + qrow;
+  const float lse = myq < p.Sq ? p.lse[rix] : INFINITY;
+  const float dvc = p.dvec[rix];
+  // Keys this row sees: [kv_first, kv_last] (rows past Sq have lse = +inf, so
+  // their probabilities vanish without a mask).
+  const int kv_first = p.win_left >= 0 ? myq - p.win_left : -(1 << 30);
+  const int kv_last = min(p.win_right >= 0 ? myq + p.win_right : (1 << 30), p.Sk - 1);
+
+  // KV range of this workgroup's rows.
+  const int q_last = min(q0 + kBwdOwn, p.Sq) - 1;
+  const int kv_lo = p.win_left >= 0 ? max(0, q0 - p.win_left) : 0;
+  const int kv_hi = p.win_right >= 0 ? min(p.Sk, q_last + p.win_right + 1) : p.Sk;
+  const int t0 = kv_lo / kBwdTile;
+  const int n_t = kv_hi > kv_lo ? (kv_hi - 1) / kBwdTile - t0 + 1 : 0;
+
+  Addr<D> ad;
+  ad.init(lane);
+  f32x16 dq[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) dq[db] = (f32x16){};
+
+  TileStage<D> kst, vst;
+  if (n_t > 0) {
+    kst.load(K, p.k_ss, t0 * kBwdTile, p.Sk);
+    vst.load(V, p.v_ss, t0 * kBwdTile, p.Sk);
+    kst.store(ks_lds[0]);
+    vst.store(vs_lds[0]);
+  }
+  __syncthreads();
+  for (int t = 0; t < n_t; ++t) {
+    const int st = t & 1;
+    const int kv0 = (t0 + t) * kBwdTile;
+    if (t + 1 < n_t) {
+      kst.load(K, p.k_ss, kv0 + kBwdTile, p.Sk);
+      vst.load(V, p.v_ss, kv0 + kBwdTile, p.Sk);
+    }
+    // Wave-level skip of tiles outside every row's window.
+    const bool skip = kv0 >= p.Sk || wq0 >= p.Sq ||
+                      (p.win_right >= 0 && kv0 > wq0 + 31 + p.win_right) ||
+                      (p.win_left >= 0 && kv0 + kBwdTile - 1 < wq0 - p.win_left);
+    // Tiles inside every row's window and below Sk need no mask.
+    const bool full = kv0 + kBwdTile <= p.Sk &&
+                      (p.win_right < 0 || kv0 + kBwdTile - 1 <= wq0 + p.win_right) &&
+                      (p.win_left < 0 || kv0 >= wq0 + 31 - p.win_left);
+    if (!skip) {
+      const uint16_t* Kt = ks_lds[st];
+      const uint16_t* Vt = vs_lds[st];
+      // One 32-key block at a time: S^T and dP^T, then dS^T, then its dQ^T terms.
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        f32x16 sb = {}, dpb = {};
+#pragma unroll
+        for (int kk = 0; kk < NKS; ++kk) {
+          const u32x4 ka = *(const u32x4*)(Kt + nb * 32 * D + ad.row[kk]);
+          const u32x4 va = *(const u32x4*)(Vt + nb * 32 * D + ad.row[kk]);
+          sb = mfma32x32x16<BF16>(ka, qf[kk], sb);
+          dpb = mfma32x32x16<BF16>(va, df[kk], dpb);
+        }
+        // Element 8h + i of the block is key kv0 + 32nb + 16h + 8g + i.
+        if (!full) {
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            const int key = kv0 + nb * 32 + 16 * (e >> 3) + 8 * g + (e & 7);
+            sb[e] = (key >= kv_first) & (key <= kv_last) ? sb[e] : -INFINITY;
+          }
+        }
+        // dsp[hh]: dS^T of keys 32nb + 16hh + 8g + 0..7, the B operand of k-step 2nb + hh.
+        u32x4 dsp[2];
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+          for (int e2 = 0; e2 < 4; ++e2) {
+            const int e = 8 * hh + 2 * e2;
+            const float p0 = fast_exp2(sb[e] * p.c - lse);
+            const float p1 = fast_exp2(sb[e + 1] * p.c - lse);
+            dsp[hh][e2] = pack2<BF16>(p0 * (dpb[e] - dvc), p1 * (dpb[e + 1] - dvc));
+          }
+        // dQ^T += K^T dS^T (K^T through the transposing read of the K tile).
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+          for (int hh = 0; hh < 2; ++hh) {
+            const int sl = 2 * nb + hh;
+            const u32x2 lo = tr_read16(Kt + ad.tr[db][0] + 16 * sl * D);
+            const u32x2 hi = tr_read16(Kt + ad.tr[db][1] + 16 * sl * D);
+            dq[db] = mfma32x32x16<BF16>((u32x4){lo[0], lo[1], hi[0], hi[1]}, dsp[hh], dq[db]);
+          }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    if (t + 1 < n_t) {
+      // Stage (t+1)%2 was last read in step t-1, before the barrier below it.
+      kst.store(ks_lds[st ^ 1]);
+      vst.store(vs_lds[st ^ 1]);
+    }
+    __syncthreads();
+  }
+  if (myq < p.Sq)
+    store_row<NDB, BF16>((uint16_t*)p.dq + b * p.dq_sb + h * p.dq_sh + (int64_t)myq * p.dq_ss,
+                         g, dq, p.scale);
+}
+
+// ---------------------------------------------------------------------------
+// dK, dV: a workgroup owns keys [128 * kt, +128) of one (batch, head); wave w
+// keys +32w. Per Q tile: S = Q K^T and dP = dO V^T (Q, dO rows from LDS, the
+// wave's K and V rows in registers; lane = key, elements = query rows),
+// P = exp2(S c - lse), dS = P * (dP - Dvec), dV^T += dO^T P, dK^T += Q^T dS.
+// ---------------------------------------------------------------------------
+template <int D, bool BF16>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void fa_bwd_dkdv_kernel(BwdParams p) {
+  constexpr int NB = kBwdTile / 32, NKS = D / 16, NDB = D / 32, NSL = kBwdTile / 16;
+  __shared__ __align__(16) uint16_t qs_lds[2][kBwdTile * D];
+  __shared__ __align__(16) uint16_t ds_lds[2][kBwdTile * D];
+  __shared__ __align__(16) float lse_lds[2][kBwdTile];
+  __shared__ __align__(16) float dvc_lds[2][kBwdTile];
+
+  const int n_kt = (p.Sk + kBwdOwn - 1) / kBwdOwn;
+  const int kt = blockIdx.x % n_kt;
+  const int bhk = blockIdx.x / n_kt;  // (batch, K/V head)
+  const int b = bhk / p.H_kv, hk = bhk % p.H_kv;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int j = lane & 31, g = lane >> 5;
+  const int k0 = kt * kBwdOwn, wk0 = k0 + wave * 32, mykey = wk0 + j;
+  const int krow = min(mykey, p.Sk - 1);
+  // Queries that see this key: [q_first, q_last] (keys past Sk are never
+  // stored, and queries past Sq have lse = +inf).
+  const int q_first = p.win_right >= 0 ? mykey - p.win_right : -(1 << 30);
+  const int q_last = p.win_left >= 0 ? mykey + p.win_left : (1 << 30);
+
+  const uint16_t* K = (const uint16_t*)p.k + b * p.k_sb + hk * p.k_sh;
+  const uint16_t* V = (const uint16_t*)p.v + b * p.v_sb + hk * p.v_sh;
+  u32x4 kf[NKS], vf[NKS];
+  load_row_frags<NKS>(K + (int64_t)krow * p.k_ss, g, kf);
+  load_row_frags<NKS>(V + (int64_t)krow * p.v_ss, g, vf);
+
+  // Query range that sees this workgroup's keys; steps run over the query
+  // heads of the K/V head's group (outer) and the query tiles (inner).
+  const int k_last = min(k0 + kBwdOwn, p.Sk) - 1;
+  const int q_lo = p.win_right >= 0 ? max(0, k0 - p.win_right) : 0;
+  const int q_hi = p.win_left >= 0 ? min(p.Sq, k_last + p.win_left + 1) : p.Sq;
+  const int t0 = q_lo / kBwdTile;
+  const int n_t = q_hi > q_lo ? (q_hi - 1) / kBwdTile - t0 + 1 : 0;
+  const int n_steps = n_t * p.kv_group;
+
+  Addr<D> ad;
+  ad.init(lane);
+  f32x16 dk[NDB], dv[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) {
+    dk[db] = (f32x16){};
+    dv[db] = (f32x16){};
+  }
+
+  TileStage<D> qst, dst;
+  float lse_r = 0.f, dvc_r = 0.f;  // row threadIdx.x of the next tile (first 64 threads)
+  // Global loads of step u's Q, dO, lse and Dvec rows into registers.
+  auto load_step = [&](int u) {
+    const int h = hk * p.kv_group + u / n_t;
+    const int row0 = (t0 + u % n_t) * kBwdTile;
+    qst.load((const uint16_t*)p.q + b * p.q_sb + h * p.q_sh, p.q_ss, row0, p.Sq);
+    dst.load((const uint16_t*)p.dout + b * p.do_sb + h * p.do_sh, p.do_ss, row0, p.Sq);
+    if (threadIdx.x < kBwdTile) {
+      const int r = row0 + threadIdx.x;
+      const int64_t rix = ((int64_t)b * p.H + h) * p.Sq + r;
+      lse_r = r < p.Sq ? p.lse[rix] : INFINITY;
+      dvc_r = r < p.Sq ? p.dvec[rix] : 0.f;
+    }
+  };
+  auto store_step = [&](int st) {
+    qst.store(qs_lds[st]);
+    dst.store(ds_lds[st]);
+    if (threadIdx.x < kBwdTile) {
+      lse_lds[st][threadIdx.x] = lse_r;
+      dvc_lds[st][threadIdx.x] = dvc_r;
+    }
+  };
+  if (n_steps > 0) {
+    load_step(0);
+    store_step(0);
+  }
+  __syncthreads();
+  for (int u = 0; u < n_steps; ++u) {
+    const int st = u & 1;
+    const int qr0 = (t0 + u % n_t) * kBwdTile;
+    if (u + 1 < n_steps) load_step(u + 1);
+    const bool skip = wk0 >= p.Sk || qr0 >= p.Sq ||
+                      (p.win_right >= 0 && wk0 > qr0 + kBwdTile - 1 + p.win_right) ||
+                      (p.win_left >= 0 && wk0 + 31 < qr0 - p.win_left);
+    const bool full = (p.win_right < 0 || wk0 + 31 <= qr0 + p.win_right) &&
+                      (p.win_left < 0 || wk0 >= qr0 + kBwdTile - 1 - p.win_left);
+    if (!skip) {
+      const uint16_t* Qt = qs_lds[st];
+      const uint16_t* Dt = ds_lds[st];
+      // One 32-query block at a time: S and dP, then P and dS, then their
+      // dV^T and dK^T terms.
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        f32x16 sb = {}, dpb = {};
+#pragma unroll
+        for (int kk = 0; kk < NKS; ++kk) {
+          const u32x4 qa = *(const u32x4*)(Qt + nb * 32 * D + ad.row[kk]);
+          const u32x4 da = *(const u32x4*)(Dt + nb * 32 * D + ad.row[kk]);
+          sb = mfma32x32x16<BF16>(qa, kf[kk], sb);
+          dpb = mfma32x32x16<BF16>(da, vf[kk], dpb);
+        }
+        // Element 8h + i of the block is query row qr0 + 32nb + 16h + 8g + i.
+        if (!full) {
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            const int q = qr0 + nb * 32 + 16 * (e >> 3) + 8 * g + (e & 7);
+            sb[e] = (q >= q_first) & (q <= q_last) ? sb[e] : -INFINITY;
+          }
+        }
+        u32x4 pp[2], dsp[2];
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          const int r8 = nb * 32 + 16 * hh + 8 * g;
+          const f32x4 l0 = *(const f32x4*)(&lse_lds[st][r8]);
+          const f32x4 l1 = *(const f32x4*)(&lse_lds[st][r8 + 4]);
+          const f32x4 d0 = *(const f32x4*)(&dvc_lds[st][r8]);
+          const f32x4 d1 = *(const f32x4*)(&dvc_lds[st][r8 + 4]);
+#pragma unroll
+          for (int e2 = 0; e2 < 4; ++e2) {
+            const int e = 8 * hh + 2 * e2;
+            const float lv0 = e2 < 2 ? l0[2 * e2] : l1[2 * e2 - 4];
+            const float lv1 = e2 < 2 ? l0[2 * e2 + 1] : l1[2 * e2 - 3];
+            const float dv0 = e2 < 2 ? d0[2 * e2] : d1[2 * e2 - 4];
+            const float dv1 = e2 < 2 ? d0[2 * e2 + 1] : d1[2 * e2 - 3];
+            const float p0 = fast_exp2(sb[e] * p.c - lv0);
+            const float p1 = fast_exp2(sb[e + 1] * p.c - lv1);
+            pp[hh][e2] = pack2<BF16>(p0, p1);
+            dsp[hh][e2] = pack2<BF16>(p0 * (dpb[e] - dv0), p1 * (dpb[e + 1] - dv1));
+          }
+        }
+        // dV^T += dO^T P and dK^T += Q^T dS (transposing reads of the tiles).
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+          for (int hh = 0; hh < 2; ++hh) {
+            const int sl = 2 * nb + hh;
+            const u32x2 dlo = tr_read16(Dt + ad.tr[db][0] + 16 * sl * D);
+            const u32x2 dhi = tr_read16(Dt + ad.tr[db][1] + 16 * sl * D);
+            dv[db] = mfma32x32x16<BF16>((u32x4){dlo[0], dlo[1], dhi[0], dhi[1]}, pp[hh], dv[db]);
+            const u32x2 qlo = tr_read16(Qt + ad.tr[db][0] + 16 * sl * D);
+            const u32x2 qhi = tr_read16(Qt + ad.tr[db][1] + 16 * sl * D);
+            dk[db] = mfma32x32x16<BF16>((u32x4){qlo[0], qlo[1], qhi[0], qhi[1]}, dsp[hh], dk[db]);
+          }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    if (u + 1 < n_steps) store_step(st ^ 1);
+    __syncthreads();
+  }
+  if (mykey < p.Sk) {
+    store_row<NDB, BF16>((uint16_t*)p.dk + b * p.dk_sb + hk * p.dk_sh + (int64_t)mykey * p.dk_ss,
+                         g, dk, p.scale);
+    store_row<NDB, BF16>((uint16_t*)p.dv + b * p.dv_sb + hk * p.dv_sh + (int64_t)mykey * p.dv_ss,
+                         g, dv, 1.f);
+  }
+}
+
+template <int D, bool BF16>
+hipError_t launch_bwd(const BwdParams& p, hipStream_t st) {
+  const int64_t rows = (int64_t)p.B * p.H * p.Sq;
+  hipLaunchKernelGGL((fa_bwd_dvec_kernel<D, BF16>),
+                     dim3((unsigned)((rows * (D / 8) + 255) / 256)), dim3(256), 0, st, p);
+  const int n_qt = (p.Sq + kBwdOwn - 1) / kBwdOwn, n_kt = (p.Sk + kBwdOwn - 1) / kBwdOwn;
+  hipLaunchKernelGGL((fa_bwd_dq_kernel<D, BF16>), dim3(p.B * p.H * n_qt), dim3(256), 0, st, p);
+  hipLaunchKernelGGL((fa_bwd_dkdv_kernel<D, BF16>), dim3(p.B * p.H_kv * n_kt), dim3(256), 0, st,
+                     p);
+  return hipGetLastError();
+}
+
+}  // namespace mpx
+
+using namespace mpx;
+
+extern "C" size_t mpx_attn_bwd_workspace_bytes(int B, int H, int Sq) {
+  if (B <= 0 || H <= 0 || Sq <= 0) return 0;
+  return (size_t)B * H * Sq * sizeof(float);
+}
+
+extern "C" int mpx_attn_bwd(const void* q, const void* k, const void* v, const void* o,
+                            const void* dout, const float* lse, void* dq, void* dk, void* dv,
+                            const int64_t* q_strides, const int64_t* k_strides,
+                            const int64_t* v_strides, const int64_t* o_strides,
+                            const int64_t* do_strides, const int64_t* dq_strides,
+                            const int64_t* dk_strides, const int64_t* dv_strides, int B, int H,
+                            int H_kv, int Sq, int Sk, int D, float scale, int causal,
+                            int window_left, int window_right, int dtype, void* workspace,
+                            size_t workspace_bytes, void* stream) {
+  clear_error();
+  if (dtype != MPX_F16 && dtype != MPX_BF16) {
+    set_error("mpx_attn_bwd: dtype code %d not supported (the backward is 16-bit only)", dtype);
+    return dtype == MPX_F32 ? MPX_EUNSUPPORTED : MPX_EINVAL;
+  }
+  MPX_CHECK_ARG(B >= 0 && H >= 0 && Sq >= 0 && Sk >= 0, "mpx_attn_bwd: negative size");
+  MPX_CHECK_ARG(H_kv > 0 ? H % H_kv == 0 : H == 0,
+                "mpx_attn_bwd: %d query heads are not a multiple of %d K/V heads", H, H_kv);
+  if (D != 64 && D != 128) {
+    set_error("mpx_attn_bwd: head_dim %d not supported (backward kernels exist for 64, 128)", D);
+    return MPX_EUNSUPPORTED;
+  }
+  MPX_CHECK_ARG(std::isfinite(scale) && scale > 0.f, "mpx_attn_bwd: scale must be positive");
+  if ((long)B * H == 0 || (Sq == 0 && Sk == 0)) return MPX_OK;
+  MPX_CHECK_ARG(Sq > 0 && Sk > 0, "mpx_attn_bwd: empty query or key sequence");
+  const void* ptrs[9] = {q, k, v, o, dout, lse, dq, dk, dv};
+  for (int i = 0; i < 9; ++i) MPX_CHECK_ARG(ptrs[i] != nullptr, "mpx_attn_bwd: null pointer");
+  for (int i = 0; i < 9; ++i)
+    MPX_CHECK_ARG(((uintptr_t)ptrs[i] & 15u) == 0, "mpx_attn_bwd: tensors must be 16-byte aligned");
+  const int64_t* all[8] = {q_strides, k_strides, v_strides, o_strides,
+                           do_strides, dq_strides, dk_strides, dv_strides};
+  for (int t = 0; t < 8; ++t) {
+    MPX_CHECK_ARG(all[t] != nullptr, "mpx_attn_bwd: null strides");
+    for (int i = 0; i < 3; ++i)
+      MPX_CHECK_ARG(all[t][i] >= 0 && all[t][i] % 8 == 0,
+                    "mpx_attn_bwd: strides must be non-negative multiples of 8 elements");
+  }
+  const size_t need = mpx_attn_bwd_workspace_bytes(B, H, Sq);
+  MPX_CHECK_ARG(workspace != nullptr && workspace_bytes >= need &&
+                    ((uintptr_t)workspace & 15u) == 0,
+                "mpx_attn_bwd: 16-byte aligned workspace of %zu bytes required, %zu given", need,
+                workspace_bytes);
+  const long tiles = (long)B * H * (((Sq > Sk ? Sq : Sk) + kBwdOwn - 1) / kBwdOwn);
+  MPX_CHECK_ARG(tiles < (1L << 31) && (long)B * H * Sq < (1L << 35),
+                "mpx_attn_bwd: problem too large");
+
+  BwdParams p = {};
+  p.q = q; p.k = k; p.v = v; p.o = o; p.dout = dout; p.lse = lse;
+  p.dvec = (float*)workspace; p.dq = dq; p.dk = dk; p.dv = dv;
+  p.q_sb = q_strides[0]; p.q_sh = q_strides[1]; p.q_ss = q_strides[2];
+  p.k_sb = k_strides[0]; p.k_sh = k_strides[1]; p.k_ss = k_strides[2];
+  p.v_sb = v_strides[0]; p.v_sh = v_strides[1]; p.v_ss = v_strides[2];
+  p.o_sb = o_strides[0]; p.o_sh = o_strides[1]; p.o_ss = o_strides[2];
+  p.do_sb = do_strides[0]; p.do_sh = do_strides[1]; p.do_ss = do_strides[2];
+  p.dq_sb = dq_strides[0]; p.dq_sh = dq_strides[1]; p.dq_ss = dq_strides[2];
+  p.dk_sb = dk_strides[0]; p.dk_sh = dk_strides[1]; p.dk_ss = dk_strides[2];
+  p.dv_sb = dv_strides[0]; p.dv_sh = dv_strides[1]; p.dv_ss = dv_strides[2];
+  p.B = B; p.H = H; p.H_kv = H_kv; p.kv_group = H / H_kv; p.Sq = Sq; p.Sk = Sk;
+  p.win_left = window_left < 0 ? -1 : window_left;
+  p.win_right = causal ? 0 : (window_right < 0 ? -1 : window_right);
+  p.scale = scale;
+  p.c = scale * kLog2e;
+  hipStream_t st = (hipStream_t)stream;
+  hipError_t e;
+  if (dtype == MPX_BF16)
+    e = D == 64 ? launch_bwd<64, true>(p, st) : launch_bwd<128, true>(p, st);
+  else
+    e = D == 64 ? launch_bwd<64, false>(p, st) : launch_bwd<128, false>(p, st);
+  MPX_CHECK_HIP(e);
+  return MPX_OK;
+}

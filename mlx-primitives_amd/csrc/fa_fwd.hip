@@ -50,6 +50,10 @@ struct FwdParams {
   int neg;  // scale < 0: Q is negated on load (exact) and |scale| used
   float eps;      // normaliser epsilon: O / (l + eps)
   int nan_empty;  // rows that see no key give NaN (exact softmax) instead of 0
+  // Optional (B, H, Sq) float32 log-sum-exp of each row in log2 units,
+  // m + log2(l + eps), +inf for a row that sees no key: with it
+  // P = exp2(s * c - lse) is recomputed by the backward kernels.
+  float* lse;
   // Paged K/V (prefill over a block-table cache; the PAGED kernels only): k
   // and v are the pools (num_blocks, bs, H, D), k_ss / v_ss their token row
   // stride H*D; the rows of batch b come through bt[b, pos / bs].
@@ -634,6 +638,9 @@ __device__ __forceinline__ void fa16_rows(const FwdParams& pin, const WorkItem w
     if (myq < p.Sq) {
       const float inv = m_max == -INFINITY ? (p.nan_empty ? __builtin_nanf("") : 0.f)
                                            : f / (l_tot * f + p.eps);
+      if (p.lse && g == 0)
+        p.lse[((int64_t)wi.b * p.H + wi.h) * p.Sq + myq] =
+            m_max == -INFINITY ? INFINITY : m_max + log2f(l_tot * f + p.eps);
       uint16_t* Op = (uint16_t*)p.o + wi.b * p.o_sb + wi.h * p.o_sh + (int64_t)myq * p.o_ss;
 #pragma unroll
       for (int db = 0; db < NDB; ++db)
@@ -1051,6 +1058,9 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& pin, const Wor
     if (myq < p.Sq) {
       const float inv = m_max == -INFINITY ? (p.nan_empty ? __builtin_nanf("") : 0.f)
                                            : f / (l_tot * f + p.eps);
+      if (p.lse && g == 0)
+        p.lse[((int64_t)wi.b * p.H + wi.h) * p.Sq + myq] =
+            m_max == -INFINITY ? INFINITY : m_max + log2f(l_tot * f + p.eps);
       uint16_t* Op = (uint16_t*)p.o + wi.b * p.o_sb + wi.h * p.o_sh + (int64_t)myq * p.o_ss;
 #pragma unroll
       for (int db = 0; db < NDB; ++db)
@@ -1351,6 +1361,9 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd32_kernel(FwdParams pin) {
     if (myq < p.Sq) {
       const float inv = m_max == -INFINITY ? (p.nan_empty ? __builtin_nanf("") : 0.f)
                                            : f / (l_tot * f + p.eps);
+      if (p.lse && g == 0)
+        p.lse[((int64_t)wi.b * p.H + wi.h) * p.Sq + myq] =
+            m_max == -INFINITY ? INFINITY : m_max + log2f(l_tot * f + p.eps);
       float* Op = (float*)p.o + wi.b * p.o_sb + wi.h * p.o_sh + (int64_t)myq * p.o_ss;
 #pragma unroll
       for (int db = 0; db < NDB; ++db)
@@ -1391,7 +1404,7 @@ __global__ __launch_bounds__(256) void fa_split_merge_kernel(const float* __rest
                                                              void* o, int64_t o_sb, int64_t o_sh,
                                                              int64_t o_ss, int B, int H, int Sq,
                                                              int D, int splits, float eps,
-                                                             int nan_empty) {
+                                                             int nan_empty, float* lse) {
   const int chunks = D / 4;
   const int64_t rows = (int64_t)B * H * Sq;
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -1413,6 +1426,7 @@ __global__ __launch_bounds__(256) void fa_split_merge_kernel(const float* __rest
   } else if (nan_empty) {
     acc = (f32x4){} + __builtin_nanf("");
   }
+  if (lse && c4 == 0) lse[row] = M == -INFINITY ? INFINITY : M + log2f(L + eps);
   const int q = (int)(row % Sq);
   const int bh = (int)(row / Sq);
   const int b = bh / H, h = bh - (bh / H) * H;
@@ -1538,7 +1552,7 @@ int run_fwd(FwdParams& p, const Plan& pl, int D, int dtype, void* workspace, hip
 #define MPX_MERGE(DT)                                                                         \
   hipLaunchKernelGGL(fa_split_merge_kernel<DT>, dim3(blocks), dim3(256), 0, st, p.ws_o, p.ws_ml, \
                      p.o, p.o_sb, p.o_sh, p.o_ss, p.B, p.H, p.Sq, D, pl.splits, p.eps,         \
-                     p.nan_empty)
+                     p.nan_empty, p.lse)
     if (dtype == MPX_F32)
       MPX_MERGE(MPX_F32);
     else if (dtype == MPX_BF16)
@@ -1590,8 +1604,8 @@ extern "C" size_t mpx_attn_fwd_workspace_bytes(int B, int H, int Sq, int Sk, int
   return make_plan(B, H, Sq, Sk, D, causal, window_left, window_right, dtype).ws_bytes;
 }
 
-extern "C" int mpx_attn_fwd_gqa(const void* q, const void* k, const void* v, void* o,
-                                const int64_t* q_strides, const int64_t* k_strides,
+extern "C" int mpx_attn_fwd_lse(const void* q, const void* k, const void* v, void* o,
+                                float* lse, const int64_t* q_strides, const int64_t* k_strides,
                                 const int64_t* v_strides, const int64_t* o_strides, int B, int H,
                                 int H_kv, int Sq, int Sk, int D, float scale, int causal,
                                 int window_left, int window_right, int dtype, void* workspace,
@@ -1648,7 +1662,19 @@ extern "C" int mpx_attn_fwd_gqa(const void* q, const void* k, const void* v, voi
   p.neg = scale < 0.f ? 1 : 0;
   p.eps = kSoftmaxEps;
   p.nan_empty = 0;
+  p.lse = lse;
   return run_fwd<false>(p, pl, D, dtype, workspace, (hipStream_t)stream);
+}
+
+extern "C" int mpx_attn_fwd_gqa(const void* q, const void* k, const void* v, void* o,
+                                const int64_t* q_strides, const int64_t* k_strides,
+                                const int64_t* v_strides, const int64_t* o_strides, int B, int H,
+                                int H_kv, int Sq, int Sk, int D, float scale, int causal,
+                                int window_left, int window_right, int dtype, void* workspace,
+                                size_t workspace_bytes, void* stream) {
+  return mpx_attn_fwd_lse(q, k, v, o, nullptr, q_strides, k_strides, v_strides, o_strides, B, H,
+                          H_kv, Sq, Sk, D, scale, causal, window_left, window_right, dtype,
+                          workspace, workspace_bytes, stream);
 }
 
 extern "C" int mpx_attn_fwd(const void* q, const void* k, const void* v, void* o,

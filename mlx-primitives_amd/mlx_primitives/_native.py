@@ -72,6 +72,22 @@ def load() -> ctypes.CDLL:
             ctypes.c_float, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
             ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
         ]
+        lib.mpx_attn_fwd_lse.restype = ctypes.c_int
+        lib.mpx_attn_fwd_lse.argtypes = [
+            ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+            _i64p, _i64p, _i64p, _i64p,
+            ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+            ctypes.c_float, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+            ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
+        ]
+        lib.mpx_attn_bwd.restype = ctypes.c_int
+        lib.mpx_attn_bwd.argtypes = [ctypes.c_void_p] * 9 + [_i64p] * 8 + [
+            ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+            ctypes.c_float, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+            ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
+        ]
+        lib.mpx_attn_bwd_workspace_bytes.restype = ctypes.c_size_t
+        lib.mpx_attn_bwd_workspace_bytes.argtypes = [ctypes.c_int] * 3
         lib.mpx_attn_fwd_workspace_bytes.restype = ctypes.c_size_t
         lib.mpx_attn_fwd_workspace_bytes.argtypes = [ctypes.c_int] * 9
         lib.mpx_paged_decode.restype = ctypes.c_int
@@ -155,8 +171,9 @@ def require_device(*tensors: torch.Tensor) -> torch.device:
 
 
 def require_no_grad(*tensors: Optional[torch.Tensor]) -> None:
-    """The kernels are forward-only: refuse inputs that autograd would track,
-    instead of returning outputs silently cut off from the graph."""
+    """For the forward-only kernels (paged attention, RoPE): refuse inputs that
+    autograd would track, instead of returning outputs silently cut off from
+    the graph."""
     if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in tensors):
         raise NotImplementedError(
             "mlx_primitives (MI355X build) implements the forward pass only; call it under "
@@ -184,22 +201,49 @@ def attn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor,
              q_strides: Sequence[int], k_strides: Sequence[int], v_strides: Sequence[int],
              o_strides: Sequence[int], B: int, H: int, Sq: int, Sk: int, D: int,
              scale: float, causal: bool, window_left: int = -1, window_right: int = -1,
-             H_kv: Optional[int] = None) -> None:
-    """Enqueue mpx_attn_fwd_gqa on the current stream (strides in (b, h, s) order;
-    K/V carry H_kv heads, default H)."""
+             H_kv: Optional[int] = None, lse: Optional[torch.Tensor] = None) -> None:
+    """Enqueue mpx_attn_fwd_lse on the current stream (strides in (b, h, s) order;
+    K/V carry H_kv heads, default H; lse: optional contiguous (B, H, Sq) float32
+    that receives each row's base-2 log-sum-exp for the backward)."""
     lib = load()
     dev = require_device(q, k, v, o)
     code = dtype_code(q.dtype)
+    if lse is not None:
+        if (lse.dtype != torch.float32 or not lse.is_contiguous() or lse.device != dev
+                or tuple(lse.shape) != (B, H, Sq)):
+            raise ValueError("lse must be a contiguous (B, H, Sq) float32 tensor on the device")
     ws_bytes = int(lib.mpx_attn_fwd_workspace_bytes(
         B, H, Sq, Sk, D, int(causal), window_left, window_right, code))
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
-    rc = lib.mpx_attn_fwd_gqa(
+    rc = lib.mpx_attn_fwd_lse(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+        lse.data_ptr() if lse is not None else None,
         _strides(q_strides), _strides(k_strides), _strides(v_strides), _strides(o_strides),
         B, H, H if H_kv is None else H_kv, Sq, Sk, D, float(scale), int(causal),
         int(window_left), int(window_right), code,
         ws.data_ptr() if ws is not None else None, ws_bytes, _stream_ptr(dev))
     _check(rc, "mpx_attn_fwd failed")
+
+
+def attn_bwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor,
+             dout: torch.Tensor, lse: torch.Tensor, dq: torch.Tensor, dk: torch.Tensor,
+             dv: torch.Tensor, strides: Sequence[Sequence[int]], B: int, H: int, H_kv: int,
+             Sq: int, Sk: int, D: int, scale: float, causal: bool, window_left: int = -1,
+             window_right: int = -1) -> None:
+    """Enqueue mpx_attn_bwd on the current stream. ``strides`` holds the (b, h, s)
+    element strides of q, k, v, o, dout, dq, dk, dv in that order."""
+    lib = load()
+    dev = require_device(q, k, v, o, dout, lse, dq, dk, dv)
+    code = dtype_code(q.dtype)
+    ws_bytes = int(lib.mpx_attn_bwd_workspace_bytes(B, H, Sq))
+    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=dev)
+    rc = lib.mpx_attn_bwd(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), dout.data_ptr(),
+        lse.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+        *[_strides(s) for s in strides],
+        B, H, H_kv, Sq, Sk, D, float(scale), int(causal), int(window_left), int(window_right),
+        code, ws.data_ptr(), ws_bytes, _stream_ptr(dev))
+    _check(rc, "mpx_attn_bwd failed")
 
 
 def paged_decode(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,

@@ -39,21 +39,78 @@ def _bhs(x: torch.Tensor, layout: Layout):
     return (s[0], s[2], s[1]) if layout == Layout.BSHD else (s[0], s[1], s[2])
 
 
+def _needs_grad(*tensors: torch.Tensor) -> bool:
+    return torch.is_grad_enabled() and any(t.requires_grad for t in tensors)
+
+
+def _dims(q: torch.Tensor, k: torch.Tensor, layout: Layout):
+    if layout == Layout.BSHD:
+        B, Sq, H, D = q.shape
+        return B, H, k.shape[2], Sq, k.shape[1], D
+    B, H, Sq, D = q.shape
+    return B, H, k.shape[1], Sq, k.shape[2], D
+
+
+class _FlashAttentionFn(torch.autograd.Function):
+    """Flash forward that keeps each row's log-sum-exp, and the gfx950 backward
+    (mpx_attn_bwd) that recomputes the probabilities from it. Inputs arrive
+    padded to the kernel head dim; padding and slicing stay outside, where
+    autograd differentiates them."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, layout, scale, causal, window_left, window_right):
+        B, H, H_kv, Sq, Sk, D = _dims(q, k, layout)
+        o = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+        lse = torch.empty((B, H, Sq), dtype=torch.float32, device=q.device)
+        _native.attn_fwd(q, k, v, o, _bhs(q, layout), _bhs(k, layout), _bhs(v, layout),
+                         _bhs(o, layout), B, H, Sq, Sk, D, scale, causal, window_left,
+                         window_right, H_kv=H_kv, lse=lse)
+        ctx.save_for_backward(q, k, v, o, lse)
+        ctx.cfg = (layout, scale, causal, window_left, window_right)
+        return o
+
+    @staticmethod
+    @torch.autograd.function.once_differentiable
+    def backward(ctx, dout):
+        q, k, v, o, lse = ctx.saved_tensors
+        layout, scale, causal, window_left, window_right = ctx.cfg
+        B, H, H_kv, Sq, Sk, D = _dims(q, k, layout)
+        dout = _prepare(dout, D)
+        dq = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+        dk = torch.empty(k.shape, dtype=k.dtype, device=k.device)
+        dv = torch.empty(v.shape, dtype=v.dtype, device=v.device)
+        strides = [_bhs(x, layout) for x in (q, k, v, o, dout, dq, dk, dv)]
+        _native.attn_bwd(q, k, v, o, dout, lse, dq, dk, dv, strides, B, H, H_kv, Sq, Sk, D,
+                         scale, causal, window_left, window_right)
+        return dq, dk, dv, None, None, None, None, None
+
+
+def _attention_with_grad(q, k, v, layout, scale, causal, window_left, window_right):
+    if q.dtype not in (torch.float16, torch.bfloat16) or not scale > 0:
+        raise NotImplementedError(
+            "mlx_primitives (MI355X build) differentiates attention for float16 / bfloat16 "
+            f"inputs with scale > 0 (got {q.dtype}, scale={scale}); run float32 attention "
+            "under torch.no_grad()")
+    D = q.shape[-1]
+    dk = 64 if D <= 64 else 128
+    qk, kk, vk = (_prepare(x, dk) for x in (q, k, v))
+    o = _FlashAttentionFn.apply(qk, kk, vk, layout, scale, causal, window_left, window_right)
+    return o[..., :D].contiguous() if dk != D else o
+
+
 def run_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, layout: Layout,
                   scale: float, causal: bool, window_left: int = -1,
                   window_right: int = -1) -> torch.Tensor:
-    """Attention forward on the GPU kernel; returns a new tensor shaped like q."""
+    """Attention forward on the GPU kernel; returns a new tensor shaped like q.
+    When autograd tracks q, k or v, the result is differentiable through the
+    gfx950 backward kernels."""
     _native.require_device(q, k, v)
-    _native.require_no_grad(q, k, v)
-    if layout == Layout.BSHD:
-        B, Sq, H, D = q.shape
-        Sk, H_kv = k.shape[1], k.shape[2]
-    else:
-        B, H, Sq, D = q.shape
-        Sk, H_kv = k.shape[2], k.shape[1]
+    B, H, H_kv, Sq, Sk, D = _dims(q, k, layout)
     if q.numel() == 0:
         return torch.empty(q.shape, dtype=q.dtype, device=q.device)
     dk = kernel_head_dim(D)
+    if _needs_grad(q, k, v):
+        return _attention_with_grad(q, k, v, layout, scale, causal, window_left, window_right)
     qk, kk, vk = (_prepare(x, dk) for x in (q, k, v))
     out_shape = list(q.shape)
     out_shape[-1] = dk

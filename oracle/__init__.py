@@ -9,4 +9,4 @@ Parity pins are listed in tests/test_oracle.py; no oracle function is left
 unpinned.
 """
 
-from oracle import attention, kv_cache, paged  # noqa: F401
+from oracle import attention, attention_grad, kv_cache, paged  # noqa: F401

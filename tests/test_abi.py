@@ -32,7 +32,8 @@ def test_header_declares_expected_entry_points():
         "mpx_version", "mpx_last_error", "mpx_attn_fwd", "mpx_attn_fwd_workspace_bytes",
         "mpx_paged_decode", "mpx_paged_decode_workspace_bytes", "mpx_paged_prefill",
         "mpx_paged_prefill_workspace_bytes", "mpx_kv_append", "mpx_rope", "mpx_attn_fwd_gqa",
-        "mpx_paged_decode_gqa", "mpx_paged_prefill_gqa"])
+        "mpx_paged_decode_gqa", "mpx_paged_prefill_gqa", "mpx_attn_fwd_lse", "mpx_attn_bwd",
+        "mpx_attn_bwd_workspace_bytes"])
 
 
 def test_library_exports_every_declared_symbol(lib):
@@ -160,3 +161,37 @@ def test_gqa_head_counts_validated(lib):
     rc = lib.mpx_paged_prefill_gqa(16, 16, 16, 16, 16, None, 16, st3, st3, 1, 64, 32, 0, 128, 64,
                                    16, 8, 0.1, 1, 1, None, 0, None)
     assert rc == _native.MPX_EINVAL and b"multiple" in lib.mpx_last_error()
+
+
+def _bwd(lib, dtype=2, D=64, B=1, H=2, H_kv=2, Sq=8, Sk=8, scale=0.1, ptr=16, ws=16,
+         ws_bytes=1 << 20, stride=64):
+    st = (ctypes.c_int64 * 3)(8 * 64 * H, 8 * 64, stride)
+    return lib.mpx_attn_bwd(ptr, ptr, ptr, ptr, ptr, ptr, ptr, ptr, ptr, st, st, st, st, st, st,
+                            st, st, B, H, H_kv, Sq, Sk, D, scale, 1, -1, -1, dtype, ws, ws_bytes,
+                            None)
+
+
+def test_bwd_validation(lib):
+    assert lib.mpx_attn_bwd_workspace_bytes(4, 32, 4096) == 4 * 32 * 4096 * 4
+    assert lib.mpx_attn_bwd_workspace_bytes(0, 32, 4096) == 0
+    assert _bwd(lib, dtype=0) == _native.MPX_EUNSUPPORTED and b"16-bit" in lib.mpx_last_error()
+    assert _bwd(lib, dtype=9) == _native.MPX_EINVAL
+    assert _bwd(lib, D=32) == _native.MPX_EUNSUPPORTED and b"head_dim" in lib.mpx_last_error()
+    assert _bwd(lib, scale=-1.0) == _native.MPX_EINVAL and b"positive" in lib.mpx_last_error()
+    assert _bwd(lib, H=6, H_kv=4) == _native.MPX_EINVAL and b"multiple" in lib.mpx_last_error()
+    assert _bwd(lib, ptr=24) == _native.MPX_EINVAL and b"aligned" in lib.mpx_last_error()
+    assert _bwd(lib, stride=68) == _native.MPX_EINVAL and b"multiples of 8" in lib.mpx_last_error()
+    assert _bwd(lib, ws_bytes=8) == _native.MPX_EINVAL and b"workspace" in lib.mpx_last_error()
+    assert _bwd(lib, ws=None) == _native.MPX_EINVAL and b"workspace" in lib.mpx_last_error()
+    assert _bwd(lib, Sq=0, Sk=5) == _native.MPX_EINVAL and b"empty" in lib.mpx_last_error()
+    assert _bwd(lib, B=0) == _native.MPX_OK and lib.mpx_last_error() == b""
+
+
+def test_fwd_lse_validates_like_fwd(lib):
+    st = (ctypes.c_int64 * 3)(8 * 64, 8 * 64, 64)
+    rc = lib.mpx_attn_fwd_lse(16, 16, 16, 16, 16, st, st, st, st, 1, 1, 1, 8, 8, 96, 0.1, 1, -1,
+                              -1, 2, None, 0, None)
+    assert rc == _native.MPX_EUNSUPPORTED and b"head_dim" in lib.mpx_last_error()
+    rc = lib.mpx_attn_fwd_lse(16, 16, 16, 16, None, st, st, st, st, 0, 1, 1, 8, 8, 64, 0.1, 1,
+                              -1, -1, 2, None, 0, None)
+    assert rc == _native.MPX_OK

@@ -1,5 +1,5 @@
-"""Pins of the CPU oracle (oracle/attention.py, oracle/paged.py, oracle/kv_cache.py,
-oracle/rope.py).
+"""Pins of the CPU oracle (oracle/attention.py, oracle/attention_grad.py,
+oracle/paged.py, oracle/kv_cache.py, oracle/rope.py).
 
 Each oracle function is checked against something that does not restate it:
   * known-answer cases from the reference's own tests (cited file:line);
@@ -10,7 +10,10 @@ Each oracle function is checked against something that does not restate it:
     tests/parity/pytorch/test_attention_parity.py:87-105);
   * invariants: block/chunk-size independence, merge associativity, full
     window == causal, large/small input scales, KV append write-then-gather
-    round trips.
+    round trips;
+  * for the gradients: torch autograd in float64 (masks built independently,
+    K/V heads expanded with repeat_interleave), torch's SDPA backward and
+    central finite differences of the pinned forward.
 The last group plants mistakes in the oracle and checks a pin catches each.
 """
 
@@ -22,6 +25,7 @@ import torch
 import torch.nn.functional as F
 
 from oracle import attention as oa
+from oracle import attention_grad as oag
 from oracle import kv_cache as ok
 from oracle import paged as op
 from oracle import rope as orope
@@ -575,6 +579,100 @@ def test_no_nan_at_extreme_scales(mult):
     assert np.isfinite(out).all()
 
 
+# ---- gradients (oracle/attention_grad.py) --------------------------------------------
+
+def _autograd_grads(q, k, v, dout, scale, allowed):
+    """float64 torch autograd of softmax attention; BSHD numpy in, BSHD numpy out.
+    allowed: (Sq, Sk) bool. K/V heads are expanded with repeat_interleave."""
+    qt, kt, vt = (torch.from_numpy(x).requires_grad_(True) for x in (q, k, v))
+    g = q.shape[2] // k.shape[2]
+    qh = qt.transpose(1, 2)
+    kh = kt.repeat_interleave(g, dim=2).transpose(1, 2)
+    vh = vt.repeat_interleave(g, dim=2).transpose(1, 2)
+    s = scale * (qh @ kh.transpose(-1, -2))
+    s = s.masked_fill(~torch.from_numpy(allowed), float("-inf"))
+    o = torch.softmax(s, dim=-1) @ vh
+    (o.transpose(1, 2) * torch.from_numpy(dout)).sum().backward()
+    return qt.grad.numpy(), kt.grad.numpy(), vt.grad.numpy()
+
+
+@pytest.mark.parametrize("causal,wl,wr", [(False, -1, -1), (True, -1, -1), (True, 5, -1),
+                                          (False, 4, 2), (False, -1, 3)])
+@pytest.mark.parametrize("H,H_kv", [(2, 2), (4, 2), (3, 1)])
+@pytest.mark.parametrize("Sq,Sk", [(9, 9), (6, 11), (11, 6)])
+def test_grad_vs_autograd(causal, wl, wr, H, H_kv, Sq, Sk):
+    q, k, v = rnd((2, Sq, H, 8), 1), rnd((2, Sk, H_kv, 8), 2), rnd((2, Sk, H_kv, 8), 3)
+    dout = rnd((2, Sq, H, 8), 4)
+    i, j = np.arange(Sq)[:, None], np.arange(Sk)[None, :]
+    allowed = np.ones((Sq, Sk), bool)
+    if causal:
+        allowed &= j <= i
+    if wl >= 0:
+        allowed &= i - j <= wl
+    if wr >= 0 and not causal:
+        allowed &= j - i <= wr
+    if not allowed.any(axis=1).all():
+        pytest.skip("rows without keys have no softmax gradient in torch")
+    got = oag.attention_grad(q, k, v, dout, 0.37, causal, wl, wr, layout="BSHD", eps=0.0)
+    want = _autograd_grads(q, k, v, dout, 0.37, allowed)
+    for a, b in zip(got, want):
+        np.testing.assert_allclose(a, b, rtol=1e-10, atol=1e-12)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_grad_vs_sdpa_backward(causal):
+    # tests/parity/pytorch/test_attention_parity.py:107-163: loss = sum(out)
+    q, k, v = (rnd((2, 64, 4, 32), s) for s in (5, 6, 7))
+    dout = np.ones_like(q)
+    ts = [torch.from_numpy(x).transpose(1, 2).requires_grad_(True) for x in (q, k, v)]
+    F.scaled_dot_product_attention(*ts, is_causal=causal).sum().backward()
+    want = [t.grad.transpose(1, 2).numpy() for t in ts]
+    got = oag.attention_grad(q, k, v, dout, 1 / math.sqrt(32), causal, eps=0.0)
+    for a, b in zip(got, want):
+        np.testing.assert_allclose(a, b, rtol=1e-9, atol=1e-12)
+
+
+def test_grad_bhsd_layout_and_eps_effect():
+    q, k, v, d = (rnd((1, 7, 2, 8), s) for s in (8, 9, 10, 11))
+    a = oag.attention_grad(q, k, v, d, 0.5, True)
+    t = lambda x: np.swapaxes(x, 1, 2)
+    b = oag.attention_grad(t(q), t(k), t(v), t(d), 0.5, True, layout="BHSD")
+    c = oag.attention_grad(q, k, v, d, 0.5, True, eps=0.0)
+    for x, y, z in zip(a, b, c):
+        np.testing.assert_allclose(x, t(y), rtol=1e-12, atol=1e-14)
+        np.testing.assert_allclose(x, z, rtol=1e-5, atol=1e-5)  # eps = 1e-6 is a tiny shift
+
+
+@pytest.mark.parametrize("causal,wl", [(True, -1), (False, 2)])
+def test_grad_finite_differences(causal, wl):
+    # Central differences of the pinned forward (oracle.attention.attention_rows,
+    # o / (l + eps) normaliser) on a tiny case: every input element perturbed.
+    B, S, H, D = 1, 5, 2, 4
+    q, k, v, dout = (rnd((B, S, H, D), s) for s in (12, 13, 14, 15))
+    scale = 0.6
+
+    def loss(q, k, v):
+        tot = 0.0
+        for h in range(H):
+            o = oa.attention_rows(q[0, :, h], k[0, :, h], v[0, :, h], np.arange(S), scale,
+                                  causal, window_left=wl)
+            tot += float(np.sum(o * dout[0, :, h]))
+        return tot
+
+    got = oag.attention_grad(q, k, v, dout, scale, causal, wl)
+    xs = [q, k, v]
+    for which in range(3):
+        num = np.zeros_like(xs[which])
+        for idx in np.ndindex(xs[which].shape):
+            plus = [x.copy() for x in xs]
+            minus = [x.copy() for x in xs]
+            plus[which][idx] += 1e-6
+            minus[which][idx] -= 1e-6
+            num[idx] = (loss(*plus) - loss(*minus)) / 2e-6
+        # atol: the closed form leaves out the O(eps) dependence through the row max
+        np.testing.assert_allclose(got[which], num, rtol=1e-6, atol=1e-5)
+
+
 # ---- planted mistakes are caught ---------------------------------------------------
 
 def test_pin_catches_merge_without_rescale(monkeypatch):
@@ -637,3 +735,11 @@ def test_pin_catches_rope_sine_sign(monkeypatch):
     monkeypatch.setattr(orope, "rope", bad)
     with pytest.raises(AssertionError):
         test_fused_rope_attention_vs_brute(3, 0, True, 2, 5)
+
+
+def test_pin_catches_grad_without_rowsum_term(monkeypatch):
+    monkeypatch.setattr(oag, "_score_grad", lambda p, dp, dout, o: p * dp)  # drops -rowsum
+    with pytest.raises(AssertionError):
+        test_grad_vs_autograd(True, -1, -1, 2, 2, 9, 9)
+    with pytest.raises(AssertionError):
+        test_grad_finite_differences(True, -1)
