@@ -15,6 +15,7 @@ import shutil
 import subprocess
 import sys
 import tempfile
+from concurrent.futures import ThreadPoolExecutor
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 REPO = os.path.dirname(HERE)
@@ -24,6 +25,10 @@ LIB_DIR = os.path.join(HERE, "mlx_primitives", "_lib")
 LIB_PATH = os.path.join(LIB_DIR, "libmpx_attn.so")
 
 SOURCES = ["abi.hip", "fa_fwd.hip", "fa_bwd.hip", "paged_decode.hip", "kv_cache.hip", "rope.hip"]
+# Per-source device-compiler options. The backward kernels hold their MFMA
+# accumulators in arch VGPRs (the default heuristic moves them through AGPRs
+# with a copy per element per tile).
+EXTRA_FLAGS = {"fa_bwd.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
 ARCH = "gfx950"
 
 
@@ -40,7 +45,6 @@ def compile_flags() -> list[str]:
         "-O3",
         "-std=c++17",
         "-fPIC",
-        "-shared",
         "-I" + INCLUDE,
         "-I" + CSRC,
         # Packed fp32 VALU ops are kept out of the device code.
@@ -49,22 +53,40 @@ def compile_flags() -> list[str]:
     ]
 
 
-def build(verbose: bool = False) -> str:
-    os.makedirs(LIB_DIR, exist_ok=True)
-    srcs = [os.path.join(CSRC, s) for s in SOURCES]
-    fd, tmp = tempfile.mkstemp(prefix="libmpx_attn.", suffix=".so.tmp", dir=LIB_DIR)
-    os.close(fd)
-    cmd = [hipcc()] + compile_flags() + srcs + ["-o", tmp]
+def _run(cmd: list[str], verbose: bool) -> None:
     if verbose:
         print(" ".join(cmd), flush=True)
     proc = subprocess.run(cmd, capture_output=True, text=True)
     noise = "is not a recognized feature for this target"
     err = "\n".join(ln for ln in proc.stderr.splitlines() if noise not in ln)
     if proc.returncode != 0:
-        os.unlink(tmp)
         raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{err}")
     if verbose and err.strip():
         print(err, file=sys.stderr)
+
+
+def build(verbose: bool = False) -> str:
+    """Compile every source to an object (in parallel), then link the library."""
+    os.makedirs(LIB_DIR, exist_ok=True)
+    with tempfile.TemporaryDirectory(prefix="mpx_build.") as tmpdir:
+        jobs = []
+        for src in SOURCES:
+            obj = os.path.join(tmpdir, src.replace(".hip", ".o"))
+            cmd = ([hipcc()] + compile_flags() + EXTRA_FLAGS.get(src, [])
+                   + ["-c", os.path.join(CSRC, src), "-o", obj])
+            jobs.append((cmd, obj))
+        workers = min(len(jobs), max(1, (os.cpu_count() or 1)), 8)
+        with ThreadPoolExecutor(max_workers=workers) as ex:
+            for f in [ex.submit(_run, cmd, verbose) for cmd, _ in jobs]:
+                f.result()
+        fd, tmp = tempfile.mkstemp(prefix="libmpx_attn.", suffix=".so.tmp", dir=LIB_DIR)
+        os.close(fd)
+        try:
+            _run([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC"]
+                 + [obj for _, obj in jobs] + ["-o", tmp], verbose)
+        except Exception:
+            os.unlink(tmp)
+            raise
     os.replace(tmp, LIB_PATH)
     return LIB_PATH
 

@@ -11,8 +11,9 @@
 //   dV = P^T dO,  dK = scale * dS^T Q                 (fa_bwd_dkdv_kernel)
 // Two MFMA kernels, no atomics: dQ is query-parallel (each workgroup owns 128
 // query rows and streams K and V), dK/dV key-parallel (each workgroup owns 128
-// keys and streams Q and dO). Both recompute S and dP; tiles of 64 rows stream
-// through LDS, double buffered, loaded one tile ahead into registers.
+// keys and streams Q and dO). Both recompute S and dP; tiles of 64 rows go
+// from HBM straight into LDS (buffer_load ... lds), double buffered: the tile
+// after the current one is in flight while the current one is computed.
 //
 // MFMA 32x32x16 layouts (lane = j + 32*g, j in [0,32)): A (32 x 16) lane holds
 // row j, k-group g (8 values); B (16 x 32) column j, k-group g; C (32 x 32)
@@ -50,13 +51,6 @@ constexpr int kBwdWaves = 4;    // waves per workgroup (one per SIMD)
 constexpr int kBwdOwn = 32 * kBwdWaves;  // rows (or keys) a workgroup owns
 constexpr int kBwdTile = 64;    // streamed rows per step
 
-__device__ __forceinline__ u32x2 tr_read16(const uint16_t* lds) {
-  typedef __attribute__((ext_vector_type(4))) short s16x4;
-  const s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (__attribute__((address_space(3))) s16x4*)(lds));
-  return __builtin_bit_cast(u32x2, r);
-}
-
 // LDS tiles are (64, D) row-major without padding; the 16-byte chunk c of row
 // r sits at slot c ^ swz(r). Each tile is read two ways, and the swizzle keeps
 // both conflict-free: 16 lanes reading one chunk of 16 consecutive rows (row
@@ -71,31 +65,47 @@ __device__ __forceinline__ int swz(int r) {
   }
 }
 
-// Rows of a 16-bit (rows, D) tensor slice through 256 threads: global ->
-// registers (rows past `rows` re-read the last one) -> swizzled LDS tile.
+// DMA of 64 rows of a 16-bit (rows, D) slice into a swizzled LDS tile. A DMA
+// instruction fills 1 KB of LDS (RPD rows); wave w issues the blocks w,
+// w + 4, ... . Lane l lands at slot l % CPR of row l / CPR of its block, so it
+// loads logical chunk (l % CPR) ^ swz(row); the swizzle only depends on the
+// low 4 row bits, which are the same in all of a lane's blocks. Rows past the
+// slice end re-read its last row (callers mask them or weight them by 0).
 template <int D>
-struct TileStage {
-  static constexpr int CPR = D / 8;                   // 16-byte chunks per row
-  static constexpr int PER_T = kBwdTile * CPR / 256;  // chunks per thread
-  u32x4 r[PER_T];
-  __device__ __forceinline__ void load(const uint16_t* base, int64_t row_stride, int row0,
-                                       int rows) {
-#pragma unroll
-    for (int i = 0; i < PER_T; ++i) {
-      const int c = threadIdx.x + 256 * i;
-      const int row = min(row0 + c / CPR, rows - 1);
-      r[i] = *(const u32x4*)(base + (int64_t)row * row_stride + (c % CPR) * 8);
-    }
+struct TileDma {
+  static constexpr int CPR = D / 8;                            // 16-byte chunks per row
+  static constexpr int RPD = 64 / CPR;                         // rows per DMA (1 KB)
+  static constexpr int NDMA = kBwdTile / (RPD * kBwdWaves);    // DMAs per wave per tile
+  int row_bytes, lrow, lchunk, voff;
+  u32 lds_off;
+  __device__ __forceinline__ void init(int64_t row_stride, int wave, int lane) {
+    row_bytes = (int)row_stride * 2;
+    lrow = wave * RPD + lane / CPR;
+    lchunk = (lane % CPR) ^ swz<D>(lrow);
+    voff = lrow * row_bytes + lchunk * 16;
+    lds_off = (u32)wave * 1024u;
   }
-  __device__ __forceinline__ void store(uint16_t* lds) const {
+  // Rows row0 .. row0 + 63 of the slice at base (rows rows) into the LDS tile at lds.
+  __device__ __forceinline__ void load(const void* base, u32 lds, int row0, int rows) const {
+    const u32x4 rs = buffer_desc(base);
+    const int so = row0 * row_bytes;
+    if (row0 + kBwdTile <= rows) {
 #pragma unroll
-    for (int i = 0; i < PER_T; ++i) {
-      const int c = threadIdx.x + 256 * i;
-      const int row = c / CPR;
-      *(u32x4*)(lds + row * D + 8 * ((c % CPR) ^ swz<D>(row))) = r[i];
+      for (int r = 0; r < NDMA; ++r)
+        dma16(rs, lds + lds_off + r * kBwdWaves * 1024u, voff,
+              so + r * kBwdWaves * RPD * row_bytes);
+    } else {
+#pragma unroll
+      for (int r = 0; r < NDMA; ++r) {
+        const int row = min(lrow + r * kBwdWaves * RPD, rows - 1 - row0);
+        dma16(rs, lds + lds_off + r * kBwdWaves * 1024u, row * row_bytes + lchunk * 16, so);
+      }
     }
   }
 };
+
+// s_waitcnt vmcnt(0) lgkmcnt(0): every load and LDS access of this wave done.
+__device__ __forceinline__ void wait_all() { __builtin_amdgcn_s_waitcnt(0x0070); }
 
 // Dvec = rowsum(dO * O) in float32: D / 8 lanes per row, 8 elements each.
 template <int D, bool BF16>
@@ -178,14 +188,15 @@ __device__ __forceinline__ void store_row(uint16_t* row, int g, const f32x16 (&a
 // ---------------------------------------------------------------------------
 // dQ: a workgroup owns query rows [128 * qt, +128) of one (batch, head); wave
 // w rows +32w. Per KV tile: S^T = K Q^T and dP^T = V dO^T (K, V rows from LDS,
-// Q, dO in registers), dS^T = P^T * (dP^T - Dvec), dQ^T += K^T dS^T.
+// Q, dO in registers), dS^T = P^T * (dP^T - Dvec), dQ^T += K^T dS^T. Two
+// workgroups per CU (two waves per SIMD) hide each other's VALU phases.
 // ---------------------------------------------------------------------------
 template <int D, bool BF16>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void fa_bwd_dq_kernel(BwdParams p) {
-  constexpr int NB = kBwdTile / 32, NKS = D / 16, NDB = D / 32, NSL = kBwdTile / 16;
-  __shared__ __align__(16) uint16_t ks_lds[2][kBwdTile * D];
-  __shared__ __align__(16) uint16_t vs_lds[2][kBwdTile * D];
+  constexpr int NKS = D / 16, NDB = D / 32, TILE = kBwdTile * D;
+  // Stage s: K tile at [2s], V tile at [2s + 1].
+  __shared__ __align__(1024) uint16_t lds[4 * TILE];
 
   const int n_qt = (p.Sq + kBwdOwn - 1) / kBwdOwn;
   const int qt = blockIdx.x % n_qt;
@@ -221,39 +232,45 @@ void fa_bwd_dq_kernel(BwdParams p) {
 
   Addr<D> ad;
   ad.init(lane);
+  TileDma<D> kd, vd;
+  kd.init(p.k_ss, wave, lane);
+  vd.init(p.v_ss, wave, lane);
+  const u32 lbase = lds_addr(lds);
   f32x16 dq[NDB];
 #pragma unroll
   for (int db = 0; db < NDB; ++db) dq[db] = (f32x16){};
 
-  TileStage<D> kst, vst;
-  if (n_t > 0) {
-    kst.load(K, p.k_ss, t0 * kBwdTile, p.Sk);
-    vst.load(V, p.v_ss, t0 * kBwdTile, p.Sk);
-    kst.store(ks_lds[0]);
-    vst.store(vs_lds[0]);
-  }
-  __syncthreads();
-  for (int t = 0; t < n_t; ++t) {
-    const int st = t & 1;
+  auto load = [&](int t, int S) __attribute__((always_inline)) {
     const int kv0 = (t0 + t) * kBwdTile;
-    if (t + 1 < n_t) {
-      kst.load(K, p.k_ss, kv0 + kBwdTile, p.Sk);
-      vst.load(V, p.v_ss, kv0 + kBwdTile, p.Sk);
-    }
-    // Wave-level skip of tiles outside every row's window.
-    const bool skip = kv0 >= p.Sk || wq0 >= p.Sq ||
+    kd.load(K, lbase + (2 * S) * TILE * 2, kv0, p.Sk);
+    vd.load(V, lbase + (2 * S + 1) * TILE * 2, kv0, p.Sk);
+  };
+  if (n_t > 0) {
+    wait_all();  // Q, dO fragments, lse and Dvec landed before the first DMA
+    load(0, 0);
+    wait_all();
+    stage_barrier();
+  }
+  // Step t computes stage t % 2 while tile t + 1 lands in the other stage
+  // (whose previous tile every wave finished before the last barrier).
+  for (int t = 0; t < n_t; ++t) {
+    const int S = t & 1;
+    if (t + 1 < n_t) load(t + 1, S ^ 1);
+    const int kv0 = (t0 + t) * kBwdTile;
+    // Wave-level skip of tiles outside every row's window; tiles inside every
+    // row's window and below Sk need no mask.
+    const bool skip = wq0 >= p.Sq ||
                       (p.win_right >= 0 && kv0 > wq0 + 31 + p.win_right) ||
                       (p.win_left >= 0 && kv0 + kBwdTile - 1 < wq0 - p.win_left);
-    // Tiles inside every row's window and below Sk need no mask.
     const bool full = kv0 + kBwdTile <= p.Sk &&
                       (p.win_right < 0 || kv0 + kBwdTile - 1 <= wq0 + p.win_right) &&
                       (p.win_left < 0 || kv0 >= wq0 + 31 - p.win_left);
     if (!skip) {
-      const uint16_t* Kt = ks_lds[st];
-      const uint16_t* Vt = vs_lds[st];
+      const uint16_t* Kt = lds + 2 * S * TILE;
+      const uint16_t* Vt = Kt + TILE;
       // One 32-key block at a time: S^T and dP^T, then dS^T, then its dQ^T terms.
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb) {
+      for (int nb = 0; nb < 2; ++nb) {
         f32x16 sb = {}, dpb = {};
 #pragma unroll
         for (int kk = 0; kk < NKS; ++kk) {
@@ -287,19 +304,14 @@ void fa_bwd_dq_kernel(BwdParams p) {
 #pragma unroll
           for (int hh = 0; hh < 2; ++hh) {
             const int sl = 2 * nb + hh;
-            const u32x2 lo = tr_read16(Kt + ad.tr[db][0] + 16 * sl * D);
-            const u32x2 hi = tr_read16(Kt + ad.tr[db][1] + 16 * sl * D);
+            const u32x2 lo = lds_read_tr16(Kt + ad.tr[db][0] + 16 * sl * D);
+            const u32x2 hi = lds_read_tr16(Kt + ad.tr[db][1] + 16 * sl * D);
             dq[db] = mfma32x32x16<BF16>((u32x4){lo[0], lo[1], hi[0], hi[1]}, dsp[hh], dq[db]);
           }
-        __builtin_amdgcn_sched_barrier(0);
       }
     }
-    if (t + 1 < n_t) {
-      // Stage (t+1)%2 was last read in step t-1, before the barrier below it.
-      kst.store(ks_lds[st ^ 1]);
-      vst.store(vs_lds[st ^ 1]);
-    }
-    __syncthreads();
+    wait_all();
+    stage_barrier();
   }
   if (myq < p.Sq)
     store_row<NDB, BF16>((uint16_t*)p.dq + b * p.dq_sb + h * p.dq_sh + (int64_t)myq * p.dq_ss,
@@ -307,17 +319,25 @@ void fa_bwd_dq_kernel(BwdParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// dK, dV: a workgroup owns keys [128 * kt, +128) of one (batch, head); wave w
-// keys +32w. Per Q tile: S = Q K^T and dP = dO V^T (Q, dO rows from LDS, the
-// wave's K and V rows in registers; lane = key, elements = query rows),
-// P = exp2(S c - lse), dS = P * (dP - Dvec), dV^T += dO^T P, dK^T += Q^T dS.
+// dK, dV: a workgroup owns keys [128 * kt, +128) of one (batch, K/V head);
+// wave w keys +32w. Per Q tile (of every query head in the K/V head's group):
+// S = Q K^T and dP = dO V^T (Q, dO rows from LDS, the wave's K and V rows in
+// registers; lane = key, elements = query rows), P = exp2(S c - lse),
+// dS = P * (dP - Dvec), dV^T += dO^T P, dK^T += Q^T dS.
+// MODE selects the outputs: kBoth (dK and dV), kOnlyK, kOnlyV. At D = 128
+// both accumulator sets take 128 registers and would leave one wave per SIMD,
+// so dK and dV run as two kernels of two waves per SIMD each (the dV kernel
+// recomputes S, and needs neither dP nor V); at D = 64 one kernel holds both.
 // ---------------------------------------------------------------------------
-template <int D, bool BF16>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+constexpr int kBoth = 0, kOnlyK = 1, kOnlyV = 2;
+
+template <int D, bool BF16, int MODE>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void fa_bwd_dkdv_kernel(BwdParams p) {
-  constexpr int NB = kBwdTile / 32, NKS = D / 16, NDB = D / 32, NSL = kBwdTile / 16;
-  __shared__ __align__(16) uint16_t qs_lds[2][kBwdTile * D];
-  __shared__ __align__(16) uint16_t ds_lds[2][kBwdTile * D];
+  constexpr bool WANT_K = MODE != kOnlyV, WANT_V = MODE != kOnlyK;
+  constexpr int NKS = D / 16, NDB = D / 32, TILE = kBwdTile * D;
+  // Stage s: Q tile at [2s], dO tile at [2s + 1].
+  __shared__ __align__(1024) uint16_t lds[4 * TILE];
   __shared__ __align__(16) float lse_lds[2][kBwdTile];
   __shared__ __align__(16) float dvc_lds[2][kBwdTile];
 
@@ -338,7 +358,7 @@ void fa_bwd_dkdv_kernel(BwdParams p) {
   const uint16_t* V = (const uint16_t*)p.v + b * p.v_sb + hk * p.v_sh;
   u32x4 kf[NKS], vf[NKS];
   load_row_frags<NKS>(K + (int64_t)krow * p.k_ss, g, kf);
-  load_row_frags<NKS>(V + (int64_t)krow * p.v_ss, g, vf);
+  if constexpr (WANT_K) load_row_frags<NKS>(V + (int64_t)krow * p.v_ss, g, vf);
 
   // Query range that sees this workgroup's keys; steps run over the query
   // heads of the K/V head's group (outer) and the query tiles (inner).
@@ -351,6 +371,10 @@ void fa_bwd_dkdv_kernel(BwdParams p) {
 
   Addr<D> ad;
   ad.init(lane);
+  TileDma<D> qd, dd;
+  qd.init(p.q_ss, wave, lane);
+  dd.init(p.do_ss, wave, lane);
+  const u32 lbase = lds_addr(lds);
   f32x16 dk[NDB], dv[NDB];
 #pragma unroll
   for (int db = 0; db < NDB; ++db) {
@@ -358,14 +382,15 @@ void fa_bwd_dkdv_kernel(BwdParams p) {
     dv[db] = (f32x16){};
   }
 
-  TileStage<D> qst, dst;
-  float lse_r = 0.f, dvc_r = 0.f;  // row threadIdx.x of the next tile (first 64 threads)
-  // Global loads of step u's Q, dO, lse and Dvec rows into registers.
-  auto load_step = [&](int u) {
+  float lse_r = 0.f, dvc_r = 0.f;  // row threadIdx.x of the tile in flight (first 64 threads)
+  // Step u's Q and dO tiles into stage S by DMA, its lse and Dvec rows into registers.
+  auto load = [&](int u, int S) __attribute__((always_inline)) {
     const int h = hk * p.kv_group + u / n_t;
     const int row0 = (t0 + u % n_t) * kBwdTile;
-    qst.load((const uint16_t*)p.q + b * p.q_sb + h * p.q_sh, p.q_ss, row0, p.Sq);
-    dst.load((const uint16_t*)p.dout + b * p.do_sb + h * p.do_sh, p.do_ss, row0, p.Sq);
+    qd.load((const uint16_t*)p.q + b * p.q_sb + h * p.q_sh, lbase + (2 * S) * TILE * 2, row0,
+            p.Sq);
+    dd.load((const uint16_t*)p.dout + b * p.do_sb + h * p.do_sh,
+            lbase + (2 * S + 1) * TILE * 2, row0, p.Sq);
     if (threadIdx.x < kBwdTile) {
       const int r = row0 + threadIdx.x;
       const int64_t rix = ((int64_t)b * p.H + h) * p.Sq + r;
@@ -373,44 +398,48 @@ void fa_bwd_dkdv_kernel(BwdParams p) {
       dvc_r = r < p.Sq ? p.dvec[rix] : 0.f;
     }
   };
-  auto store_step = [&](int st) {
-    qst.store(qs_lds[st]);
-    dst.store(ds_lds[st]);
+  auto store_vec = [&](int S) __attribute__((always_inline)) {
     if (threadIdx.x < kBwdTile) {
-      lse_lds[st][threadIdx.x] = lse_r;
-      dvc_lds[st][threadIdx.x] = dvc_r;
+      lse_lds[S][threadIdx.x] = lse_r;
+      dvc_lds[S][threadIdx.x] = dvc_r;
     }
   };
   if (n_steps > 0) {
-    load_step(0);
-    store_step(0);
+    wait_all();  // K, V fragments landed before the first DMA
+    load(0, 0);
+    wait_all();
+    store_vec(0);
+    stage_barrier();
   }
-  __syncthreads();
+  // Step u computes stage u % 2 while step u + 1's tiles land in the other
+  // stage (whose previous tiles every wave finished before the last barrier).
   for (int u = 0; u < n_steps; ++u) {
-    const int st = u & 1;
+    const int S = u & 1;
+    if (u + 1 < n_steps) load(u + 1, S ^ 1);
     const int qr0 = (t0 + u % n_t) * kBwdTile;
-    if (u + 1 < n_steps) load_step(u + 1);
-    const bool skip = wk0 >= p.Sk || qr0 >= p.Sq ||
+    const bool skip = wk0 >= p.Sk ||
                       (p.win_right >= 0 && wk0 > qr0 + kBwdTile - 1 + p.win_right) ||
                       (p.win_left >= 0 && wk0 + 31 < qr0 - p.win_left);
     const bool full = (p.win_right < 0 || wk0 + 31 <= qr0 + p.win_right) &&
                       (p.win_left < 0 || wk0 >= qr0 + kBwdTile - 1 - p.win_left);
     if (!skip) {
-      const uint16_t* Qt = qs_lds[st];
-      const uint16_t* Dt = ds_lds[st];
-      // One 32-query block at a time: S and dP, then P and dS, then their
-      // dV^T and dK^T terms.
+      const uint16_t* Qt = lds + 2 * S * TILE;
+      const uint16_t* Dt = Qt + TILE;
+      const float* lsv = lse_lds[S];
+      const float* dvv = dvc_lds[S];
+      // One 32-query block at a time (element 8h + i of a block: query row
+      // qr0 + 32nb + 16h + 8g + i): S and dP, then P and dS packed as the B
+      // operands of k-steps 2nb, 2nb + 1, then their dV^T and dK^T terms.
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb) {
+      for (int nb = 0; nb < 2; ++nb) {
         f32x16 sb = {}, dpb = {};
 #pragma unroll
         for (int kk = 0; kk < NKS; ++kk) {
           const u32x4 qa = *(const u32x4*)(Qt + nb * 32 * D + ad.row[kk]);
           const u32x4 da = *(const u32x4*)(Dt + nb * 32 * D + ad.row[kk]);
           sb = mfma32x32x16<BF16>(qa, kf[kk], sb);
-          dpb = mfma32x32x16<BF16>(da, vf[kk], dpb);
+          if constexpr (WANT_K) dpb = mfma32x32x16<BF16>(da, vf[kk], dpb);
         }
-        // Element 8h + i of the block is query row qr0 + 32nb + 16h + 8g + i.
         if (!full) {
 #pragma unroll
           for (int e = 0; e < 16; ++e) {
@@ -422,10 +451,10 @@ void fa_bwd_dkdv_kernel(BwdParams p) {
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
           const int r8 = nb * 32 + 16 * hh + 8 * g;
-          const f32x4 l0 = *(const f32x4*)(&lse_lds[st][r8]);
-          const f32x4 l1 = *(const f32x4*)(&lse_lds[st][r8 + 4]);
-          const f32x4 d0 = *(const f32x4*)(&dvc_lds[st][r8]);
-          const f32x4 d1 = *(const f32x4*)(&dvc_lds[st][r8 + 4]);
+          const f32x4 l0 = *(const f32x4*)(lsv + r8);
+          const f32x4 l1 = *(const f32x4*)(lsv + r8 + 4);
+          const f32x4 d0 = *(const f32x4*)(dvv + r8);
+          const f32x4 d1 = *(const f32x4*)(dvv + r8 + 4);
 #pragma unroll
           for (int e2 = 0; e2 < 4; ++e2) {
             const int e = 8 * hh + 2 * e2;
@@ -435,8 +464,9 @@ void fa_bwd_dkdv_kernel(BwdParams p) {
             const float dv1 = e2 < 2 ? d0[2 * e2 + 1] : d1[2 * e2 - 3];
             const float p0 = fast_exp2(sb[e] * p.c - lv0);
             const float p1 = fast_exp2(sb[e + 1] * p.c - lv1);
-            pp[hh][e2] = pack2<BF16>(p0, p1);
-            dsp[hh][e2] = pack2<BF16>(p0 * (dpb[e] - dv0), p1 * (dpb[e + 1] - dv1));
+            if constexpr (WANT_V) pp[hh][e2] = pack2<BF16>(p0, p1);
+            if constexpr (WANT_K)
+              dsp[hh][e2] = pack2<BF16>(p0 * (dpb[e] - dv0), p1 * (dpb[e + 1] - dv1));
           }
         }
         // dV^T += dO^T P and dK^T += Q^T dS (transposing reads of the tiles).
@@ -445,24 +475,33 @@ void fa_bwd_dkdv_kernel(BwdParams p) {
 #pragma unroll
           for (int hh = 0; hh < 2; ++hh) {
             const int sl = 2 * nb + hh;
-            const u32x2 dlo = tr_read16(Dt + ad.tr[db][0] + 16 * sl * D);
-            const u32x2 dhi = tr_read16(Dt + ad.tr[db][1] + 16 * sl * D);
-            dv[db] = mfma32x32x16<BF16>((u32x4){dlo[0], dlo[1], dhi[0], dhi[1]}, pp[hh], dv[db]);
-            const u32x2 qlo = tr_read16(Qt + ad.tr[db][0] + 16 * sl * D);
-            const u32x2 qhi = tr_read16(Qt + ad.tr[db][1] + 16 * sl * D);
-            dk[db] = mfma32x32x16<BF16>((u32x4){qlo[0], qlo[1], qhi[0], qhi[1]}, dsp[hh], dk[db]);
+            if constexpr (WANT_V) {
+              const u32x2 dlo = lds_read_tr16(Dt + ad.tr[db][0] + 16 * sl * D);
+              const u32x2 dhi = lds_read_tr16(Dt + ad.tr[db][1] + 16 * sl * D);
+              dv[db] =
+                  mfma32x32x16<BF16>((u32x4){dlo[0], dlo[1], dhi[0], dhi[1]}, pp[hh], dv[db]);
+            }
+            if constexpr (WANT_K) {
+              const u32x2 qlo = lds_read_tr16(Qt + ad.tr[db][0] + 16 * sl * D);
+              const u32x2 qhi = lds_read_tr16(Qt + ad.tr[db][1] + 16 * sl * D);
+              dk[db] =
+                  mfma32x32x16<BF16>((u32x4){qlo[0], qlo[1], qhi[0], qhi[1]}, dsp[hh], dk[db]);
+            }
           }
-        __builtin_amdgcn_sched_barrier(0);
       }
     }
-    if (u + 1 < n_steps) store_step(st ^ 1);
-    __syncthreads();
+    wait_all();
+    if (u + 1 < n_steps) store_vec(S ^ 1);
+    stage_barrier();
   }
   if (mykey < p.Sk) {
-    store_row<NDB, BF16>((uint16_t*)p.dk + b * p.dk_sb + hk * p.dk_sh + (int64_t)mykey * p.dk_ss,
-                         g, dk, p.scale);
-    store_row<NDB, BF16>((uint16_t*)p.dv + b * p.dv_sb + hk * p.dv_sh + (int64_t)mykey * p.dv_ss,
-                         g, dv, 1.f);
+    if constexpr (WANT_K)
+      store_row<NDB, BF16>(
+          (uint16_t*)p.dk + b * p.dk_sb + hk * p.dk_sh + (int64_t)mykey * p.dk_ss, g, dk,
+          p.scale);
+    if constexpr (WANT_V)
+      store_row<NDB, BF16>(
+          (uint16_t*)p.dv + b * p.dv_sb + hk * p.dv_sh + (int64_t)mykey * p.dv_ss, g, dv, 1.f);
   }
 }
 
@@ -473,8 +512,13 @@ hipError_t launch_bwd(const BwdParams& p, hipStream_t st) {
                      dim3((unsigned)((rows * (D / 8) + 255) / 256)), dim3(256), 0, st, p);
   const int n_qt = (p.Sq + kBwdOwn - 1) / kBwdOwn, n_kt = (p.Sk + kBwdOwn - 1) / kBwdOwn;
   hipLaunchKernelGGL((fa_bwd_dq_kernel<D, BF16>), dim3(p.B * p.H * n_qt), dim3(256), 0, st, p);
-  hipLaunchKernelGGL((fa_bwd_dkdv_kernel<D, BF16>), dim3(p.B * p.H_kv * n_kt), dim3(256), 0, st,
-                     p);
+  const dim3 grid_kv(p.B * p.H_kv * n_kt);
+  if constexpr (D == 128) {
+    hipLaunchKernelGGL((fa_bwd_dkdv_kernel<D, BF16, kOnlyK>), grid_kv, dim3(256), 0, st, p);
+    hipLaunchKernelGGL((fa_bwd_dkdv_kernel<D, BF16, kOnlyV>), grid_kv, dim3(256), 0, st, p);
+  } else {
+    hipLaunchKernelGGL((fa_bwd_dkdv_kernel<D, BF16, kBoth>), grid_kv, dim3(256), 0, st, p);
+  }
   return hipGetLastError();
 }
 
@@ -528,6 +572,14 @@ extern "C" int mpx_attn_bwd(const void* q, const void* k, const void* v, const v
                     ((uintptr_t)workspace & 15u) == 0,
                 "mpx_attn_bwd: 16-byte aligned workspace of %zu bytes required, %zu given", need,
                 workspace_bytes);
+  // The kernels address one (batch, head) of q, dout, k, v with 32-bit byte offsets.
+  const int64_t span = std::max((int64_t)Sq + kBwdTile, (int64_t)Sk + kBwdTile) * 2 *
+                       std::max(std::max(q_strides[2], do_strides[2]),
+                                std::max(k_strides[2], v_strides[2]));
+  if (span >= (1LL << 31)) {
+    set_error("mpx_attn_bwd: seq_len * seq_stride exceeds the 2 GiB addressing range of one head");
+    return MPX_EUNSUPPORTED;
+  }
   const long tiles = (long)B * H * (((Sq > Sk ? Sq : Sk) + kBwdOwn - 1) / kBwdOwn);
   MPX_CHECK_ARG(tiles < (1L << 31) && (long)B * H * Sq < (1L << 35),
                 "mpx_attn_bwd: problem too large");

@@ -108,14 +108,6 @@ __device__ __forceinline__ int page_of(const FwdParams& p, int pos) {
 // LDS stages of the register-staged 16-bit kernel.
 constexpr int kFa16Stages = 2;
 
-// Compile-time integer tag (selects a register set in the unrolled loop).
-template <int N>
-struct Const {
-  static constexpr int value = N;
-};
-
-// Raw buffer resource flags (word 3) for gfx950 buffer loads.
-constexpr int kBufferFlags = 0x00020000;
 
 // Rescale threshold of the lazy running max, in log2 units.
 constexpr float kRescaleThreshold = 8.0f;
@@ -687,49 +679,10 @@ __device__ __forceinline__ void fa16_rows(const FwdParams& pin, const WorkItem w
 // group of 16 lanes whose lane s addresses row base + s/4, columns
 // c0 + 4*(s%4) .. +3, lane s receives column c0 + s of rows base .. base + 3.
 // ---------------------------------------------------------------------------
-// Workgroup barrier without the memory fence of __syncthreads (which would wait
-// for every outstanding load, including the DMA of the tile two steps ahead);
-// the caller has already waited for the loads the other waves need. The empty
-// asm statements keep the compiler from moving LDS accesses across it.
-__device__ __forceinline__ void stage_barrier() {
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
-
-// One 16-byte-per-lane DMA: lane l's bytes land at LDS address lds_addr +
-// 16*l. Issued as inline assembly so the compiler does not track it: its
-// waitcnt pass would otherwise make LDS reads after the loop back-edge wait
-// for every DMA in flight (it cannot tell their target stages apart there).
-// The caller waits for completion with explicit s_waitcnt vmcnt. M0 carries
-// the LDS address; nothing else in these kernels uses M0.
-__device__ __forceinline__ void dma16(u32x4 rsrc, unsigned lds_addr, int voff, int soff) {
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
-               :
-               : "s"(lds_addr), "v"(voff), "s"(rsrc), "s"(soff)
-               : "memory", "m0");
-}
-
 // Offset of a key row without a page: past any pool the host accepts, so its
 // buffer loads return zeros.
 constexpr u32 kNoRowDirect = 0xFFFFFF00u;
 
-// Raw buffer descriptor words (base, stride 0, num_records, gfx950 flags).
-__device__ __forceinline__ u32x4 buffer_desc(const void* base, u32 records = 0x7fffffffu) {
-  const unsigned long long a = (unsigned long long)base;
-  return (u32x4){(u32)a, (u32)(a >> 32) & 0xffffu, records, (u32)kBufferFlags};
-}
-
-__device__ __forceinline__ u32 lds_addr(const void* p) {
-  return (u32)(unsigned long long)(__attribute__((address_space(3))) const void*)p;
-}
-
-__device__ __forceinline__ u32x2 lds_read_tr16(const unsigned char* p) {
-  typedef __attribute__((ext_vector_type(4))) short s16x4;
-  const s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (__attribute__((address_space(3))) s16x4*)(p));
-  return __builtin_bit_cast(u32x2, r);
-}
 
 // PAGED: K/V rows come from the pools through this item's page-table slice,
 // staged in LDS (pages); each lane's DMA offset is its row's (page, slot), and

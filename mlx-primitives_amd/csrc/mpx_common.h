@@ -106,4 +106,58 @@ __device__ __forceinline__ f32x16 mfma32x32x2f32(float a, float b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
 }
 
+// ---- LDS staging helpers (gfx950) ---------------------------------------------
+
+// Compile-time integer tag (selects a register set in the unrolled loop).
+template <int N>
+struct Const {
+  static constexpr int value = N;
+};
+
+// Raw buffer resource flags (word 3) for gfx950 buffer loads.
+constexpr int kBufferFlags = 0x00020000;
+
+// Raw buffer descriptor words (base, stride 0, num_records, gfx950 flags).
+__device__ __forceinline__ u32x4 buffer_desc(const void* base, u32 records = 0x7fffffffu) {
+  const unsigned long long a = (unsigned long long)base;
+  return (u32x4){(u32)a, (u32)(a >> 32) & 0xffffu, records, (u32)kBufferFlags};
+}
+
+__device__ __forceinline__ u32 lds_addr(const void* p) {
+  return (u32)(unsigned long long)(__attribute__((address_space(3))) const void*)p;
+}
+
+// Workgroup barrier without the memory fence of __syncthreads (which would wait
+// for every outstanding load, including DMA into a later stage); the caller
+// has already waited for the loads the other waves need. The empty asm
+// statements keep the compiler from moving LDS accesses across it.
+__device__ __forceinline__ void stage_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// One 16-byte-per-lane DMA: lane l's bytes land at LDS address lds_addr +
+// 16*l. Issued as inline assembly so the compiler does not track it: its
+// waitcnt pass would otherwise make LDS reads after the loop back-edge wait
+// for every DMA in flight (it cannot tell their target stages apart there).
+// The caller waits for completion with explicit s_waitcnt vmcnt. M0 carries
+// the LDS address; nothing else in the kernels that use it touches M0.
+__device__ __forceinline__ void dma16(u32x4 rsrc, unsigned lds_addr, int voff, int soff) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :
+               : "s"(lds_addr), "v"(voff), "s"(rsrc), "s"(soff)
+               : "memory", "m0");
+}
+
+// ds_read_b64_tr_b16: for a group of 16 lanes whose lane s addresses row
+// base + s/4, columns c0 + 4*(s%4) .. +3 of a row-major 16-bit tile, lane s
+// receives column c0 + s of rows base .. base + 3.
+__device__ __forceinline__ u32x2 lds_read_tr16(const void* p) {
+  typedef __attribute__((ext_vector_type(4))) short s16x4;
+  const s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s16x4*)(p));
+  return __builtin_bit_cast(u32x2, r);
+}
+
 }  // namespace mpx
