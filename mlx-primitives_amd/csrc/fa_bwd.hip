@@ -198,9 +198,12 @@ void fa_bwd_dq_kernel(BwdParams p) {
   // Stage s: K tile at [2s], V tile at [2s + 1].
   __shared__ __align__(1024) uint16_t lds[4 * TILE];
 
+  // Grid order: q-tile major, last (under a causal mask the longest) tiles
+  // first; workgroup i runs on XCD i % 8, so with B * H a multiple of 8 every
+  // tile of a head shares one XCD's L2 for its K and V.
   const int n_qt = (p.Sq + kBwdOwn - 1) / kBwdOwn;
-  const int qt = blockIdx.x % n_qt;
-  const int bh = blockIdx.x / n_qt;
+  const int qt = n_qt - 1 - (int)(blockIdx.x / (p.B * p.H));
+  const int bh = blockIdx.x % (p.B * p.H);
   const int b = bh / p.H, h = bh % p.H;
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int j = lane & 31, g = lane >> 5;
@@ -341,9 +344,10 @@ void fa_bwd_dkdv_kernel(BwdParams p) {
   __shared__ __align__(16) float lse_lds[2][kBwdTile];
   __shared__ __align__(16) float dvc_lds[2][kBwdTile];
 
-  const int n_kt = (p.Sk + kBwdOwn - 1) / kBwdOwn;
-  const int kt = blockIdx.x % n_kt;
-  const int bhk = blockIdx.x / n_kt;  // (batch, K/V head)
+  // Grid order: key-tile major, first (under a causal mask the longest) tiles
+  // first, every tile of a K/V head on one XCD when B * H_kv is a multiple of 8.
+  const int kt = (int)(blockIdx.x / (p.B * p.H_kv));
+  const int bhk = blockIdx.x % (p.B * p.H_kv);  // (batch, K/V head)
   const int b = bhk / p.H_kv, hk = bhk % p.H_kv;
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int j = lane & 31, g = lane >> 5;
