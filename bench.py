@@ -6,12 +6,14 @@ on). The same run also times paged-KV decode fp16 (64 sequences, H=32, D=128,
 context ~ U{512..8192}, 16-token pages) under "paged_decode", paged prefill of
 the headline shape over 16-token pages under "paged_prefill", the KV append
 that writes those prompts into pages under "kv_append", and fused RoPE + flash
-attention at the headline shape (BSHD) under "rope_attention".
+attention at the headline shape (BSHD) under "rope_attention", and the backward pass of the
+headline attention (dQ, dK, dV from the saved output and row log-sum-exp)
+under "flash_backward".
 Inputs are synthetic (seeded N(0,1)) and resident in HBM before timing.
 
 Prints ONE JSON line. Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 
-`--only flash|paged|prefill|append|rope|copy` runs a single leg (no CPU baseline) for profiler
+`--only flash|paged|prefill|append|rope|bwd|copy` runs a single leg (no CPU baseline) for profiler
 passes; `copy` streams a 1 GiB float32 buffer through an elementwise kernel,
 the known-size reference for scaling the HBM byte counters. The HBM traffic
 per launch measured by those passes (rocprofv3 FETCH_SIZE / WRITE_SIZE) is read
@@ -42,6 +44,8 @@ FLASH_KERNEL = "fa_fwd16_kernel<128,64,8,bf16>"
 PAGED_KERNELS = "paged_decode_part_kernel + paged_decode_merge_kernel"
 PREFILL_KERNEL = "fa_fwd16_kernel<128,64,8,bf16,paged>"
 APPEND_KERNEL = "kv_append_kernel"
+BWD_KERNELS = ("fa_bwd_dvec_kernel + fa_bwd_dq_kernel<128,bf16> + fa_bwd_dkdv_kernel<128,bf16,K> "
+               "+ fa_bwd_dkdv_kernel<128,bf16,V>")
 
 
 def measured_traffic(key: str):
@@ -212,6 +216,46 @@ def cpu_baseline_append(inp, cfg: dict, budget_s: float) -> dict:
                       f"oracle page-chunk loop in numpy, {t_total:.1f} s"}
 
 
+def cpu_baseline_bwd(cfg: dict, q, k, v, dout, budget_s: float) -> dict:
+    """The oracle's closed-form attention gradient (oracle/attention_grad.py)
+    in float32 numpy on host cores, whole heads of the same workload until
+    ~budget_s of CPU work."""
+    from oracle import attention_grad as oag
+
+    B, H, S, D = q.shape
+    scale = wl.default_scale(D)
+    t_total, done = 0.0, 0
+    for b in range(B):
+        for h in range(H):
+            xs = [x[b:b + 1, h:h + 1].float().cpu().numpy() for x in (q, k, v, dout)]
+            t0 = time.perf_counter()
+            oag.attention_grad(*xs, scale, True, layout="BHSD")
+            t_total += time.perf_counter() - t0
+            done += 1
+            if t_total >= budget_s:
+                break
+        if t_total >= budget_s:
+            break
+    flops = wl.flash_bwd_flops(1, done, S, D, True)
+    return {"value": flops / t_total / 1e12, "unit": "TFLOP/s", "cores": blas_threads(),
+            "kind": "port",
+            "sample": f"{done} of {B * H} (batch, head) pairs of the same workload, oracle "
+                      f"closed-form gradient in float32 numpy, {t_total:.1f} s"}
+
+
+def bwd_step(dev):
+    """dQ, dK, dV of the headline attention: the forward (with its row
+    log-sum-exp) runs once; a step is the backward alone."""
+    from mlx_primitives.attention import flash_attention
+
+    cfg = wl.CONFIGS["flash_bf16_bhsd"]
+    q, k, v = (x.requires_grad_(True) for x in wl.make_qkv(cfg, device=dev))
+    dout = wl.make_qkv(cfg, device=dev, seed=wl.SEED + 1)[0]
+    out = flash_attention(q, k, v, causal=True, layout="BHSD")
+    fn = lambda: torch.autograd.grad(out, (q, k, v), dout, retain_graph=True)
+    return (q, k, v, dout), fn
+
+
 def prefill_step(dev):
     from mlx_primitives.cache import paged_attention
 
@@ -274,6 +318,9 @@ def run_one_leg(args) -> int:
     elif args.only == "rope":
         fn = rope_attention_step(dev)
         work, unit = wl.config_work("flash_bf16_bhsd"), "flop"
+    elif args.only == "bwd":
+        _, fn = bwd_step(dev)
+        work, unit = 2.5 * wl.config_work("flash_bf16_bhsd"), "flop"
     else:
         from mlx_primitives.cache import paged_attention
 
@@ -297,7 +344,8 @@ def main() -> int:
     ap.add_argument("--cpu-budget", type=float, default=10.0,
                     help="seconds of CPU work per baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=["flash", "paged", "prefill", "append", "rope", "copy"],
+    ap.add_argument("--only",
+                    choices=["flash", "paged", "prefill", "append", "rope", "bwd", "copy"],
                     default=None,
                     help="run one leg only (profiler passes); prints that leg's timing")
     args = ap.parse_args()
@@ -374,13 +422,24 @@ def main() -> int:
     log(f"[bench] rope_attention: {r_wall:.3f} ms/step wall, kernels {r_ev:.3f} ms -> "
         f"{r_tf:.1f} TFLOP/s")
 
-    cpu = pcpu = fcpu = acpu = None
+    # ---- backward of the headline attention (dQ, dK, dV), bf16 BHSD -------------------
+    (bq, bk, bv, bdo), bstep = bwd_step(dev)
+    bflops = 2.5 * flops
+    log(f"[bench] flash_backward: warmup {args.warmup}, steps {args.steps}")
+    b_wall, b_ev, b_min, b_med = time_steps(bstep, args.steps, args.warmup)
+    b_tf = bflops / (b_ev * 1e-3) / 1e12
+    log(f"[bench] flash_backward: {b_wall:.3f} ms/step wall, kernels {b_ev:.3f} ms -> "
+        f"{b_tf:.1f} TFLOP/s")
+
+    cpu = pcpu = fcpu = acpu = bcpu = None
     if not args.no_cpu_baseline:
         log("[bench] cpu baselines (oracle restatement on host cores)")
         cpu = cpu_baseline_flash(cfg, q, k, v, args.cpu_budget)
         pcpu = cpu_baseline_paged(pin, pcfg, args.cpu_budget)
         fcpu = cpu_baseline_prefill(finp, wl.CONFIGS[fname], args.cpu_budget)
         acpu = cpu_baseline_append(ainp, wl.CONFIGS[aname], args.cpu_budget)
+        bcpu = cpu_baseline_bwd(cfg, bq.detach(), bk.detach(), bv.detach(), bdo,
+                                args.cpu_budget)
 
     result = {
         "metric": "causal fwd TFLOP/s @S=4096,D=128 + paged-decode HBM GB/s, % of roofline",
@@ -448,6 +507,17 @@ def main() -> int:
                          "kernel": APPEND_KERNEL, "traffic_unit": "bytes per launch"},
             "d2d_copy_same_bytes_gbs": c_gbs,
             "cpu_baseline": acpu,
+        },
+        "flash_backward": {
+            "workload": "flash_attention backward bf16 BHSD B=4 H=32 S=4096 D=128 causal: dQ, dK, "
+                        "dV from the saved output and row log-sum-exp (autograd.grad)",
+            "value": b_tf, "unit": "TFLOP/s", "ms_per_step": b_wall, "kernel_ms": b_ev,
+            "kernel_ms_median": b_med, "kernel_ms_min": b_min, "flop_per_step": bflops,
+            "roofline": {"bound": "mfma", "achieved": b_tf, "peak": PEAK_BF16_TFLOPS,
+                         "unit": "TFLOP/s", "frac": b_tf / PEAK_BF16_TFLOPS,
+                         "kernel": BWD_KERNELS,
+                         "flop_convention": "2.5x forward (5 S^2*D products)"},
+            "cpu_baseline": bcpu,
         },
     }
     print(json.dumps(result), flush=True)

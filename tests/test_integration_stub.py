@@ -34,7 +34,7 @@ def test_stub_loads_and_binds():
     with pytest.raises(ValueError):
         ns["_raise"](-1)
     for fn in ("flash_attention_fwd", "paged_attention_decode", "paged_attention_prefill",
-               "store_kv", "rope"):
+               "store_kv", "rope", "flash_attention_fwd_lse", "flash_attention_bwd"):
         assert callable(ns[fn]), fn
 
 
@@ -164,3 +164,40 @@ def test_stub_rope_matches_api(device):
     ref = rope(x, cos, sin, 5)
     torch.cuda.synchronize()
     assert torch.equal(out, ref)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("layout", ["BSHD", "BHSD"])
+def test_stub_backward_matches_autograd(device, layout):
+    from mlx_primitives.attention import flash_attention
+
+    ns = stub_namespace()
+    g = torch.Generator().manual_seed(9)
+    B, H, S, D = 2, 4, 300, 128
+    shape = (B, S, H, D) if layout == "BSHD" else (B, H, S, D)
+    q, k, v, do = (torch.randn(shape, generator=g).to(torch.bfloat16).to(device)
+                   for _ in range(4))
+    bufs = []
+
+    def alloc(n):
+        bufs.append(torch.empty(n, dtype=torch.uint8, device=device))
+        return bufs[-1].data_ptr()
+
+    st = torch.cuda.current_stream().cuda_stream
+    o = torch.empty_like(q)
+    lse = torch.empty(B, H, S, dtype=torch.float32, device=device)
+    ns["flash_attention_fwd_lse"](q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+                                  lse.data_ptr(), B, H, S, S, D, layout, ns["BF16"],
+                                  1 / math.sqrt(D), 1, alloc=alloc, stream=st)
+    dq, dk, dv = (torch.empty_like(x) for x in (q, k, v))
+    ns["flash_attention_bwd"](q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+                              do.data_ptr(), lse.data_ptr(), dq.data_ptr(), dk.data_ptr(),
+                              dv.data_ptr(), B, H, S, S, D, layout, ns["BF16"],
+                              1 / math.sqrt(D), 1, alloc=alloc, stream=st)
+    qg, kg, vg = (x.clone().requires_grad_(True) for x in (q, k, v))
+    out = flash_attention(qg, kg, vg, causal=True, layout=layout)
+    out.backward(do)
+    torch.cuda.synchronize()
+    assert torch.equal(o, out.detach())
+    for mine, ref in ((dq, qg.grad), (dk, kg.grad), (dv, vg.grad)):
+        assert torch.equal(mine, ref)

@@ -168,6 +168,12 @@ def flash_flops(B: int, H: int, S: int, D: int, causal: bool) -> float:
     return f / 2 if causal else f
 
 
+def flash_bwd_flops(B: int, H: int, S: int, D: int, causal: bool) -> float:
+    """2.5x the forward: the five S^2*D products of the gradient (S = QK^T
+    recomputed, dP = dO V^T, dV, dQ, dK), FlashAttention-2's convention."""
+    return 2.5 * flash_flops(B, H, S, D, causal)
+
+
 def window_flops(B: int, H: int, S: int, D: int, window: int) -> float:
     """4*D per (query, visible key) pair; query i sees min(i, W) + 1 keys."""
     pairs = sum(min(i, window) + 1 for i in range(S))
