@@ -229,6 +229,25 @@ int mpx_rope(const void* x, void* out, const void* cos_cache, const void* sin_ca
              int offset, int n_pos, int dtype, int cache_dtype, void* stream);
 
 /*
+ * mpx_attn_fwd_gqa with Q rotated on load: query row i is rotated to position
+ * q_offset + i (half-split RoPE with the contiguous (n_pos, D/2) cos / sin
+ * tables of cache_dtype, float32 arithmetic, one rounding to dtype; the same
+ * values as mpx_rope applied to q first). K must already be rotated.
+ *
+ * Replaces the Q side of the reference's fused kernel, which rotates Q and K
+ * while loading them (mlx_primitives/kernels/fused_rope_attention.py:766-800,
+ * 939-985). 16-bit dtypes only (float32: MPX_EUNSUPPORTED); q_offset + Sq <=
+ * n_pos; 16-byte aligned tables.
+ */
+int mpx_attn_fwd_rope(const void* q, const void* k, const void* v, void* o,
+                      const int64_t* q_strides, const int64_t* k_strides,
+                      const int64_t* v_strides, const int64_t* o_strides,
+                      int B, int H, int H_kv, int Sq, int Sk, int D, float scale, int causal,
+                      int window_left, int window_right, int dtype,
+                      const void* cos_cache, const void* sin_cache, int q_offset, int n_pos,
+                      int cache_dtype, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Backward pass of the flash attention forward.
  *
  * The reference differentiates flash_attention (and sliding_window_attention,

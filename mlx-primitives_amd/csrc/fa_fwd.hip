@@ -54,6 +54,12 @@ struct FwdParams {
   // m + log2(l + eps), +inf for a row that sees no key: with it
   // P = exp2(s * c - lse) is recomputed by the backward kernels.
   float* lse;
+  // Optional rotary embedding of Q on load (16-bit kernels): query row i is
+  // rotated to position rope_offset + i with the (positions, D/2) cos / sin
+  // tables (element type rope_cdt), as the RoPE kernel would before the call.
+  const void* rope_cos;
+  const void* rope_sin;
+  int rope_offset, rope_cdt;
   // Paged K/V (prefill over a block-table cache; the PAGED kernels only): k
   // and v are the pools (num_blocks, bs, H, D), k_ss / v_ss their token row
   // stride H*D; the rows of batch b come through bt[b, pos / bs].
@@ -67,6 +73,60 @@ struct FwdParams {
 
 // Page-table slice of one work item staged in LDS (entries).
 constexpr int kMaxItemPages = 2048;
+
+// Eight consecutive cos or sin entries of a RoPE table as floats.
+__device__ __forceinline__ void load_angles8(const void* table, int64_t idx, int cdt,
+                                             float (&out)[8]) {
+  if (cdt == MPX_F32) {
+    const f32x4 a = *(const f32x4*)((const float*)table + idx);
+    const f32x4 b = *(const f32x4*)((const float*)table + idx + 4);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      out[i] = a[i];
+      out[4 + i] = b[i];
+    }
+  } else {
+    const u32x4 w = *(const u32x4*)((const uint16_t*)table + idx);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      out[2 * i] = cdt == MPX_BF16 ? h2f<true>((uint16_t)(w[i] & 0xffffu))
+                                   : h2f<false>((uint16_t)(w[i] & 0xffffu));
+      out[2 * i + 1] = cdt == MPX_BF16 ? h2f<true>((uint16_t)(w[i] >> 16))
+                                       : h2f<false>((uint16_t)(w[i] >> 16));
+    }
+  }
+}
+
+// Rotate a lane's Q fragments (dims 16 ks + 8 g .. +7 for ks < NKS) to position
+// pos: the half-split partner of dim 16 ks + 8 g + i is dim 16 (ks + NKS/2) +
+// 8 g + i, held by the same lane, so the rotation needs no data exchange. The
+// arithmetic and rounding are those of the RoPE kernel (rope_pair, one
+// rounding to the 16-bit type).
+template <int NKS, bool BF16>
+__device__ __forceinline__ void rope_q_frags(const FwdParams& p, int pos, int g,
+                                             u32x4 (&qreg)[NKS]) {
+  constexpr int HALF = NKS * 8;
+#pragma unroll
+  for (int ks = 0; ks < NKS / 2; ++ks) {
+    float c[8], sn[8];
+    const int64_t idx = (int64_t)pos * HALF + 16 * ks + 8 * g;
+    load_angles8(p.rope_cos, idx, p.rope_cdt, c);
+    load_angles8(p.rope_sin, idx, p.rope_cdt, sn);
+    u32x4 lo = qreg[ks], hi = qreg[ks + NKS / 2];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      float y1a, y2a, y1b, y2b;
+      rope_pair(h2f<BF16>((uint16_t)(lo[w] & 0xffffu)), h2f<BF16>((uint16_t)(hi[w] & 0xffffu)),
+                c[2 * w], sn[2 * w], y1a, y2a);
+      rope_pair(h2f<BF16>((uint16_t)(lo[w] >> 16)), h2f<BF16>((uint16_t)(hi[w] >> 16)),
+                c[2 * w + 1], sn[2 * w + 1], y1b, y2b);
+      lo[w] = pack2<BF16>(y1a, y1b);
+      hi[w] = pack2<BF16>(y2a, y2b);
+    }
+    qreg[ks] = lo;
+    qreg[ks + NKS / 2] = hi;
+  }
+}
 
 __device__ __forceinline__ int page_of(const FwdParams& p, int pos) {
   return p.bs_log2 >= 0 ? pos >> p.bs_log2 : pos / p.bs;
@@ -288,6 +348,7 @@ __device__ __forceinline__ void fa16_rows(const FwdParams& pin, const WorkItem w
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks) qreg[ks] = src[2 * ks + g];
   }
+  if (p.rope_cos) rope_q_frags<NKS, BF16>(p, p.rope_offset + min(myq, p.Sq - 1), g, qreg);
   if (p.neg) {
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks) qreg[ks] ^= 0x80008000u;
@@ -743,6 +804,7 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& pin, const Wor
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks) qreg[ks] = src[2 * ks + g];
   }
+  if (p.rope_cos) rope_q_frags<NKS, BF16>(p, p.rope_offset + min(myq, p.Sq - 1), g, qreg);
   if (p.neg) {
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks) qreg[ks] ^= 0x80008000u;
@@ -1557,13 +1619,22 @@ extern "C" size_t mpx_attn_fwd_workspace_bytes(int B, int H, int Sq, int Sk, int
   return make_plan(B, H, Sq, Sk, D, causal, window_left, window_right, dtype).ws_bytes;
 }
 
-extern "C" int mpx_attn_fwd_lse(const void* q, const void* k, const void* v, void* o,
-                                float* lse, const int64_t* q_strides, const int64_t* k_strides,
-                                const int64_t* v_strides, const int64_t* o_strides, int B, int H,
-                                int H_kv, int Sq, int Sk, int D, float scale, int causal,
-                                int window_left, int window_right, int dtype, void* workspace,
-                                size_t workspace_bytes, void* stream) {
-  clear_error();
+namespace {
+// Optional extras of the dense forward entries.
+struct FwdExtras {
+  float* lse = nullptr;
+  const void* rope_cos = nullptr;
+  const void* rope_sin = nullptr;
+  int rope_offset = 0, rope_cdt = 0;
+};
+}  // namespace
+
+static int attn_fwd_entry(const void* q, const void* k, const void* v, void* o,
+                          const int64_t* q_strides, const int64_t* k_strides,
+                          const int64_t* v_strides, const int64_t* o_strides, int B, int H,
+                          int H_kv, int Sq, int Sk, int D, float scale, int causal,
+                          int window_left, int window_right, int dtype, void* workspace,
+                          size_t workspace_bytes, void* stream, const FwdExtras& ex) {
   MPX_CHECK_ARG(dtype == MPX_F32 || dtype == MPX_F16 || dtype == MPX_BF16,
                 "mpx_attn_fwd: unknown dtype code %d", dtype);
   MPX_CHECK_ARG(B >= 0 && H >= 0 && Sq >= 0 && Sk >= 0, "mpx_attn_fwd: negative size");
@@ -1615,8 +1686,58 @@ extern "C" int mpx_attn_fwd_lse(const void* q, const void* k, const void* v, voi
   p.neg = scale < 0.f ? 1 : 0;
   p.eps = kSoftmaxEps;
   p.nan_empty = 0;
-  p.lse = lse;
+  p.lse = ex.lse;
+  p.rope_cos = ex.rope_cos;
+  p.rope_sin = ex.rope_sin;
+  p.rope_offset = ex.rope_offset;
+  p.rope_cdt = ex.rope_cdt;
   return run_fwd<false>(p, pl, D, dtype, workspace, (hipStream_t)stream);
+}
+
+extern "C" int mpx_attn_fwd_lse(const void* q, const void* k, const void* v, void* o,
+                                float* lse, const int64_t* q_strides, const int64_t* k_strides,
+                                const int64_t* v_strides, const int64_t* o_strides, int B, int H,
+                                int H_kv, int Sq, int Sk, int D, float scale, int causal,
+                                int window_left, int window_right, int dtype, void* workspace,
+                                size_t workspace_bytes, void* stream) {
+  clear_error();
+  FwdExtras ex;
+  ex.lse = lse;
+  return attn_fwd_entry(q, k, v, o, q_strides, k_strides, v_strides, o_strides, B, H, H_kv, Sq,
+                        Sk, D, scale, causal, window_left, window_right, dtype, workspace,
+                        workspace_bytes, stream, ex);
+}
+
+extern "C" int mpx_attn_fwd_rope(const void* q, const void* k, const void* v, void* o,
+                                 const int64_t* q_strides, const int64_t* k_strides,
+                                 const int64_t* v_strides, const int64_t* o_strides, int B,
+                                 int H, int H_kv, int Sq, int Sk, int D, float scale, int causal,
+                                 int window_left, int window_right, int dtype,
+                                 const void* cos_cache, const void* sin_cache, int q_offset,
+                                 int n_pos, int cache_dtype, void* workspace,
+                                 size_t workspace_bytes, void* stream) {
+  clear_error();
+  if (dtype == MPX_F32) {
+    set_error("mpx_attn_fwd_rope: Q is rotated on load by the 16-bit kernels only");
+    return MPX_EUNSUPPORTED;
+  }
+  MPX_CHECK_ARG(cache_dtype == MPX_F32 || cache_dtype == MPX_F16 || cache_dtype == MPX_BF16,
+                "mpx_attn_fwd_rope: unknown cache dtype code %d", cache_dtype);
+  MPX_CHECK_ARG(q_offset >= 0 && (Sq == 0 || (long)q_offset + Sq <= n_pos),
+                "mpx_attn_fwd_rope: positions %d..%d exceed the %d-row cos/sin caches",
+                q_offset, q_offset + Sq - 1, n_pos);
+  MPX_CHECK_ARG((long)B * H * Sq == 0 || (cos_cache && sin_cache),
+                "mpx_attn_fwd_rope: null cos/sin cache");
+  MPX_CHECK_ARG(aligned16(cos_cache) && aligned16(sin_cache),
+                "mpx_attn_fwd_rope: cos/sin caches must be 16-byte aligned");
+  FwdExtras ex;
+  ex.rope_cos = cos_cache;
+  ex.rope_sin = sin_cache;
+  ex.rope_offset = q_offset;
+  ex.rope_cdt = cache_dtype;
+  return attn_fwd_entry(q, k, v, o, q_strides, k_strides, v_strides, o_strides, B, H, H_kv, Sq,
+                        Sk, D, scale, causal, window_left, window_right, dtype, workspace,
+                        workspace_bytes, stream, ex);
 }
 
 extern "C" int mpx_attn_fwd_gqa(const void* q, const void* k, const void* v, void* o,
@@ -1625,9 +1746,10 @@ extern "C" int mpx_attn_fwd_gqa(const void* q, const void* k, const void* v, voi
                                 int H_kv, int Sq, int Sk, int D, float scale, int causal,
                                 int window_left, int window_right, int dtype, void* workspace,
                                 size_t workspace_bytes, void* stream) {
-  return mpx_attn_fwd_lse(q, k, v, o, nullptr, q_strides, k_strides, v_strides, o_strides, B, H,
-                          H_kv, Sq, Sk, D, scale, causal, window_left, window_right, dtype,
-                          workspace, workspace_bytes, stream);
+  clear_error();
+  return attn_fwd_entry(q, k, v, o, q_strides, k_strides, v_strides, o_strides, B, H, H_kv, Sq,
+                        Sk, D, scale, causal, window_left, window_right, dtype, workspace,
+                        workspace_bytes, stream, FwdExtras());
 }
 
 extern "C" int mpx_attn_fwd(const void* q, const void* k, const void* v, void* o,

@@ -106,6 +106,18 @@ __device__ __forceinline__ f32x16 mfma32x32x2f32(float a, float b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
 }
 
+// Half-split rotary embedding of one dimension pair (x1 = x[i], x2 = x[i + D/2])
+// by the angle whose cosine and sine are c, s, in float32:
+//   y1 = x1 c - x2 s,  y2 = x1 s + x2 c
+// (kernels/rope.py:477-497). Written with explicit fused multiply-adds so every
+// kernel that rotates rounds identically (the standalone RoPE kernel and the
+// flash kernel's rotation of Q on load agree bit for bit).
+__device__ __forceinline__ void rope_pair(float x1, float x2, float c, float s, float& y1,
+                                          float& y2) {
+  y1 = __builtin_fmaf(x1, c, -(x2 * s));
+  y2 = __builtin_fmaf(x1, s, x2 * c);
+}
+
 // ---- LDS staging helpers (gfx950) ---------------------------------------------
 
 // Compile-time integer tag (selects a register set in the unrolled loop).

@@ -103,10 +103,10 @@ __global__ __launch_bounds__(256) void rope_kernel(RopeParams p) {
     V8<T> y1, y2;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const float a = to_f(x1.v[e]), bb = to_f(x2.v[e]);
-      const float c = to_f(cs.v[e]), sv = to_f(sn.v[e]);
-      y1.v[e] = from_f<T>(a * c - bb * sv);
-      y2.v[e] = from_f<T>(a * sv + bb * c);
+      float r1, r2;
+      rope_pair(to_f(x1.v[e]), to_f(x2.v[e]), to_f(cs.v[e]), to_f(sn.v[e]), r1, r2);
+      y1.v[e] = from_f<T>(r1);
+      y2.v[e] = from_f<T>(r2);
     }
     store8(o + d, y1);
     store8(o + half + d, y2);

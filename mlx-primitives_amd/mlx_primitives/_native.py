@@ -80,6 +80,12 @@ def load() -> ctypes.CDLL:
             ctypes.c_float, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
             ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
         ]
+        lib.mpx_attn_fwd_rope.restype = ctypes.c_int
+        lib.mpx_attn_fwd_rope.argtypes = [ctypes.c_void_p] * 4 + [_i64p] * 4 + [
+            ctypes.c_int] * 6 + [ctypes.c_float, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                 ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
+                                 ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t,
+                                 ctypes.c_void_p]
         lib.mpx_attn_bwd.restype = ctypes.c_int
         lib.mpx_attn_bwd.argtypes = [ctypes.c_void_p] * 9 + [_i64p] * 8 + [
             ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
@@ -201,13 +207,33 @@ def attn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor,
              q_strides: Sequence[int], k_strides: Sequence[int], v_strides: Sequence[int],
              o_strides: Sequence[int], B: int, H: int, Sq: int, Sk: int, D: int,
              scale: float, causal: bool, window_left: int = -1, window_right: int = -1,
-             H_kv: Optional[int] = None, lse: Optional[torch.Tensor] = None) -> None:
+             H_kv: Optional[int] = None, lse: Optional[torch.Tensor] = None,
+             q_rope: Optional[tuple] = None) -> None:
     """Enqueue mpx_attn_fwd_lse on the current stream (strides in (b, h, s) order;
     K/V carry H_kv heads, default H; lse: optional contiguous (B, H, Sq) float32
-    that receives each row's base-2 log-sum-exp for the backward)."""
+    that receives each row's base-2 log-sum-exp for the backward). With
+    q_rope = (cos_cache, sin_cache, q_offset) the kernel rotates Q on load
+    (mpx_attn_fwd_rope)."""
     lib = load()
     dev = require_device(q, k, v, o)
     code = dtype_code(q.dtype)
+    if q_rope is not None:
+        if lse is not None:
+            raise ValueError("q_rope and lse cannot be combined")
+        cos, sin, q_offset = q_rope
+        require_device(q, cos, sin)
+        ws_bytes = int(lib.mpx_attn_fwd_workspace_bytes(
+            B, H, Sq, Sk, D, int(causal), window_left, window_right, code))
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
+        rc = lib.mpx_attn_fwd_rope(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+            _strides(q_strides), _strides(k_strides), _strides(v_strides), _strides(o_strides),
+            B, H, H if H_kv is None else H_kv, Sq, Sk, D, float(scale), int(causal),
+            int(window_left), int(window_right), code, cos.data_ptr(), sin.data_ptr(),
+            int(q_offset), int(cos.shape[0]), dtype_code(cos.dtype),
+            ws.data_ptr() if ws is not None else None, ws_bytes, _stream_ptr(dev))
+        _check(rc, "mpx_attn_fwd_rope failed")
+        return
     if lse is not None:
         if (lse.dtype != torch.float32 or not lse.is_contiguous() or lse.device != dev
                 or tuple(lse.shape) != (B, H, Sq)):

@@ -8,6 +8,8 @@ off), allocates the output and calls the HIP kernel.
 
 from __future__ import annotations
 
+from typing import Optional
+
 import torch
 import torch.nn.functional as F
 
@@ -100,16 +102,21 @@ def _attention_with_grad(q, k, v, layout, scale, causal, window_left, window_rig
 
 def run_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, layout: Layout,
                   scale: float, causal: bool, window_left: int = -1,
-                  window_right: int = -1) -> torch.Tensor:
+                  window_right: int = -1, q_rope: Optional[tuple] = None) -> torch.Tensor:
     """Attention forward on the GPU kernel; returns a new tensor shaped like q.
     When autograd tracks q, k or v, the result is differentiable through the
-    gfx950 backward kernels."""
+    gfx950 backward kernels. q_rope = (cos_cache, sin_cache, q_offset) rotates Q
+    inside the kernel (16-bit, D in 32/64/128, no gradients)."""
     _native.require_device(q, k, v)
     B, H, H_kv, Sq, Sk, D = _dims(q, k, layout)
     if q.numel() == 0:
         return torch.empty(q.shape, dtype=q.dtype, device=q.device)
     dk = kernel_head_dim(D)
-    if _needs_grad(q, k, v):
+    if q_rope is not None:
+        if dk != D or q.dtype == torch.float32 or _needs_grad(q, k, v):
+            raise ValueError("in-kernel Q rotation needs 16-bit inputs, D in (32, 64, 128) "
+                             "and no gradients")
+    elif _needs_grad(q, k, v):
         return _attention_with_grad(q, k, v, layout, scale, causal, window_left, window_right)
     qk, kk, vk = (_prepare(x, dk) for x in (q, k, v))
     out_shape = list(q.shape)
@@ -117,7 +124,7 @@ def run_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, layout: Lay
     o = torch.empty(out_shape, dtype=q.dtype, device=q.device)
     _native.attn_fwd(qk, kk, vk, o, _bhs(qk, layout), _bhs(kk, layout), _bhs(vk, layout),
                      _bhs(o, layout), B, H, Sq, Sk, dk, scale, causal, window_left,
-                     window_right, H_kv=H_kv)
+                     window_right, H_kv=H_kv, q_rope=q_rope)
     if dk != D:
         o = o[..., :D].contiguous()
     return o

@@ -2,9 +2,11 @@
 
 Drop-in for mlx_primitives/kernels/fused_rope_attention.py:
 ``fast_fused_rope_attention`` (637-733), ``fused_rope_attention`` (939-985)
-and ``FusedRoPEFlashAttention`` (988-1109). Q and K are rotated by the gfx950
-RoPE kernel into scratch tensors and attention runs on the gfx950 flash
-kernel, with the reference's position-based causal rule
+and ``FusedRoPEFlashAttention`` (988-1109). K is rotated by the gfx950 RoPE
+kernel into a scratch tensor; for 16-bit inputs with head_dim 32, 64 or 128
+the flash kernel rotates Q itself as it loads it (as the reference's fused
+kernel does, fused_rope_attention.py:766-800), otherwise Q goes through the
+RoPE kernel too. Attention uses the reference's position-based causal rule
 (fused_rope_attention.py:125-131): query i at position q_offset + i sees key j
 at position kv_offset + j when kv_offset + j <= q_offset + i. Tensors are
 (batch, seq, heads, head_dim).
@@ -17,6 +19,7 @@ from typing import Optional, Tuple
 
 import torch
 
+from mlx_primitives import _native
 from mlx_primitives.attention._launch import run_attention
 from mlx_primitives.constants import Layout
 from mlx_primitives.kernels.rope import precompute_rope_cache, rope
@@ -63,6 +66,7 @@ def fast_fused_rope_attention(
     703-709). ``use_tiled`` is ignored, as in the reference.
     """
     _check_inputs(q, k, v)
+    _native.require_no_grad(q, k, v)
     batch, seq_q, heads, dim = q.shape
     seq_kv = k.shape[1]
     if scale is None:
@@ -73,19 +77,27 @@ def fast_fused_rope_attention(
         max_pos = max(seq_q + q_offset, seq_kv + kv_offset)
         cos_cache, sin_cache = precompute_rope_cache(max_pos, dim, base=rope_base,
                                                      dtype=q.dtype, device=q.device)
-    q_rot = rope(q, cos_cache, sin_cache, q_offset)
-    k_rot = rope(k, cos_cache, sin_cache, kv_offset)
-    if not causal:
-        return run_attention(q_rot, k_rot, v, Layout.BSHD, scale, False)
     shift = q_offset - kv_offset
-    if shift < 0:
+    if causal and shift < 0:
         raise NotImplementedError(
             "causal fused RoPE attention with kv_offset > q_offset (queries before the first "
             "key) is not supported by the MI355X kernels")
+    k_rot = rope(k, cos_cache, sin_cache, kv_offset)
     # kv_offset + j <= q_offset + i  <=>  j <= i + shift
-    if shift == 0:
-        return run_attention(q_rot, k_rot, v, Layout.BSHD, scale, True)
-    return run_attention(q_rot, k_rot, v, Layout.BSHD, scale, False, window_right=shift)
+    mask = (dict(causal=False) if not causal else
+            dict(causal=True) if shift == 0 else dict(causal=False, window_right=shift))
+    if q.dtype != torch.float32 and dim in (32, 64, 128):
+        # Q is rotated by the attention kernel as it loads it (same arithmetic
+        # and rounding as the RoPE kernel); caches go in as given.
+        if seq_q + q_offset > cos_cache.shape[0]:
+            raise ValueError(f"positions up to {seq_q + q_offset - 1} exceed the cache length "
+                             f"{cos_cache.shape[0]}")
+        cos_c, sin_c = (c if c.is_contiguous() and c.data_ptr() % 16 == 0 else c.contiguous()
+                        for c in (cos_cache, sin_cache))
+        return run_attention(q, k_rot, v, Layout.BSHD, scale,
+                             q_rope=(cos_c, sin_c, q_offset), **mask)
+    q_rot = rope(q, cos_cache, sin_cache, q_offset)
+    return run_attention(q_rot, k_rot, v, Layout.BSHD, scale, **mask)
 
 
 def fused_rope_attention(

@@ -33,7 +33,7 @@ def test_header_declares_expected_entry_points():
         "mpx_paged_decode", "mpx_paged_decode_workspace_bytes", "mpx_paged_prefill",
         "mpx_paged_prefill_workspace_bytes", "mpx_kv_append", "mpx_rope", "mpx_attn_fwd_gqa",
         "mpx_paged_decode_gqa", "mpx_paged_prefill_gqa", "mpx_attn_fwd_lse", "mpx_attn_bwd",
-        "mpx_attn_bwd_workspace_bytes"])
+        "mpx_attn_bwd_workspace_bytes", "mpx_attn_fwd_rope"])
 
 
 def test_library_exports_every_declared_symbol(lib):
@@ -195,3 +195,19 @@ def test_fwd_lse_validates_like_fwd(lib):
     rc = lib.mpx_attn_fwd_lse(16, 16, 16, 16, None, st, st, st, st, 0, 1, 1, 8, 8, 64, 0.1, 1,
                               -1, -1, 2, None, 0, None)
     assert rc == _native.MPX_OK
+
+
+def _fwd_rope(lib, dtype=2, cdt=2, q_offset=0, n_pos=8, ptr=16, cos=16, Sq=8):
+    st = (ctypes.c_int64 * 3)(8 * 64, 8 * 64, 64)
+    return lib.mpx_attn_fwd_rope(ptr, ptr, ptr, ptr, st, st, st, st, 1, 1, 1, Sq, 8, 64, 0.1, 1,
+                                 -1, -1, dtype, cos, cos, q_offset, n_pos, cdt, None, 0, None)
+
+
+def test_fwd_rope_validation(lib):
+    assert _fwd_rope(lib, dtype=0) == _native.MPX_EUNSUPPORTED
+    assert b"16-bit" in lib.mpx_last_error()
+    assert _fwd_rope(lib, cdt=5) == _native.MPX_EINVAL and b"cache dtype" in lib.mpx_last_error()
+    assert _fwd_rope(lib, q_offset=1) == _native.MPX_EINVAL and b"exceed" in lib.mpx_last_error()
+    assert _fwd_rope(lib, cos=None) == _native.MPX_EINVAL and b"null" in lib.mpx_last_error()
+    assert _fwd_rope(lib, cos=24) == _native.MPX_EINVAL and b"aligned" in lib.mpx_last_error()
+    assert _fwd_rope(lib, Sq=0, cos=None) == _native.MPX_OK

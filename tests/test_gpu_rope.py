@@ -187,3 +187,32 @@ def test_module_matches_oracle(device):
                                          causal=True)
         ref = torch.from_numpy(att).reshape(1, 20, 128) @ m.out_proj.weight.double().cpu().T
     np.testing.assert_allclose(out.double().cpu().numpy(), ref.numpy(), rtol=1e-4, atol=1e-4)
+
+
+@pytest.mark.parametrize("dt", ["f16", "bf16"])
+@pytest.mark.parametrize("D", [32, 64, 128, 80])
+@pytest.mark.parametrize("cache_dt", ["same", "f32"])
+@pytest.mark.parametrize("q_off,kv_off,causal", [(0, 0, True), (37, 5, True), (9, 9, False)])
+def test_q_rotation_on_load_bit_identical(device, dt, D, cache_dt, q_off, kv_off, causal):
+    # 16-bit, D in (32, 64, 128): the flash kernel rotates Q as it loads it; the
+    # result equals the RoPE kernel followed by the flash kernel bit for bit
+    # (same rotation arithmetic and rounding). D = 80 takes the RoPE-kernel path.
+    dtype = DT[dt]
+    q = rnd((2, 70, 3, D), 21, dtype).to(device)
+    k = rnd((2, 90, 3, D), 22, dtype).to(device)
+    v = rnd((2, 90, 3, D), 23, dtype).to(device)
+    cdt = torch.float32 if cache_dt == "f32" else dtype
+    n = max(70 + q_off, 90 + kv_off) + 3
+    cos, sin = precompute_rope_cache(n, D, dtype=cdt, device=device)
+    out = fused_rope_attention(q, k, v, cos_cache=cos, sin_cache=sin, q_offset=q_off,
+                               kv_offset=kv_off, causal=causal)
+    qr, kr = rope(q, cos, sin, q_off), rope(k, cos, sin, kv_off)
+    shift = q_off - kv_off
+    if causal and shift:
+        from mlx_primitives.attention._launch import run_attention
+        from mlx_primitives.constants import Layout
+        ref = run_attention(qr, kr, v, Layout.BSHD, 1 / math.sqrt(D), False, window_right=shift)
+    else:
+        ref = flash_attention(qr, kr, v, causal=causal)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)

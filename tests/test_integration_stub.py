@@ -34,7 +34,8 @@ def test_stub_loads_and_binds():
     with pytest.raises(ValueError):
         ns["_raise"](-1)
     for fn in ("flash_attention_fwd", "paged_attention_decode", "paged_attention_prefill",
-               "store_kv", "rope", "flash_attention_fwd_lse", "flash_attention_bwd"):
+               "store_kv", "rope", "flash_attention_fwd_lse", "flash_attention_bwd",
+               "fused_rope_attention_fwd"):
         assert callable(ns[fn]), fn
 
 
@@ -201,3 +202,34 @@ def test_stub_backward_matches_autograd(device, layout):
     assert torch.equal(o, out.detach())
     for mine, ref in ((dq, qg.grad), (dk, kg.grad), (dv, vg.grad)):
         assert torch.equal(mine, ref)
+
+
+@pytest.mark.gpu
+def test_stub_fused_rope_matches_api(device):
+    from mlx_primitives.kernels import fused_rope_attention, precompute_rope_cache
+
+    ns = stub_namespace()
+    g = torch.Generator().manual_seed(11)
+    B, S, H, D, q_off = 2, 150, 4, 128, 20
+    q, k, v = (torch.randn(B, S, H, D, generator=g).to(torch.bfloat16).to(device)
+               for _ in range(3))
+    cos, sin = precompute_rope_cache(S + q_off, D, dtype=torch.bfloat16, device=device)
+    st = torch.cuda.current_stream().cuda_stream
+    kr = torch.empty_like(k)
+    ns["rope"](k.data_ptr(), kr.data_ptr(), cos.data_ptr(), sin.data_ptr(), B, S, H, D, q_off,
+               cos.shape[0], ns["BF16"], ns["BF16"], stream=st)
+    o = torch.empty_like(q)
+    bufs = []
+
+    def alloc(n):
+        bufs.append(torch.empty(n, dtype=torch.uint8, device=device))
+        return bufs[-1].data_ptr()
+
+    ns["fused_rope_attention_fwd"](q.data_ptr(), kr.data_ptr(), v.data_ptr(), o.data_ptr(),
+                                   cos.data_ptr(), sin.data_ptr(), B, H, S, S, D, ns["BF16"],
+                                   ns["BF16"], cos.shape[0], 1 / math.sqrt(D), q_offset=q_off,
+                                   kv_offset=q_off, causal=1, alloc=alloc, stream=st)
+    ref = fused_rope_attention(q, k, v, cos_cache=cos, sin_cache=sin, q_offset=q_off,
+                               kv_offset=q_off, causal=True)
+    torch.cuda.synchronize()
+    assert torch.equal(o, ref)
