@@ -266,9 +266,9 @@ int mpx_attn_fwd_rope(const void* q, const void* k, const void* v, void* o,
  * sums over its group of query heads). All tensors use {batch, head, seq}
  * element strides like mpx_attn_fwd, D contiguous; dq, dk, dv must not
  * overlap the inputs. Masks (causal, windows) are those of the forward call.
- * Scope: dtype float16 / bfloat16 (float32: MPX_EUNSUPPORTED), D in {64, 128},
- * scale > 0. Workspace: mpx_attn_bwd_workspace_bytes(B, H, Sq) bytes, 16-byte
- * aligned (per-row rowsum(dout * o)).
+ * Scope: dtype float32 / float16 / bfloat16, D in {64, 128}, scale > 0.
+ * Workspace: mpx_attn_bwd_workspace_bytes(B, H, Sq) bytes, 16-byte aligned
+ * (per-row rowsum(dout * o)).
  */
 int mpx_attn_fwd_lse(const void* q, const void* k, const void* v, void* o, float* lse,
                      const int64_t* q_strides, const int64_t* k_strides,

@@ -24,7 +24,8 @@ INCLUDE = os.path.join(REPO, "include")
 LIB_DIR = os.path.join(HERE, "mlx_primitives", "_lib")
 LIB_PATH = os.path.join(LIB_DIR, "libmpx_attn.so")
 
-SOURCES = ["abi.hip", "fa_fwd.hip", "fa_bwd.hip", "paged_decode.hip", "kv_cache.hip", "rope.hip"]
+SOURCES = ["abi.hip", "fa_fwd.hip", "fa_bwd.hip", "fa_bwd32.hip", "paged_decode.hip",
+           "kv_cache.hip", "rope.hip"]
 # Per-source device-compiler options. The backward kernels hold their MFMA
 # accumulators in arch VGPRs (the default heuristic moves them through AGPRs
 # with a copy per element per tile).

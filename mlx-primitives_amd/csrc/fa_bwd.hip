@@ -22,34 +22,13 @@
 // exchanged) so that C elements 8h..8h+7 of a lane are 8 consecutive rows:
 // packed, they are directly the B operand of the next product over those rows.
 // Transposed operands come from the row-major tiles through ds_read_b64_tr_b16.
-#include "mpx_common.h"
+#include "fa_bwd.h"
 
 #include <algorithm>
 #include <cmath>
 
 namespace mpx {
 
-struct BwdParams {
-  const void* q;
-  const void* k;
-  const void* v;
-  const void* o;
-  const void* dout;
-  const float* lse;   // (B, H, Sq) log2 units, +inf for rows without keys
-  float* dvec;        // (B, H, Sq) workspace
-  void* dq;
-  void* dk;
-  void* dv;
-  int64_t q_sb, q_sh, q_ss, k_sb, k_sh, k_ss, v_sb, v_sh, v_ss, o_sb, o_sh, o_ss;
-  int64_t do_sb, do_sh, do_ss, dq_sb, dq_sh, dq_ss, dk_sb, dk_sh, dk_ss, dv_sb, dv_sh, dv_ss;
-  int B, H, H_kv, kv_group, Sq, Sk;  // K/V (and dK/dV) carry H_kv = H / kv_group heads
-  int win_left, win_right;  // -1 = unbounded (causal: win_right = 0)
-  float scale, c;           // c = scale * log2(e)
-};
-
-constexpr int kBwdWaves = 4;    // waves per workgroup (one per SIMD)
-constexpr int kBwdOwn = 32 * kBwdWaves;  // rows (or keys) a workgroup owns
-constexpr int kBwdTile = 64;    // streamed rows per step
 
 // LDS tiles are (64, D) row-major without padding; the 16-byte chunk c of row
 // r sits at slot c ^ swz(r). Each tile is read two ways, and the swizzle keeps
@@ -545,10 +524,8 @@ extern "C" int mpx_attn_bwd(const void* q, const void* k, const void* v, const v
                             int window_left, int window_right, int dtype, void* workspace,
                             size_t workspace_bytes, void* stream) {
   clear_error();
-  if (dtype != MPX_F16 && dtype != MPX_BF16) {
-    set_error("mpx_attn_bwd: dtype code %d not supported (the backward is 16-bit only)", dtype);
-    return dtype == MPX_F32 ? MPX_EUNSUPPORTED : MPX_EINVAL;
-  }
+  MPX_CHECK_ARG(dtype == MPX_F32 || dtype == MPX_F16 || dtype == MPX_BF16,
+                "mpx_attn_bwd: unknown dtype code %d", dtype);
   MPX_CHECK_ARG(B >= 0 && H >= 0 && Sq >= 0 && Sk >= 0, "mpx_attn_bwd: negative size");
   MPX_CHECK_ARG(H_kv > 0 ? H % H_kv == 0 : H == 0,
                 "mpx_attn_bwd: %d query heads are not a multiple of %d K/V heads", H, H_kv);
@@ -565,11 +542,12 @@ extern "C" int mpx_attn_bwd(const void* q, const void* k, const void* v, const v
     MPX_CHECK_ARG(((uintptr_t)ptrs[i] & 15u) == 0, "mpx_attn_bwd: tensors must be 16-byte aligned");
   const int64_t* all[8] = {q_strides, k_strides, v_strides, o_strides,
                            do_strides, dq_strides, dk_strides, dv_strides};
+  const int vec = dtype == MPX_F32 ? 4 : 8;
   for (int t = 0; t < 8; ++t) {
     MPX_CHECK_ARG(all[t] != nullptr, "mpx_attn_bwd: null strides");
     for (int i = 0; i < 3; ++i)
-      MPX_CHECK_ARG(all[t][i] >= 0 && all[t][i] % 8 == 0,
-                    "mpx_attn_bwd: strides must be non-negative multiples of 8 elements");
+      MPX_CHECK_ARG(all[t][i] >= 0 && all[t][i] % vec == 0,
+                    "mpx_attn_bwd: strides must be non-negative multiples of %d elements", vec);
   }
   const size_t need = mpx_attn_bwd_workspace_bytes(B, H, Sq);
   MPX_CHECK_ARG(workspace != nullptr && workspace_bytes >= need &&
@@ -580,7 +558,7 @@ extern "C" int mpx_attn_bwd(const void* q, const void* k, const void* v, const v
   const int64_t span = std::max((int64_t)Sq + kBwdTile, (int64_t)Sk + kBwdTile) * 2 *
                        std::max(std::max(q_strides[2], do_strides[2]),
                                 std::max(k_strides[2], v_strides[2]));
-  if (span >= (1LL << 31)) {
+  if (dtype != MPX_F32 && span >= (1LL << 31)) {
     set_error("mpx_attn_bwd: seq_len * seq_stride exceeds the 2 GiB addressing range of one head");
     return MPX_EUNSUPPORTED;
   }
@@ -606,7 +584,9 @@ extern "C" int mpx_attn_bwd(const void* q, const void* k, const void* v, const v
   p.c = scale * kLog2e;
   hipStream_t st = (hipStream_t)stream;
   hipError_t e;
-  if (dtype == MPX_BF16)
+  if (dtype == MPX_F32)
+    e = launch_bwd32(p, D, st);
+  else if (dtype == MPX_BF16)
     e = D == 64 ? launch_bwd<64, true>(p, st) : launch_bwd<128, true>(p, st);
   else
     e = D == 64 ? launch_bwd<64, false>(p, st) : launch_bwd<128, false>(p, st);

@@ -88,11 +88,10 @@ class _FlashAttentionFn(torch.autograd.Function):
 
 
 def _attention_with_grad(q, k, v, layout, scale, causal, window_left, window_right):
-    if q.dtype not in (torch.float16, torch.bfloat16) or not scale > 0:
+    if not scale > 0:
         raise NotImplementedError(
-            "mlx_primitives (MI355X build) differentiates attention for float16 / bfloat16 "
-            f"inputs with scale > 0 (got {q.dtype}, scale={scale}); run float32 attention "
-            "under torch.no_grad()")
+            "mlx_primitives (MI355X build) differentiates attention with scale > 0 only "
+            f"(got scale={scale}); run it under torch.no_grad()")
     D = q.shape[-1]
     dk = 64 if D <= 64 else 128
     qk, kk, vk = (_prepare(x, dk) for x in (q, k, v))

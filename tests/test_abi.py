@@ -174,7 +174,7 @@ def _bwd(lib, dtype=2, D=64, B=1, H=2, H_kv=2, Sq=8, Sk=8, scale=0.1, ptr=16, ws
 def test_bwd_validation(lib):
     assert lib.mpx_attn_bwd_workspace_bytes(4, 32, 4096) == 4 * 32 * 4096 * 4
     assert lib.mpx_attn_bwd_workspace_bytes(0, 32, 4096) == 0
-    assert _bwd(lib, dtype=0) == _native.MPX_EUNSUPPORTED and b"16-bit" in lib.mpx_last_error()
+    assert _bwd(lib, stride=66, dtype=0) == _native.MPX_EINVAL  # f32: multiples of 4 elements
     assert _bwd(lib, dtype=9) == _native.MPX_EINVAL
     assert _bwd(lib, D=32) == _native.MPX_EUNSUPPORTED and b"head_dim" in lib.mpx_last_error()
     assert _bwd(lib, scale=-1.0) == _native.MPX_EINVAL and b"positive" in lib.mpx_last_error()
