@@ -6,7 +6,7 @@ float64 and a JSON `meta` string (no pickled objects: np.load with
 allow_pickle=False reads them).
 
 The expected output is the float64 oracle (oracle/attention.py,
-oracle/paged.py, oracle/kv_cache.py). Before a fixture is written it is checked
+oracle/attention_grad.py, oracle/paged.py, oracle/kv_cache.py). Before a fixture is written it is checked
 against an independent evaluation: for attention,
 torch.nn.functional.scaled_dot_product_attention in float64 with an explicit
 mask, the library routine the reference's own
@@ -36,6 +36,7 @@ if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
 from oracle import attention as oa  # noqa: E402
+from oracle import attention_grad as oag  # noqa: E402
 from oracle import kv_cache as ok  # noqa: E402
 from oracle import paged as op  # noqa: E402
 
@@ -102,6 +103,30 @@ def flash_case(name, shape, dtype, layout, causal, seed, scale=None):
     agree(name, to_bhsd(exp, layout), ref)
     save(name, {"kind": "flash", "dtype": dtype, "layout": layout, "causal": causal,
                 "scale": scale}, q=q, k=k, v=v, expected=exp)
+
+
+def grad_case(name, shape, dtype, layout, causal, window, seed):
+    """dq, dk, dv (stacked) of sum(out * dout) for flash (window < 0) or sliding
+    window attention; checked against torch autograd through float64 SDPA."""
+    g = torch.Generator().manual_seed(seed)
+    q, k, v, d = (rounded(shape, dtype, g) for _ in range(4))
+    D = shape[-1]
+    s = 1.0 / math.sqrt(D)
+    wl, wr = (window, -1 if causal else window) if window >= 0 else (-1, -1)
+    exp = np.stack(oag.attention_grad(*(x.astype(np.float64) for x in (q, k, v, d)), s, causal,
+                                      wl, wr, layout=layout))
+    ts = [torch.from_numpy(np.ascontiguousarray(to_bhsd(x, layout))).double().requires_grad_(True)
+          for x in (q, k, v)]
+    Sq = ts[0].shape[2]
+    keep = torch.from_numpy(window_keep(Sq, Sq, causal, wl, wr))
+    out = torch.nn.functional.scaled_dot_product_attention(*ts, attn_mask=keep, scale=s)
+    (out * torch.from_numpy(np.ascontiguousarray(to_bhsd(d, layout))).double()).sum().backward()
+    ref = np.stack([t.grad.numpy() for t in ts])
+    if layout == "BSHD":
+        ref = np.swapaxes(ref, 2, 3)
+    agree(name, exp, ref)
+    save(name, {"kind": "grad", "dtype": dtype, "layout": layout, "causal": causal,
+                "window": window}, q=q, k=k, v=v, dout=d, expected=exp)
 
 
 def window_case(name, shape, dtype, W, causal, seed):
@@ -255,6 +280,10 @@ def main():
     # append: starts inside a page, spans over pages, a decode-style single token, nothing
     kv_append_case("kv_append_ragged_bf16", 20, [3, 16, 0], [20, 1, 0],
                    [[5, 0, 7], [2, 6, 1], [3, 4, 8]], 9, 8, 2, 64, "bfloat16", 113)
+    # gradients (dq, dk, dv of sum(out * dout)): flash causal / full, sliding window
+    grad_case("grad_causal_bf16_bhsd", (1, 2, 50, 64), "bfloat16", "BHSD", True, -1, 114)
+    grad_case("grad_full_f16_bshd_d128", (1, 33, 2, 128), "float16", "BSHD", False, -1, 115)
+    grad_case("grad_window_f32_w9", (1, 60, 2, 64), "float32", "BSHD", True, 9, 116)
 
 
 if __name__ == "__main__":

@@ -17,6 +17,7 @@ import pytest
 import torch
 
 from oracle import attention as oa
+from oracle import attention_grad as oag
 from oracle import kv_cache as ok
 from oracle import paged as op
 
@@ -48,6 +49,13 @@ def oracle_output(meta, a):
     if kind == "chunked":
         return oa.chunked_cross_attention(f64["q"], f64["k"], f64["v"],
                                           chunk_size=meta["chunk_size"], causal=meta["causal"])
+    if kind == "grad":
+        W = meta["window"]
+        wl, wr = (W, -1 if meta["causal"] else W) if W >= 0 else (-1, -1)
+        D = a["q"].shape[-1]
+        return np.stack(oag.attention_grad(f64["q"], f64["k"], f64["v"], f64["dout"],
+                                           1.0 / math.sqrt(D), meta["causal"], wl, wr,
+                                           layout=meta["layout"]))
     if kind == "kv_append":
         kp, vp = f64["k_pool"].copy(), f64["v_pool"].copy()
         ok.kv_append(kp, vp, a["block_tables"], f64["k"], f64["v"], a["start_pos"],
@@ -66,7 +74,7 @@ def oracle_output(meta, a):
 
 
 def test_fixtures_present():
-    assert len(FIXTURES) >= 13
+    assert len(FIXTURES) >= 16
 
 
 @pytest.mark.parametrize("path", FIXTURES, ids=fixture_id)
@@ -86,6 +94,20 @@ def test_kernel_matches_golden(device, path):
     t = {k: torch.from_numpy(v).to(dt if v.dtype == np.float32 else torch.int32).to(device)
          for k, v in a.items() if k != "expected"}
     kind = meta["kind"]
+    if kind == "grad":
+        # gradients through autograd -> mpx_attn_bwd, at the reference's gradient bar
+        # (tests/parity/shared/tolerance_config.py:57, 363-387: 10x the forward's)
+        qg, kg, vg = (t[n].clone().requires_grad_(True) for n in ("q", "k", "v"))
+        if meta["window"] >= 0:
+            out = sliding_window_attention(qg, kg, vg, meta["window"], causal=meta["causal"])
+        else:
+            out = flash_attention(qg, kg, vg, causal=meta["causal"], layout=meta["layout"])
+        out.backward(t["dout"])
+        got = torch.stack([qg.grad, kg.grad, vg.grad]).double().cpu().numpy()
+        rtol, atol = {torch.float32: (1e-3, 1e-4), torch.float16: (1e-2, 1e-2),
+                      torch.bfloat16: (1e-1, 1e-1)}[dt]
+        np.testing.assert_allclose(got, a["expected"], rtol=rtol, atol=atol)
+        return
     if kind == "flash":
         out = flash_attention(t["q"], t["k"], t["v"], scale=meta["scale"], causal=meta["causal"],
                               layout=meta["layout"])
