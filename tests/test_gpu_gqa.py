@@ -103,3 +103,27 @@ def test_paged_gqa(device, dtype, Sq, H, H_kv, D):
     ref = op.paged_attention(q.double().numpy(), kpe.double().numpy(), vpe.double().numpy(),
                              tables.numpy(), lens_t.numpy(), block_size=16, causal=True)
     check(out, ref, dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("H,H_kv,D", [(16, 8, 128), (16, 4, 64), (64, 8, 128), (8, 1, 32),
+                                      (24, 8, 128)])
+def test_gqa_decode_alibi_ragged(device, dtype, H, H_kv, D):
+    # groups 2, 3, 4, 8 with ALiBi, ragged contexts incl. a missing page and an
+    # empty sequence (NaN row)
+    from mlx_primitives.cache import get_alibi_slopes
+
+    lens = [1000, 1, 0, 517]
+    q, kp, vp, tables, lens_t = paged_inputs(dtype, 4, 1, H, H_kv, D, 16, lens, H + D)
+    tables[3, 5] = -1
+    d = lambda x: x.to(device)
+    slopes = get_alibi_slopes(H)
+    out = paged_attention(d(q), d(kp), d(vp), d(tables), d(lens_t), alibi_slopes=d(slopes),
+                          enable_gqa=True)
+    g = H // H_kv
+    ref = op.paged_attention(q.double().numpy(), kp.repeat_interleave(g, dim=2).double().numpy(),
+                             vp.repeat_interleave(g, dim=2).double().numpy(), tables.numpy(),
+                             lens_t.numpy(), block_size=16, alibi_slopes=slopes.double().numpy())
+    got = out.double().cpu().numpy()
+    assert np.isnan(got[2]).all() and np.isnan(ref[2]).all()
+    check(out[[0, 1, 3]], ref[[0, 1, 3]], dtype)
