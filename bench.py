@@ -6,9 +6,10 @@ on). The same run also times paged-KV decode fp16 (64 sequences, H=32, D=128,
 context ~ U{512..8192}, 16-token pages) under "paged_decode", paged prefill of
 the headline shape over 16-token pages under "paged_prefill", the KV append
 that writes those prompts into pages under "kv_append", and fused RoPE + flash
-attention at the headline shape (BSHD) under "rope_attention", and the backward pass of the
+attention at the headline shape (BSHD) under "rope_attention", the backward pass of the
 headline attention (dQ, dK, dV from the saved output and row log-sum-exp)
-under "flash_backward".
+under "flash_backward", and the sliding-window (config 3) and chunked
+cross-attention (config 5) workloads under "sliding_window" and "chunked_cross".
 Inputs are synthetic (seeded N(0,1)) and resident in HBM before timing.
 
 Prints ONE JSON line. Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
@@ -431,6 +432,30 @@ def main() -> int:
     log(f"[bench] flash_backward: {b_wall:.3f} ms/step wall, kernels {b_ev:.3f} ms -> "
         f"{b_tf:.1f} TFLOP/s")
 
+    # ---- config 3: sliding window W=4096, config 5: chunked cross attention ------------
+    from mlx_primitives.attention import chunked_cross_attention, sliding_window_attention
+
+    wcfg = wl.CONFIGS["window_bf16_bshd"]
+    wq, wk, wv = wl.make_qkv(wcfg, device=dev)
+    wflops = wl.config_work("window_bf16_bshd")
+    wstep = lambda: sliding_window_attention(wq, wk, wv, wcfg["window"], causal=True)
+    log(f"[bench] sliding_window: warmup {args.warmup}, steps {args.steps}")
+    w_wall, w_ev, w_min, w_med = time_steps(wstep, args.steps, args.warmup)
+    w_tf = wflops / (w_ev * 1e-3) / 1e12
+    log(f"[bench] sliding_window: kernel {w_ev:.3f} ms -> {w_tf:.1f} TFLOP/s")
+    del wq, wk, wv
+    ccfg = wl.CONFIGS["chunked_bf16"]
+    cq, ck, cv = wl.make_qkv(ccfg, device=dev)
+    cflops = wl.config_work("chunked_bf16")
+    cbytes = 2.0 * (cq.numel() * 2 + ck.numel() + cv.numel())  # q, o + k, v once, bf16
+    cstep2 = lambda: chunked_cross_attention(cq, ck, cv, chunk_size=ccfg["chunk_size"])
+    log(f"[bench] chunked_cross: warmup {args.warmup}, steps {args.steps}")
+    k_wall, k_ev, k_min, k_med = time_steps(cstep2, args.steps, args.warmup)
+    k_tf = cflops / (k_ev * 1e-3) / 1e12
+    k_gbs = cbytes / (k_ev * 1e-3) / 1e9
+    log(f"[bench] chunked_cross: kernels {k_ev:.3f} ms -> {k_tf:.1f} TFLOP/s, {k_gbs:.0f} GB/s")
+    del cq, ck, cv
+
     cpu = pcpu = fcpu = acpu = bcpu = None
     if not args.no_cpu_baseline:
         log("[bench] cpu baselines (oracle restatement on host cores)")
@@ -507,6 +532,28 @@ def main() -> int:
                          "kernel": APPEND_KERNEL, "traffic_unit": "bytes per launch"},
             "d2d_copy_same_bytes_gbs": c_gbs,
             "cpu_baseline": acpu,
+        },
+        "sliding_window": {
+            "workload": "sliding_window_attention bf16 BSHD B=2 S=8192 H=32 D=128 causal, "
+                        "window_size=4096 (keys [i-4096, i])",
+            "value": w_tf, "unit": "TFLOP/s", "ms_per_step": w_wall, "kernel_ms": w_ev,
+            "kernel_ms_median": w_med, "kernel_ms_min": w_min, "flop_per_step": wflops,
+            "roofline": {"bound": "mfma", "achieved": w_tf, "peak": PEAK_BF16_TFLOPS,
+                         "unit": "TFLOP/s", "frac": w_tf / PEAK_BF16_TFLOPS,
+                         "kernel": "fa_fwd16_kernel<128,64,8,bf16>"},
+        },
+        "chunked_cross": {
+            "workload": "chunked_cross_attention bf16 BSHD q (1,512,16,64), k/v (1,65536,16,64), "
+                        "non-causal, chunk_size 1024",
+            "value": k_tf, "unit": "TFLOP/s", "ms_per_step": k_wall, "kernel_ms": k_ev,
+            "kernel_ms_median": k_med, "kernel_ms_min": k_min, "flop_per_step": cflops,
+            "bytes_per_step": cbytes,
+            "roofline": {"bound": "mfma", "achieved": k_tf, "peak": PEAK_BF16_TFLOPS,
+                         "unit": "TFLOP/s", "frac": k_tf / PEAK_BF16_TFLOPS,
+                         "kernel": "fa_fwd16_kernel<64,64,8,bf16> (split-KV) + "
+                                   "fa_split_merge_kernel"},
+            "hbm_roofline": {"achieved": k_gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                             "frac": k_gbs / PEAK_HBM_GBS},
         },
         "flash_backward": {
             "workload": "flash_attention backward bf16 BHSD B=4 H=32 S=4096 D=128 causal: dQ, dK, "
