@@ -749,19 +749,28 @@ constexpr u32 kNoRowDirect = 0xFFFFFF00u;
 // staged in LDS (pages); each lane's DMA offset is its row's (page, slot), and
 // a row without a page gets an offset past the pool, which the buffer range
 // check turns into zeros; those keys are masked.
-template <int NW, bool BF16, int NST, bool PAGED>
+// Swizzle of the D = 64 direct tiles (128-byte rows, 8 chunks): chunk c of row
+// r sits at slot c ^ swz64(r), conflict-free both for 16 lanes reading one
+// chunk of 16 consecutive rows (K operands) and for the transposing read of 4
+// consecutive rows x 4 consecutive chunks (V^T operands).
+__device__ __forceinline__ int swz64(int r) { return (((r >> 1) & 1) << 2) | ((r >> 2) & 3); }
+
+template <int D, int NW, bool BF16, int NST, bool PAGED>
 __device__ __forceinline__ void fa16_rows_direct(const FwdParams& pin, const WorkItem wi,
                                                  unsigned char* __restrict__ st0,
                                                  unsigned char* __restrict__ st1,
                                                  unsigned char* __restrict__ st2,
                                                  unsigned char* __restrict__ st3,
                                                  int* __restrict__ pages) {
-  constexpr int D = 128, BN = 64, BM = 32 * NW;
+  constexpr int BN = 64, BM = 32 * NW;
   constexpr int NB = BN / 32, NSL = BN / 16, NKS = D / 16, NDB = D / 32;
   constexpr int ROWB = 2 * D;          // bytes per K or V row
   constexpr int KBYTES = BN * ROWB;    // one K (or V) tile
   constexpr int STAGEB = 2 * KBYTES;   // K then V
-  static_assert(NW == 8, "each wave stages rows 4*wave .. +3 and +32 .. +35");
+  constexpr int RPD = 1024 / ROWB;     // rows per DMA instruction (64 lanes x 16 bytes)
+  constexpr int NDMA = BN / (RPD * NW);  // DMA instructions per wave per K (or V) tile
+  static_assert(NW == 8 && (D == 128 || D == 64),
+                "each wave stages rows RPD*wave .. +RPD-1 (and +32 .. for D = 128)");
   // Paged: keys exist up to this sequence's context length.
   FwdParams p = pin;
   if constexpr (PAGED) p.Sk = max(0, min(pin.ctx[wi.b], pin.max_blocks * pin.bs));
@@ -814,10 +823,17 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& pin, const Wor
   __builtin_amdgcn_s_waitcnt(0x0F70);
 
   // DMA lane mapping: this wave's first instruction fills LDS rows
-  // 4*wave .. +3 (lane -> row lr, slot lane%16), the second rows lr + 32.
-  const int lr = 4 * wave + (lane >> 4);
-  const int kchunk = (lane & 15) ^ (lr & 15);
-  const int vchunk = (lane & 15) ^ (4 * (lr & 3));
+  // RPD*wave .. +RPD-1 (lane -> row lr, slot lane % (ROWB/16)); for D = 128 the
+  // second fills rows lr + 32.
+  int lr, kchunk, vchunk;
+  if constexpr (D == 128) {
+    lr = 4 * wave + (lane >> 4);
+    kchunk = (lane & 15) ^ (lr & 15);
+    vchunk = (lane & 15) ^ (4 * (lr & 3));
+  } else {
+    lr = 8 * wave + (lane >> 3);
+    kchunk = vchunk = (lane & 7) ^ swz64(lr);
+  }
   const int kgo = (lr * (int)p.k_ss + kchunk * 8) * 2;
   const int vgo = (lr * (int)p.v_ss + vchunk * 8) * 2;
   const int k32 = 32 * (int)p.k_ss * 2, v32 = 32 * (int)p.v_ss * 2;
@@ -826,14 +842,14 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& pin, const Wor
     return S == 0 ? st0 : (S == 1 ? st1 : (S == 2 ? st2 : st3));
   };
   auto load_tile = [&](int kv0, unsigned char* stbase) __attribute__((always_inline)) {
-    const u32 kdst = lds_addr(stbase + wave * 4 * ROWB);
+    const u32 kdst = lds_addr(stbase + wave * RPD * ROWB);
     const u32 vdst = kdst + KBYTES;
     if constexpr (PAGED) {
-      // Rows lr and lr + 32 through the page table (32-bit offsets: the
+      // Rows lr (and lr + 32) through the page table (32-bit offsets: the
       // host keeps each pool below 4 GiB - 256 bytes).
       const u32 row_bytes = (u32)p.k_ss * 2u;
 #pragma unroll
-      for (int r = 0; r < 2; ++r) {
+      for (int r = 0; r < NDMA; ++r) {
         const int pos = kv0 + lr + 32 * r;
         u32 koff = kNoRowDirect, voff = kNoRowDirect;
         if (pos < p.Sk) {
@@ -853,15 +869,15 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& pin, const Wor
     const int kso = kv0 * (int)p.k_ss * 2, vso = kv0 * (int)p.v_ss * 2;
     if (kv0 + BN <= p.Sk) {
       dma16(krs, kdst, kgo, kso);
-      dma16(krs, kdst + 32 * ROWB, kgo, kso + k32);
+      if constexpr (NDMA == 2) dma16(krs, kdst + 32 * ROWB, kgo, kso + k32);
       dma16(vrs, vdst, vgo, vso);
-      dma16(vrs, vdst + 32 * ROWB, vgo, vso + v32);
+      if constexpr (NDMA == 2) dma16(vrs, vdst + 32 * ROWB, vgo, vso + v32);
     } else {
       // Tail tile: rows past Sk re-read the last valid row (their scores are
       // masked, so their weights are exactly 0).
       const int lim = p.Sk - 1 - kv0;
 #pragma unroll
-      for (int r = 0; r < 2; ++r) {
+      for (int r = 0; r < NDMA; ++r) {
         const int row = min(lr + 32 * r, lim);
         dma16(krs, kdst + r * 32 * ROWB, (row * (int)p.k_ss + kchunk * 8) * 2, kso);
         dma16(vrs, vdst + r * 32 * ROWB, (row * (int)p.v_ss + vchunk * 8) * 2, vso);
@@ -872,7 +888,7 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& pin, const Wor
   // QK operand (A = K rows) of lane (j, g): row nb*32 + krow_perm, logical
   // chunk 2*ks + g, stored at slot (2*ks + g) ^ (row & 15).
   const int krow_perm = (j & ~12) | ((j & 4) << 1) | ((j & 8) >> 1);
-  const int ky = krow_perm & 15;
+  const int ky = D == 128 ? krow_perm & 15 : swz64(krow_perm);
   int kaddr[NKS];
 #pragma unroll
   for (int ks = 0; ks < NKS; ++ks)
@@ -880,11 +896,23 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& pin, const Wor
   // PV operand (A = V^T) of lane L = j + 32g: rows 16*sl + 8g + 4h + s/4,
   // columns 32*db + 16*(L/16 % 2) + 4*(s%4) of the transposing read, s = L%16.
   const int s16 = lane & 15;
-  int vaddr[NDB];
+  int vaddr[NDB], vaddr_hi[NDB];  // rows +16 sl (lo), +16 sl + 4 (hi)
 #pragma unroll
-  for (int db = 0; db < NDB; ++db)
-    vaddr[db] = (8 * g + (s16 >> 2)) * ROWB + 64 * (db ^ (s16 >> 2)) + 32 * ((lane >> 4) & 1) +
-                8 * (s16 & 3);
+  for (int db = 0; db < NDB; ++db) {
+    if constexpr (D == 128) {
+      vaddr[db] = (8 * g + (s16 >> 2)) * ROWB + 64 * (db ^ (s16 >> 2)) +
+                  32 * ((lane >> 4) & 1) + 8 * (s16 & 3);
+      vaddr_hi[db] = vaddr[db] + 4 * ROWB;
+    } else {
+      // the swizzle of D = 64 depends on bit 2 of the row, so hi is not lo + 4 rows
+      const int chunk = 4 * db + 2 * ((lane >> 4) & 1) + ((s16 & 3) >> 1);
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) {
+        const int r = 8 * g + 4 * hf + (s16 >> 2);
+        (hf ? vaddr_hi : vaddr)[db] = r * ROWB + 16 * (chunk ^ swz64(r)) + 8 * (s16 & 1);
+      }
+    }
+  }
 
   f32x16 o[NDB];
 #pragma unroll
@@ -991,7 +1019,7 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& pin, const Wor
 #pragma unroll
       for (int sl = 0; sl < NSL; ++sl) {
         const u32x2 lo = lds_read_tr16(Vb + vaddr[db] + (16 * sl) * ROWB);
-        const u32x2 hi = lds_read_tr16(Vb + vaddr[db] + (16 * sl + 4) * ROWB);
+        const u32x2 hi = lds_read_tr16(Vb + vaddr_hi[db] + (16 * sl) * ROWB);
         va[sl] = (u32x4){lo[0], lo[1], hi[0], hi[1]};
       }
 #pragma unroll
@@ -1030,13 +1058,15 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& pin, const Wor
     pv_sched();
   };
 
-  // Every tile is 4 DMA instructions per wave; after issuing tiles up to
-  // `last`, tile t has landed once at most 4 * (last - t) loads are pending.
+  // Every tile is 2 * NDMA DMA instructions per wave (4 at D = 128, 2 at
+  // D = 64); after issuing tiles up to `last`, tile t has landed once at most
+  // 2 * NDMA * (last - t) loads are pending.
+  constexpr int kTileLoads = 2 * NDMA;
   auto wait_tiles_after = [&](int pending_tiles) __attribute__((always_inline)) {
     if (pending_tiles >= 2) {
-      __builtin_amdgcn_s_waitcnt(0x0F78);  // vmcnt(8)
+      __builtin_amdgcn_s_waitcnt(0x0F70 | (2 * kTileLoads));  // vmcnt(2 tiles)
     } else if (pending_tiles == 1) {
-      __builtin_amdgcn_s_waitcnt(0x0F74);  // vmcnt(4)
+      __builtin_amdgcn_s_waitcnt(0x0F70 | kTileLoads);  // vmcnt(1 tile)
     } else {
       __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     }
@@ -1110,7 +1140,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(MPX_FA_
 void fa_fwd16_kernel(FwdParams p) {
   // Stay within 128 KB of LDS per workgroup (a 136 KB configuration gave wrong
   // results on gfx950).
-  constexpr bool kDirect = MPX_FA_DIRECT && D == 128 && BN == 64 && NW == 8;
+  constexpr bool kDirect = MPX_FA_DIRECT && (D == 128 || D == 64) && BN == 64 && NW == 8;
   // Paged: three stages, which leaves room for the page-table slice.
   constexpr int kDStages = PAGED ? 3 : MPX_FA_DSTAGES;
   constexpr int kLdsBytes =
@@ -1133,8 +1163,8 @@ void fa_fwd16_kernel(FwdParams p) {
 #pragma nounroll
   for (int item = 0; item < n_items; ++item) {
     if constexpr (kDirect)
-      fa16_rows_direct<NW, BF16, kDStages, PAGED>(p, slot_item(p, ws, item), dst0, dst1, dst2,
-                                                 dst3, pages);
+      fa16_rows_direct<D, NW, BF16, kDStages, PAGED>(p, slot_item(p, ws, item), dst0, dst1,
+                                                    dst2, dst3, pages);
     else
       fa16_rows<D, BN, NW, BF16, PAGED>(p, slot_item(p, ws, item), smem, pages);
   }
