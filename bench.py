@@ -515,12 +515,13 @@ def main() -> int:
         },
         "rope_attention": {
             "workload": "fused_rope_attention bf16 BSHD B=4 S=4096 H=32 D=128 causal, cos/sin "
-                        "caches precomputed (rotation of Q and K + the flash kernel)",
+                        "caches precomputed (K rotated by the rope kernel, Q rotated on load "
+                        "inside the flash kernel)",
             "value": r_tf, "unit": "TFLOP/s", "ms_per_step": r_wall, "kernel_ms": r_ev,
             "kernel_ms_median": r_med, "kernel_ms_min": r_min, "flop_per_step": flops,
             "roofline": {"bound": "mfma", "achieved": r_tf, "peak": PEAK_BF16_TFLOPS,
                          "unit": "TFLOP/s", "frac": r_tf / PEAK_BF16_TFLOPS,
-                         "kernel": "rope_kernel x2 + fa_fwd16_kernel<128,64,8,bf16>"},
+                         "kernel": "rope_kernel (K) + fa_fwd16_kernel<128,64,8,bf16> (Q)"},
         },
         "kv_append": {
             "workload": "KV append bf16 through the C ABI: 4 sequences x 4096 new tokens, H=32, "
