@@ -768,9 +768,14 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& pin, const Wor
   constexpr int KBYTES = BN * ROWB;    // one K (or V) tile
   constexpr int STAGEB = 2 * KBYTES;   // K then V
   constexpr int RPD = 1024 / ROWB;     // rows per DMA instruction (64 lanes x 16 bytes)
-  constexpr int NDMA = BN / (RPD * NW);  // DMA instructions per wave per K (or V) tile
-  static_assert(NW == 8 && (D == 128 || D == 64),
-                "each wave stages rows RPD*wave .. +RPD-1 (and +32 .. for D = 128)");
+  constexpr int RSTEP = RPD * NW;      // rows one DMA instruction of every wave covers
+  constexpr int NDMA = BN / RSTEP;     // DMA instructions per wave per K (or V) tile
+  static_assert((NW == 8 || NW == 4) && (D == 128 || D == 64) && NDMA * RSTEP == BN,
+                "each wave stages rows RPD*wave .. +RPD-1, +RSTEP, ...");
+  // The row swizzles depend on row bits below RSTEP only (bits 0-3 at D = 128,
+  // 1-3 at D = 64), so every DMA instruction of a lane uses the same chunk.
+  static_assert(RSTEP % 16 == 0, "swizzle period");
+  static_assert((NST - 2) * 2 * NDMA <= 15, "vmcnt immediate");
   // Paged: keys exist up to this sequence's context length.
   FwdParams p = pin;
   if constexpr (PAGED) p.Sk = max(0, min(pin.ctx[wi.b], pin.max_blocks * pin.bs));
@@ -823,8 +828,8 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& pin, const Wor
   __builtin_amdgcn_s_waitcnt(0x0F70);
 
   // DMA lane mapping: this wave's first instruction fills LDS rows
-  // RPD*wave .. +RPD-1 (lane -> row lr, slot lane % (ROWB/16)); for D = 128 the
-  // second fills rows lr + 32.
+  // RPD*wave .. +RPD-1 (lane -> row lr, slot lane % (ROWB/16)); instruction r
+  // fills rows lr + RSTEP*r.
   int lr, kchunk, vchunk;
   if constexpr (D == 128) {
     lr = 4 * wave + (lane >> 4);
@@ -836,7 +841,7 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& pin, const Wor
   }
   const int kgo = (lr * (int)p.k_ss + kchunk * 8) * 2;
   const int vgo = (lr * (int)p.v_ss + vchunk * 8) * 2;
-  const int k32 = 32 * (int)p.k_ss * 2, v32 = 32 * (int)p.v_ss * 2;
+  const int kstep = RSTEP * (int)p.k_ss * 2, vstep = RSTEP * (int)p.v_ss * 2;
   auto stage_ptr = [&](auto ST) __attribute__((always_inline)) -> unsigned char* {
     constexpr int S = decltype(ST)::value;
     return S == 0 ? st0 : (S == 1 ? st1 : (S == 2 ? st2 : st3));
@@ -850,7 +855,7 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& pin, const Wor
       const u32 row_bytes = (u32)p.k_ss * 2u;
 #pragma unroll
       for (int r = 0; r < NDMA; ++r) {
-        const int pos = kv0 + lr + 32 * r;
+        const int pos = kv0 + lr + RSTEP * r;
         u32 koff = kNoRowDirect, voff = kNoRowDirect;
         if (pos < p.Sk) {
           const int pg = page_of(p, pos);
@@ -861,26 +866,26 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& pin, const Wor
             voff = base + (u32)vchunk * 16u;
           }
         }
-        dma16(krs, kdst + r * 32 * ROWB, (int)koff, 0);
-        dma16(vrs, vdst + r * 32 * ROWB, (int)voff, 0);
+        dma16(krs, kdst + r * RSTEP * ROWB, (int)koff, 0);
+        dma16(vrs, vdst + r * RSTEP * ROWB, (int)voff, 0);
       }
       return;
     }
     const int kso = kv0 * (int)p.k_ss * 2, vso = kv0 * (int)p.v_ss * 2;
     if (kv0 + BN <= p.Sk) {
-      dma16(krs, kdst, kgo, kso);
-      if constexpr (NDMA == 2) dma16(krs, kdst + 32 * ROWB, kgo, kso + k32);
-      dma16(vrs, vdst, vgo, vso);
-      if constexpr (NDMA == 2) dma16(vrs, vdst + 32 * ROWB, vgo, vso + v32);
+#pragma unroll
+      for (int r = 0; r < NDMA; ++r) dma16(krs, kdst + r * RSTEP * ROWB, kgo, kso + r * kstep);
+#pragma unroll
+      for (int r = 0; r < NDMA; ++r) dma16(vrs, vdst + r * RSTEP * ROWB, vgo, vso + r * vstep);
     } else {
       // Tail tile: rows past Sk re-read the last valid row (their scores are
       // masked, so their weights are exactly 0).
       const int lim = p.Sk - 1 - kv0;
 #pragma unroll
       for (int r = 0; r < NDMA; ++r) {
-        const int row = min(lr + 32 * r, lim);
-        dma16(krs, kdst + r * 32 * ROWB, (row * (int)p.k_ss + kchunk * 8) * 2, kso);
-        dma16(vrs, vdst + r * 32 * ROWB, (row * (int)p.v_ss + vchunk * 8) * 2, vso);
+        const int row = min(lr + RSTEP * r, lim);
+        dma16(krs, kdst + r * RSTEP * ROWB, (row * (int)p.k_ss + kchunk * 8) * 2, kso);
+        dma16(vrs, vdst + r * RSTEP * ROWB, (row * (int)p.v_ss + vchunk * 8) * 2, vso);
       }
     }
   };
@@ -1073,7 +1078,7 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& pin, const Wor
   };
   const int n_tiles = t_end - t_begin;
   if (n_tiles > 0) load_tile(kv_lo + t_begin * BN, st0);
-  if (n_tiles > 1) load_tile(kv_lo + (t_begin + 1) * BN, st1);
+  if (NST >= 3 && n_tiles > 1) load_tile(kv_lo + (t_begin + 1) * BN, st1);
   if (NST == 4 && n_tiles > 2) load_tile(kv_lo + (t_begin + 2) * BN, st2);
   wait_tiles_after(min(n_tiles, NST - 1) - 1);  // tile 0 landed
   stage_barrier();
@@ -1093,7 +1098,7 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& pin, const Wor
   for (int i = 0; i < n_tiles; i += NST) {
     step(i, Const<0>{});
     if (i + 1 < n_tiles) step(i + 1, Const<1>{});
-    if (i + 2 < n_tiles) step(i + 2, Const<2 % NST>{});
+    if (NST >= 3 && i + 2 < n_tiles) step(i + 2, Const<2 % NST>{});
     if (NST == 4 && i + 3 < n_tiles) step(i + 3, Const<3 % NST>{});
   }
 
@@ -1140,7 +1145,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(MPX_FA_
 void fa_fwd16_kernel(FwdParams p) {
   // Stay within 128 KB of LDS per workgroup (a 136 KB configuration gave wrong
   // results on gfx950).
-  constexpr bool kDirect = MPX_FA_DIRECT && (D == 128 || D == 64) && BN == 64 && NW == 8;
+  constexpr bool kDirect = MPX_FA_DIRECT && (D == 128 || D == 64) && BN == 64 && (NW == 8 || NW == 4);
   // Paged: three stages, which leaves room for the page-table slice.
   constexpr int kDStages = PAGED ? 3 : MPX_FA_DSTAGES;
   constexpr int kLdsBytes =
@@ -1153,7 +1158,7 @@ void fa_fwd16_kernel(FwdParams p) {
   __shared__ __align__(16) uint16_t smem[kDirect ? 8 : kLdsBytes / 2];
   __shared__ __align__(16) unsigned char dst0[kStageB];
   __shared__ __align__(16) unsigned char dst1[kStageB];
-  __shared__ __align__(16) unsigned char dst2[kStageB];
+  __shared__ __align__(16) unsigned char dst2[kDStages >= 3 ? kStageB : 16];
   __shared__ __align__(16) unsigned char dst3[kDStages == 4 ? kStageB : 16];
   __shared__ int pages[PAGED ? kMaxItemPages : 1];
   const WorkSlot ws = decode_slot(p);
