@@ -148,8 +148,10 @@ __device__ __forceinline__ int page_of(const FwdParams& p, int pos) {
 #ifndef MPX_FA_NWAVES_F32
 #define MPX_FA_NWAVES_F32 4
 #endif
+// Keys per KV tile of the direct 16-bit kernels (D = 64, 128); the paged,
+// D = 32 and register-staged 16-bit kernels take 64.
 #ifndef MPX_FA_BN16
-#define MPX_FA_BN16 64
+#define MPX_FA_BN16 128
 #endif
 // K/V tiles held in registers ahead of their LDS staging: 2 (tile i+2 is
 // loaded while tile i computes) or 1 (tile i+1).
@@ -160,10 +162,10 @@ __device__ __forceinline__ int page_of(const FwdParams& p, int pos) {
 #ifndef MPX_FA_DIRECT
 #define MPX_FA_DIRECT 1
 #endif
-// LDS stages of the direct path (3: tile i+2 in flight while tile i
-// computes; 4: tile i+3, 128 KB of LDS).
+// LDS stages of the direct path (tile i+NST-1 in flight while tile i
+// computes); 0 = as many as fit 128 KB, at most 4.
 #ifndef MPX_FA_DSTAGES
-#define MPX_FA_DSTAGES 4
+#define MPX_FA_DSTAGES 0
 #endif
 // LDS stages of the register-staged 16-bit kernel.
 constexpr int kFa16Stages = 2;
@@ -724,12 +726,14 @@ __device__ __forceinline__ void fa16_rows(const FwdParams& pin, const WorkItem w
 }
 
 // ---------------------------------------------------------------------------
-// D = 128 with direct global->LDS staging (gfx950 LDS DMA): the K and V tiles
-// go from HBM/L2 straight into LDS with buffer_load ... lds, without passing
-// through registers; three LDS stages hold tiles i (computing), i+1 (landed)
-// and i+2 (in flight).
+// D = 128 / 64 with direct global->LDS staging (gfx950 LDS DMA): the K and V
+// tiles (BN = 128 keys by default, 64 for the paged kernels) go from HBM/L2
+// straight into LDS with buffer_load ... lds, without passing through
+// registers; NST LDS stages hold tile i (computing) and tiles i+1 .. i+NST-1
+// (landed or in flight): two stages at D = 128 with 128-key tiles (128 KB),
+// four at D = 64.
 //
-// LDS rows are 256 bytes, unpadded (a DMA instruction writes 64 consecutive
+// LDS rows are 256 bytes (D = 128), unpadded (a DMA instruction writes 64 consecutive
 // 16-byte slots), so bank conflicts are avoided by XOR-swizzling 16-byte
 // chunks instead:
 //   K row r: chunk c stored at slot c ^ (r & 15)      (QK operand reads:
@@ -755,15 +759,16 @@ constexpr u32 kNoRowDirect = 0xFFFFFF00u;
 // consecutive rows x 4 consecutive chunks (V^T operands).
 __device__ __forceinline__ int swz64(int r) { return (((r >> 1) & 1) << 2) | ((r >> 2) & 3); }
 
-template <int D, int NW, bool BF16, int NST, bool PAGED>
+template <int D, int BN, int NW, bool BF16, int NST, bool PAGED>
 __device__ __forceinline__ void fa16_rows_direct(const FwdParams& pin, const WorkItem wi,
                                                  unsigned char* __restrict__ st0,
                                                  unsigned char* __restrict__ st1,
                                                  unsigned char* __restrict__ st2,
                                                  unsigned char* __restrict__ st3,
                                                  int* __restrict__ pages) {
-  constexpr int BN = 64, BM = 32 * NW;
+  constexpr int BM = 32 * NW;
   constexpr int NB = BN / 32, NSL = BN / 16, NKS = D / 16, NDB = D / 32;
+  static_assert(!PAGED || BN == 64, "the paged key-validity ballot covers 64 keys");
   constexpr int ROWB = 2 * D;          // bytes per K or V row
   constexpr int KBYTES = BN * ROWB;    // one K (or V) tile
   constexpr int STAGEB = 2 * KBYTES;   // K then V
@@ -1145,9 +1150,13 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(MPX_FA_
 void fa_fwd16_kernel(FwdParams p) {
   // Stay within 128 KB of LDS per workgroup (a 136 KB configuration gave wrong
   // results on gfx950).
-  constexpr bool kDirect = MPX_FA_DIRECT && (D == 128 || D == 64) && BN == 64 && (NW == 8 || NW == 4);
+  constexpr bool kDirect = MPX_FA_DIRECT && (D == 128 || D == 64) &&
+                           (BN == 64 || (BN == 128 && !PAGED)) && (NW == 8 || NW == 4);
   // Paged: three stages, which leaves room for the page-table slice.
-  constexpr int kDStages = PAGED ? 3 : MPX_FA_DSTAGES;
+  constexpr int kDStages =
+      PAGED ? 3
+            : (MPX_FA_DSTAGES > 0 ? MPX_FA_DSTAGES
+                                  : (131072 / (4 * BN * D) < 4 ? 131072 / (4 * BN * D) : 4));
   constexpr int kLdsBytes =
       kDirect ? kDStages * 2 * BN * 2 * D : kFa16Stages * fa16_stage_elems<D, BN>() * 2;
   static_assert(kLdsBytes + (PAGED ? kMaxItemPages * 4 : 0) <= 131072, "LDS budget");
@@ -1168,7 +1177,7 @@ void fa_fwd16_kernel(FwdParams p) {
 #pragma nounroll
   for (int item = 0; item < n_items; ++item) {
     if constexpr (kDirect)
-      fa16_rows_direct<D, NW, BF16, kDStages, PAGED>(p, slot_item(p, ws, item), dst0, dst1,
+      fa16_rows_direct<D, BN, NW, BF16, kDStages, PAGED>(p, slot_item(p, ws, item), dst0, dst1,
                                                     dst2, dst3, pages);
     else
       fa16_rows<D, BN, NW, BF16, PAGED>(p, slot_item(p, ws, item), smem, pages);
@@ -1505,16 +1514,18 @@ struct Plan {
   size_t ws_bytes;
 };
 
-int tile_n(int D, int dtype) {
+// Keys per KV tile (the paged and D = 32 16-bit kernels always take 64).
+int tile_n(int D, int dtype, bool paged = false) {
   if (dtype == MPX_F32) return D > 64 ? 32 : 64;
-  return MPX_FA_BN16;
+  return paged || D < 64 || !MPX_FA_DIRECT ? 64 : MPX_FA_BN16;
 }
 
 Plan make_plan(int B, int H, int Sq, int Sk, int D, int causal, int window_left,
-               int window_right, int dtype, int max_tiles_per_split = 1 << 30) {
+               int window_right, int dtype, int max_tiles_per_split = 1 << 30,
+               bool paged = false) {
   Plan pl;
   pl.BM = 32 * (dtype == MPX_F32 ? kNumWaves32 : kNumWaves16);
-  pl.BN = tile_n(D, dtype);
+  pl.BN = tile_n(D, dtype, paged);
   pl.win_left = window_left < 0 ? -1 : window_left;
   pl.win_right = causal ? 0 : (window_right < 0 ? -1 : window_right);
   pl.n_qtiles = (Sq + pl.BM - 1) / pl.BM;
@@ -1561,6 +1572,11 @@ hipError_t launch_fwd(const FwdParams& p, int grid, hipStream_t stream) {
   return hipGetLastError();
 }
 
+// KV tile of the 16-bit kernels (the paged, D = 32 and register-staged ones
+// take 64 keys).
+template <bool PAGED, int D>
+constexpr int kBN16 = PAGED || D < 64 || !MPX_FA_DIRECT ? 64 : MPX_FA_BN16;
+
 template <bool PAGED>
 hipError_t dispatch_fwd(const FwdParams& p, int D, int dtype, int grid, hipStream_t st) {
   if (dtype == MPX_F32) {
@@ -1571,15 +1587,15 @@ hipError_t dispatch_fwd(const FwdParams& p, int D, int dtype, int grid, hipStrea
     }
   } else if (dtype == MPX_BF16) {
     switch (D) {
-      case 32: return launch_fwd<32, MPX_FA_BN16, false, true, PAGED>(p, grid, st);
-      case 64: return launch_fwd<64, MPX_FA_BN16, false, true, PAGED>(p, grid, st);
-      default: return launch_fwd<128, MPX_FA_BN16, false, true, PAGED>(p, grid, st);
+      case 32: return launch_fwd<32, kBN16<PAGED, 32>, false, true, PAGED>(p, grid, st);
+      case 64: return launch_fwd<64, kBN16<PAGED, 64>, false, true, PAGED>(p, grid, st);
+      default: return launch_fwd<128, kBN16<PAGED, 128>, false, true, PAGED>(p, grid, st);
     }
   } else {
     switch (D) {
-      case 32: return launch_fwd<32, MPX_FA_BN16, false, false, PAGED>(p, grid, st);
-      case 64: return launch_fwd<64, MPX_FA_BN16, false, false, PAGED>(p, grid, st);
-      default: return launch_fwd<128, MPX_FA_BN16, false, false, PAGED>(p, grid, st);
+      case 32: return launch_fwd<32, kBN16<PAGED, 32>, false, false, PAGED>(p, grid, st);
+      case 64: return launch_fwd<64, kBN16<PAGED, 64>, false, false, PAGED>(p, grid, st);
+      default: return launch_fwd<128, kBN16<PAGED, 128>, false, false, PAGED>(p, grid, st);
     }
   }
 }
@@ -1801,9 +1817,9 @@ extern "C" int mpx_attn_fwd(const void* q, const void* k, const void* v, void* o
 extern "C" size_t mpx_paged_prefill_workspace_bytes(int B, int Sq, int H, int D, int block_size,
                                                     int max_blocks, int causal, int dtype) {
   if (B <= 0 || H <= 0 || Sq <= 0 || D <= 0 || block_size <= 0 || max_blocks <= 0) return 0;
-  const int BN = tile_n(D, dtype);
+  const int BN = tile_n(D, dtype, true);
   return make_plan(B, H, Sq, max_blocks * block_size, D, causal, -1, -1, dtype,
-                   paged_tile_cap(block_size, BN))
+                   paged_tile_cap(block_size, BN), true)
       .ws_bytes;
 }
 
@@ -1865,9 +1881,9 @@ extern "C" int mpx_paged_prefill_gqa(const void* q, const void* k_pool, const vo
     MPX_CHECK_HIP(hipGetLastError());
     return MPX_OK;
   }
-  const int BN = tile_n(D, dtype);
+  const int BN = tile_n(D, dtype, true);
   const Plan pl = make_plan(B, H, Sq, (int)max_tokens, D, causal, -1, -1, dtype,
-                            paged_tile_cap(block_size, BN));
+                            paged_tile_cap(block_size, BN), true);
   if (pl.splits > 1) {
     MPX_CHECK_ARG(workspace != nullptr && workspace_bytes >= pl.ws_bytes,
                   "mpx_paged_prefill: workspace of %zu bytes required, %zu given", pl.ws_bytes,
