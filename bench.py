@@ -41,7 +41,7 @@ import workloads as wl  # noqa: E402
 PEAK_BF16_TFLOPS = 2516.6   # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 TRAFFIC_FILE = os.path.join(REPO, "profiles", "hbm_traffic.json")
-FLASH_KERNEL = "fa_fwd16_kernel<128,64,8,bf16>"
+FLASH_KERNEL = "fa_fwd16_kernel<128,128,8,bf16>"
 PAGED_KERNELS = "paged_decode_part_kernel + paged_decode_merge_kernel"
 PREFILL_KERNEL = "fa_fwd16_kernel<128,64,8,bf16,paged>"
 APPEND_KERNEL = "kv_append_kernel"
@@ -521,7 +521,7 @@ def main() -> int:
             "kernel_ms_median": r_med, "kernel_ms_min": r_min, "flop_per_step": flops,
             "roofline": {"bound": "mfma", "achieved": r_tf, "peak": PEAK_BF16_TFLOPS,
                          "unit": "TFLOP/s", "frac": r_tf / PEAK_BF16_TFLOPS,
-                         "kernel": "rope_kernel (K) + fa_fwd16_kernel<128,64,8,bf16> (Q)"},
+                         "kernel": "rope_kernel (K) + fa_fwd16_kernel<128,128,8,bf16> (Q)"},
         },
         "kv_append": {
             "workload": "KV append bf16 through the C ABI: 4 sequences x 4096 new tokens, H=32, "
@@ -541,7 +541,7 @@ def main() -> int:
             "kernel_ms_median": w_med, "kernel_ms_min": w_min, "flop_per_step": wflops,
             "roofline": {"bound": "mfma", "achieved": w_tf, "peak": PEAK_BF16_TFLOPS,
                          "unit": "TFLOP/s", "frac": w_tf / PEAK_BF16_TFLOPS,
-                         "kernel": "fa_fwd16_kernel<128,64,8,bf16>"},
+                         "kernel": "fa_fwd16_kernel<128,128,8,bf16>"},
         },
         "chunked_cross": {
             "workload": "chunked_cross_attention bf16 BSHD q (1,512,16,64), k/v (1,65536,16,64), "
@@ -551,7 +551,7 @@ def main() -> int:
             "bytes_per_step": cbytes,
             "roofline": {"bound": "mfma", "achieved": k_tf, "peak": PEAK_BF16_TFLOPS,
                          "unit": "TFLOP/s", "frac": k_tf / PEAK_BF16_TFLOPS,
-                         "kernel": "fa_fwd16_kernel<64,64,8,bf16> (split-KV) + "
+                         "kernel": "fa_fwd16_kernel<64,128,8,bf16> (split-KV) + "
                                    "fa_split_merge_kernel"},
             "hbm_roofline": {"achieved": k_gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                              "frac": k_gbs / PEAK_HBM_GBS},
