@@ -5,7 +5,7 @@
 // batched over sequences: token t of sequence b goes to position
 // start[b] + t, page block_tables[b, pos / bs], slot pos % bs of the pools
 // (num_blocks, bs, H, D). Memory bound: one thread per 16-byte chunk of a
-// (token, head) row, coalesced reads and writes.
+// token row, coalesced reads and writes.
 //
 // A token that cannot be placed is skipped and reported through the caller's
 // int32[3] error words, each set to 1 with a plain store (no read-modify-write,
@@ -34,18 +34,19 @@ struct AppendParams {
   int num_blocks, bs, max_blocks;
 };
 
-__global__ __launch_bounds__(256) void kv_append_kernel(AppendParams p) {
+// Grid: each workgroup handles 256 consecutive 16-byte chunks of one token
+// row (b, t) (H * cpr chunks, split over nbr workgroups), so the row's
+// position, page lookup and checks are per-workgroup scalar work and each
+// thread only splits its chunk index into (head, chunk).
+__global__ __launch_bounds__(256) void kv_append_kernel(AppendParams p, int nbr) {
   const int row_chunks = p.H * p.cpr;
-  const int64_t n = (int64_t)p.B * p.T * row_chunks;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
-       i += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t row = i / row_chunks;  // b * T + t
-    const int rem = (int)(i - row * row_chunks);
-    const int h = rem / p.cpr;
-    const int c = rem - h * p.cpr;
-    const int b = (int)(row / p.T);
-    const int t = (int)(row - (int64_t)b * p.T);
-    if (t >= p.ntok[b]) continue;
+  const int n_blk = p.B * p.T * nbr;  // < 2^31 (checked by the host)
+  for (int blk = blockIdx.x; blk < n_blk; blk += gridDim.x) {
+    const int row = blk / nbr;  // b * T + t
+    const int rc = (blk - row * nbr) * 256 + (int)threadIdx.x;
+    const int b = row / p.T;
+    const int t = row - b * p.T;
+    if (rc >= row_chunks || t >= p.ntok[b]) continue;
     const int pos = p.start[b] + t;
     if (pos < 0) {
       p.err[0] = 1;
@@ -61,6 +62,8 @@ __global__ __launch_bounds__(256) void kv_append_kernel(AppendParams p) {
       p.err[2] = 1;
       continue;
     }
+    const int h = rc / p.cpr;
+    const int c = rc - h * p.cpr;
     const int64_t slot = ((int64_t)page * p.bs + (pos - bi * p.bs)) * p.H + h;
     const int64_t dst = (slot * p.cpr + c) * 16;
     const int64_t ks = ((int64_t)b * p.k_sb + (int64_t)t * p.k_st + (int64_t)h * p.k_sh) * p.es;
@@ -110,9 +113,13 @@ extern "C" int mpx_kv_append(const void* k, const void* v, void* k_pool, void* v
   p.v_sb = v_strides[0]; p.v_st = v_strides[1]; p.v_sh = v_strides[2];
   p.B = B; p.T = T; p.H = H; p.cpr = D * es / 16; p.es = es;
   p.num_blocks = num_blocks; p.bs = block_size; p.max_blocks = max_blocks;
-  const int64_t n = (int64_t)B * T * H * p.cpr;
-  const int blocks = (int)std::min<int64_t>((n + 255) / 256, 65536);
-  hipLaunchKernelGGL(kv_append_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream, p);
+  MPX_CHECK_ARG((int64_t)H * p.cpr < (1 << 30), "mpx_kv_append: head count too large");
+  const int nbr = (H * p.cpr + 255) / 256;  // workgroups per token row
+  const int64_t n_blk = (int64_t)B * T * nbr;
+  MPX_CHECK_ARG(n_blk < (1L << 31), "mpx_kv_append: too many tokens in one call");
+  const int blocks = (int)std::min<int64_t>(n_blk, 1 << 20);
+  if (blocks > 0)
+    hipLaunchKernelGGL(kv_append_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream, p, nbr);
   MPX_CHECK_HIP(hipGetLastError());
   return MPX_OK;
 }
