@@ -167,7 +167,9 @@ size_t mpx_paged_prefill_workspace_bytes(int B, int Sq, int H, int D, int block_
  *                 [0, num_blocks). Such tokens are skipped; all others are
  *                 written. Two tokens aimed at the same slot race.
  *
- * D * element size must be a multiple of 16 bytes.
+ * D * element size must be a multiple of 16 bytes; H * D * element size
+ * below 2^34 bytes and B * T * ceil(H * D * element size / 4096) below 2^31
+ * (MPX_EINVAL otherwise).
  */
 int mpx_kv_append(const void* k, const void* v, void* k_pool, void* v_pool,
                   const int32_t* block_tables, const int32_t* start_pos,
