@@ -19,6 +19,10 @@
 
 namespace mpx {
 
+#ifndef MPX_KV_NT
+#define MPX_KV_NT 1
+#endif
+
 struct AppendParams {
   const unsigned char* k;
   const unsigned char* v;
@@ -68,10 +72,18 @@ __global__ __launch_bounds__(256) void kv_append_kernel(AppendParams p, int nbr)
     const int64_t dst = (slot * p.cpr + c) * 16;
     const int64_t ks = ((int64_t)b * p.k_sb + (int64_t)t * p.k_st + (int64_t)h * p.k_sh) * p.es;
     const int64_t vs = ((int64_t)b * p.v_sb + (int64_t)t * p.v_st + (int64_t)h * p.v_sh) * p.es;
+#if MPX_KV_NT
+    // Every byte is moved once: non-temporal (streaming) loads and stores.
+    const u32x4 kx = __builtin_nontemporal_load((const u32x4*)(p.k + ks + c * 16));
+    const u32x4 vx = __builtin_nontemporal_load((const u32x4*)(p.v + vs + c * 16));
+    __builtin_nontemporal_store(kx, (u32x4*)(p.kpool + dst));
+    __builtin_nontemporal_store(vx, (u32x4*)(p.vpool + dst));
+#else
     const u32x4 kx = *(const u32x4*)(p.k + ks + c * 16);
     const u32x4 vx = *(const u32x4*)(p.v + vs + c * 16);
     *(u32x4*)(p.kpool + dst) = kx;
     *(u32x4*)(p.vpool + dst) = vx;
+#endif
   }
 }
 

@@ -64,6 +64,17 @@ __device__ __forceinline__ float elem(const u32x4& v, int i) {
   }
 }
 
+#ifndef MPX_PD_NT
+#define MPX_PD_NT 1
+#endif
+__device__ __forceinline__ u32x4 ld_stream(const u32x4* ptr) {
+  if constexpr (MPX_PD_NT != 0) {
+    return __builtin_nontemporal_load(ptr);
+  } else {
+    return *ptr;
+  }
+}
+
 __device__ __forceinline__ float wave_max(float x) {
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) x = fmaxf(x, __shfl_xor(x, off, 64));
@@ -138,8 +149,9 @@ __global__ __launch_bounds__(256) void paged_decode_part_kernel(DecodeParams p) 
       if (tk < p1) blk = btl[tk / p.bs - pg0];
       ok[u] = blk >= 0;
       const int64_t off = (((int64_t)blk * p.bs + tk % p.bs) * row_elems + hoff) * ES;
-      kr[u] = ok[u] ? *(const u32x4*)(kbase + off) : (u32x4){0u, 0u, 0u, 0u};
-      vr[u] = ok[u] ? *(const u32x4*)(vbase + off) : (u32x4){0u, 0u, 0u, 0u};
+      // K/V rows are read once per call: non-temporal loads (streaming hint).
+      kr[u] = ok[u] ? ld_stream((const u32x4*)(kbase + off)) : (u32x4){0u, 0u, 0u, 0u};
+      vr[u] = ok[u] ? ld_stream((const u32x4*)(vbase + off)) : (u32x4){0u, 0u, 0u, 0u};
     }
     float sc[U];
     float mb = m;
