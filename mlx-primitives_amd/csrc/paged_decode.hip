@@ -51,7 +51,10 @@ struct DecodeParams {
 #define MPX_PD_U 16
 #endif
 constexpr int kPart = MPX_PD_PART;
-constexpr int kHeadsPerWG = 4;
+#ifndef MPX_PD_HEADS
+#define MPX_PD_HEADS 4
+#endif
+constexpr int kHeadsPerWG = MPX_PD_HEADS;
 
 template <int DT>
 __device__ __forceinline__ float elem(const u32x4& v, int i) {
@@ -90,7 +93,7 @@ __device__ __forceinline__ float wave_sum(float x) {
 }
 
 template <int D, int DT, bool NT>
-__global__ __launch_bounds__(256) void paged_decode_part_kernel(DecodeParams p) {
+__global__ __launch_bounds__(64 * kHeadsPerWG) void paged_decode_part_kernel(DecodeParams p) {
   constexpr int ES = DT == MPX_F32 ? 4 : 2;  // element bytes
   constexpr int EPC = 16 / ES;               // elements per 16-byte chunk
   constexpr int LPT = D / EPC;               // lanes per token row
@@ -109,7 +112,7 @@ __global__ __launch_bounds__(256) void paged_decode_part_kernel(DecodeParams p) 
   const int p1 = min(p0 + kPart, ctx);
   const int pg0 = p0 / p.bs;
   const int npg = (p1 - 1) / p.bs - pg0 + 1;
-  for (int i = tid; i < npg; i += 256) {
+  for (int i = tid; i < npg; i += 64 * kHeadsPerWG) {
     const int blk = p.bt[(int64_t)b * p.max_blocks + pg0 + i];
     btl[i] = (blk >= 0 && blk < p.num_blocks) ? blk : -1;
   }
@@ -265,9 +268,9 @@ template <int D, int DT>
 hipError_t launch_decode(const DecodeParams& p, hipStream_t st) {
   const dim3 grid((p.H + kHeadsPerWG - 1) / kHeadsPerWG, p.max_parts, p.B);
   if (p.kv_group == 1)
-    hipLaunchKernelGGL((paged_decode_part_kernel<D, DT, true>), grid, dim3(256), 0, st, p);
+    hipLaunchKernelGGL((paged_decode_part_kernel<D, DT, true>), grid, dim3(64 * kHeadsPerWG), 0, st, p);
   else
-    hipLaunchKernelGGL((paged_decode_part_kernel<D, DT, false>), grid, dim3(256), 0, st, p);
+    hipLaunchKernelGGL((paged_decode_part_kernel<D, DT, false>), grid, dim3(64 * kHeadsPerWG), 0, st, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(paged_decode_merge_kernel<DT>, dim3(p.B * p.H), dim3(64), 0, st, p, D);

@@ -65,11 +65,21 @@ def test_flash_parity(device, dtype, layout, causal, D):
     check(out, ref, dtype)
 
 
-@pytest.mark.parametrize("S", [1, 2, 31, 47, 64, 127, 129, 513])
+@pytest.mark.parametrize("S", [1, 2, 31, 47, 64, 127, 129, 192, 320, 513])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_flash_ragged_lengths(device, S, dtype):
+    # 192 and 320 end on a 64-key half of a 128-key tile.
     (q, k, v), (qn, kn, vn) = inputs([(1, S, 2, 64)] * 3, dtype, S, device)
     check(flash_attention(q, k, v, causal=True), oa.flash_attention(qn, kn, vn, causal=True), dtype)
+
+
+@pytest.mark.parametrize("S", [192, 320])
+@pytest.mark.parametrize("causal", [True, False])
+def test_flash_half_tile_d128(device, S, causal):
+    """D = 128 (two 64 KB stages of 128-key tiles) ending on a 64-key half tile."""
+    (q, k, v), (qn, kn, vn) = inputs([(1, S, 2, 128)] * 3, torch.bfloat16, S + 7, device)
+    check(flash_attention(q, k, v, causal=causal), oa.flash_attention(qn, kn, vn, causal=causal),
+          torch.bfloat16)
 
 
 @pytest.mark.parametrize("S,D", [(1100, 64), (1100, 128), (1536, 64), (1280, 32)])
