@@ -8,8 +8,9 @@
 //
 // Design (memory bound, ~1 FLOP/byte):
 //   * split-K: each sequence's tokens are cut into partitions of PART tokens;
-//     a workgroup = 4 waves = 4 consecutive heads of one (sequence, partition),
-//     so the four waves stream adjacent 256-byte head rows of the same pages;
+//     a workgroup = 2 or 4 waves = consecutive query heads of one (sequence,
+//     partition), so its waves stream adjacent head rows of the same pages
+//     (or, with grouped-query heads, share them);
 //   * one pass over the partition: a token row of one head is read by LPT
 //     lanes with 16-byte loads; the K and V rows of U tokens per lane are
 //     requested together, partial dot products are reduced across the LPT
@@ -51,10 +52,11 @@ struct DecodeParams {
 #define MPX_PD_U 16
 #endif
 constexpr int kPart = MPX_PD_PART;
-#ifndef MPX_PD_HEADS
-#define MPX_PD_HEADS 4
-#endif
-constexpr int kHeadsPerWG = MPX_PD_HEADS;
+// Query heads (waves) per workgroup: 4 with grouped-query heads, whose waves
+// share K/V rows in L2; 2 when every K/V head serves one query head (measured
+// 0.7% faster there, 14-23% slower with grouping).
+template <bool NT>
+constexpr int kHeadsPerWG = NT ? 2 : 4;
 
 template <int DT>
 __device__ __forceinline__ float elem(const u32x4& v, int i) {
@@ -93,7 +95,7 @@ __device__ __forceinline__ float wave_sum(float x) {
 }
 
 template <int D, int DT, bool NT>
-__global__ __launch_bounds__(64 * kHeadsPerWG) void paged_decode_part_kernel(DecodeParams p) {
+__global__ __launch_bounds__(64 * kHeadsPerWG<NT>) void paged_decode_part_kernel(DecodeParams p) {
   constexpr int ES = DT == MPX_F32 ? 4 : 2;  // element bytes
   constexpr int EPC = 16 / ES;               // elements per 16-byte chunk
   constexpr int LPT = D / EPC;               // lanes per token row
@@ -104,7 +106,7 @@ __global__ __launch_bounds__(64 * kHeadsPerWG) void paged_decode_part_kernel(Dec
   __shared__ int btl[kPart + 1];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int h = blockIdx.x * kHeadsPerWG + wave;
+  const int h = blockIdx.x * kHeadsPerWG<NT> + wave;
   const int part = blockIdx.y, b = blockIdx.z;
   const int ctx = max(0, min(p.cl[b], p.max_blocks * p.bs));
   const int p0 = part * kPart;
@@ -112,7 +114,7 @@ __global__ __launch_bounds__(64 * kHeadsPerWG) void paged_decode_part_kernel(Dec
   const int p1 = min(p0 + kPart, ctx);
   const int pg0 = p0 / p.bs;
   const int npg = (p1 - 1) / p.bs - pg0 + 1;
-  for (int i = tid; i < npg; i += 64 * kHeadsPerWG) {
+  for (int i = tid; i < npg; i += 64 * kHeadsPerWG<NT>) {
     const int blk = p.bt[(int64_t)b * p.max_blocks + pg0 + i];
     btl[i] = (blk >= 0 && blk < p.num_blocks) ? blk : -1;
   }
@@ -266,11 +268,15 @@ int max_parts_for(int block_size, int max_blocks) {
 
 template <int D, int DT>
 hipError_t launch_decode(const DecodeParams& p, hipStream_t st) {
-  const dim3 grid((p.H + kHeadsPerWG - 1) / kHeadsPerWG, p.max_parts, p.B);
-  if (p.kv_group == 1)
-    hipLaunchKernelGGL((paged_decode_part_kernel<D, DT, true>), grid, dim3(64 * kHeadsPerWG), 0, st, p);
-  else
-    hipLaunchKernelGGL((paged_decode_part_kernel<D, DT, false>), grid, dim3(64 * kHeadsPerWG), 0, st, p);
+  if (p.kv_group == 1) {
+    constexpr int W = kHeadsPerWG<true>;
+    const dim3 grid((p.H + W - 1) / W, p.max_parts, p.B);
+    hipLaunchKernelGGL((paged_decode_part_kernel<D, DT, true>), grid, dim3(64 * W), 0, st, p);
+  } else {
+    constexpr int W = kHeadsPerWG<false>;
+    const dim3 grid((p.H + W - 1) / W, p.max_parts, p.B);
+    hipLaunchKernelGGL((paged_decode_part_kernel<D, DT, false>), grid, dim3(64 * W), 0, st, p);
+  }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(paged_decode_merge_kernel<DT>, dim3(p.B * p.H), dim3(64), 0, st, p, D);
