@@ -98,7 +98,9 @@ size_t mpx_attn_fwd_workspace_bytes(int B, int H, int Sq, int Sk, int D, int cau
  *   alibi_slopes  float32 (H,) or NULL; bias = slope_h * (kv_pos - context_len)
  *   o             (B, H, D) via o_strides
  *
- * Token t of sequence b is valid iff t < context_lens[b] and
+ * D is the head dim of q, the pools and o: any multiple of 8 elements (16-bit
+ * dtypes) or 4 (float32) up to 128, read in place (no padded copy of the
+ * pools). Token t of sequence b is valid iff t < context_lens[b] and
  * 0 <= block_tables[b, t / block_size] < num_blocks; the softmax runs over
  * valid tokens only (exact, no epsilon). A sequence with no valid token gets
  * NaN, as the reference's softmax over an all -inf row does.

@@ -40,6 +40,7 @@ struct DecodeParams {
   float* ws_ml;  // (B, H, max_parts, 2), m in log2 units
   int B, H, num_blocks, bs, max_blocks, max_parts;
   int H_kv, kv_group;  // K/V heads of the pools; query heads per K/V head
+  int dp;   // head dim of q, the pools and o (elements, <= the kernel's D)
   float c;  // scale * log2(e)
 };
 
@@ -123,16 +124,21 @@ __global__ __launch_bounds__(64 * kHeadsPerWG<NT>) void paged_decode_part_kernel
 
   // Lane (tl, cidx): 16-byte chunk cidx of the head row of tokens tl, tl+TPI, ...
   const int cidx = lane % LPT, tl = lane / LPT;
+  // Head rows of dp <= D elements: the lanes of chunks past dp read nothing
+  // and hold zeros (they add nothing to q.k and their output is not written).
+  const bool lane_on = cidx * EPC < p.dp;
   // Pool token rows hold H_kv heads; query head h reads K/V head h / kv_group.
-  const int64_t row_elems = (int64_t)p.H_kv * D;
-  const int64_t hoff = (int64_t)(h / p.kv_group) * D + cidx * EPC;
+  const int64_t row_elems = (int64_t)p.H_kv * p.dp;
+  const int64_t hoff = (int64_t)(h / p.kv_group) * p.dp + cidx * EPC;
   const char* kbase = (const char*)p.kpool;
   const char* vbase = (const char*)p.vpool;
 
   float qv[EPC];
   {
-    const u32x4 qr = *(const u32x4*)((const char*)p.q +
-                                     ((int64_t)b * p.q_sb + (int64_t)h * p.q_sh + cidx * EPC) * ES);
+    const u32x4 qr = lane_on ? *(const u32x4*)((const char*)p.q +
+                                               ((int64_t)b * p.q_sb + (int64_t)h * p.q_sh +
+                                                cidx * EPC) * ES)
+                             : (u32x4){0u, 0u, 0u, 0u};
 #pragma unroll
     for (int i = 0; i < EPC; ++i) qv[i] = elem<DT>(qr, i) * p.c;
   }
@@ -155,9 +161,10 @@ __global__ __launch_bounds__(64 * kHeadsPerWG<NT>) void paged_decode_part_kernel
       int blk = -1;
       if (tk < p1) blk = btl[tk / p.bs - pg0];
       ok[u] = blk >= 0;
+      const bool ld = ok[u] && lane_on;
       const int64_t off = (((int64_t)blk * p.bs + tk % p.bs) * row_elems + hoff) * ES;
-      kr[u] = ok[u] ? ld_kv<NT>((const u32x4*)(kbase + off)) : (u32x4){0u, 0u, 0u, 0u};
-      vr[u] = ok[u] ? ld_kv<NT>((const u32x4*)(vbase + off)) : (u32x4){0u, 0u, 0u, 0u};
+      kr[u] = ld ? ld_kv<NT>((const u32x4*)(kbase + off)) : (u32x4){0u, 0u, 0u, 0u};
+      vr[u] = ld ? ld_kv<NT>((const u32x4*)(vbase + off)) : (u32x4){0u, 0u, 0u, 0u};
     }
     float sc[U];
     float mb = m;
@@ -216,7 +223,8 @@ __global__ __launch_bounds__(64 * kHeadsPerWG<NT>) void paged_decode_part_kernel
 
 // Combine the partitions of one (sequence, head): the online-softmax merge
 // (mlx_primitives/attention/_online_softmax.py:42-106) over all partitions,
-// then the exact normalisation o / l of the reference's softmax.
+// then the exact normalisation o / l of the reference's softmax. D is the
+// kernel head dim (the partials' row length); dp <= D columns are written.
 template <int DT>
 __global__ __launch_bounds__(64) void paged_decode_merge_kernel(DecodeParams p, int D) {
   const int bh = blockIdx.x;
@@ -227,7 +235,7 @@ __global__ __launch_bounds__(64) void paged_decode_merge_kernel(DecodeParams p, 
   const int64_t base = (int64_t)bh * p.max_parts;
   float M = -INFINITY;
   for (int i = 0; i < nparts; ++i) M = fmaxf(M, p.ws_ml[2 * (base + i)]);
-  for (int d = lane; d < D; d += 64) {
+  for (int d = lane; d < p.dp; d += 64) {
     float acc = 0.f, L = 0.f;
     int i = 0;
     // Eight partials per round, their loads issued together.
@@ -266,6 +274,9 @@ int max_parts_for(int block_size, int max_blocks) {
   return (int)((tokens + kPart - 1) / kPart);
 }
 
+// Kernel head dim serving pools of head dim D (<= 128): 32, 64 or 128.
+int kernel_dim(int D) { return D <= 32 ? 32 : D <= 64 ? 64 : 128; }
+
 template <int D, int DT>
 hipError_t launch_decode(const DecodeParams& p, hipStream_t st) {
   if (p.kv_group == 1) {
@@ -292,6 +303,81 @@ hipError_t dispatch_decode_d(const DecodeParams& p, int D, hipStream_t st) {
   }
 }
 
+// Workspace bytes of one call: (o, m, l) per (sequence, head, partition).
+size_t decode_ws_bytes(int B, int H, int D, int block_size, int max_blocks) {
+  const int parts = std::max(1, max_parts_for(block_size, max_blocks));
+  return (size_t)B * H * parts * (kernel_dim(D) + 2) * sizeof(float);
+}
+
+// Validation, parameters and launches shared by the workspace entry and the
+// no-allocation entry. `workspace` == nullptr with need > 0 is an error.
+int paged_decode_run(const void* q, const void* k_pool, const void* v_pool,
+                     const int32_t* block_tables, const int32_t* context_lens,
+                     const float* alibi_slopes, void* o, const int64_t* q_strides,
+                     const int64_t* o_strides, int B, int H, int H_kv, int D, int num_blocks,
+                     int block_size, int max_blocks, float scale, int dtype, void* workspace,
+                     size_t workspace_bytes, void* stream, const char* who) {
+  MPX_CHECK_ARG(dtype == MPX_F32 || dtype == MPX_F16 || dtype == MPX_BF16,
+                "%s: unknown dtype code %d", who, dtype);
+  MPX_CHECK_ARG(B >= 0 && H >= 0 && num_blocks >= 0 && max_blocks >= 0, "%s: negative size",
+                who);
+  MPX_CHECK_ARG(H_kv > 0 ? H % H_kv == 0 : H == 0,
+                "%s: %d query heads are not a multiple of %d K/V heads", who, H, H_kv);
+  MPX_CHECK_ARG(block_size > 0, "%s: block_size must be positive", who);
+  const int vec = dtype == MPX_F32 ? 4 : 8;
+  if (D <= 0 || D > 128 || D % vec != 0) {
+    set_error("%s: head_dim %d not supported (a multiple of %d elements up to 128)", who, D,
+              vec);
+    return MPX_EUNSUPPORTED;
+  }
+  MPX_CHECK_ARG(std::isfinite(scale), "%s: scale must be finite", who);
+  if ((long)B * H == 0) return MPX_OK;
+  MPX_CHECK_ARG(q && o && context_lens && q_strides && o_strides, "%s: null pointer argument",
+                who);
+  MPX_CHECK_ARG(max_blocks == 0 || (k_pool && v_pool && block_tables) || num_blocks == 0,
+                "%s: null pool/table pointer", who);
+  MPX_CHECK_ARG(((uintptr_t)q & 15u) == 0 && ((uintptr_t)k_pool & 15u) == 0 &&
+                    ((uintptr_t)v_pool & 15u) == 0,
+                "%s: q and pools must be 16-byte aligned", who);
+  MPX_CHECK_ARG(q_strides[0] % vec == 0 && q_strides[1] % vec == 0,
+                "%s: q strides must be multiples of %d elements", who, vec);
+  const long max_tokens = (long)max_blocks * block_size;
+  MPX_CHECK_ARG(max_tokens < (1L << 30), "%s: block table too large", who);
+
+  const int kd = kernel_dim(D);
+  DecodeParams p;
+  p.q = q; p.kpool = k_pool; p.vpool = v_pool; p.bt = block_tables; p.cl = context_lens;
+  p.slopes = alibi_slopes; p.o = o;
+  p.q_sb = q_strides[0]; p.q_sh = q_strides[1]; p.o_sb = o_strides[0]; p.o_sh = o_strides[1];
+  p.B = B; p.H = H; p.num_blocks = num_blocks; p.bs = block_size; p.max_blocks = max_blocks;
+  p.H_kv = H_kv; p.kv_group = H / H_kv;
+  p.dp = D;
+  p.max_parts = std::max(1, max_parts_for(block_size, max_blocks));
+  p.c = scale * kLog2e;
+  const size_t need = decode_ws_bytes(B, H, D, block_size, max_blocks);
+  MPX_CHECK_ARG(workspace != nullptr && workspace_bytes >= need && ((uintptr_t)workspace & 15u) == 0,
+                "%s: 16-byte aligned workspace of %zu bytes required, %zu given", who, need,
+                workspace_bytes);
+  MPX_CHECK_ARG(p.max_parts <= 65535 && B <= 65535, "%s: grid too large", who);
+  p.ws_o = (float*)workspace;
+  p.ws_ml = (float*)workspace + (size_t)B * H * p.max_parts * kd;
+  if (num_blocks == 0 || max_blocks == 0) {
+    // No page can be valid; the partition kernel has no work, the merge writes NaN.
+    p.max_blocks = 0;
+  }
+
+  hipStream_t st = (hipStream_t)stream;
+  hipError_t e;
+  if (dtype == MPX_F32)
+    e = dispatch_decode_d<MPX_F32>(p, kd, st);
+  else if (dtype == MPX_BF16)
+    e = dispatch_decode_d<MPX_BF16>(p, kd, st);
+  else
+    e = dispatch_decode_d<MPX_F16>(p, kd, st);
+  MPX_CHECK_HIP(e);
+  return MPX_OK;
+}
+
 }  // namespace
 }  // namespace mpx
 
@@ -300,7 +386,7 @@ using namespace mpx;
 extern "C" size_t mpx_paged_decode_workspace_bytes(int B, int H, int D, int block_size,
                                                    int max_blocks) {
   if (B <= 0 || H <= 0 || D <= 0 || block_size <= 0 || max_blocks <= 0) return 0;
-  return (size_t)B * H * max_parts_for(block_size, max_blocks) * (D + 2) * sizeof(float);
+  return decode_ws_bytes(B, H, D, block_size, max_blocks);
 }
 
 extern "C" int mpx_paged_decode_gqa(const void* q, const void* k_pool, const void* v_pool,
@@ -311,62 +397,10 @@ extern "C" int mpx_paged_decode_gqa(const void* q, const void* k_pool, const voi
                                     int max_blocks, float scale, int dtype, void* workspace,
                                     size_t workspace_bytes, void* stream) {
   clear_error();
-  MPX_CHECK_ARG(dtype == MPX_F32 || dtype == MPX_F16 || dtype == MPX_BF16,
-                "mpx_paged_decode: unknown dtype code %d", dtype);
-  MPX_CHECK_ARG(B >= 0 && H >= 0 && num_blocks >= 0 && max_blocks >= 0,
-                "mpx_paged_decode: negative size");
-  MPX_CHECK_ARG(H_kv > 0 ? H % H_kv == 0 : H == 0,
-                "mpx_paged_decode: %d query heads are not a multiple of %d K/V heads", H, H_kv);
-  MPX_CHECK_ARG(block_size > 0, "mpx_paged_decode: block_size must be positive");
-  if (D != 32 && D != 64 && D != 128) {
-    set_error("mpx_paged_decode: head_dim %d not supported (kernels exist for 32, 64, 128)", D);
-    return MPX_EUNSUPPORTED;
-  }
-  MPX_CHECK_ARG(std::isfinite(scale), "mpx_paged_decode: scale must be finite");
-  if ((long)B * H == 0) return MPX_OK;
-  MPX_CHECK_ARG(q && o && context_lens && q_strides && o_strides,
-                "mpx_paged_decode: null pointer argument");
-  MPX_CHECK_ARG(max_blocks == 0 || (k_pool && v_pool && block_tables) || num_blocks == 0,
-                "mpx_paged_decode: null pool/table pointer");
-  const int vec = dtype == MPX_F32 ? 4 : 8;
-  MPX_CHECK_ARG(((uintptr_t)q & 15u) == 0 && ((uintptr_t)k_pool & 15u) == 0 &&
-                    ((uintptr_t)v_pool & 15u) == 0,
-                "mpx_paged_decode: q and pools must be 16-byte aligned");
-  MPX_CHECK_ARG(q_strides[0] % vec == 0 && q_strides[1] % vec == 0,
-                "mpx_paged_decode: q strides must be multiples of %d elements", vec);
-  const long max_tokens = (long)max_blocks * block_size;
-  MPX_CHECK_ARG(max_tokens < (1L << 30), "mpx_paged_decode: block table too large");
-
-  DecodeParams p;
-  p.q = q; p.kpool = k_pool; p.vpool = v_pool; p.bt = block_tables; p.cl = context_lens;
-  p.slopes = alibi_slopes; p.o = o;
-  p.q_sb = q_strides[0]; p.q_sh = q_strides[1]; p.o_sb = o_strides[0]; p.o_sh = o_strides[1];
-  p.B = B; p.H = H; p.num_blocks = num_blocks; p.bs = block_size; p.max_blocks = max_blocks;
-  p.H_kv = H_kv; p.kv_group = H / H_kv;
-  p.max_parts = std::max(1, max_parts_for(block_size, max_blocks));
-  p.c = scale * kLog2e;
-  const size_t need = (size_t)B * H * p.max_parts * (D + 2) * sizeof(float);
-  MPX_CHECK_ARG(workspace != nullptr && workspace_bytes >= need && ((uintptr_t)workspace & 15u) == 0,
-                "mpx_paged_decode: 16-byte aligned workspace of %zu bytes required, %zu given",
-                need, workspace_bytes);
-  MPX_CHECK_ARG(p.max_parts <= 65535 && B <= 65535, "mpx_paged_decode: grid too large");
-  p.ws_o = (float*)workspace;
-  p.ws_ml = (float*)workspace + (size_t)B * H * p.max_parts * D;
-  if (num_blocks == 0 || max_blocks == 0) {
-    // No page can be valid; the partition kernel has no work, the merge writes NaN.
-    p.max_blocks = 0;
-  }
-
-  hipStream_t st = (hipStream_t)stream;
-  hipError_t e;
-  if (dtype == MPX_F32)
-    e = dispatch_decode_d<MPX_F32>(p, D, st);
-  else if (dtype == MPX_BF16)
-    e = dispatch_decode_d<MPX_BF16>(p, D, st);
-  else
-    e = dispatch_decode_d<MPX_F16>(p, D, st);
-  MPX_CHECK_HIP(e);
-  return MPX_OK;
+  return paged_decode_run(q, k_pool, v_pool, block_tables, context_lens, alibi_slopes, o,
+                          q_strides, o_strides, B, H, H_kv, D, num_blocks, block_size,
+                          max_blocks, scale, dtype, workspace, workspace_bytes, stream,
+                          "mpx_paged_decode");
 }
 
 extern "C" int mpx_paged_decode(const void* q, const void* k_pool, const void* v_pool,

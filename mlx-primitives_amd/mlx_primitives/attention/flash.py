@@ -89,8 +89,13 @@ def flash_attention(
       q, k, v: (B, S, H, D) for layout "BSHD" (default) or (B, H, S, D) for
         "BHSD"; float32, float16 or bfloat16 ROCm tensors of one dtype.
       scale: defaults to 1/sqrt(D).
-      causal: key j visible to query i iff j <= i (top-left aligned, as the
-        reference's tiled path).
+      causal: key j visible to query i iff j <= i + max(0, Sk - Sq): the
+        causal rule of the reference's default route, which hands
+        mask="causal" to SDPA for every size and layout (flash.py:177-181,
+        211-235, 479-506). With more keys than queries (a decode step over a
+        cache) the diagonal sits at the bottom right, so the last query sees
+        every key (utils/masking.py:52-56); otherwise it is the tiled path's
+        top-left rule (kv <= q).
       block_q, block_kv, use_metal: accepted, no effect on the result.
       dropout_p, training: dropout on the attention weights is not
         implemented by the MI355X kernels (raises NotImplementedError when
@@ -112,6 +117,13 @@ def flash_attention(
         raise NotImplementedError(
             "flash_attention: dropout_p > 0 in training mode is not supported by the "
             "MI355X kernels")
+    if causal:
+        seq_q, seq_kv = ((q.shape[1], k.shape[1]) if layout == Layout.BSHD
+                         else (q.shape[2], k.shape[2]))
+        if seq_kv > seq_q:
+            # bottom-right diagonal: j <= i + (Sk - Sq)
+            return run_attention(q, k, v, layout, scale, causal=False,
+                                 window_right=seq_kv - seq_q)
     return run_attention(q, k, v, layout, scale, causal=causal)
 
 

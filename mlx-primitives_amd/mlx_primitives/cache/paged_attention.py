@@ -99,14 +99,18 @@ def paged_attention(
         if alibi_slopes.numel() != heads:
             raise ValueError(f"alibi_slopes must have {heads} entries, got {alibi_slopes.numel()}")
     dk = kernel_head_dim(dim)
-    if dk != dim:
-        pad = (0, dk - dim)
-        q = torch.nn.functional.pad(q, pad)
-        k_pool = torch.nn.functional.pad(k_pool, pad)
-        v_pool = torch.nn.functional.pad(v_pool, pad)
+    vec = 4 if q.dtype == torch.float32 else 8
+    if dk != dim and not (seq_q == 1 and dim % vec == 0):
+        # The decode kernel reads pools of any head dim that is a multiple of
+        # the 16-byte vector in place. Otherwise only the pages the tables
+        # reference are copied, zero-padded to the kernel head dim (exact:
+        # zero dims add nothing to q.k); the pools themselves are never copied.
+        k_pool, v_pool, block_tables = _referenced_pages_padded(k_pool, v_pool, block_tables, dk)
+        q = torch.nn.functional.pad(q, (0, dk - dim))
+    else:
+        dk = dim
     k_pool = k_pool.contiguous()
     v_pool = v_pool.contiguous()
-    vec = 4 if q.dtype == torch.float32 else 8
     if (q.stride(-1) != 1 or q.stride(0) % vec or q.stride(1) % vec or q.stride(2) % vec
             or q.data_ptr() % 16):
         q = q.contiguous()
@@ -128,6 +132,23 @@ def paged_attention(
     if dk != dim:
         out = out[..., :dim].contiguous()
     return out
+
+
+def _referenced_pages_padded(k_pool: torch.Tensor, v_pool: torch.Tensor,
+                             block_tables: torch.Tensor, dk: int):
+    """Pools holding only the pages block_tables references (ids in range),
+    zero-padded to head dim dk, and the tables renumbered to them (-1 kept).
+    Moves O(referenced tokens) bytes; reads the number of distinct pages back
+    to the host (one synchronisation)."""
+    nb = k_pool.shape[0]
+    t = block_tables.to(torch.int64)
+    valid = (t >= 0) & (t < nb)
+    used = torch.unique(t[valid])
+    remap = torch.full_like(t, -1)
+    remap[valid] = torch.searchsorted(used, t[valid])
+    pad = (0, dk - k_pool.shape[-1])
+    return (torch.nn.functional.pad(k_pool[used], pad), torch.nn.functional.pad(v_pool[used], pad),
+            remap.to(torch.int32))
 
 
 def paged_attention_with_bias(

@@ -6,10 +6,16 @@ and ``FusedRoPEFlashAttention`` (988-1109). K is rotated by the gfx950 RoPE
 kernel into a scratch tensor; for 16-bit inputs with head_dim 32, 64 or 128
 the flash kernel rotates Q itself as it loads it (as the reference's fused
 kernel does, fused_rope_attention.py:766-800), otherwise Q goes through the
-RoPE kernel too. Attention uses the reference's position-based causal rule
-(fused_rope_attention.py:125-131): query i at position q_offset + i sees key j
-at position kv_offset + j when kv_offset + j <= q_offset + i. Tensors are
-(batch, seq, heads, head_dim).
+RoPE kernel too. Tensors are (batch, seq, heads, head_dim).
+
+The two entry points mask differently, as in the reference:
+  * ``fused_rope_attention`` / ``FusedRoPEFlashAttention`` follow the fused
+    kernel's position rule (fused_rope_attention.py:125-131): query i at
+    position q_offset + i sees key j at position kv_offset + j when
+    kv_offset + j <= q_offset + i;
+  * ``fast_fused_rope_attention`` rotates, then hands mask="causal" to SDPA
+    (fused_rope_attention.py:716-727): the offsets move the rotation only and
+    key j is visible to query i when j <= i + max(0, seq_kv - seq_q).
 """
 
 from __future__ import annotations
@@ -45,26 +51,11 @@ def _check_inputs(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> None:
         raise ValueError(f"Q/K/V dtype mismatch: {q.dtype}, {k.dtype}, {v.dtype}")
 
 
-def fast_fused_rope_attention(
-    q: torch.Tensor,
-    k: torch.Tensor,
-    v: torch.Tensor,
-    scale: Optional[float] = None,
-    cos_cache: Optional[torch.Tensor] = None,
-    sin_cache: Optional[torch.Tensor] = None,
-    rope_base: float = 10000.0,
-    q_offset: int = 0,
-    kv_offset: int = 0,
-    causal: bool = False,
-    use_tiled: Optional[bool] = None,
-) -> torch.Tensor:
-    """softmax(scale * rope(Q) rope(K)^T + mask) V on the gfx950 kernels.
-
-    cos_cache / sin_cache: (positions, head_dim // 2), built with
-    ``precompute_rope_cache(max(seq_q + q_offset, seq_kv + kv_offset),
-    head_dim, rope_base, q.dtype)`` when not given (fused_rope_attention.py:
-    703-709). ``use_tiled`` is ignored, as in the reference.
-    """
+def _rope_attention(q, k, v, scale, cos_cache, sin_cache, rope_base, q_offset, kv_offset,
+                    causal, position_rule: bool) -> torch.Tensor:
+    """softmax(scale * rope(Q) rope(K)^T + mask) V on the gfx950 kernels, with
+    the position rule (kv_offset + j <= q_offset + i) or SDPA's causal rule
+    (j <= i + max(0, seq_kv - seq_q))."""
     _check_inputs(q, k, v)
     _native.require_no_grad(q, k, v)
     batch, seq_q, heads, dim = q.shape
@@ -77,7 +68,7 @@ def fast_fused_rope_attention(
         max_pos = max(seq_q + q_offset, seq_kv + kv_offset)
         cos_cache, sin_cache = precompute_rope_cache(max_pos, dim, base=rope_base,
                                                      dtype=q.dtype, device=q.device)
-    shift = q_offset - kv_offset
+    shift = q_offset - kv_offset if position_rule else max(0, seq_kv - seq_q)
     if causal and shift < 0:
         raise NotImplementedError(
             "causal fused RoPE attention with kv_offset > q_offset (queries before the first "
@@ -100,6 +91,33 @@ def fast_fused_rope_attention(
     return run_attention(q_rot, k_rot, v, Layout.BSHD, scale, **mask)
 
 
+def fast_fused_rope_attention(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    scale: Optional[float] = None,
+    cos_cache: Optional[torch.Tensor] = None,
+    sin_cache: Optional[torch.Tensor] = None,
+    rope_base: float = 10000.0,
+    q_offset: int = 0,
+    kv_offset: int = 0,
+    causal: bool = False,
+    use_tiled: Optional[bool] = None,
+) -> torch.Tensor:
+    """rope(Q) at q_offset, rope(K) at kv_offset, then attention with SDPA's
+    causal rule (fused_rope_attention.py:637-733): with ``causal`` key j is
+    visible to query i iff j <= i + max(0, seq_kv - seq_q), whatever the
+    offsets.
+
+    cos_cache / sin_cache: (positions, head_dim // 2), built with
+    ``precompute_rope_cache(max(seq_q + q_offset, seq_kv + kv_offset),
+    head_dim, rope_base, q.dtype)`` when not given (fused_rope_attention.py:
+    703-709). ``use_tiled`` is ignored, as in the reference.
+    """
+    return _rope_attention(q, k, v, scale, cos_cache, sin_cache, rope_base, q_offset,
+                           kv_offset, causal, position_rule=False)
+
+
 def fused_rope_attention(
     q: torch.Tensor,
     k: torch.Tensor,
@@ -113,13 +131,15 @@ def fused_rope_attention(
     causal: bool = False,
     use_metal: bool = True,
 ) -> torch.Tensor:
-    """Fused RoPE + flash attention (fused_rope_attention.py:939-985).
+    """Fused RoPE + flash attention (fused_rope_attention.py:939-985) with the
+    fused kernel's position rule: with ``causal`` key j is visible to query i
+    iff kv_offset + j <= q_offset + i (fused_rope_attention.py:125-131).
 
     ``use_metal`` is accepted for signature compatibility; the gfx950 kernels
     always run (there is no CPU path).
     """
-    return fast_fused_rope_attention(q, k, v, scale, cos_cache, sin_cache, rope_base,
-                                     q_offset, kv_offset, causal)
+    return _rope_attention(q, k, v, scale, cos_cache, sin_cache, rope_base, q_offset,
+                           kv_offset, causal, position_rule=True)
 
 
 class FusedRoPEFlashAttention(torch.nn.Module):

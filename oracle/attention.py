@@ -175,6 +175,56 @@ def dense_attention_bhsd(
     return out
 
 
+def sdpa_causal_keep(seq_q: int, seq_kv: int) -> np.ndarray:
+    """(Sq, Sk) visibility of ``mx.fast.scaled_dot_product_attention(mask="causal")``.
+
+    The reference's default routes (attention/flash.py:177-181 BHSD, 211-215 and
+    479-506 short BSHD, 221-235 long BSHD; kernels/fused_rope_attention.py:716-727)
+    hand the causal mask to MLX's SDPA (MLX >= 0.20.0, pyproject.toml:37; not
+    under /root/reference). Its causal rule aligns the diagonal at the bottom
+    right when the keys outnumber the queries, so the last query sees every key
+    (the intent stated at utils/masking.py:52-56, triu with k = Sk - Sq + 1), and
+    at the top left otherwise (offset max(0, Sk - Sq)): key j is visible to
+    query i iff j <= i + max(0, Sk - Sq). For Sq <= Sk this is exactly
+    create_causal_mask (causal_additive_mask below); for Sq > Sk it is the
+    top-left rule of the tiled path (_online_softmax.py:149-154), where the
+    dense fallback's (Sq, Sq) mask (flash.py:188) cannot broadcast.
+    """
+    off = max(0, seq_kv - seq_q)
+    return np.arange(seq_kv)[None, :] <= np.arange(seq_q)[:, None] + off
+
+
+def sdpa_attention(
+    q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float, causal: bool,
+) -> np.ndarray:
+    """BHSD exact-softmax attention with SDPA's causal rule (sdpa_causal_keep).
+
+    The arithmetic of the reference's SDPA routes (no epsilon); q (B, H, Sq, D),
+    k / v (B, H, Sk, D).
+    """
+    scores = np.matmul(q, np.swapaxes(k, -1, -2)) * q.dtype.type(scale)
+    if causal:
+        keep = sdpa_causal_keep(q.shape[2], k.shape[2])
+        scores = np.where(keep[None, None], scores, -np.inf)
+    return np.matmul(_softmax_last(scores), v)
+
+
+def flash_attention_default_route(
+    q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: Optional[float] = None,
+    causal: bool = True, layout: str = "BSHD",
+) -> np.ndarray:
+    """flash_attention on the reference's default route (use_metal=True, no
+    dropout): every size and layout goes to SDPA (flash.py:177-181, 211-235,
+    479-506), so the result is sdpa_attention in the caller's layout."""
+    layout = getattr(layout, "value", layout)
+    if scale is None:
+        scale = 1.0 / math.sqrt(q.shape[-1])
+    if layout == "BHSD":
+        return sdpa_attention(q, k, v, scale, causal)
+    t = lambda x: np.ascontiguousarray(np.transpose(x, (0, 2, 1, 3)))
+    return np.transpose(sdpa_attention(t(q), t(k), t(v), scale, causal), (0, 2, 1, 3))
+
+
 def flash_attention(
     q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: Optional[float] = None,
     causal: bool = True, block_q: int = 32, block_kv: int = 32, layout: str = "BSHD",
@@ -184,7 +234,10 @@ def flash_attention(
     mlx_primitives/attention/flash.py:52-254: BHSD goes to the dense branch
     (172-192); BSHD goes to the tiled path (254 -> 257-316). The reference's
     short-sequence shortcut (211-215) computes the same attention without the
-    epsilon; the oracle keeps the tiled path for every BSHD size.
+    epsilon; the oracle keeps the tiled path for every BSHD size. With Sq == Sk
+    (every causal BASELINE configuration) this equals the default route
+    (flash_attention_default_route); for causal Sq != Sk the routes differ
+    (the tiled path is top-left aligned, SDPA bottom-right when Sk > Sq).
     """
     layout = getattr(layout, "value", layout)
     dim = q.shape[-1]
@@ -285,9 +338,11 @@ def chunked_cross_attention_impl(
 def reference_cross_attention(
     q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float, causal: bool,
 ) -> np.ndarray:
-    """Dense cross attention (top-left causal, -1e38 mask).
+    """Dense cross attention (top-left causal, -1e38 mask, exact softmax).
 
-    Restates mlx_primitives/attention/chunked.py:172-203.
+    Restates mlx_primitives/attention/chunked.py:172-203, the branch
+    chunked_cross_attention takes when Skv <= chunk_size (113-114): key j is
+    visible to query i iff j <= i (absolute positions from 0 on both sides).
     """
     qt, kt, vt = (np.transpose(x, (0, 2, 1, 3)) for x in (q, k, v))
     scores = np.matmul(qt, np.swapaxes(kt, -1, -2)) * q.dtype.type(scale)

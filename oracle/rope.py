@@ -7,7 +7,9 @@ half-split rotation of rope 476-497) and the fused attention of
 kernels/fused_rope_attention.py: rotate Q at positions q_offset + i and K at
 kv_offset + j (711-714), then exact softmax attention with the position-based
 causal rule of the reference's fused kernel (125-131: key j is visible to
-query i when kv_offset + j <= q_offset + i).
+query i when kv_offset + j <= q_offset + i). fast_fused_rope_attention
+(637-733) instead hands the rotated tensors to SDPA (716-727), whose causal
+rule ignores the offsets (oracle.attention.sdpa_causal_keep).
 
 Parity pins (tests/test_oracle.py): rotation at position 0 is the identity;
 rotations preserve each (i, i + D/2) pair's norm; rope(q, m) . rope(k, n)
@@ -74,3 +76,28 @@ def fused_rope_attention(q: np.ndarray, k: np.ndarray, v: np.ndarray,
         e = np.exp(s - m)
         w = e / np.sum(e, axis=-1, keepdims=True)
     return np.transpose(np.matmul(w, np.transpose(v, (0, 2, 1, 3))), (0, 2, 1, 3))
+
+
+def fast_fused_rope_attention(q: np.ndarray, k: np.ndarray, v: np.ndarray,
+                              scale: Optional[float] = None,
+                              cos_cache: Optional[np.ndarray] = None,
+                              sin_cache: Optional[np.ndarray] = None,
+                              rope_base: float = 10000.0, q_offset: int = 0,
+                              kv_offset: int = 0, causal: bool = False) -> np.ndarray:
+    """rope(Q), rope(K) (fused_rope_attention.py:703-714), then SDPA with
+    mask="causal" (716-727): the offsets move the rotation only; the causal
+    diagonal is SDPA's (key j visible to query i iff j <= i + max(0, Skv - Sq)).
+    (B, Sq, H, D)."""
+    from oracle.attention import sdpa_attention
+
+    seq_q, dim = q.shape[1], q.shape[-1]
+    seq_kv = k.shape[1]
+    if scale is None:
+        scale = 1.0 / math.sqrt(dim)
+    if cos_cache is None or sin_cache is None:
+        cos_cache, sin_cache = precompute_rope_cache(
+            max(seq_q + q_offset, seq_kv + kv_offset), dim, rope_base)
+    t = lambda x: np.ascontiguousarray(np.transpose(x, (0, 2, 1, 3)))
+    qr = rope(q, cos_cache, sin_cache, q_offset)
+    kr = rope(k, cos_cache, sin_cache, kv_offset)
+    return np.transpose(sdpa_attention(t(qr), t(kr), t(v), scale, causal), (0, 2, 1, 3))

@@ -17,7 +17,8 @@ these fixtures follow the same idea at small sizes. Windows follow the
 production convention |i - j| <= W (W+1 keys including self with causal,
 attention/sliding_window.py:151-157), not the generator's W-key variant.
 
-Run from the repository root:  python tests/golden/make_golden.py
+Run from the repository root:  python tests/golden/make_golden.py [name ...]
+(with names, only those fixtures are rewritten).
 """
 
 from __future__ import annotations
@@ -79,7 +80,12 @@ def to_bhsd(x, layout):
     return x if layout == "BHSD" else np.transpose(x, (0, 2, 1, 3))
 
 
+ONLY = set(sys.argv[1:])  # fixture names to (re)write; empty = all
+
+
 def save(name, meta, **arrays):
+    if ONLY and name not in ONLY:
+        return
     path = os.path.join(HERE, f"{name}.npz")
     np.savez_compressed(path, meta=np.array(json.dumps(meta, sort_keys=True)), **arrays)
     print(f"{name}: {', '.join(f'{k}{tuple(v.shape)}' for k, v in arrays.items())}")
@@ -103,6 +109,25 @@ def flash_case(name, shape, dtype, layout, causal, seed, scale=None):
     agree(name, to_bhsd(exp, layout), ref)
     save(name, {"kind": "flash", "dtype": dtype, "layout": layout, "causal": causal,
                 "scale": scale}, q=q, k=k, v=v, expected=exp)
+
+
+def flash_default_case(name, qshape, kvlen, dtype, layout, seed):
+    """Causal flash_attention with Sq != Sk on the reference's default (SDPA)
+    route: key j visible to query i iff j <= i + max(0, Sk - Sq)."""
+    g = torch.Generator().manual_seed(seed)
+    q = rounded(qshape, dtype, g)
+    kshape = list(qshape)
+    kshape[2 if layout == "BHSD" else 1] = kvlen
+    k, v = (rounded(tuple(kshape), dtype, g) for _ in range(2))
+    exp = oa.flash_attention_default_route(q.astype(np.float64), k.astype(np.float64),
+                                           v.astype(np.float64), causal=True, layout=layout)
+    Sq = qshape[2] if layout == "BHSD" else qshape[1]
+    keep = np.tril(np.ones((Sq, kvlen), dtype=bool), k=max(0, kvlen - Sq))
+    ref = sdpa_rows(to_bhsd(q, layout), to_bhsd(k, layout), to_bhsd(v, layout),
+                    1.0 / math.sqrt(qshape[-1]), keep)
+    agree(name, to_bhsd(exp, layout), ref, AGREE_EXACT)
+    save(name, {"kind": "flash_default", "dtype": dtype, "layout": layout, "causal": True},
+         q=q, k=k, v=v, expected=exp)
 
 
 def grad_case(name, shape, dtype, layout, causal, window, seed):
@@ -154,7 +179,8 @@ def chunked_case(name, qshape, kvlen, dtype, chunk, causal, seed):
     keep = window_keep(Sq, kvlen, causal, -1, -1)
     ref = sdpa_rows(to_bhsd(q, "BSHD"), to_bhsd(k, "BSHD"), to_bhsd(v, "BSHD"),
                     1.0 / math.sqrt(D), keep)
-    agree(name, to_bhsd(exp, "BSHD"), ref)
+    # Skv <= chunk takes the exact dense branch (chunked.py:113-114, 172-203)
+    agree(name, to_bhsd(exp, "BSHD"), ref, AGREE_EXACT if kvlen <= chunk else AGREE_TILED)
     save(name, {"kind": "chunked", "dtype": dtype, "chunk_size": chunk, "causal": causal},
          q=q, k=k, v=v, expected=exp)
 
@@ -267,6 +293,13 @@ def main():
     window_case("window_full_bf16_w16", (1, 90, 2, 32), "bfloat16", 16, False, 106)
     chunked_case("chunked_full_f32", (1, 16, 2, 64), 300, "float32", 64, False, 107)
     chunked_case("chunked_causal_bf16", (1, 40, 2, 64), 200, "bfloat16", 64, True, 108)
+    # Skv <= chunk_size: the dense branch, top-left causal with more queries than keys
+    chunked_case("chunked_dense_causal_f16", (1, 48, 2, 64), 40, "float16", 64, True, 117)
+    # causal with Sq != Sk on the default route: decode-style (bottom right) and Sq > Sk
+    flash_default_case("flash_default_causal_bf16_bhsd_sq5_sk70", (1, 2, 5, 64), 70, "bfloat16",
+                       "BHSD", 118)
+    flash_default_case("flash_default_causal_f32_bshd_sq40_sk17", (1, 40, 2, 32), 17, "float32",
+                       "BSHD", 119)
     # tests/cache/test_paged_attention.py:164-197 (hand-built tables, page 8 unused)
     paged_case("paged_ref_tables_f32", [16, 32, 48, 25], [[0, -1, -1], [1, 2, -1], [3, 4, 5],
                                                           [6, 7, -1]], 9, 16, 2, 32, "float32", 109)

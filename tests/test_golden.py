@@ -43,6 +43,9 @@ def oracle_output(meta, a):
     if kind == "flash":
         return oa.flash_attention(f64["q"], f64["k"], f64["v"], scale=meta["scale"],
                                   causal=meta["causal"], layout=meta["layout"])
+    if kind == "flash_default":
+        return oa.flash_attention_default_route(f64["q"], f64["k"], f64["v"],
+                                                causal=meta["causal"], layout=meta["layout"])
     if kind == "window":
         return oa.sliding_window_attention(f64["q"], f64["k"], f64["v"], meta["window"],
                                            causal=meta["causal"])
@@ -111,6 +114,8 @@ def test_kernel_matches_golden(device, path):
     if kind == "flash":
         out = flash_attention(t["q"], t["k"], t["v"], scale=meta["scale"], causal=meta["causal"],
                               layout=meta["layout"])
+    elif kind == "flash_default":
+        out = flash_attention(t["q"], t["k"], t["v"], causal=meta["causal"], layout=meta["layout"])
     elif kind == "window":
         out = sliding_window_attention(t["q"], t["k"], t["v"], meta["window"], causal=meta["causal"])
     elif kind == "chunked":

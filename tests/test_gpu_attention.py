@@ -65,6 +65,23 @@ def test_flash_parity(device, dtype, layout, causal, D):
     check(out, ref, dtype)
 
 
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("layout", ["BSHD", "BHSD"])
+@pytest.mark.parametrize("Sq,Sk,D", [(1, 300, 64), (77, 300, 128), (300, 77, 64),
+                                     (5, 5000, 128), (257, 513, 32), (1, 1, 64)])
+def test_flash_causal_alignment(device, dtype, layout, Sq, Sk, D):
+    # causal=True with Sq != Sk follows the reference's default (SDPA) route:
+    # key j visible to query i iff j <= i + max(0, Sk - Sq) -- a decode step
+    # over a cache sees every key, Sq > Sk is top-left aligned.
+    B, H = 2, 3
+    qs = (B, Sq, H, D) if layout == "BSHD" else (B, H, Sq, D)
+    ks = (B, Sk, H, D) if layout == "BSHD" else (B, H, Sk, D)
+    (q, k, v), (qn, kn, vn) = inputs([qs, ks, ks], dtype, 7 * Sq + Sk, device)
+    out = flash_attention(q, k, v, causal=True, layout=layout)
+    assert out.dtype == dtype and out.shape == q.shape
+    check(out, oa.flash_attention_default_route(qn, kn, vn, causal=True, layout=layout), dtype)
+
+
 @pytest.mark.parametrize("S", [1, 2, 31, 47, 64, 127, 129, 192, 320, 513])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_flash_ragged_lengths(device, S, dtype):
@@ -224,6 +241,22 @@ def _sample_rows_check(out, q, k, v, cfg, rows_per_head=24, heads=4, seed=0, **m
     return worst
 
 
+def _slice_check(out, q, k, v, cfg, bh, block=1024, **mask):
+    """Exact oracle on every query row of the (batch, head) slices in bh."""
+    bhsd = cfg.get("layout") == "BHSD"
+    Sq = q.shape[2] if bhsd else q.shape[1]
+    scale = 1.0 / math.sqrt(q.shape[-1])
+    worst = 0.0
+    for b, h in bh:
+        sel = lambda x: (x[b, h] if bhsd else x[b, :, h]).double().cpu().numpy()
+        qs, ks, vs, os_ = sel(q), sel(k), sel(v), sel(out)
+        for r0 in range(0, Sq, block):
+            rows = np.arange(r0, min(Sq, r0 + block))
+            ref = oa.attention_rows(qs[rows], ks, vs, rows, scale, **mask)
+            worst = max(worst, float(np.abs(os_[rows] - ref).max()))
+    return worst
+
+
 def test_config1_flash_fp32_full(device):
     cfg = wl.CONFIGS["flash_fp32_bshd"]
     q, k, v = wl.make_qkv(cfg)
@@ -238,6 +271,8 @@ def test_config2_flash_bf16_full(device):
     out = flash_attention(q, k, v, causal=True, layout="BHSD")
     assert torch.isfinite(out.float()).all()
     assert _sample_rows_check(out, q, k, v, cfg, causal=True) <= LOWP_MAXABS
+    # two whole (batch, head) slices: the first and the last
+    assert _slice_check(out, q, k, v, cfg, [(0, 0), (3, 31)], causal=True) <= LOWP_MAXABS
     assert torch.equal(out, flash_attention(q, k, v, causal=True, layout="BHSD"))
 
 
@@ -248,6 +283,8 @@ def test_config3_window_bf16_full(device):
     assert torch.isfinite(out.float()).all()
     err = _sample_rows_check(out, q, k, v, cfg, causal=True, window_left=cfg["window"])
     assert err <= LOWP_MAXABS
+    err = _slice_check(out, q, k, v, cfg, [(1, 17)], causal=True, window_left=cfg["window"])
+    assert err <= LOWP_MAXABS
 
 
 def test_config5_chunked_bf16_full(device):
@@ -256,3 +293,4 @@ def test_config5_chunked_bf16_full(device):
     out = ChunkedCrossAttention(cfg["H"], cfg["D"], cfg["chunk_size"])(q, k, v)
     assert torch.isfinite(out.float()).all()
     assert _sample_rows_check(out, q, k, v, cfg, causal=False) <= LOWP_MAXABS
+    assert _slice_check(out, q, k, v, cfg, [(0, 0), (0, 15)], causal=False) <= LOWP_MAXABS

@@ -84,7 +84,10 @@ def test_flash_grad_ragged(device, dtype, Sq, Sk, causal):
     d = rnd((2, Sq, 4, 128), 4, dtype)
     fn = lambda q, k, v: flash_attention(q, k, v, causal=causal)
     out, *g = run_grads(fn, device, q, k, v, d)
-    check_grads(g, q, k, v, d, dtype, 1 / math.sqrt(128), causal)
+    if causal and Sk > Sq:  # SDPA's causal rule: bottom-right diagonal, j <= i + Sk - Sq
+        check_grads(g, q, k, v, d, dtype, 1 / math.sqrt(128), False, -1, Sk - Sq)
+    else:
+        check_grads(g, q, k, v, d, dtype, 1 / math.sqrt(128), causal)
 
 
 @pytest.mark.parametrize("dtype", DTYPES)

@@ -73,7 +73,7 @@ def test_reference_small_cases(device, lens, tables, nb):
 @pytest.mark.parametrize("D", [32, 64, 128])
 def test_random_tables(device, dtype, bs, D):
     rng = np.random.default_rng(bs * 1000 + D)
-    B, H = 5, 6  # H not a multiple of the 4 heads per workgroup
+    B, H = 5, 6  # three workgroups of 2 heads; not a multiple of the grouped launch's 4
     lens = rng.integers(1, 2000, B)
     pages = (lens + bs - 1) // bs
     nb = int(pages.sum()) + 3
@@ -86,6 +86,83 @@ def test_random_tables(device, dtype, bs, D):
         off += pages[b]
     out, ref = run_case(device, dtype, lens.tolist(), tables, nb, bs, H, D, alibi=(bs == 16))
     check(out, ref, dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("H", [1, 5, 7])
+@pytest.mark.parametrize("alibi", [False, True])
+def test_odd_head_counts(device, dtype, H, alibi):
+    # The decode launch runs 2 query heads per workgroup without grouped heads
+    # (4 with them): an odd H leaves the last workgroup one wave with no head.
+    rng = np.random.default_rng(40 + H)
+    lens = [700, 1, 1500]
+    nb = sum((n + 15) // 16 for n in lens) + 2
+    perm = rng.permutation(nb)
+    tables = np.full((3, 100), -1, np.int32)
+    off = 0
+    for b, n in enumerate(lens):
+        p = (n + 15) // 16
+        tables[b, :p] = perm[off:off + p]
+        off += p
+    out, ref = run_case(device, dtype, lens, tables, nb, 16, H, 64, alibi=alibi, seed=H)
+    check(out, ref, dtype)
+
+
+@pytest.mark.parametrize("dtype,D", [(torch.float16, 80), (torch.bfloat16, 96),
+                                     (torch.bfloat16, 48), (torch.float32, 100),
+                                     (torch.float32, 20), (torch.float16, 8),
+                                     (torch.bfloat16, 100), (torch.float16, 30)])
+def test_unpadded_head_dims(device, dtype, D):
+    # Head dims that are multiples of the 16-byte vector are read in place by
+    # the decode kernel; others copy only the referenced pages, padded.
+    out, ref = run_case(device, dtype, [40, 300, 17], [[3, 0, 5, -1, -1, -1, -1, -1, -1, -1, -1,
+                                                        -1, -1, -1, -1, -1, -1, -1, -1, -1],
+                                                       list(range(6, 25)) + [-1],
+                                                       [1, 2] + [-1] * 18], 26, 16, 3, D,
+                        alibi=True, seed=D)
+    check(out, ref, dtype)
+
+
+def test_decode_reads_pools_in_place(device):
+    # Decode over pools of a head dim the kernel does not instantiate (80 ->
+    # the 128 kernel) allocates nothing of the pools' size.
+    g = torch.Generator().manual_seed(3)
+    nb, bs, H, D = 4096, 16, 8, 80
+    kp = torch.randn(nb, bs, H, D, generator=g).to(torch.float16).to(device)
+    vp = torch.randn(nb, bs, H, D, generator=g).to(torch.float16).to(device)
+    q = torch.randn(2, 1, H, D, generator=g).to(torch.float16).to(device)
+    tables = torch.arange(2 * 64, dtype=torch.int32, device=device).reshape(2, 64)
+    lens = torch.tensor([1000, 64 * 16], dtype=torch.int32, device=device)
+    paged_attention(q, kp, vp, tables, lens, block_size=bs)  # warm the allocator
+    torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats(device)
+    base = torch.cuda.memory_allocated(device)
+    out = paged_attention(q, kp, vp, tables, lens, block_size=bs)
+    torch.cuda.synchronize()
+    peak = torch.cuda.max_memory_allocated(device) - base
+    assert peak < kp.numel() * kp.element_size() // 16, peak
+    ref = op.paged_attention(q.double().cpu().numpy(), kp.double().cpu().numpy(),
+                             vp.double().cpu().numpy(), tables.cpu().numpy(),
+                             lens.cpu().numpy(), block_size=bs)
+    check(out, ref, torch.float16)
+
+
+@pytest.mark.parametrize("D", [80, 30])
+def test_prefill_unpadded_head_dims(device, D):
+    # Prefill with a head dim the kernels do not instantiate: only the
+    # referenced pages are copied (padded); page 2 is referenced by neither row.
+    g = torch.Generator().manual_seed(D)
+    nb, bs, H = 6, 16, 2
+    q = torch.randn(2, 20, H, D, generator=g).to(torch.bfloat16)
+    kp = torch.randn(nb, bs, H, D, generator=g).to(torch.bfloat16)
+    vp = torch.randn(nb, bs, H, D, generator=g).to(torch.bfloat16)
+    tables = torch.tensor([[5, 0, -1], [3, 1, 4]], dtype=torch.int32)
+    lens = torch.tensor([25, 40], dtype=torch.int32)
+    out = paged_attention(q.to(device), kp.to(device), vp.to(device), tables.to(device),
+                          lens.to(device), block_size=bs)
+    ref = op.paged_attention(q.double().numpy(), kp.double().numpy(), vp.double().numpy(),
+                             tables.numpy(), lens.numpy(), block_size=bs)
+    check(out, ref, torch.bfloat16)
 
 
 def test_invalid_pages_are_masked(device):

@@ -113,6 +113,33 @@ def test_fused_rope_attention(device, dt, qs, ks, q_off, kv_off, causal):
     check(out, oracle_attention(q, k, v, dtype, scale, q_off, kv_off, causal), dtype)
 
 
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+@pytest.mark.parametrize("qs,ks,q_off,kv_off", [
+    ((1, 4, 4, 64), (1, 64, 4, 64), 0, 0),      # zero offsets, Sq < Skv: bottom right
+    ((2, 1, 4, 64), (2, 64, 4, 64), 63, 0),     # decode step
+    ((1, 8, 4, 64), (1, 8, 4, 64), 16, 16),
+    ((2, 40, 3, 128), (2, 24, 3, 128), 3, 10),  # Sq > Skv: top left; kv_offset > q_offset
+])
+def test_fast_fused_rope_attention_sdpa_rule(device, dt, qs, ks, q_off, kv_off):
+    # fast_fused_rope_attention hands mask="causal" to SDPA
+    # (fused_rope_attention.py:716-727): offsets rotate only.
+    dtype = DT[dt]
+    q, k, v = rnd(qs, 21, dtype), rnd(ks, 22, dtype), rnd(ks, 23, dtype)
+    out = fast_fused_rope_attention(q.to(device), k.to(device), v.to(device), q_offset=q_off,
+                                    kv_offset=kv_off, causal=True)
+    D = qs[-1]
+    n = max(qs[1] + q_off, ks[1] + kv_off)
+    cos, sin = precompute_rope_cache(n, D, dtype=dtype)
+    c64, s64 = cos.double().numpy(), sin.double().numpy()
+    qr = torch.from_numpy(orope.rope(q.double().numpy(), c64, s64, q_off)).to(dtype)
+    kr = torch.from_numpy(orope.rope(k.double().numpy(), c64, s64, kv_off)).to(dtype)
+    one, zero = np.ones((n, D // 2)), np.zeros((n, D // 2))
+    ref = orope.fast_fused_rope_attention(qr.double().numpy(), kr.double().numpy(),
+                                          v.double().numpy(), 1 / math.sqrt(D), one, zero,
+                                          q_offset=q_off, kv_offset=kv_off, causal=True)
+    check(out, ref, dtype)
+
+
 @pytest.mark.parametrize("base", [10000.0, 500000.0, 100.0])
 def test_rope_bases(device, base):
     # test_fused_rope_attention_correctness.py:271-295
@@ -208,10 +235,13 @@ def test_q_rotation_on_load_bit_identical(device, dt, D, cache_dt, q_off, kv_off
                                kv_offset=kv_off, causal=causal)
     qr, kr = rope(q, cos, sin, q_off), rope(k, cos, sin, kv_off)
     shift = q_off - kv_off
-    if causal and shift:
+    if causal:
+        # the position rule kv_offset + j <= q_offset + i (top-left when shift == 0;
+        # flash_attention's causal rule would align Sq < Sk at the bottom right)
         from mlx_primitives.attention._launch import run_attention
         from mlx_primitives.constants import Layout
-        ref = run_attention(qr, kr, v, Layout.BSHD, 1 / math.sqrt(D), False, window_right=shift)
+        ref = run_attention(qr, kr, v, Layout.BSHD, 1 / math.sqrt(D), shift == 0,
+                            window_right=shift if shift else -1)
     else:
         ref = flash_attention(qr, kr, v, causal=causal)
     torch.cuda.synchronize()

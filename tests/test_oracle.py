@@ -183,6 +183,69 @@ def test_chunked_cross_vs_brute(causal):
     np.testing.assert_allclose(out, ref, rtol=1e-12, atol=1e-12)
 
 
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("sq,skv", [(5, 11), (11, 5), (7, 7), (1, 9)])
+def test_reference_cross_dense_branch_vs_brute(causal, sq, skv):
+    # Skv <= chunk_size routes to the dense branch (chunked.py:113-114 -> 172-203):
+    # exact softmax (no epsilon, so 1e-12 here rejects an O(1e-6) normaliser) and
+    # the top-left rule j <= i on absolute positions.
+    q = rnd((2, sq, 2, 3), 60); k = rnd((2, skv, 2, 3), 61); v = rnd((2, skv, 2, 3), 62)
+    out = oa.chunked_cross_attention(q, k, v, chunk_size=16, scale=0.7, causal=causal)
+    ref = brute_attention(q, k, v, 0.7, (lambda i, j: j <= i) if causal else (lambda i, j: True))
+    np.testing.assert_allclose(out, ref, rtol=1e-12, atol=1e-12)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("sq,skv", [(33, 64), (64, 20)])
+def test_reference_cross_dense_branch_vs_sdpa(causal, sq, skv):
+    q = rnd((1, sq, 2, 8), 63); k = rnd((1, skv, 2, 8), 64); v = rnd((1, skv, 2, 8), 65)
+    out = oa.chunked_cross_attention(q, k, v, chunk_size=64, scale=0.4, causal=causal)
+    ref = sdpa(q, k, v, 0.4, causal_mask(sq, skv) if causal else None)
+    np.testing.assert_allclose(out, ref, rtol=1e-12, atol=1e-12)
+
+
+def test_sdpa_causal_rule_kats():
+    # utils/masking.py:44-50: one new token over 100 cached keys sees all 100.
+    assert oa.sdpa_causal_keep(1, 100).all()
+    # Sq <= Sk: the reference's create_causal_mask (triu, k = Sk - Sq + 1) keeps
+    # exactly the zero entries of the additive mask.
+    for sq, sk in [(4, 4), (3, 8), (1, 5)]:
+        np.testing.assert_array_equal(oa.sdpa_causal_keep(sq, sk),
+                                      oa.causal_additive_mask(sq, sk) == 0)
+    # Sq > Sk: the top-left rule of the tiled path; every row sees key 0.
+    np.testing.assert_array_equal(oa.sdpa_causal_keep(6, 3), causal_mask(6, 3))
+    assert oa.sdpa_causal_keep(6, 3)[:, 0].all()
+
+
+@pytest.mark.parametrize("sq,sk", [(5, 12), (12, 5), (9, 9), (1, 7)])
+@pytest.mark.parametrize("layout", ["BSHD", "BHSD"])
+def test_flash_default_route_vs_brute_and_sdpa(sq, sk, layout):
+    q = rnd((2, sq, 3, 8), 66); k = rnd((2, sk, 3, 8), 67); v = rnd((2, sk, 3, 8), 68)
+    off = max(0, sk - sq)
+    brute = brute_attention(q, k, v, 0.3, lambda i, j: j <= i + off)
+    # torch's own causal variants: lower-right aligned for Sk >= Sq, is_causal
+    # (upper-left) for Sq > Sk.
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).double().transpose(1, 2)
+    if sk >= sq:
+        from torch.nn.attention.bias import causal_lower_right
+        lib = F.scaled_dot_product_attention(t(q), t(k), t(v), attn_mask=causal_lower_right(sq, sk),
+                                             scale=0.3)
+    else:
+        lib = F.scaled_dot_product_attention(t(q), t(k), t(v), is_causal=True, scale=0.3)
+    lib = lib.transpose(1, 2).numpy()
+    if layout == "BHSD":
+        tr = lambda x: np.ascontiguousarray(x.transpose(0, 2, 1, 3))
+        out = oa.flash_attention_default_route(tr(q), tr(k), tr(v), 0.3, True,
+                                               layout="BHSD").transpose(0, 2, 1, 3)
+    else:
+        out = oa.flash_attention_default_route(q, k, v, 0.3, True)
+    np.testing.assert_allclose(out, brute, rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(out, lib, rtol=1e-12, atol=1e-12)
+    if sq == sk:  # the default and CPU routes agree on square causal attention
+        np.testing.assert_allclose(oa.flash_attention(q, k, v, 0.3, True, 4, 4), out,
+                                   rtol=2e-6, atol=2e-6)
+
+
 def test_attention_rows_vs_brute():
     q, k, v = (rnd((1, 12, 1, 4), s) for s in (29, 30, 31))
     rows = np.array([0, 5, 11])
@@ -442,7 +505,7 @@ def test_rope_identity_norm_and_relative_position():
     assert abs(dots[0] - float(np.sum(orope.rope(q, cos, sin, 6) * orope.rope(k, cos, sin, 2)))) > 1e-2
 
 
-def _brute_rope_attention(q, k, v, scale, base, q_off, kv_off, causal):
+def _brute_rope_attention(q, k, v, scale, base, q_off, kv_off, causal, allowed=None):
     B, Sq, H, D = q.shape
     Sk = k.shape[1]
     half = D // 2
@@ -460,7 +523,10 @@ def _brute_rope_attention(q, k, v, scale, base, q_off, kv_off, causal):
             ks = [rot(k[b, j, h], kv_off + j) for j in range(Sk)]
             for i in range(Sq):
                 qi = rot(q[b, i, h], q_off + i)
-                js = [j for j in range(Sk) if not causal or kv_off + j <= q_off + i]
+                if allowed is not None:
+                    js = [j for j in range(Sk) if not causal or allowed(i, j)]
+                else:
+                    js = [j for j in range(Sk) if not causal or kv_off + j <= q_off + i]
                 sc = [scale * float(np.dot(qi, ks[j])) for j in js]
                 m = max(sc)
                 w = [math.exp(x - m) for x in sc]
@@ -480,6 +546,21 @@ def test_fused_rope_attention_vs_brute(q_off, kv_off, causal, sq, sk):
                                      kv_offset=kv_off, causal=causal)
     ref = _brute_rope_attention(q, k, v, 0.4, 100.0, q_off, kv_off, causal)
     # the oracle's angles are float32 (as the reference's cache): ~1e-6 agreement
+    np.testing.assert_allclose(out, ref, rtol=2e-5, atol=2e-6)
+
+
+@pytest.mark.parametrize("q_off,kv_off,sq,sk", [(0, 0, 2, 6), (5, 0, 3, 7), (0, 0, 6, 3),
+                                                  (4, 4, 3, 3)])
+def test_fast_fused_rope_attention_vs_brute(q_off, kv_off, sq, sk):
+    # fast_fused_rope_attention: offsets rotate only; SDPA's causal diagonal.
+    rng = np.random.default_rng(53 + q_off + sk)
+    q = rng.standard_normal((1, sq, 2, 8)); k = rng.standard_normal((1, sk, 2, 8))
+    v = rng.standard_normal((1, sk, 2, 8))
+    out = orope.fast_fused_rope_attention(q, k, v, scale=0.4, rope_base=100.0, q_offset=q_off,
+                                          kv_offset=kv_off, causal=True)
+    off = max(0, sk - sq)
+    ref = _brute_rope_attention(q, k, v, 0.4, 100.0, q_off, kv_off, True,
+                                allowed=lambda i, j: j <= i + off)
     np.testing.assert_allclose(out, ref, rtol=2e-5, atol=2e-6)
 
 
@@ -743,3 +824,38 @@ def test_pin_catches_grad_without_rowsum_term(monkeypatch):
         test_grad_vs_autograd(True, -1, -1, 2, 2, 9, 9)
     with pytest.raises(AssertionError):
         test_grad_finite_differences(True, -1)
+
+
+def test_pin_catches_cross_dense_bottom_right(monkeypatch):
+    def bad(q, k, v, scale, causal):
+        qt, kt, vt = (np.transpose(x, (0, 2, 1, 3)) for x in (q, k, v))
+        sc = np.matmul(qt, np.swapaxes(kt, -1, -2)) * scale
+        if causal:  # diagonal aligned at the bottom right instead of the top left
+            keep = oa.sdpa_causal_keep(q.shape[1], k.shape[1])
+            sc = np.where(keep[None, None], sc, oa.ATTENTION_MASK_VALUE)
+        return np.transpose(np.matmul(oa._softmax_last(sc), vt), (0, 2, 1, 3))
+    monkeypatch.setattr(oa, "reference_cross_attention", bad)
+    with pytest.raises(AssertionError):
+        test_reference_cross_dense_branch_vs_brute(True, 5, 11)
+    with pytest.raises(AssertionError):
+        test_reference_cross_dense_branch_vs_sdpa(True, 33, 64)
+
+
+def test_pin_catches_cross_dense_epsilon(monkeypatch):
+    orig = oa.reference_cross_attention
+    monkeypatch.setattr(oa, "reference_cross_attention",
+                        lambda q, k, v, s, c: orig(q, k, v, s, c) / (1 + 1e-6))  # l + 1e-6
+    with pytest.raises(AssertionError):
+        test_reference_cross_dense_branch_vs_brute(False, 7, 7)
+
+
+@pytest.mark.parametrize("rule", ["top_left", "unclamped"])
+def test_pin_catches_sdpa_causal_alignment(monkeypatch, rule):
+    def bad(sq, sk):
+        off = 0 if rule == "top_left" else sk - sq  # unclamped: rows before key 0
+        return np.arange(sk)[None, :] <= np.arange(sq)[:, None] + off
+    monkeypatch.setattr(oa, "sdpa_causal_keep", bad)
+    case = (5, 12) if rule == "top_left" else (12, 5)
+    with pytest.raises(AssertionError):
+        with np.errstate(invalid="ignore"):
+            test_flash_default_route_vs_brute_and_sdpa(*case, "BSHD")
