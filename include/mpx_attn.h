@@ -292,6 +292,32 @@ int mpx_attn_bwd(const void* q, const void* k, const void* v, const void* o, con
                  int window_left, int window_right, int dtype,
                  void* workspace, size_t workspace_bytes, void* stream);
 
+/*
+ * Paged-KV decode that allocates nothing: mpx_paged_decode_gqa without the
+ * workspace arguments. It has no counterpart in the reference; it is for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).
+ *
+ * The per-partition (o, m, l) partials go to a static device array of
+ * MPX_NOALLOC_SCRATCH_BYTES that the library holds on each GPU it runs on
+ * until the process ends. Calls needing more (B * H *
+ * ceil(max_blocks * block_size / 512) * (kernel head dim + 2) * 4 bytes,
+ * kernel head dim = 32, 64 or 128 >= D) return MPX_EINVAL. Nothing in the
+ * array has to start at zero: each call writes every partial it reads. All
+ * calls on one GPU share that GPU's array, so two calls that overlap on one
+ * GPU (different streams, or threads without ordering) race and corrupt each
+ * other; calls on one stream are ordered and safe. `stream` must belong to the
+ * calling thread's current device. Results are identical to mpx_paged_decode_gqa.
+ */
+#define MPX_NOALLOC_SCRATCH_BYTES (32u << 20)
+
+int mpx_paged_decode_noalloc(const void* q, const void* k_pool, const void* v_pool,
+                             const int32_t* block_tables, const int32_t* context_lens,
+                             const float* alibi_slopes, void* o,
+                             const int64_t* q_strides, const int64_t* o_strides,
+                             int B, int H, int H_kv, int D, int num_blocks, int block_size,
+                             int max_blocks, float scale, int dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

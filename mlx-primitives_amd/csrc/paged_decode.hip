@@ -23,7 +23,9 @@
 #include "mpx_common.h"
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
+#include <mutex>
 
 namespace mpx {
 
@@ -378,6 +380,50 @@ int paged_decode_run(const void* q, const void* k_pool, const void* v_pool,
   return MPX_OK;
 }
 
+// ---- device scratch of the no-allocation entry --------------------------------
+//
+// mpx_paged_decode_noalloc keeps its (o, m, l) partials in this file-scope
+// array instead of a caller workspace. Every GPU the library runs on holds its
+// own copy (MPX_NOALLOC_SCRATCH_BYTES) until the process ends. In host code
+// the name `scratch` is only a stand-in for the symbol: its device address is
+// looked up once per device with hipGetSymbolAddress, and only that address is
+// handed to kernels.
+static __device__ __align__(256) unsigned char scratch[MPX_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_scratch_ptr[kMaxDevices];
+std::mutex g_scratch_mu;
+
+// Device address of `scratch` on the calling thread's current device, which
+// must also be the device of `stream`.
+int scratch_for_stream(void* stream, void** out) {
+  int dev = -1;
+  MPX_CHECK_HIP(hipGetDevice(&dev));
+  if (stream != nullptr) {
+    hipDevice_t sdev = -1;
+    MPX_CHECK_HIP(hipStreamGetDevice((hipStream_t)stream, &sdev));
+    MPX_CHECK_ARG(sdev == dev,
+                  "mpx_paged_decode_noalloc: the stream belongs to device %d, the current "
+                  "device is %d",
+                  (int)sdev, dev);
+  }
+  MPX_CHECK_ARG(dev >= 0 && dev < kMaxDevices, "mpx_paged_decode_noalloc: device %d out of range",
+                dev);
+  void* ptr = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (ptr == nullptr) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    ptr = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (ptr == nullptr) {
+      MPX_CHECK_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+      MPX_CHECK_ARG(ptr != nullptr && ((uintptr_t)ptr & 255u) == 0,
+                    "mpx_paged_decode_noalloc: no device address for the scratch array");
+      g_scratch_ptr[dev].store(ptr, std::memory_order_release);
+    }
+  }
+  *out = ptr;
+  return MPX_OK;
+}
+
 }  // namespace
 }  // namespace mpx
 
@@ -413,4 +459,29 @@ extern "C" int mpx_paged_decode(const void* q, const void* k_pool, const void* v
                               q_strides, o_strides, B, H, H > 0 ? H : 1, D, num_blocks,
                               block_size, max_blocks, scale, dtype, workspace, workspace_bytes,
                               stream);
+}
+
+extern "C" int mpx_paged_decode_noalloc(const void* q, const void* k_pool, const void* v_pool,
+                                        const int32_t* block_tables, const int32_t* context_lens,
+                                        const float* alibi_slopes, void* o,
+                                        const int64_t* q_strides, const int64_t* o_strides,
+                                        int B, int H, int H_kv, int D, int num_blocks,
+                                        int block_size, int max_blocks, float scale, int dtype,
+                                        void* stream) {
+  clear_error();
+  if (B > 0 && H > 0 && D > 0 && block_size > 0 && max_blocks >= 0) {
+    const size_t need = decode_ws_bytes(B, H, D, block_size, max_blocks);
+    MPX_CHECK_ARG(need <= (size_t)MPX_NOALLOC_SCRATCH_BYTES,
+                  "mpx_paged_decode_noalloc: the call needs %zu bytes of partials, more than "
+                  "the %zu-byte device scratch (B * H * ceil(max_blocks * block_size / 512) * "
+                  "(kernel head dim + 2) * 4 bytes); use mpx_paged_decode with a workspace",
+                  need, (size_t)MPX_NOALLOC_SCRATCH_BYTES);
+  }
+  void* ws = nullptr;
+  const int rc = scratch_for_stream(stream, &ws);
+  if (rc != MPX_OK) return rc;
+  return paged_decode_run(q, k_pool, v_pool, block_tables, context_lens, alibi_slopes, o,
+                          q_strides, o_strides, B, H, H_kv, D, num_blocks, block_size,
+                          max_blocks, scale, dtype, ws, (size_t)MPX_NOALLOC_SCRATCH_BYTES, stream,
+                          "mpx_paged_decode_noalloc");
 }

@@ -33,7 +33,7 @@ def test_header_declares_expected_entry_points():
         "mpx_paged_decode", "mpx_paged_decode_workspace_bytes", "mpx_paged_prefill",
         "mpx_paged_prefill_workspace_bytes", "mpx_kv_append", "mpx_rope", "mpx_attn_fwd_gqa",
         "mpx_paged_decode_gqa", "mpx_paged_prefill_gqa", "mpx_attn_fwd_lse", "mpx_attn_bwd",
-        "mpx_attn_bwd_workspace_bytes", "mpx_attn_fwd_rope"])
+        "mpx_attn_bwd_workspace_bytes", "mpx_attn_fwd_rope", "mpx_paged_decode_noalloc"])
 
 
 def test_library_exports_every_declared_symbol(lib):
