@@ -12,10 +12,15 @@ under "flash_backward", and the sliding-window (config 3) and chunked
 cross-attention (config 5) workloads under "sliding_window" and "chunked_cross".
 Inputs are synthetic (seeded N(0,1)) and resident in HBM before timing.
 
+BASELINE config 1 (flash_attention fp32 BSHD B=2 S=1024 H=12 D=64 causal, the
+reference's CPU-runnable case) is timed under "flash_fp32" against the fp32
+matrix peak, next to the oracle's restatement of the reference's Python tiled
+path (32x32 blocks) on host cores.
+
 Prints ONE JSON line. Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 
-`--only flash|paged|prefill|append|rope|bwd|copy` runs a single leg (no CPU baseline) for profiler
-passes; `copy` streams a 1 GiB float32 buffer through an elementwise kernel,
+`--only flash|fp32|window|chunked|paged|prefill|append|rope|bwd|copy` runs a single leg
+(no CPU baseline) for profiler passes; `copy` streams a 1 GiB float32 buffer through an elementwise kernel,
 the known-size reference for scaling the HBM byte counters. The HBM traffic
 per launch measured by those passes (rocprofv3 FETCH_SIZE / WRITE_SIZE) is read
 from profiles/hbm_traffic.json when present.
@@ -39,9 +44,13 @@ import torch  # noqa: E402
 import workloads as wl  # noqa: E402
 
 PEAK_BF16_TFLOPS = 2516.6   # MI355X dense bf16 MFMA
+PEAK_F32_TFLOPS = 157.3     # MI355X fp32 matrix (MFMA)
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 TRAFFIC_FILE = os.path.join(REPO, "profiles", "hbm_traffic.json")
 FLASH_KERNEL = "fa_fwd16_kernel<128,128,8,bf16>"
+FP32_KERNEL = "fa_fwd32_kernel<64,64,4>"
+WINDOW_KERNEL = "fa_fwd16_kernel<128,128,8,bf16>"
+CHUNKED_KERNELS = "fa_fwd16_kernel<64,128,8,bf16> (split-KV) + fa_split_merge_kernel"
 PAGED_KERNELS = "paged_decode_part_kernel + paged_decode_merge_kernel"
 PREFILL_KERNEL = "fa_fwd16_kernel<128,64,8,bf16,paged>"
 APPEND_KERNEL = "kv_append_kernel"
@@ -136,6 +145,89 @@ def cpu_baseline_flash(cfg: dict, q: torch.Tensor, k: torch.Tensor, v: torch.Ten
             "kind": "port",
             "sample": f"{heads_done} of {B * H} (batch, head) pairs of the same workload, "
                       f"oracle dense BHSD branch in float32 numpy, {t_total:.1f} s"}
+
+
+def cpu_baseline_tiled(cfg: dict, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                       budget_s: float) -> dict:
+    """The oracle's restatement of the reference's Python tiled path
+    (_tiled_flash_attention, flash.py:257-316: 32x32 blocks, online softmax
+    merge, o / (l + 1e-6)) in float32 numpy over the whole config-1 workload,
+    repeated until ~budget_s of CPU work."""
+    from oracle import attention as oa
+
+    B, S, H, D = q.shape
+    scale = wl.default_scale(D)
+    qs, ks, vs = (x.float().cpu().numpy() for x in (q, k, v))
+    t_total, runs = 0.0, 0
+    while t_total < budget_s:
+        t0 = time.perf_counter()
+        oa.tiled_flash_attention(qs, ks, vs, scale, True, 32, 32)
+        t_total += time.perf_counter() - t0
+        runs += 1
+    flops = runs * wl.flash_flops(B, H, S, D, True)
+    return {"value": flops / t_total / 1e12, "unit": "TFLOP/s", "cores": blas_threads(),
+            "kind": "port",
+            "sample": f"the whole workload {runs} times, oracle tiled path (32x32 blocks, "
+                      f"flash.py:257-316) in float32 numpy, {t_total:.1f} s"}
+
+
+def cpu_baseline_window(cfg: dict, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                        budget_s: float) -> dict:
+    """The oracle's restatement of the reference's tiled window path
+    (_tiled_sliding_window_attention, sliding_window.py:363-511: 32-query
+    blocks, KV from q0 - W in 32-key steps) in float32 numpy, whole (batch,
+    head) slices of the config-3 workload until ~budget_s of CPU work."""
+    from oracle import attention as oa
+
+    B, S, H, D = q.shape
+    W = cfg["window"]
+    scale = wl.default_scale(D)
+    t_total, done = 0.0, 0
+    for b in range(B):
+        for h in range(H):
+            qs, ks, vs = (x[b:b + 1, :, h:h + 1].float().cpu().numpy() for x in (q, k, v))
+            t0 = time.perf_counter()
+            oa.tiled_sliding_window_attention(qs, ks, vs, W, scale, True, block_q=32)
+            t_total += time.perf_counter() - t0
+            done += 1
+            if t_total >= budget_s:
+                break
+        if t_total >= budget_s:
+            break
+    flops = wl.window_flops(1, done, S, D, W)
+    return {"value": flops / t_total / 1e12, "unit": "TFLOP/s", "cores": blas_threads(),
+            "kind": "port",
+            "sample": f"{done} of {B * H} (batch, head) slices of the same workload, oracle tiled "
+                      f"window path (sliding_window.py:363-511) in float32 numpy, {t_total:.1f} s"}
+
+
+def cpu_baseline_chunked(cfg: dict, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                         budget_s: float) -> dict:
+    """The oracle's restatement of the reference's chunk loop
+    (_chunked_cross_attention_impl, chunked.py:129-169, chunk 1024) in float32
+    numpy, whole heads of the config-5 workload until ~budget_s of CPU work."""
+    from oracle import attention as oa
+
+    B, Sq, H, D = q.shape
+    Skv = k.shape[1]
+    scale = wl.default_scale(D)
+    t_total, done = 0.0, 0
+    for b in range(B):
+        for h in range(H):
+            qs, ks, vs = (x[b:b + 1, :, h:h + 1].float().cpu().numpy() for x in (q, k, v))
+            t0 = time.perf_counter()
+            oa.chunked_cross_attention_impl(qs, ks, vs, cfg["chunk_size"], scale, False)
+            t_total += time.perf_counter() - t0
+            done += 1
+            if t_total >= budget_s:
+                break
+        if t_total >= budget_s:
+            break
+    flops = wl.chunked_flops(1, done, Sq, Skv, D)
+    return {"value": flops / t_total / 1e12, "unit": "TFLOP/s", "cores": blas_threads(),
+            "kind": "port",
+            "sample": f"{done} of {B * H} (batch, head) slices of the same workload, oracle chunk "
+                      f"loop (chunked.py:129-169, chunk 1024) in float32 numpy, {t_total:.1f} s"}
 
 
 def cpu_baseline_paged(inp, cfg: dict, budget_s: float) -> dict:
@@ -293,6 +385,32 @@ def rope_attention_step(dev):
     return fn
 
 
+def fp32_step(dev):
+    """flash_attention fp32 BSHD (2, 1024, 12, 64), causal."""
+    from mlx_primitives.attention import flash_attention
+
+    q, k, v = wl.make_qkv(wl.CONFIGS["flash_fp32_bshd"], device=dev)
+    return (q, k, v), lambda: flash_attention(q, k, v, causal=True)
+
+
+def window_step(dev):
+    """sliding_window_attention bf16 BSHD, W = 4096, causal."""
+    from mlx_primitives.attention import sliding_window_attention
+
+    cfg = wl.CONFIGS["window_bf16_bshd"]
+    q, k, v = wl.make_qkv(cfg, device=dev)
+    return (q, k, v), lambda: sliding_window_attention(q, k, v, cfg["window"], causal=True)
+
+
+def chunked_step(dev):
+    """chunked_cross_attention bf16, 512 queries x 65536 keys."""
+    from mlx_primitives.attention import chunked_cross_attention
+
+    cfg = wl.CONFIGS["chunked_bf16"]
+    q, k, v = wl.make_qkv(cfg, device=dev)
+    return (q, k, v), lambda: chunked_cross_attention(q, k, v, chunk_size=cfg["chunk_size"])
+
+
 def run_one_leg(args) -> int:
     """One leg for a profiler pass: warmup + steps calls, timing on stderr/stdout."""
     dev = torch.device("cuda:0")
@@ -310,6 +428,15 @@ def run_one_leg(args) -> int:
         q, k, v = wl.make_qkv(cfg, device=dev)
         fn = lambda: flash_attention(q, k, v, causal=True, layout="BHSD")
         work, unit = wl.config_work("flash_bf16_bhsd"), "flop"
+    elif args.only == "fp32":
+        fn = fp32_step(dev)[1]
+        work, unit = wl.config_work("flash_fp32_bshd"), "flop"
+    elif args.only == "window":
+        fn = window_step(dev)[1]
+        work, unit = wl.config_work("window_bf16_bshd"), "flop"
+    elif args.only == "chunked":
+        fn = chunked_step(dev)[1]
+        work, unit = wl.config_work("chunked_bf16"), "flop"
     elif args.only == "prefill":
         _, fn = prefill_step(dev)
         work, unit = wl.config_work("paged_prefill_bf16"), "flop"
@@ -329,11 +456,16 @@ def run_one_leg(args) -> int:
         fn = lambda: paged_attention(pin.q, pin.k_pool, pin.v_pool, pin.block_tables,
                                      pin.context_lens, block_size=pin.block_size)
         work, unit = wl.config_work("paged_decode_fp16", pin), "bytes"
-    # Counter passes profile every dispatch: no settling phase here.
-    wall_ms, ev_ms, ev_min, _ = time_steps(fn, args.steps, args.warmup, settle_s=0.0)
+    # Counter passes profile every dispatch: no settling phase by default. A
+    # kernel-trace pass settles the clocks like the full bench (--settle 0.3);
+    # its timed calls are the last `steps` dispatches of each kernel.
+    wall_ms, ev_ms, ev_min, ev_med = time_steps(fn, args.steps, args.warmup,
+                                                settle_s=args.settle)
     print(json.dumps({"leg": args.only, "steps": args.steps, "warmup": args.warmup,
-                      "ms_per_call": ev_ms, "min_ms": ev_min, "work_per_call": work,
-                      "work_unit": unit}), flush=True)
+                      "settle_s": args.settle, "ms_per_call": ev_ms, "median_ms": ev_med,
+                      "min_ms": ev_min, "work_per_call": work, "work_unit": unit,
+                      "rate": work / (ev_ms * 1e-3) / (1e12 if unit == "flop" else 1e9),
+                      "rate_unit": "TFLOP/s" if unit == "flop" else "GB/s"}), flush=True)
     return 0
 
 
@@ -346,9 +478,12 @@ def main() -> int:
                     help="seconds of CPU work per baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only",
-                    choices=["flash", "paged", "prefill", "append", "rope", "bwd", "copy"],
+                    choices=["flash", "fp32", "window", "chunked", "paged", "prefill", "append",
+                             "rope", "bwd", "copy"],
                     default=None,
                     help="run one leg only (profiler passes); prints that leg's timing")
+    ap.add_argument("--settle", type=float, default=0.0,
+                    help="--only: seconds of untimed calls before the warmup")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
@@ -433,30 +568,32 @@ def main() -> int:
         f"{b_tf:.1f} TFLOP/s")
 
     # ---- config 3: sliding window W=4096, config 5: chunked cross attention ------------
-    from mlx_primitives.attention import chunked_cross_attention, sliding_window_attention
-
     wcfg = wl.CONFIGS["window_bf16_bshd"]
-    wq, wk, wv = wl.make_qkv(wcfg, device=dev)
+    (wq, wk, wv), wstep = window_step(dev)
     wflops = wl.config_work("window_bf16_bshd")
-    wstep = lambda: sliding_window_attention(wq, wk, wv, wcfg["window"], causal=True)
     log(f"[bench] sliding_window: warmup {args.warmup}, steps {args.steps}")
     w_wall, w_ev, w_min, w_med = time_steps(wstep, args.steps, args.warmup)
     w_tf = wflops / (w_ev * 1e-3) / 1e12
     log(f"[bench] sliding_window: kernel {w_ev:.3f} ms -> {w_tf:.1f} TFLOP/s")
-    del wq, wk, wv
     ccfg = wl.CONFIGS["chunked_bf16"]
-    cq, ck, cv = wl.make_qkv(ccfg, device=dev)
+    (cq, ck, cv), cstep2 = chunked_step(dev)
     cflops = wl.config_work("chunked_bf16")
     cbytes = 2.0 * (cq.numel() * 2 + ck.numel() + cv.numel())  # q, o + k, v once, bf16
-    cstep2 = lambda: chunked_cross_attention(cq, ck, cv, chunk_size=ccfg["chunk_size"])
     log(f"[bench] chunked_cross: warmup {args.warmup}, steps {args.steps}")
     k_wall, k_ev, k_min, k_med = time_steps(cstep2, args.steps, args.warmup)
     k_tf = cflops / (k_ev * 1e-3) / 1e12
     k_gbs = cbytes / (k_ev * 1e-3) / 1e9
     log(f"[bench] chunked_cross: kernels {k_ev:.3f} ms -> {k_tf:.1f} TFLOP/s, {k_gbs:.0f} GB/s")
-    del cq, ck, cv
 
-    cpu = pcpu = fcpu = acpu = bcpu = None
+    # ---- config 1: flash fp32 BSHD (2, 1024, 12, 64), causal ----------------------------
+    (oq, ok_, ov), ostep = fp32_step(dev)
+    oflops = wl.config_work("flash_fp32_bshd")
+    log(f"[bench] flash_fp32: warmup {args.warmup}, steps {args.steps}")
+    o_wall, o_ev, o_min, o_med = time_steps(ostep, args.steps, args.warmup)
+    o_tf = oflops / (o_ev * 1e-3) / 1e12
+    log(f"[bench] flash_fp32: kernel {o_ev:.4f} ms -> {o_tf:.1f} TFLOP/s")
+
+    cpu = pcpu = fcpu = acpu = bcpu = wcpu = kcpu = ocpu = None
     if not args.no_cpu_baseline:
         log("[bench] cpu baselines (oracle restatement on host cores)")
         cpu = cpu_baseline_flash(cfg, q, k, v, args.cpu_budget)
@@ -465,6 +602,10 @@ def main() -> int:
         acpu = cpu_baseline_append(ainp, wl.CONFIGS[aname], args.cpu_budget)
         bcpu = cpu_baseline_bwd(cfg, bq.detach(), bk.detach(), bv.detach(), bdo,
                                 args.cpu_budget)
+        wcpu = cpu_baseline_window(wcfg, wq, wk, wv, args.cpu_budget)
+        kcpu = cpu_baseline_chunked(ccfg, cq, ck, cv, args.cpu_budget)
+        ocpu = cpu_baseline_tiled(wl.CONFIGS["flash_fp32_bshd"], oq, ok_, ov, args.cpu_budget)
+    del wq, wk, wv, cq, ck, cv
 
     result = {
         "metric": "causal fwd TFLOP/s @S=4096,D=128 + paged-decode HBM GB/s, % of roofline",
@@ -541,7 +682,9 @@ def main() -> int:
             "kernel_ms_median": w_med, "kernel_ms_min": w_min, "flop_per_step": wflops,
             "roofline": {"bound": "mfma", "achieved": w_tf, "peak": PEAK_BF16_TFLOPS,
                          "unit": "TFLOP/s", "frac": w_tf / PEAK_BF16_TFLOPS,
-                         "kernel": "fa_fwd16_kernel<128,128,8,bf16>"},
+                         "traffic": measured_traffic("window_bf16_bshd"),
+                         "kernel": WINDOW_KERNEL, "traffic_unit": "bytes per launch"},
+            "cpu_baseline": wcpu,
         },
         "chunked_cross": {
             "workload": "chunked_cross_attention bf16 BSHD q (1,512,16,64), k/v (1,65536,16,64), "
@@ -551,10 +694,23 @@ def main() -> int:
             "bytes_per_step": cbytes,
             "roofline": {"bound": "mfma", "achieved": k_tf, "peak": PEAK_BF16_TFLOPS,
                          "unit": "TFLOP/s", "frac": k_tf / PEAK_BF16_TFLOPS,
-                         "kernel": "fa_fwd16_kernel<64,128,8,bf16> (split-KV) + "
-                                   "fa_split_merge_kernel"},
+                         "traffic": measured_traffic("chunked_bf16"),
+                         "kernel": CHUNKED_KERNELS, "traffic_unit": "bytes per launch"},
             "hbm_roofline": {"achieved": k_gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                              "frac": k_gbs / PEAK_HBM_GBS},
+            "cpu_baseline": kcpu,
+        },
+        "flash_fp32": {
+            "workload": "flash_attention fp32 BSHD B=2 S=1024 H=12 D=64 causal, scale 1/8 "
+                        "(BASELINE config 1)",
+            "value": o_tf, "unit": "TFLOP/s", "ms_per_step": o_wall, "kernel_ms": o_ev,
+            "kernel_ms_median": o_med, "kernel_ms_min": o_min, "flop_per_step": oflops,
+            "roofline": {"bound": "mfma", "achieved": o_tf, "peak": PEAK_F32_TFLOPS,
+                         "unit": "TFLOP/s", "frac": o_tf / PEAK_F32_TFLOPS,
+                         "traffic": measured_traffic("flash_fp32_bshd"),
+                         "kernel": FP32_KERNEL, "traffic_unit": "bytes per launch",
+                         "peak_note": "fp32 matrix (v_mfma_f32_32x32x2f32) peak"},
+            "cpu_baseline": ocpu,
         },
         "flash_backward": {
             "workload": "flash_attention backward bf16 BHSD B=4 H=32 S=4096 D=128 causal: dQ, dK, "
