@@ -575,7 +575,7 @@ __device__ __forceinline__ void fa16_rows(const FwdParams& pin, const WorkItem w
     for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
       for (int e = 0; e < 16; ++e) mt = fmaxf(mt, s[nb][e]);
-    mt = fmaxf(mt, xor32(mt)) * c;
+    mt = pair_max32(mt) * c;
     m_max = fmaxf(m_max, mt);
 
     if (__any(mt > m_run + kRescaleThreshold)) {
@@ -687,7 +687,7 @@ __device__ __forceinline__ void fa16_rows(const FwdParams& pin, const WorkItem w
   }
 
   // Epilogue: move o and l to the true max, then normalise (or emit partials).
-  const float l_tot = l_run + xor32(l_run);
+  const float l_tot = pair_sum32(l_run);
   const float f = m_max == -INFINITY ? 0.f : fast_exp2(m_run - m_max);
   if (p.num_splits == 1) {
     if (myq < p.Sq) {
@@ -983,12 +983,14 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& pin, const Wor
           s[nb][e] = ok ? sv : -INFINITY;
         }
     }
-    float mt = -INFINITY;
+    // Four independent max chains (not one serial chain of 64).
+    float mx[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) mt = fmaxf(mt, s[nb][e]);
-    mt = fmaxf(mt, xor32(mt)) * c;
+      for (int e = 0; e < 16; ++e) mx[e & 3] = fmaxf(mx[e & 3], s[nb][e]);
+    float mt = fmaxf(fmaxf(mx[0], mx[1]), fmaxf(mx[2], mx[3]));
+    mt = pair_max32(mt) * c;
     m_max = fmaxf(m_max, mt);
     if (__any(mt > m_run + kRescaleThreshold)) {
       asm volatile("" ::: "memory");
@@ -1002,48 +1004,46 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& pin, const Wor
       m_run = m_new;
     }
   };
-  // P^T = exp2(s*c - m) packed to 16 bits; the row sum accumulates the packed
-  // (rounded) weights, the exact weights the PV product uses.
-  auto exp_p = [&](const f32x16 (&s)[NB], u32x4 (&pop)[NSL]) __attribute__((always_inline)) {
+  // P^T = exp2(s*c - m) packed to 16 bits and O += P V, fused slice by slice:
+  // the four PV MFMAs of 16-key slice sl need only that slice's weights, so
+  // the exponentials of slice sl+1 run while the MFMAs of slice sl execute.
+  // The row sum accumulates the packed (rounded) weights, the exact weights
+  // the PV product uses. V^T operands come through the transposing read, one
+  // slice ahead of their MFMAs.
+  auto exp_pv = [&](const f32x16 (&s)[NB], const unsigned char* Vb) __attribute__((always_inline)) {
     const float msub = m_run == -INFINITY ? 0.f : m_run;
-    float lsum = 0.f;
+    float lsum[2] = {0.f, 0.f};
+    auto vread = [&](int sl, u32x4 (&va)[NDB]) __attribute__((always_inline)) {
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh)
-#pragma unroll
-        for (int e2 = 0; e2 < 4; ++e2) {
-          const float x0 = fast_exp2(s[nb][8 * hh + 2 * e2] * c - msub);
-          const float x1 = fast_exp2(s[nb][8 * hh + 2 * e2 + 1] * c - msub);
-          const u32 pk = pack2<BF16>(x0, x1);
-          pop[2 * nb + hh][e2] = pk;
-          lsum = dot2_sum<BF16>(pk, lsum);
-        }
-    l_run += lsum;
-  };
-  // O += P V for the V tile at Vb (operands through the transposing read).
-  auto pv_mfma = [&](const unsigned char* Vb, const u32x4 (&pop)[NSL]) __attribute__((always_inline)) {
-#pragma unroll
-    for (int db = 0; db < NDB; ++db) {
-      u32x4 va[NSL];
-#pragma unroll
-      for (int sl = 0; sl < NSL; ++sl) {
+      for (int db = 0; db < NDB; ++db) {
         const u32x2 lo = lds_read_tr16(Vb + vaddr[db] + (16 * sl) * ROWB);
         const u32x2 hi = lds_read_tr16(Vb + vaddr_hi[db] + (16 * sl) * ROWB);
-        va[sl] = (u32x4){lo[0], lo[1], hi[0], hi[1]};
+        va[db] = (u32x4){lo[0], lo[1], hi[0], hi[1]};
       }
+    };
+    u32x4 vcur[NDB], vnext[NDB];
+    vread(0, vcur);
 #pragma unroll
-      for (int sl = 0; sl < NSL; ++sl) o[db] = mfma32x32x16<BF16>(va[sl], pop[sl], o[db]);
-    }
-  };
-  auto pv_sched = [&]() __attribute__((always_inline)) {
-    __builtin_amdgcn_sched_group_barrier(0x100, 2 * NSL, 1);
+    for (int sl = 0; sl < NSL; ++sl) {
+      const int nb = sl >> 1, hh = sl & 1;
+      u32x4 pk4;
 #pragma unroll
-    for (int i = 0; i < NSL * (NDB - 1); ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
-      __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
+      for (int e2 = 0; e2 < 4; ++e2) {
+        const float x0 = fast_exp2(s[nb][8 * hh + 2 * e2] * c - msub);
+        const float x1 = fast_exp2(s[nb][8 * hh + 2 * e2 + 1] * c - msub);
+        const u32 pk = pack2<BF16>(x0, x1);
+        pk4[e2] = pk;
+        lsum[e2 & 1] = dot2_sum<BF16>(pk, lsum[e2 & 1]);
+      }
+      if (sl + 1 < NSL) vread(sl + 1, vnext);
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) o[db] = mfma32x32x16<BF16>(vcur[db], pk4, o[db]);
+      if (sl + 1 < NSL) {
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) vcur[db] = vnext[db];
+      }
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, NSL, 1);
+    l_run += lsum[0] + lsum[1];
   };
 
   auto compute_tile = [&](const unsigned char* Kb, int kv0) __attribute__((always_inline)) {
@@ -1062,10 +1062,7 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& pin, const Wor
     qk_mfma(Kb, s);
     qk_sched();
     max_rescale(s, kv0, full);
-    u32x4 pop[NSL];
-    exp_p(s, pop);
-    pv_mfma(Kb + KBYTES, pop);
-    pv_sched();
+    exp_pv(s, Kb + KBYTES);
   };
 
   // Every tile is 2 * NDMA DMA instructions per wave (4 at D = 128, 2 at
@@ -1107,7 +1104,7 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& pin, const Wor
     if (NST == 4 && i + 3 < n_tiles) step(i + 3, Const<3 % NST>{});
   }
 
-  const float l_tot = l_run + xor32(l_run);
+  const float l_tot = pair_sum32(l_run);
   const float f = m_max == -INFINITY ? 0.f : fast_exp2(m_run - m_max);
   if (p.num_splits == 1) {
     if (myq < p.Sq) {
@@ -1372,7 +1369,7 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd32_kernel(FwdParams pin) {
       for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
         for (int e = 0; e < 16; ++e) mt = fmaxf(mt, s[nb][e]);
-      mt = fmaxf(mt, xor32(mt)) * c;
+      mt = pair_max32(mt) * c;
       m_max = fmaxf(m_max, mt);
 
       if (__any(mt > m_run + kRescaleThreshold)) {
@@ -1414,7 +1411,7 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd32_kernel(FwdParams pin) {
     __syncthreads();
   }
 
-  const float l_tot = l_run + xor32(l_run);
+  const float l_tot = pair_sum32(l_run);
   const float f = m_max == -INFINITY ? 0.f : fast_exp2(m_run - m_max);
   if (p.num_splits == 1) {
     if (myq < p.Sq) {

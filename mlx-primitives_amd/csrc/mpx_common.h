@@ -53,8 +53,19 @@ void clear_error();
 // Raw v_exp_f32 (base-2 exponential); exp2(-inf) = 0.
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// Value held by lane (lane ^ 32).
-__device__ __forceinline__ float xor32(float x) { return __shfl_xor(x, 32, 64); }
+// max / sum of x over the lane pair (l, l ^ 32) with v_permlane32_swap (no LDS
+// round trip): after the upper half of one copy is swapped with the lower half
+// of another, every lane holds both values of its pair.
+__device__ __forceinline__ float pair_max32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pair_sum32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
 
 // 16-bit storage type <-> float.
 template <bool BF16>
