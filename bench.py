@@ -53,7 +53,7 @@ WINDOW_KERNEL = "fa_fwd16_kernel<128,128,8,bf16>"
 CHUNKED_KERNELS = "fa_fwd16_kernel<64,128,8,bf16> (split-KV) + fa_split_merge_kernel"
 PAGED_KERNELS = "paged_decode_part_kernel + paged_decode_merge_kernel"
 PREFILL_KERNEL = "fa_fwd16_kernel<128,64,8,bf16,paged>"
-APPEND_KERNEL = "kv_append_kernel"
+APPEND_KERNEL = "kv_append_kernel (+ the 12-byte fill that clears the error words)"
 BWD_KERNELS = ("fa_bwd_dvec_kernel + fa_bwd_dq_kernel<128,bf16> + fa_bwd_dkdv_kernel<128,bf16,K> "
                "+ fa_bwd_dkdv_kernel<128,bf16,V>")
 
@@ -359,17 +359,17 @@ def prefill_step(dev):
 
 
 def append_step(dev):
-    """The C-ABI append over the whole workload, error words preallocated."""
-    from mlx_primitives import _native
+    """store_kv over the whole workload, as a serving step calls it: no wait
+    for the error words, which go to a buffer the caller keeps (the call
+    allocates nothing)."""
+    from mlx_primitives.cache import store_kv
 
     inp = wl.make_append(wl.CONFIGS["kv_append_bf16"], device=dev)
     B, T, H, D = inp.k.shape
     errors = torch.zeros(3, dtype=torch.int32, device=dev)
     counts = torch.full((B,), T, dtype=torch.int32, device=dev)
-    fn = lambda: _native.kv_append(inp.k, inp.v, inp.k_pool, inp.v_pool, inp.block_tables,
-                                   inp.start_pos, counts, errors, inp.k.stride()[:3],
-                                   inp.v.stride()[:3], B, T, H, D, inp.k_pool.shape[0],
-                                   inp.k_pool.shape[1], inp.block_tables.shape[1])
+    fn = lambda: store_kv(inp.k_pool, inp.v_pool, inp.block_tables, inp.k, inp.v, inp.start_pos,
+                          counts, check=False, errors=errors)
     return inp, fn, errors
 
 
@@ -665,8 +665,8 @@ def main() -> int:
                          "kernel": "rope_kernel (K) + fa_fwd16_kernel<128,128,8,bf16> (Q)"},
         },
         "kv_append": {
-            "workload": "KV append bf16 through the C ABI: 4 sequences x 4096 new tokens, H=32, "
-                        "D=128, into 16-token pages of a permuted pool",
+            "workload": "KV append bf16 (store_kv, caller's error words, no wait): 4 sequences "
+                        "x 4096 new tokens, H=32, D=128, into 16-token pages of a permuted pool",
             "value": a_gbs, "unit": "GB/s", "ms_per_step": a_wall, "kernel_ms": a_ev,
             "kernel_ms_median": a_med, "kernel_ms_min": a_min, "bytes_per_step": abytes,
             "roofline": {"bound": "hbm", "achieved": a_gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",

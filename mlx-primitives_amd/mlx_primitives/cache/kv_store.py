@@ -47,6 +47,7 @@ def store_kv(
     start_positions: Union[int, torch.Tensor],
     num_tokens: Optional[Union[int, torch.Tensor]] = None,
     check: bool = True,
+    errors: Optional[torch.Tensor] = None,
 ) -> Optional[torch.Tensor]:
     """Write new tokens into their pages, in place.
 
@@ -63,6 +64,11 @@ def store_kv(
     Unlike the reference, which stops at the failing chunk, every token that
     can be placed is written. With ``check=False`` nothing waits and the int32
     (3,) error words [negative start, past table, bad page] are returned.
+
+    errors: optional int32 (3,) device tensor that receives the error words
+    (cleared by a fill kernel, then set by the append kernel), so that a call
+    allocates nothing, e.g. inside a captured HIP graph; without it a
+    temporary is allocated per call.
     """
     if k.ndim == 3:
         k, v = k[None], v[None]
@@ -101,7 +107,14 @@ def store_kv(
             return x.contiguous()
         return x
     k, v = fit(k), fit(v)
-    errors = torch.zeros(3, dtype=torch.int32, device=dev)
+    if errors is None:
+        errors = torch.zeros(3, dtype=torch.int32, device=dev)
+    else:
+        if (errors.dtype != torch.int32 or errors.numel() != 3 or errors.device != dev
+                or not errors.is_contiguous()):
+            raise ValueError("errors must be a contiguous int32 tensor of 3 entries on the "
+                             "pools' device")
+        errors.zero_()
     _native.kv_append(k, v, k_pool, v_pool, tables, starts, counts, errors, k.stride()[:3],
                       v.stride()[:3], batch, T, heads, dim, num_blocks, block_size,
                       tables.shape[1])

@@ -59,9 +59,12 @@ def test_decode_step_graph(device):
     vn = torch.empty_like(kn)
     pos = torch.empty(B, dtype=torch.int32, device=device)
     ones = torch.ones(B, dtype=torch.int32, device=device)
+    errors = torch.full((3,), 7, dtype=torch.int32, device=device)
 
     def step():
-        store_kv(k_pool, v_pool, tables, kn, vn, pos, num_tokens=ones, check=False)
+        # the caller's error words: the append allocates nothing under capture
+        store_kv(k_pool, v_pool, tables, kn, vn, pos, num_tokens=ones, check=False,
+                 errors=errors)
         return paged_attention(q, k_pool, v_pool, tables, lens, block_size=bs)
 
     def fresh():
@@ -84,3 +87,4 @@ def test_decode_step_graph(device):
         torch.cuda.synchronize()
         assert torch.equal(k_pool, kp1) and torch.equal(v_pool, vp1)
         assert torch.equal(got, eager)
+        assert errors.tolist() == [0, 0, 0]
