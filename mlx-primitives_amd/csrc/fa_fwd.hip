@@ -824,9 +824,19 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& pin, const Wor
     for (int ks = 0; ks < NKS; ++ks) qreg[ks] = src[2 * ks + g];
   }
   if (p.rope_cos) rope_q_frags<NKS, BF16>(p, p.rope_offset + min(myq, p.Sq - 1), g, qreg);
-  if (p.neg) {
+  // Q times the signed softmax scale in log2 units, rounded to the storage
+  // type: Q K^T then comes out of the MFMAs in log2 units, and with the
+  // accumulators started at -m (below) it is already the exponent.
+  {
+    const float cq = p.neg ? -p.c : p.c;
 #pragma unroll
-    for (int ks = 0; ks < NKS; ++ks) qreg[ks] ^= 0x80008000u;
+    for (int ks = 0; ks < NKS; ++ks)
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const u32 x = qreg[ks][w];
+        qreg[ks][w] = pack2<BF16>(h2f<BF16>((uint16_t)(x & 0xffffu)) * cq,
+                                  h2f<BF16>((uint16_t)(x >> 16)) * cq);
+      }
   }
   // Q has landed (and the previous item's stores retired) before any tile
   // DMA, so the explicit vmcnt waits below count tile loads only.
@@ -927,17 +937,19 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& pin, const Wor
   f32x16 o[NDB];
 #pragma unroll
   for (int db = 0; db < NDB; ++db) o[db] = (f32x16){};
+  // m_run: reference point of o and l_run (log2 units); the S^T accumulators
+  // start at -m_run (negm), so a tile's scores arrive relative to it.
   float m_run = -INFINITY, m_max = -INFINITY, l_run = 0.f;
-  const float c = p.c;
+  f32x16 negm = {};
   const int kv_first = p.win_left >= 0 ? myq - p.win_left : -(1 << 30);
   const int kv_last = min(p.win_right >= 0 ? myq + p.win_right : (1 << 30), p.Sk - 1);
   // Paged: validity of the tile's keys (bit r = key kv0 + r) and the ALiBi
-  // slope divided by |scale| (added to raw scores), applied as
-  // slope * (kv - kv_last): it differs from slope * (kv - q) by a per-row
+  // slope in log2 units (added to the scores, which are in log2 units), applied
+  // as slope * (kv - kv_last): it differs from slope * (kv - q) by a per-row
   // constant, which softmax ignores, and stays small for the keys that carry
   // the weight.
   uint64_t vmask = ~0ull;
-  const float alibi = (PAGED && p.slopes) ? p.slopes[wi.h] * kLog2e / p.c : 0.f;
+  const float alibi = (PAGED && p.slopes) ? p.slopes[wi.h] * kLog2e : 0.f;
 
   // S^T of this wave's rows against the K tile at Kb (MFMAs only; the
   // caller orders them against other work).
@@ -947,9 +959,9 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& pin, const Wor
       u32x4 ka[NKS];
 #pragma unroll
       for (int ks = 0; ks < NKS; ++ks) ka[ks] = *(const u32x4*)(Kb + kaddr[ks] + nb * 32 * ROWB);
-      s[nb] = (f32x16){};
+      s[nb] = mfma32x32x16<BF16>(ka[0], qreg[0], negm);
 #pragma unroll
-      for (int ks = 0; ks < NKS; ++ks) s[nb] = mfma32x32x16<BF16>(ka[ks], qreg[ks], s[nb]);
+      for (int ks = 1; ks < NKS; ++ks) s[nb] = mfma32x32x16<BF16>(ka[ks], qreg[ks], s[nb]);
     }
   };
   // K reads of block nb+1 in flight under the MFMAs of block nb.
@@ -962,7 +974,9 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& pin, const Wor
     }
     __builtin_amdgcn_sched_group_barrier(0x008, NKS, 0);
   };
-  // Masks, row max and (rare) rescale of O for the tile at kv0.
+  // Masks, row max and (rare) rescale of O for the tile at kv0. Scores are
+  // relative to m_run (to 0 while it is -inf); a rescale moves m_run, O,
+  // l_run, this tile's scores and negm to the new reference.
   auto max_rescale = [&](f32x16 (&s)[NB], int kv0, bool full) __attribute__((always_inline)) {
     if (!full) {
       asm volatile("" ::: "memory");
@@ -990,28 +1004,36 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& pin, const Wor
 #pragma unroll
       for (int e = 0; e < 16; ++e) mx[e & 3] = fmaxf(mx[e & 3], s[nb][e]);
     float mt = fmaxf(fmaxf(mx[0], mx[1]), fmaxf(mx[2], mx[3]));
-    mt = pair_max32(mt) * c;
-    m_max = fmaxf(m_max, mt);
-    if (__any(mt > m_run + kRescaleThreshold)) {
+    mt = pair_max32(mt);  // relative to msub
+    const float msub = m_run == -INFINITY ? 0.f : m_run;
+    m_max = fmaxf(m_max, mt + msub);
+    if (__any(m_run == -INFINITY ? mt > -INFINITY : mt > kRescaleThreshold)) {
       asm volatile("" ::: "memory");
-      const float m_new = fmaxf(m_run, mt);
+      const float m_new = fmaxf(m_run, mt + msub);
       const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(m_run - m_new);
+      const float delta = m_new == -INFINITY ? 0.f : m_new - msub;
       l_run *= alpha;
 #pragma unroll
       for (int db = 0; db < NDB; ++db)
 #pragma unroll
         for (int e = 0; e < 16; ++e) o[db][e] *= alpha;
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) s[nb][e] -= delta;
       m_run = m_new;
+      const float nm = m_new == -INFINITY ? 0.f : -m_new;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) negm[e] = nm;
     }
   };
-  // P^T = exp2(s*c - m) packed to 16 bits and O += P V, fused slice by slice:
+  // P^T = exp2(s), s already relative to m_run, packed to 16 bits and O += P V, fused slice by slice:
   // the four PV MFMAs of 16-key slice sl need only that slice's weights, so
   // the exponentials of slice sl+1 run while the MFMAs of slice sl execute.
   // The row sum accumulates the packed (rounded) weights, the exact weights
   // the PV product uses. V^T operands come through the transposing read, one
   // slice ahead of their MFMAs.
   auto exp_pv = [&](const f32x16 (&s)[NB], const unsigned char* Vb) __attribute__((always_inline)) {
-    const float msub = m_run == -INFINITY ? 0.f : m_run;
     float lsum[2] = {0.f, 0.f};
     auto vread = [&](int sl, u32x4 (&va)[NDB]) __attribute__((always_inline)) {
 #pragma unroll
@@ -1029,8 +1051,8 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& pin, const Wor
       u32x4 pk4;
 #pragma unroll
       for (int e2 = 0; e2 < 4; ++e2) {
-        const float x0 = fast_exp2(s[nb][8 * hh + 2 * e2] * c - msub);
-        const float x1 = fast_exp2(s[nb][8 * hh + 2 * e2 + 1] * c - msub);
+        const float x0 = fast_exp2(s[nb][8 * hh + 2 * e2]);
+        const float x1 = fast_exp2(s[nb][8 * hh + 2 * e2 + 1]);
         const u32 pk = pack2<BF16>(x0, x1);
         pk4[e2] = pk;
         lsum[e2 & 1] = dot2_sum<BF16>(pk, lsum[e2 & 1]);
@@ -1452,8 +1474,12 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd32_kernel(FwdParams pin) {
 // Split-KV merge: the reference's online_softmax_merge
 // (mlx_primitives/attention/_online_softmax.py:42-106) folded over all splits,
 // then O / (l + eps) (rows that saw no key: 0, or NaN for the exact softmax).
-// One thread per (row, 4 dims).
+// One thread per (row, 4 dims), one pass over the splits in batches of
+// kMergeBatch: the batch's (m, l) and O loads are all issued before any is
+// used, then the batch is folded in against the running maximum.
 // ---------------------------------------------------------------------------
+constexpr int kMergeBatch = 8;
+
 template <int DT>
 __global__ __launch_bounds__(256) void fa_split_merge_kernel(const float* __restrict__ ws_o,
                                                              const float* __restrict__ ws_ml,
@@ -1467,17 +1493,37 @@ __global__ __launch_bounds__(256) void fa_split_merge_kernel(const float* __rest
   if (idx >= rows * chunks) return;
   const int64_t row = idx / chunks;
   const int c4 = (int)(idx - row * chunks);
-  float M = -INFINITY;
-  for (int s = 0; s < splits; ++s) M = fmaxf(M, ws_ml[2 * (s * rows + row)]);
+  float M = -INFINITY, L = 0.f;
   f32x4 acc = {};
-  float L = 0.f;
-  if (M != -INFINITY) {
-    for (int s = 0; s < splits; ++s) {
-      const int64_t r = s * rows + row;
-      const float wgt = fast_exp2(ws_ml[2 * r] - M);
-      L += wgt * ws_ml[2 * r + 1];
-      acc += wgt * *(const f32x4*)(ws_o + r * D + 4 * c4);
+  for (int s0 = 0; s0 < splits; s0 += kMergeBatch) {
+    float2 ml[kMergeBatch];
+    f32x4 os[kMergeBatch];
+#pragma unroll
+    for (int i = 0; i < kMergeBatch; ++i) {
+      ml[i] = make_float2(-INFINITY, 0.f);
+      os[i] = (f32x4){};
+      if (s0 + i < splits) {
+        const int64_t r = (s0 + i) * rows + row;
+        ml[i] = *(const float2*)(ws_ml + 2 * r);
+        os[i] = *(const f32x4*)(ws_o + r * D + 4 * c4);
+      }
     }
+    float mb = M;
+#pragma unroll
+    for (int i = 0; i < kMergeBatch; ++i) mb = fmaxf(mb, ml[i].x);
+    if (mb == -INFINITY) continue;  // nothing seen yet
+    const float keep = fast_exp2(M - mb);  // 0 while M is -inf
+    L *= keep;
+    acc *= keep;
+#pragma unroll
+    for (int i = 0; i < kMergeBatch; ++i) {
+      const float wgt = fast_exp2(ml[i].x - mb);  // 0 for splits that saw no key
+      L += wgt * ml[i].y;
+      acc += wgt * os[i];
+    }
+    M = mb;
+  }
+  if (M != -INFINITY) {
     acc = acc / (L + eps);
   } else if (nan_empty) {
     acc = (f32x4){} + __builtin_nanf("");
@@ -1502,8 +1548,14 @@ namespace {
 
 constexpr int kNumWaves16 = MPX_FA_NWAVES;     // waves per workgroup, 16-bit kernel
 constexpr int kNumWaves32 = MPX_FA_NWAVES_F32; // waves per workgroup, fp32 kernel
-constexpr int kTargetWorkgroups = 512; // 256 CUs x 2 resident workgroups
 constexpr int kNumCUs = 256;
+
+// Workgroups a split launch aims for: one full wave of resident workgroups.
+// The 16-bit kernels at D >= 64 hold 96-128 KB of LDS (one workgroup per CU);
+// the others fit two per CU.
+int target_workgroups(int D, int dtype) {
+  return dtype != MPX_F32 && D >= 64 ? kNumCUs : 2 * kNumCUs;
+}
 
 struct Plan {
   int BM, BN, n_qtiles, splits, tiles_per_split, win_left, win_right;
@@ -1538,8 +1590,9 @@ Plan make_plan(int B, int H, int Sq, int Sk, int D, int causal, int window_left,
   }
   const long base = (long)B * H * pl.n_qtiles;
   int splits = 1;
-  if (base > 0 && base < kTargetWorkgroups && max_tiles >= 8) {
-    splits = (int)std::min<long>((kTargetWorkgroups + base - 1) / base, max_tiles / 4);
+  const long target = target_workgroups(D, dtype);
+  if (base > 0 && base < target && max_tiles >= 8) {
+    splits = (int)std::min<long>((target + base - 1) / base, max_tiles / 4);
     splits = std::max(splits, 1);
   }
   pl.tiles_per_split = splits > 1 ? (max_tiles + splits - 1) / splits : std::max(max_tiles, 1);
