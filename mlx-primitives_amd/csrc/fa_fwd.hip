@@ -768,7 +768,16 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& pin, const Wor
                                                  int* __restrict__ pages) {
   constexpr int BM = 32 * NW;
   constexpr int NB = BN / 32, NSL = BN / 16, NKS = D / 16, NDB = D / 32;
-  static_assert(!PAGED || BN == 64, "the paged key-validity ballot covers 64 keys");
+  // Paged, 64-key tiles: the item's page ids are staged in LDS (any page
+  // size, ALiBi). Paged, 128-key tiles: page ids come from the block table,
+  // one per DMA instruction of a wave; the host picks this form for
+  // power-of-two page sizes of at least RPD tokens (so the RPD rows one wave's
+  // instruction stages lie in one page) and no ALiBi. A tile with a page that
+  // is missing (-1) or past the pool has each key checked against the table.
+  constexpr bool kSlice = PAGED && BN == 64;
+  constexpr bool kScalarPages = PAGED && BN == 128;
+  constexpr bool kChecked = kScalarPages;
+  static_assert(!PAGED || kSlice || kScalarPages, "paged tiles are 64 or 128 keys");
   constexpr int ROWB = 2 * D;          // bytes per K or V row
   constexpr int KBYTES = BN * ROWB;    // one K (or V) tile
   constexpr int STAGEB = 2 * KBYTES;   // K then V
@@ -803,7 +812,8 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& pin, const Wor
 
   // Paged: this item's slice of the page table, validated, in LDS.
   int pg_first = 0;
-  if constexpr (PAGED) {
+  const int32_t* __restrict__ bt_row = PAGED ? p.bt + (int64_t)wi.b * p.max_blocks : nullptr;
+  if constexpr (kSlice) {
     const int kv_a = kv_lo + t_begin * BN, kv_b = min(kv_lo + t_end * BN, p.Sk);
     pg_first = page_of(p, kv_a);
     const int npg = kv_b > kv_a ? page_of(p, kv_b - 1) - pg_first + 1 : 0;
@@ -855,15 +865,76 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& pin, const Wor
     kchunk = vchunk = (lane & 7) ^ swz64(lr);
   }
   const int kgo = (lr * (int)p.k_ss + kchunk * 8) * 2;
+  // Paged, 128-key tiles: the lane part of a DMA offset (row lr % RPD of the
+  // instruction's RPD rows, this lane's chunk).
+  const int klane = ((lr % RPD) * (int)p.k_ss + kchunk * 8) * 2;
+  const int vlane = ((lr % RPD) * (int)p.v_ss + vchunk * 8) * 2;
   const int vgo = (lr * (int)p.v_ss + vchunk * 8) * 2;
   const int kstep = RSTEP * (int)p.k_ss * 2, vstep = RSTEP * (int)p.v_ss * 2;
   auto stage_ptr = [&](auto ST) __attribute__((always_inline)) -> unsigned char* {
     constexpr int S = decltype(ST)::value;
     return S == 0 ? st0 : (S == 1 ? st1 : (S == 2 ? st2 : st3));
   };
+  // Paged, 128-key tiles: lane l of pg_cur holds the table entry of page l of
+  // the next tile to stage, counted from the page of its first key (a tile
+  // spans max(1, 128 / page size) pages; lanes past the context read the last
+  // page's entry). A step issues the next tile's DMAs, then loads the entries
+  // of the tile after it, which land under the step's compute and are waited
+  // for by its closing vmcnt(0) (two stages); pg_cur is read only after that.
+  // tile_ok_next / tile_ok: every page a key of the staged / computed tile
+  // lies in is valid (else compute_tile checks each key against the table).
+  static_assert(!kScalarPages || NST == 2, "paged 128-key tiles use two stages");
+  int pg_cur = 0;
+  bool tile_ok = true, tile_ok_next = true;
+  auto fetch_pages = [&](int kv0) __attribute__((always_inline)) {
+    const int last = (p.Sk - 1) >> p.bs_log2;
+    pg_cur = bt_row[min((kv0 >> p.bs_log2) + lane, last)];
+  };
   auto load_tile = [&](int kv0, unsigned char* stbase) __attribute__((always_inline)) {
     const u32 kdst = lds_addr(stbase + wave * RPD * ROWB);
     const u32 vdst = kdst + KBYTES;
+    if constexpr (kScalarPages) {
+      // Row lr + RSTEP * r of the tile sits in page pg_next[r] (32-bit
+      // offsets: the host keeps each pool below 4 GiB - 256 bytes).
+      const u32 row_bytes = (u32)p.k_ss * 2u;
+      const int bmask = (1 << p.bs_log2) - 1;
+      const int pg0 = kv0 >> p.bs_log2;
+      if constexpr (kChecked) {
+        // Pages of the tile's keys below the context length: lanes 0 .. npg-1.
+        const int npg = ((min(kv0 + BN, p.Sk) - 1) >> p.bs_log2) - pg0 + 1;
+        tile_ok_next = !__any((lane < npg) & ((pg_cur < 0) | (pg_cur >= p.num_blocks)));
+      }
+      int pg_next[NDMA];
+#pragma unroll
+      for (int r = 0; r < NDMA; ++r)
+        pg_next[r] = __builtin_amdgcn_readlane(
+            pg_cur, ((kv0 + RPD * wave + RSTEP * r) >> p.bs_log2) - pg0);
+      if ((!kChecked || tile_ok_next) && kv0 + BN <= p.Sk) {
+        // Every row exists: the page part of the offset is uniform (row
+        // RPD * wave + RSTEP * r of the tile, in the scalar offset); the lane
+        // part (row lr % RPD, chunk) is fixed.
+#pragma unroll
+        for (int r = 0; r < NDMA; ++r) {
+          const int row0 = kv0 + RPD * wave + RSTEP * r;
+          const u32 soff = (((u32)pg_next[r] << p.bs_log2) + (u32)(row0 & bmask)) * row_bytes;
+          dma16(krs, kdst + r * RSTEP * ROWB, klane, (int)soff);
+          dma16(vrs, vdst + r * RSTEP * ROWB, vlane, (int)soff);
+        }
+        return;
+      }
+#pragma unroll
+      for (int r = 0; r < NDMA; ++r) {
+        const int page = pg_next[r];
+        const int pos = kv0 + lr + RSTEP * r;
+        const bool ok = pos < p.Sk && page >= 0 && page < p.num_blocks;
+        const u32 base = (((u32)page << p.bs_log2) + (u32)(pos & bmask)) * row_bytes;
+        dma16(krs, kdst + r * RSTEP * ROWB, (int)(ok ? base + (u32)kchunk * 16u : kNoRowDirect),
+              0);
+        dma16(vrs, vdst + r * RSTEP * ROWB, (int)(ok ? base + (u32)vchunk * 16u : kNoRowDirect),
+              0);
+      }
+      return;
+    }
     if constexpr (PAGED) {
       // Rows lr (and lr + 32) through the page table (32-bit offsets: the
       // host keeps each pool below 4 GiB - 256 bytes).
@@ -948,8 +1019,8 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& pin, const Wor
   // as slope * (kv - kv_last): it differs from slope * (kv - q) by a per-row
   // constant, which softmax ignores, and stays small for the keys that carry
   // the weight.
-  uint64_t vmask = ~0ull;
-  const float alibi = (PAGED && p.slopes) ? p.slopes[wi.h] * kLog2e : 0.f;
+  uint64_t vmask = ~0ull, vmask_hi = ~0ull;  // keys kv0 .. +63, kv0 + 64 .. +127
+  const float alibi = (kSlice && p.slopes) ? p.slopes[wi.h] * kLog2e : 0.f;
 
   // S^T of this wave's rows against the K tile at Kb (MFMAs only; the
   // caller orders them against other work).
@@ -977,10 +1048,25 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& pin, const Wor
   // Masks, row max and (rare) rescale of O for the tile at kv0. Scores are
   // relative to m_run (to 0 while it is -inf); a rescale moves m_run, O,
   // l_run, this tile's scores and negm to the new reference.
-  auto max_rescale = [&](f32x16 (&s)[NB], int kv0, bool full) __attribute__((always_inline)) {
-    if (!full) {
+  // pmask (paged, 64-key tiles): the tile needs the per-key page mask or the
+  // ALiBi bias; otherwise its masks are the dense kernel's. (The 128-key
+  // kernel always takes the paged masks: a second copy of the mask loop costs
+  // it registers.)
+  auto max_rescale = [&](f32x16 (&s)[NB], int kv0, bool full, bool pmask)
+                         __attribute__((always_inline)) {
+    if (!full && !(PAGED && (kScalarPages || pmask))) {
+      asm volatile("" ::: "memory");
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int kv = kv0 + nb * 32 + 16 * (e >> 3) + (e & 7) + 8 * g;
+          s[nb][e] = ((kv >= kv_first) & (kv <= kv_last)) ? s[nb][e] : -INFINITY;
+        }
+    } else if (!full) {
       asm volatile("" ::: "memory");
       const uint64_t vm = PAGED ? vmask >> (8 * g) : 0;
+      const uint64_t vm_hi = PAGED ? vmask_hi >> (8 * g) : 0;
       const float dq0 = PAGED ? (float)(kv0 + 8 * g - kv_last) : 0.f;
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb)
@@ -991,7 +1077,7 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& pin, const Wor
           bool ok = (kv >= kv_first) & (kv <= kv_last);
           float sv = s[nb][e];
           if constexpr (PAGED) {
-            ok = ok & (((vm >> kc) & 1ull) != 0);
+            ok = ok & ((((kc < 64 ? vm : vm_hi) >> (kc & 63)) & 1ull) != 0);
             sv += alibi * (dq0 + (float)kc);
           }
           s[nb][e] = ok ? sv : -INFINITY;
@@ -1072,18 +1158,36 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& pin, const Wor
     bool skip, full;
     classify_tile<BN>(p, kv0, wq0, wq0 + 31, skip, full);
     if (skip) return;
-    if constexpr (PAGED) {
+    bool pmask = false;
+    if constexpr (kSlice) {
       // Lane l checks key kv0 + l (one 64-bit ballot per tile).
       const int key = kv0 + lane;
       bool ok = key < p.Sk;
       if (ok) ok = pages[page_of(p, key) - pg_first] >= 0;
       vmask = __ballot(ok);
-      if (vmask != ~0ull || alibi != 0.f) full = false;
+      pmask = vmask != ~0ull || alibi != 0.f;
     }
+    if constexpr (kChecked) {
+      if (!tile_ok) {
+        // Lane l checks keys kv0 + l and kv0 + 64 + l against the table. The
+        // loads are waited for here (vmcnt(0)), so the tile waits below
+        // still count DMA loads only.
+        const int k0 = kv0 + lane, k1 = k0 + 64;
+        const int b0 = bt_row[min(k0, p.Sk - 1) >> p.bs_log2];
+        const int b1 = bt_row[min(k1, p.Sk - 1) >> p.bs_log2];
+        __builtin_amdgcn_s_waitcnt(0x0F70);
+        vmask = __ballot((k0 < p.Sk) & (b0 >= 0) & (b0 < p.num_blocks));
+        vmask_hi = __ballot((k1 < p.Sk) & (b1 >= 0) & (b1 < p.num_blocks));
+      } else {
+        vmask = vmask_hi = ~0ull;  // (a previous tile may have set them)
+      }
+      pmask = !tile_ok;
+    }
+    if (pmask) full = false;
     f32x16 s[NB];
     qk_mfma(Kb, s);
     qk_sched();
-    max_rescale(s, kv0, full);
+    max_rescale(s, kv0, full, pmask);
     exp_pv(s, Kb + KBYTES);
   };
 
@@ -1101,7 +1205,14 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& pin, const Wor
     }
   };
   const int n_tiles = t_end - t_begin;
+  if constexpr (kScalarPages) {
+    if (n_tiles > 0) fetch_pages(kv_lo + t_begin * BN);
+  }
   if (n_tiles > 0) load_tile(kv_lo + t_begin * BN, st0);
+  if constexpr (kChecked) tile_ok = tile_ok_next;
+  if constexpr (kScalarPages) {
+    if (n_tiles > 1) fetch_pages(kv_lo + (t_begin + 1) * BN);
+  }
   if (NST >= 3 && n_tiles > 1) load_tile(kv_lo + (t_begin + 1) * BN, st1);
   if (NST == 4 && n_tiles > 2) load_tile(kv_lo + (t_begin + 2) * BN, st2);
   wait_tiles_after(min(n_tiles, NST - 1) - 1);  // tile 0 landed
@@ -1113,7 +1224,11 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& pin, const Wor
     const int kv0 = kv_lo + (t_begin + i) * BN;
     if (i + NST - 1 < n_tiles)
       load_tile(kv0 + (NST - 1) * BN, stage_ptr(Const<(S + NST - 1) % NST>{}));
+    if constexpr (kScalarPages) {
+      if (i + NST < n_tiles) fetch_pages(kv0 + NST * BN);
+    }
     compute_tile(stage_ptr(Const<S>{}), kv0);
+    if constexpr (kChecked) tile_ok = tile_ok_next;
     // Tile i+1 must have landed before the barrier that hands it to every
     // wave; the tiles issued after it may stay in flight.
     wait_tiles_after(min(n_tiles - 1, i + NST - 1) - (i + 1));
@@ -1169,16 +1284,18 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(MPX_FA_
 void fa_fwd16_kernel(FwdParams p) {
   // Stay within 128 KB of LDS per workgroup (a 136 KB configuration gave wrong
   // results on gfx950).
-  constexpr bool kDirect = MPX_FA_DIRECT && (D == 128 || D == 64) &&
-                           (BN == 64 || (BN == 128 && !PAGED)) && (NW == 8 || NW == 4);
-  // Paged: three stages, which leaves room for the page-table slice.
+  constexpr bool kDirect = MPX_FA_DIRECT && (D == 128 || D == 64) && (BN == 64 || BN == 128) &&
+                           (NW == 8 || NW == 4);
+  // Paged with 64-key tiles: three stages, which leaves room for the
+  // page-table slice.
+  constexpr bool kSlice = PAGED && BN == 64;
   constexpr int kDStages =
-      PAGED ? 3
+      kSlice ? 3
             : (MPX_FA_DSTAGES > 0 ? MPX_FA_DSTAGES
                                   : (131072 / (4 * BN * D) < 4 ? 131072 / (4 * BN * D) : 4));
   constexpr int kLdsBytes =
       kDirect ? kDStages * 2 * BN * 2 * D : kFa16Stages * fa16_stage_elems<D, BN>() * 2;
-  static_assert(kLdsBytes + (PAGED ? kMaxItemPages * 4 : 0) <= 131072, "LDS budget");
+  static_assert(kLdsBytes + (kSlice ? kMaxItemPages * 4 : 0) <= 131072, "LDS budget");
   // Direct staging uses three separate stage arrays (so alias analysis can
   // tell a stage being read from the stage a DMA is writing); smem is used by
   // the register-staged path.
@@ -1188,7 +1305,7 @@ void fa_fwd16_kernel(FwdParams p) {
   __shared__ __align__(16) unsigned char dst1[kStageB];
   __shared__ __align__(16) unsigned char dst2[kDStages >= 3 ? kStageB : 16];
   __shared__ __align__(16) unsigned char dst3[kDStages == 4 ? kStageB : 16];
-  __shared__ int pages[PAGED ? kMaxItemPages : 1];
+  __shared__ int pages[kSlice ? kMaxItemPages : 1];
   const WorkSlot ws = decode_slot(p);
   const int n_items = slot_items(p, ws);
   // Every item ends with a barrier after its last LDS read, so the next item
@@ -1563,18 +1680,27 @@ struct Plan {
   size_t ws_bytes;
 };
 
-// Keys per KV tile (the paged and D = 32 16-bit kernels always take 64).
-int tile_n(int D, int dtype, bool paged = false) {
+// Paged 16-bit kernels at D = 128 take 128-key tiles (page ids read from the
+// table a step ahead) when pages are a power of two of at least the 4 rows one
+// DMA instruction of a wave stages, and no ALiBi bias is given.
+bool paged_wide_tiles(int D, int dtype, int bs_log2, bool alibi) {
+  return MPX_FA_DIRECT && dtype != MPX_F32 && D == 128 && bs_log2 >= 2 && !alibi;
+}
+
+// Keys per KV tile (the D = 32 16-bit kernels, and the paged ones at other
+// page sizes, take 64).
+int tile_n(int D, int dtype, bool paged = false, int bs_log2 = -1, bool alibi = false) {
   if (dtype == MPX_F32) return D > 64 ? 32 : 64;
-  return paged || D < 64 || !MPX_FA_DIRECT ? 64 : MPX_FA_BN16;
+  if (paged) return paged_wide_tiles(D, dtype, bs_log2, alibi) ? 128 : 64;
+  return D < 64 || !MPX_FA_DIRECT ? 64 : MPX_FA_BN16;
 }
 
 Plan make_plan(int B, int H, int Sq, int Sk, int D, int causal, int window_left,
                int window_right, int dtype, int max_tiles_per_split = 1 << 30,
-               bool paged = false) {
+               bool paged = false, int bs_log2 = -1, bool alibi = false) {
   Plan pl;
   pl.BM = 32 * (dtype == MPX_F32 ? kNumWaves32 : kNumWaves16);
-  pl.BN = tile_n(D, dtype, paged);
+  pl.BN = tile_n(D, dtype, paged, bs_log2, alibi);
   pl.win_left = window_left < 0 ? -1 : window_left;
   pl.win_right = causal ? 0 : (window_right < 0 ? -1 : window_right);
   pl.n_qtiles = (Sq + pl.BM - 1) / pl.BM;
@@ -1629,6 +1755,12 @@ constexpr int kBN16 = PAGED || D < 64 || !MPX_FA_DIRECT ? 64 : MPX_FA_BN16;
 
 template <bool PAGED>
 hipError_t dispatch_fwd(const FwdParams& p, int D, int dtype, int grid, hipStream_t st) {
+  if constexpr (PAGED) {
+    if (paged_wide_tiles(D, dtype, p.bs_log2, p.slopes != nullptr)) {
+      return dtype == MPX_BF16 ? launch_fwd<128, 128, false, true, true>(p, grid, st)
+                               : launch_fwd<128, 128, false, false, true>(p, grid, st);
+    }
+  }
   if (dtype == MPX_F32) {
     switch (D) {
       case 32: return launch_fwd<32, 64, true, false, PAGED>(p, grid, st);
@@ -1703,9 +1835,15 @@ __global__ void fill_nan_kernel(void* o, int64_t o_sb, int64_t o_sh, int64_t o_s
 }
 
 // Tiles per split so that one work item's pages fit the LDS page table.
+// Tiles per split item of a paged launch: the 64-key kernels stage the item's
+// page ids in LDS (at most kMaxItemPages); the 128-key ones read them from the
+// table and take any number.
 int paged_tile_cap(int block_size, int BN) {
+  if (BN == 128) return 1 << 30;
   return std::max(1, (int)std::min<long>(1L << 30, (long)(kMaxItemPages - 2) * block_size / BN));
 }
+
+int log2_if_pow2(int x) { return x > 0 && (x & (x - 1)) == 0 ? __builtin_ctz((unsigned)x) : -1; }
 
 bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
 
@@ -1867,10 +2005,17 @@ extern "C" int mpx_attn_fwd(const void* q, const void* k, const void* v, void* o
 extern "C" size_t mpx_paged_prefill_workspace_bytes(int B, int Sq, int H, int D, int block_size,
                                                     int max_blocks, int causal, int dtype) {
   if (B <= 0 || H <= 0 || Sq <= 0 || D <= 0 || block_size <= 0 || max_blocks <= 0) return 0;
-  const int BN = tile_n(D, dtype, true);
-  return make_plan(B, H, Sq, max_blocks * block_size, D, causal, -1, -1, dtype,
-                   paged_tile_cap(block_size, BN), true)
-      .ws_bytes;
+  // The size covers both tile widths (the width also depends on whether an
+  // ALiBi bias is given, which this query does not name).
+  size_t bytes = 0;
+  for (int alibi = 0; alibi < 2; ++alibi) {
+    const int bl = log2_if_pow2(block_size);
+    const int BN = tile_n(D, dtype, true, bl, alibi);
+    bytes = std::max(bytes, make_plan(B, H, Sq, max_blocks * block_size, D, causal, -1, -1,
+                                      dtype, paged_tile_cap(block_size, BN), true, bl, alibi)
+                                .ws_bytes);
+  }
+  return bytes;
 }
 
 extern "C" int mpx_paged_prefill_gqa(const void* q, const void* k_pool, const void* v_pool,
@@ -1931,9 +2076,10 @@ extern "C" int mpx_paged_prefill_gqa(const void* q, const void* k_pool, const vo
     MPX_CHECK_HIP(hipGetLastError());
     return MPX_OK;
   }
-  const int BN = tile_n(D, dtype, true);
+  const int BN = tile_n(D, dtype, true, log2_if_pow2(block_size), alibi_slopes != nullptr);
   const Plan pl = make_plan(B, H, Sq, (int)max_tokens, D, causal, -1, -1, dtype,
-                            paged_tile_cap(block_size, BN), true);
+                            paged_tile_cap(block_size, BN), true, log2_if_pow2(block_size),
+                            alibi_slopes != nullptr);
   if (pl.splits > 1) {
     MPX_CHECK_ARG(workspace != nullptr && workspace_bytes >= pl.ws_bytes,
                   "mpx_paged_prefill: workspace of %zu bytes required, %zu given", pl.ws_bytes,
@@ -1955,7 +2101,7 @@ extern "C" int mpx_paged_prefill_gqa(const void* q, const void* k_pool, const vo
   p.nan_empty = 1;
   p.bt = block_tables; p.ctx = context_lens; p.slopes = alibi_slopes;
   p.bs = block_size;
-  p.bs_log2 = (block_size & (block_size - 1)) == 0 ? __builtin_ctz((unsigned)block_size) : -1;
+  p.bs_log2 = log2_if_pow2(block_size);
   p.max_blocks = max_blocks; p.num_blocks = num_blocks;
   p.pool_bytes = (uint32_t)std::min<uint64_t>(pool_bytes, 0xFFFFFFFFull);
   return run_fwd<true>(p, pl, D, dtype, workspace, st);

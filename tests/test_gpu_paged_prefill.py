@@ -126,11 +126,26 @@ def test_causal_long_context_alibi_f32(device):
     check(out, ref, torch.float32)
 
 
-def test_invalid_page_ids_masked(device):
+@pytest.mark.parametrize("dtype,D", [(torch.float32, 64), (torch.bfloat16, 128),
+                                     (torch.float16, 64)])
+def test_invalid_page_ids_masked(device, dtype, D):
     # ids past the pool are masked like -1 and never dereferenced
-    out, ref = run_case(device, torch.float32, 40, [40, 40], [[0, -1, 2], [1, 99, 3]], 4, 16, 4,
-                        64, causal=False, oracle_tables=[[0, -1, 2], [1, -1, 3]])
-    check(out, ref, torch.float32)
+    out, ref = run_case(device, dtype, 40, [40, 40], [[0, -1, 2], [1, 99, 3]], 4, 16, 4,
+                        D, causal=False, oracle_tables=[[0, -1, 2], [1, -1, 3]])
+    check(out, ref, dtype)
+
+
+@pytest.mark.parametrize("bs,D", [(4, 128), (8, 64), (4, 64), (256, 64), (32, 128)])
+@pytest.mark.parametrize("holes", [False, True])
+def test_block_sizes_wide_tiles(device, bs, D, holes):
+    # 128-key tiles read page ids from the table (power-of-two pages of at
+    # least 4 rows at D = 128, 8 at D = 64); other page sizes take the 64-key
+    # kernel. Tables with and without missing pages inside the context.
+    rng = np.random.default_rng(bs * D + int(holes))
+    lens = [700, 129, 1]
+    tables, nb = random_tables(rng, lens, bs, holes=holes)
+    out, ref = run_case(device, torch.float16, 200, lens, tables, nb, bs, 3, D, seed=bs + D)
+    check(out, ref, torch.float16)
 
 
 def test_empty_rows_are_nan(device):
