@@ -3,7 +3,8 @@
 A step is one forward pass of the headline workload, flash_attention bf16
 BHSD B=4 H=32 S=4096 D=128 causal (the configuration the metric is quoted
 on). The same run also times paged-KV decode fp16 (64 sequences, H=32, D=128,
-context ~ U{512..8192}, 16-token pages) under "paged_decode", paged prefill of
+context ~ U{512..8192}, 16-token pages) under "paged_decode", the same decode
+with 32 query heads over 8 K/V heads (enable_gqa) under "paged_decode_gqa", paged prefill of
 the headline shape over 16-token pages under "paged_prefill", the KV append
 that writes those prompts into pages under "kv_append", and fused RoPE + flash
 attention at the headline shape (BSHD) under "rope_attention", the backward pass of the
@@ -19,7 +20,7 @@ path (32x32 blocks) on host cores.
 
 Prints ONE JSON line. Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 
-`--only flash|fp32|window|chunked|paged|prefill|append|rope|bwd|copy` runs a single leg
+`--only flash|fp32|window|chunked|paged|gqa|prefill|append|rope|bwd|copy` runs a single leg
 (no CPU baseline) for profiler passes; `copy` streams a 1 GiB float32 buffer through an elementwise kernel,
 the known-size reference for scaling the HBM byte counters. The HBM traffic
 per launch measured by those passes (rocprofv3 FETCH_SIZE / WRITE_SIZE) is read
@@ -52,7 +53,8 @@ FP32_KERNEL = "fa_fwd32_kernel<64,64,4>"
 WINDOW_KERNEL = "fa_fwd16_kernel<128,128,8,bf16>"
 CHUNKED_KERNELS = "fa_fwd16_kernel<64,128,8,bf16> (split-KV) + fa_split_merge_kernel"
 PAGED_KERNELS = "paged_decode_part_kernel + paged_decode_merge_kernel"
-PREFILL_KERNEL = "fa_fwd16_kernel<128,64,8,bf16,paged>"
+GQA_KERNELS = "paged_decode_gqa_kernel + paged_decode_merge_kernel"
+PREFILL_KERNEL = "fa_fwd16_kernel<128,128,8,bf16,paged>"
 APPEND_KERNEL = "kv_append_kernel (+ the 12-byte fill that clears the error words)"
 BWD_KERNELS = ("fa_bwd_dvec_kernel + fa_bwd_dq_kernel<128,bf16> + fa_bwd_dkdv_kernel<128,bf16,K> "
                "+ fa_bwd_dkdv_kernel<128,bf16,V>")
@@ -452,10 +454,12 @@ def run_one_leg(args) -> int:
     else:
         from mlx_primitives.cache import paged_attention
 
-        pin = wl.make_paged(wl.CONFIGS["paged_decode_fp16"], device=dev)
+        pname = "paged_decode_gqa_fp16" if args.only == "gqa" else "paged_decode_fp16"
+        pin = wl.make_paged(wl.CONFIGS[pname], device=dev)
         fn = lambda: paged_attention(pin.q, pin.k_pool, pin.v_pool, pin.block_tables,
-                                     pin.context_lens, block_size=pin.block_size)
-        work, unit = wl.config_work("paged_decode_fp16", pin), "bytes"
+                                     pin.context_lens, block_size=pin.block_size,
+                                     enable_gqa=args.only == "gqa")
+        work, unit = wl.config_work(pname, pin), "bytes"
     # Counter passes profile every dispatch: no settling phase by default. A
     # kernel-trace pass settles the clocks like the full bench (--settle 0.3);
     # its timed calls are the last `steps` dispatches of each kernel.
@@ -478,8 +482,8 @@ def main() -> int:
                     help="seconds of CPU work per baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only",
-                    choices=["flash", "fp32", "window", "chunked", "paged", "prefill", "append",
-                             "rope", "bwd", "copy"],
+                    choices=["flash", "fp32", "window", "chunked", "paged", "gqa", "prefill",
+                             "append", "rope", "bwd", "copy"],
                     default=None,
                     help="run one leg only (profiler passes); prints that leg's timing")
     ap.add_argument("--settle", type=float, default=0.0,
@@ -521,6 +525,20 @@ def main() -> int:
     p_wall, p_ev, p_min, p_med = time_steps(pstep, args.steps, args.warmup)
     p_gbs = pbytes / (p_ev * 1e-3) / 1e9
     log(f"[bench] {pname}: {p_wall:.3f} ms/step wall, kernels {p_ev:.3f} ms -> {p_gbs:.1f} GB/s")
+
+    # ---- paged decode, fp16, grouped-query heads (32 over 8) --------------------------
+    gname = "paged_decode_gqa_fp16"
+    gcfg = wl.CONFIGS[gname]
+    gin = wl.make_paged(gcfg, device=dev)
+    gbytes = wl.config_work(gname, gin)
+    gstep = lambda: paged_attention(gin.q, gin.k_pool, gin.v_pool, gin.block_tables,
+                                    gin.context_lens, block_size=gin.block_size, enable_gqa=True)
+    log(f"[bench] {gname}: warmup {args.warmup}, steps {args.steps}")
+    g_wall, g_ev, g_min, g_med = time_steps(gstep, args.steps, args.warmup)
+    g_gbs = gbytes / (g_ev * 1e-3) / 1e9
+    log(f"[bench] {gname}: {g_wall:.3f} ms/step wall, kernels {g_ev:.3f} ms -> {g_gbs:.1f} GB/s "
+        f"(distinct K/V bytes)")
+    del gin
 
     # ---- paged prefill, bf16 (prompt processing over pages) ------------------------
     fname = "paged_prefill_bf16"
@@ -642,6 +660,18 @@ def main() -> int:
                          "traffic": measured_traffic("paged_decode_fp16"),
                          "kernel": PAGED_KERNELS, "traffic_unit": "bytes per launch"},
             "cpu_baseline": pcpu,
+        },
+        "paged_decode_gqa": {
+            "workload": "paged_attention decode fp16, enable_gqa, 64 seqs, 32 query heads over "
+                        "8 K/V heads, D=128, ctx~U{512..8192}, 16-token pages, permuted block "
+                        "table",
+            "value": g_gbs, "unit": "GB/s", "ms_per_step": g_wall, "kernel_ms": g_ev,
+            "kernel_ms_median": g_med, "kernel_ms_min": g_min, "bytes_per_step": gbytes,
+            "bytes_note": "distinct bytes: each K/V head's rows once, + q, o, tables",
+            "roofline": {"bound": "hbm", "achieved": g_gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                         "frac": g_gbs / PEAK_HBM_GBS,
+                         "traffic": measured_traffic(gname),
+                         "kernel": GQA_KERNELS, "traffic_unit": "bytes per launch"},
         },
         "paged_prefill": {
             "workload": "paged_attention prefill bf16, 4 prompts x 4096 tokens, H=32, D=128, "

@@ -44,6 +44,7 @@ struct DecodeParams {
   int H_kv, kv_group;  // K/V heads of the pools; query heads per K/V head
   int dp;   // head dim of q, the pools and o (elements, <= the kernel's D)
   float c;  // scale * log2(e)
+  u32 pool_bytes;  // bytes of one pool (grouped-query MFMA kernel: < 4 GiB - 256)
 };
 
 // Tokens per partition and 16-byte loads in flight per lane (overridable at
@@ -225,8 +226,11 @@ __global__ __launch_bounds__(64 * kHeadsPerWG<NT>) void paged_decode_part_kernel
 
 // Combine the partitions of one (sequence, head): the online-softmax merge
 // (mlx_primitives/attention/_online_softmax.py:42-106) over all partitions,
-// then the exact normalisation o / l of the reference's softmax. D is the
-// kernel head dim (the partials' row length); dp <= D columns are written.
+// then the exact normalisation o / l of the reference's softmax. One wave per
+// (sequence, head): lane i takes the (m, l) of partition i and its weight
+// 2^(m_i - M), lane l accumulates dims 2l, 2l+1 over the partitions (16
+// partition rows in flight, each a coalesced 2 D-float read). D is the kernel
+// head dim (the partials' row length); dp <= D columns are written.
 template <int DT>
 __global__ __launch_bounds__(64) void paged_decode_merge_kernel(DecodeParams p, int D) {
   const int bh = blockIdx.x;
@@ -235,36 +239,274 @@ __global__ __launch_bounds__(64) void paged_decode_merge_kernel(DecodeParams p, 
   const int ctx = max(0, min(p.cl[b], p.max_blocks * p.bs));
   const int nparts = (ctx + kPart - 1) / kPart;
   const int64_t base = (int64_t)bh * p.max_parts;
-  float M = -INFINITY;
-  for (int i = 0; i < nparts; ++i) M = fmaxf(M, p.ws_ml[2 * (base + i)]);
-  for (int d = lane; d < p.dp; d += 64) {
-    float acc = 0.f, L = 0.f;
-    int i = 0;
-    // Eight partials per round, their loads issued together.
-    for (; i + 8 <= nparts; i += 8) {
-      float ov[8];
+  const int d = 2 * lane;
+  const bool dl = d < D;
+  // Online over chunks of 64 partitions (one chunk up to 32768 tokens): a
+  // chunk's (m, l) and its first 16 partition rows are requested together.
+  float M = -INFINITY, L = 0.f, acc0 = 0.f, acc1 = 0.f;
+  for (int i0 = 0; i0 < nparts; i0 += 64) {
+    const int n = min(64, nparts - i0);
+    float mi = -INFINITY, li = 0.f;
+    if (lane < n) {
+      mi = p.ws_ml[2 * (base + i0 + lane)];
+      li = p.ws_ml[2 * (base + i0 + lane) + 1];
+    }
+    float w = 0.f;
+    for (int k = 0; k < n; k += 16) {
+      float2 ov[16];
 #pragma unroll
-      for (int k = 0; k < 8; ++k) ov[k] = p.ws_o[(base + i + k) * D + d];
+      for (int u = 0; u < 16; ++u)
+        ov[u] = (k + u < n && dl) ? *(const float2*)(p.ws_o + (base + i0 + k + u) * D + d)
+                                  : make_float2(0.f, 0.f);
+      if (k == 0) {
+        const float mn = fmaxf(M, wave_max(mi));
+        const float keep = M == -INFINITY ? 0.f : fast_exp2(M - mn);
+        acc0 *= keep;
+        acc1 *= keep;
+        L *= keep;
+        M = mn;
+        // 0 for partitions that saw no key (and while no partition has)
+        w = (lane < n && M != -INFINITY) ? fast_exp2(mi - M) : 0.f;
+        L += w * li;
+      }
 #pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const float w = fast_exp2(p.ws_ml[2 * (base + i + k)] - M);
-        L += w * p.ws_ml[2 * (base + i + k) + 1];
-        acc += w * ov[k];
+      for (int u = 0; u < 16; ++u) {
+        const float wk = __shfl(w, k + u, 64);
+        acc0 = fmaf(wk, ov[u].x, acc0);
+        acc1 = fmaf(wk, ov[u].y, acc1);
       }
     }
-    for (; i < nparts; ++i) {
-      const float w = fast_exp2(p.ws_ml[2 * (base + i)] - M);
-      L += w * p.ws_ml[2 * (base + i) + 1];
-      acc += w * p.ws_o[(base + i) * D + d];
-    }
-    const float out = acc / L;  // no valid token: 0 / 0 = NaN, as the reference
-    const int64_t off = (int64_t)b * p.o_sb + (int64_t)h * p.o_sh + d;
-    if constexpr (DT == MPX_F32) {
-      ((float*)p.o)[off] = out;
-    } else if constexpr (DT == MPX_BF16) {
-      ((__bf16*)p.o)[off] = (__bf16)out;
+  }
+  L = wave_sum(L);
+  if (d >= p.dp) return;
+  // no valid token: 0 / 0 = NaN, as the reference
+  const float out0 = acc0 / L, out1 = acc1 / L;
+  const int64_t off = (int64_t)b * p.o_sb + (int64_t)h * p.o_sh + d;
+  if constexpr (DT == MPX_F32) {
+    float* dst = (float*)p.o + off;
+    dst[0] = out0;
+    dst[1] = out1;
+  } else {
+    uint16_t* dst = (uint16_t*)p.o + off;
+    const u32 pk = pack2<DT == MPX_BF16>(out0, out1);
+    if (((uintptr_t)dst & 3u) == 0) {
+      *(u32*)dst = pk;
     } else {
-      ((_Float16*)p.o)[off] = (_Float16)out;
+      dst[0] = (uint16_t)(pk & 0xffffu);
+      dst[1] = (uint16_t)(pk >> 16);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Grouped-query decode on MFMAs (16-bit, head dim 128, 2..16 query heads per
+// K/V head). A wave owns one (sequence, K/V head, partition of kPart tokens)
+// and scores every K row against all query heads of the group at once:
+//   S^T (16 tokens x 16 heads) = K (16 x 128) Q^T (128 x 16): four 16x16x32
+//   MFMAs per 16 tokens (columns past the group are zero heads);
+//   O^T (16 dims x 16 heads) += V^T (16 dims x 32 tokens) P^T (32 x 16): eight
+//   MFMAs per 32 tokens, one per 16 dims.
+// So each K/V byte of the partition is read once for the whole group, and
+// the per-(head, token) work is one exponential. K and V tiles of 32 tokens
+// are staged in LDS by buffer-load DMA, two tiles in flight; 16-byte chunk c
+// of token row r sits at chunk c ^ f(r), f(r) = r % 4 + 4 ((r / 8) % 4), so
+// the 16 rows one operand read touches get 16 different XOR patterns. Lane
+// l = i + 16 q reads the K operand as row i of a 16-token half (half h row i
+// = token 8 (i / 4) + 4 h + i % 4), which makes the S^T values it holds (C
+// rows 4q .. 4q+3 of both halves) the tokens 8q .. 8q+7 of its head: exactly
+// its slice of the P^T operand. V^T comes through the transposing read
+// (ds_read_b64_tr_b16). Waves are independent (no barriers): a wave whose
+// partition starts past the context returns at once.
+// ---------------------------------------------------------------------------
+#ifndef MPX_GQA_WAVES
+#define MPX_GQA_WAVES 1
+#endif
+#ifndef MPX_GQA_STAGES
+#define MPX_GQA_STAGES 2
+#endif
+constexpr int kGqaWaves = MPX_GQA_WAVES;    // partitions per workgroup
+constexpr int kGqaStages = MPX_GQA_STAGES;  // (K, V) tiles per wave in LDS
+constexpr int kGqaTile = 32;                // tokens per step
+constexpr u32 kGqaNoRow = 0xFFFFFF00u;  // DMA offset past any accepted pool: reads zeros
+
+__device__ __forceinline__ int gqa_swz(int row) { return (row & 3) | (((row >> 3) & 3) << 2); }
+
+template <bool BF16>
+__global__ __launch_bounds__(64 * kGqaWaves) void paged_decode_gqa_kernel(DecodeParams p) {
+  constexpr int D = 128, ROWB = 2 * D, TILEB = kGqaTile * ROWB;
+  // Per wave: kGqaStages stages of (K tile, V tile).
+  __shared__ __align__(16) unsigned char kvt[kGqaWaves][kGqaStages][2][TILEB];
+  __shared__ int btl[kGqaWaves][kPart + 1];
+  static_assert(sizeof(kvt) + sizeof(btl) <= 131072, "LDS budget");
+  static_assert(kGqaStages >= 2 && kGqaStages <= 4, "vmcnt counts up to 3 later tiles");
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  // K/V heads vary fastest over the launch, so the workgroups running together
+  // read all heads of the same token rows (whole rows of the pool's pages).
+  const int hk = blockIdx.x, part = blockIdx.y * kGqaWaves + wave, b = blockIdx.z;
+  const int ctx = max(0, min(p.cl[b], p.max_blocks * p.bs));
+  const int p0 = part * kPart;
+  if (p0 >= ctx) return;  // uniform over the wave
+  const int p1 = min(p0 + kPart, ctx);
+  const int pg0 = p0 / p.bs;
+  const int npg = (p1 - 1) / p.bs - pg0 + 1;
+  int* bl = btl[wave];
+  for (int i = lane; i < npg; i += 64) {
+    const int blk = p.bt[(int64_t)b * p.max_blocks + pg0 + i];
+    bl[i] = (blk >= 0 && blk < p.num_blocks) ? blk : -1;
+  }
+  // (this wave's own LDS writes: its later reads see them in order)
+
+  const int i16 = lane & 15, q4 = lane >> 4;
+  const int G = p.kv_group;
+  const bool hv = i16 < G;        // column i16 is a query head of the group
+  const int h = hk * G + i16;
+  // Q^T operand (column i16, dims 32 kb + 8 q4 .. +7) times scale * log2(e),
+  // rounded to the storage type: S^T comes out of the MFMAs in log2 units.
+  u32x4 qb[4];
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb) {
+    u32x4 x = {0u, 0u, 0u, 0u};
+    if (hv) x = *(const u32x4*)((const uint16_t*)p.q + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh +
+                               32 * kb + 8 * q4);
+#pragma unroll
+    for (int w = 0; w < 4; ++w)
+      x[w] = pack2<BF16>(h2f<BF16>((uint16_t)(x[w] & 0xffffu)) * p.c,
+                         h2f<BF16>((uint16_t)(x[w] >> 16)) * p.c);
+    qb[kb] = x;
+  }
+  const float slope2 = (p.slopes && hv) ? p.slopes[h] * kLog2e : 0.f;
+  // Q (and the table) have landed before any DMA, so the waits below count
+  // DMAs only.
+  __builtin_amdgcn_s_waitcnt(0x0F70);
+
+  // Buffers of this K/V head's column of the pools (32-bit offsets: the host
+  // keeps each pool below 4 GiB - 256 bytes).
+  const u32 rec = p.pool_bytes - (u32)(hk * D * 2);
+  const u32x4 krs = buffer_desc((const uint16_t*)p.kpool + (int64_t)hk * D, rec);
+  const u32x4 vrs = buffer_desc((const uint16_t*)p.vpool + (int64_t)hk * D, rec);
+  const u32 row_bytes = (u32)p.H_kv * (u32)D * 2u;
+
+  // K and V rows of the tile at t0 into stage sb: 8 DMA instructions each;
+  // lane l fills slot l % 16 of row 4v + l / 16 with its chunk (l % 16) ^ f(row).
+  auto load_tile = [&](int t0, int sb) __attribute__((always_inline)) {
+    const u32 kdst = lds_addr(kvt[wave][sb][0]), vdst = lds_addr(kvt[wave][sb][1]);
+#pragma unroll
+    for (int v = 0; v < kGqaTile / 4; ++v) {
+      const int r = 4 * v + q4;
+      const int t = t0 + r;
+      const int pg = t < p1 ? bl[t / p.bs - pg0] : -1;
+      const u32 off = pg >= 0 ? ((u32)pg * (u32)p.bs + (u32)(t % p.bs)) * row_bytes +
+                                    (u32)((i16 ^ gqa_swz(r)) * 16)
+                              : kGqaNoRow;
+      dma16(krs, kdst + 4 * v * ROWB, (int)off, 0);
+      dma16(vrs, vdst + 4 * v * ROWB, (int)off, 0);
+    }
+  };
+
+  f32x4 o[D / 16];
+#pragma unroll
+  for (int db = 0; db < D / 16; ++db) o[db] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  float m = -INFINITY, lsum = 0.f;
+
+  const int n_tiles = (p1 - p0 + kGqaTile - 1) / kGqaTile;
+#pragma unroll
+  for (int i = 0; i < kGqaStages - 1; ++i)
+    if (i < n_tiles) load_tile(p0 + i * kGqaTile, i);
+  int sb = 0;
+  for (int it = 0; it < n_tiles; ++it) {
+    const int t0 = p0 + it * kGqaTile;
+    if (it + kGqaStages - 1 < n_tiles)
+      load_tile(t0 + (kGqaStages - 1) * kGqaTile,
+                sb == 0 ? kGqaStages - 1 : sb - 1);
+    // Tile it has landed once at most the 16 DMAs of each later tile are
+    // pending.
+    const int later = min(n_tiles - 1, it + kGqaStages - 1) - it;
+    if (later >= 3) {
+      asm volatile("s_waitcnt vmcnt(48)" ::: "memory");
+    } else if (later == 2) {
+      asm volatile("s_waitcnt vmcnt(32)" ::: "memory");
+    } else if (later == 1) {
+      asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+    } else {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+    const unsigned char* kt = kvt[wave][sb][0];
+    const unsigned char* vt = kvt[wave][sb][1];
+    // S^T of the two 16-token halves.
+    f32x4 s[2];
+#pragma unroll
+    for (int f = 0; f < 2; ++f) {
+      const int r = 8 * (i16 >> 2) + 4 * f + (i16 & 3);
+      s[f] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+        const u32x4 ka = *(const u32x4*)(kt + r * ROWB + (((4 * kb + q4) ^ gqa_swz(r)) * 16));
+        s[f] = mfma16x16x32<BF16>(ka, qb[kb], s[f]);
+      }
+    }
+    // Masks (missing pages, the context end), ALiBi, the tile max of head i16.
+    const int tl = t0 + (lane & 31);
+    const uint64_t vm = __ballot(tl < p1 && bl[min(tl, p1 - 1) / p.bs - pg0] >= 0);
+    float mx = -INFINITY;
+#pragma unroll
+    for (int f = 0; f < 2; ++f)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int tok = 8 * q4 + 4 * f + r;
+        float x = s[f][r] + slope2 * (float)(t0 + tok - ctx);
+        x = ((vm >> tok) & 1ull) ? x : -INFINITY;
+        s[f][r] = x;
+        mx = fmaxf(mx, x);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    if (__any(mx > m)) {
+      const float mn = fmaxf(m, mx);
+      const float alpha = m == -INFINITY ? 0.f : fast_exp2(m - mn);
+      lsum *= alpha;
+#pragma unroll
+      for (int db = 0; db < D / 16; ++db) o[db] *= alpha;
+      m = mn;
+    }
+    const float msub = m == -INFINITY ? 0.f : m;
+    // P^T slice of this lane: tokens 8 q4 .. 8 q4 + 7 of head i16.
+    u32x4 pb;
+#pragma unroll
+    for (int f = 0; f < 2; ++f)
+#pragma unroll
+      for (int r2 = 0; r2 < 2; ++r2) {
+        const u32 pk = pack2<BF16>(fast_exp2(s[f][2 * r2] - msub),
+                                   fast_exp2(s[f][2 * r2 + 1] - msub));
+        pb[2 * f + r2] = pk;
+        lsum = dot2_sum<BF16>(pk, lsum);
+      }
+#pragma unroll
+    for (int db = 0; db < D / 16; ++db) {
+      const int c = 2 * db + ((i16 & 3) >> 1);
+      const int r0 = 8 * q4 + (i16 >> 2);
+      const u32x2 lo = lds_read_tr16(vt + r0 * ROWB + ((c ^ gqa_swz(r0)) * 16) + (i16 & 1) * 8);
+      const u32x2 hi =
+          lds_read_tr16(vt + (r0 + 4) * ROWB + ((c ^ gqa_swz(r0 + 4)) * 16) + (i16 & 1) * 8);
+      o[db] = mfma16x16x32<BF16>((u32x4){lo[0], lo[1], hi[0], hi[1]}, pb, o[db]);
+    }
+    // Every read of stage sb is done before a later iteration's DMAs refill
+    // it (the MFMAs above consumed them).
+    sb = sb + 1 == kGqaStages ? 0 : sb + 1;
+  }
+
+  // Sum of head i16 over the four lanes holding its tokens.
+  lsum += __shfl_xor(lsum, 16, 64);
+  lsum += __shfl_xor(lsum, 32, 64);
+  if (hv) {
+    const int64_t slot = ((int64_t)b * p.H + h) * p.max_parts + part;
+    float* wo = p.ws_o + slot * D + 4 * q4;
+#pragma unroll
+    for (int db = 0; db < D / 16; ++db) *(f32x4*)(wo + 16 * db) = o[db];
+    if (q4 == 0) {
+      p.ws_ml[2 * slot] = m;
+      p.ws_ml[2 * slot + 1] = lsum;
     }
   }
 }
@@ -279,8 +521,25 @@ int max_parts_for(int block_size, int max_blocks) {
 // Kernel head dim serving pools of head dim D (<= 128): 32, 64 or 128.
 int kernel_dim(int D) { return D <= 32 ? 32 : D <= 64 ? 64 : 128; }
 
+// The grouped-query MFMA kernel serves 16-bit pools of head dim 128 with 2 to
+// 16 query heads per K/V head and pools below 4 GiB - 256 bytes
+// (pool_bytes != 0).
+template <int D, int DT>
+constexpr bool kGqaMfmaType = D == 128 && DT != MPX_F32;
+
 template <int D, int DT>
 hipError_t launch_decode(const DecodeParams& p, hipStream_t st) {
+  if constexpr (kGqaMfmaType<D, DT>) {
+    if (p.kv_group >= 2 && p.kv_group <= 16 && p.dp == D && p.pool_bytes != 0) {
+      const dim3 grid(p.H_kv, (p.max_parts + kGqaWaves - 1) / kGqaWaves, p.B);
+      hipLaunchKernelGGL((paged_decode_gqa_kernel<DT == MPX_BF16>), grid, dim3(64 * kGqaWaves),
+                         0, st, p);
+      hipError_t e = hipGetLastError();
+      if (e != hipSuccess) return e;
+      hipLaunchKernelGGL(paged_decode_merge_kernel<DT>, dim3(p.B * p.H), dim3(64), 0, st, p, D);
+      return hipGetLastError();
+    }
+  }
   if (p.kv_group == 1) {
     constexpr int W = kHeadsPerWG<true>;
     const dim3 grid((p.H + W - 1) / W, p.max_parts, p.B);
@@ -356,6 +615,9 @@ int paged_decode_run(const void* q, const void* k_pool, const void* v_pool,
   p.dp = D;
   p.max_parts = std::max(1, max_parts_for(block_size, max_blocks));
   p.c = scale * kLog2e;
+  const uint64_t pool_bytes =
+      (uint64_t)num_blocks * block_size * H_kv * D * (dtype == MPX_F32 ? 4 : 2);
+  p.pool_bytes = pool_bytes < 0xFFFFFF00ull ? (u32)pool_bytes : 0u;
   const size_t need = decode_ws_bytes(B, H, D, block_size, max_blocks);
   MPX_CHECK_ARG(workspace != nullptr && workspace_bytes >= need && ((uintptr_t)workspace & 15u) == 0,
                 "%s: 16-byte aligned workspace of %zu bytes required, %zu given", who, need,

@@ -29,6 +29,9 @@ CONFIGS: Dict[str, dict] = {
                              B=2, S=8192, H=32, D=128, causal=True, window=4096),
     "paged_decode_fp16": dict(kind="paged", dtype=torch.float16, B=64, H=32, D=128,
                               ctx_lo=512, ctx_hi=8192, block_size=16),
+    # The same decode with grouped-query heads: 32 query heads over 8 K/V heads.
+    "paged_decode_gqa_fp16": dict(kind="paged", dtype=torch.float16, B=64, H=32, H_kv=8,
+                                  D=128, ctx_lo=512, ctx_hi=8192, block_size=16),
     "chunked_bf16": dict(kind="chunked", dtype=torch.bfloat16, B=1, H=16, D=64,
                          Sq=512, Skv=65536, chunk_size=1024, causal=False),
     # Prompt processing over a paged cache: the headline shape (4 x 4096 tokens,
@@ -80,6 +83,7 @@ def make_paged(cfg: dict, device="cpu", seed: int = SEED) -> PagedInputs:
     pool cut consecutively in sequence order, -1 padded tables."""
     gen = torch.Generator(device="cpu").manual_seed(seed)
     B, H, D, bs = cfg["B"], cfg["H"], cfg["D"], cfg["block_size"]
+    H_kv = cfg.get("H_kv", H)
     ctx = torch.randint(cfg["ctx_lo"], cfg["ctx_hi"] + 1, (B,), generator=gen, dtype=torch.int64)
     pages = (ctx + bs - 1) // bs
     n_pages = int(pages.sum())
@@ -94,13 +98,13 @@ def make_paged(cfg: dict, device="cpu", seed: int = SEED) -> PagedInputs:
     dgen = gen if device == "cpu" else torch.Generator(device=device).manual_seed(seed + 1)
     dt = cfg["dtype"]
     q = _randn(dgen, (B, 1, H, D), device).to(dt)
-    k_pool = torch.empty((n_pages, bs, H, D), dtype=dt, device=device)
-    v_pool = torch.empty((n_pages, bs, H, D), dtype=dt, device=device)
+    k_pool = torch.empty((n_pages, bs, H_kv, D), dtype=dt, device=device)
+    v_pool = torch.empty((n_pages, bs, H_kv, D), dtype=dt, device=device)
     step = 1024
     for pool in (k_pool, v_pool):
         for s in range(0, n_pages, step):
             e = min(s + step, n_pages)
-            pool[s:e] = _randn(dgen, (e - s, bs, H, D), device).to(dt)
+            pool[s:e] = _randn(dgen, (e - s, bs, H_kv, D), device).to(dt)
     return PagedInputs(q, k_pool, v_pool, tables.to(device), ctx.to(torch.int32).to(device), bs)
 
 
@@ -184,10 +188,12 @@ def chunked_flops(B: int, H: int, Sq: int, Skv: int, D: int) -> float:
     return 4.0 * B * H * Sq * Skv * D
 
 
-def paged_bytes(ctx: torch.Tensor, H: int, D: int, elem_bytes: int, max_blocks: int) -> float:
-    """Valid K+V bytes + q + o + block tables + context lengths (no padding)."""
+def paged_bytes(ctx: torch.Tensor, H: int, D: int, elem_bytes: int, max_blocks: int,
+                H_kv: Optional[int] = None) -> float:
+    """Valid K+V bytes (each K/V head once) + q + o + block tables + context
+    lengths (no padding)."""
     B = int(ctx.numel())
-    kv = 2.0 * float(ctx.to(torch.int64).sum()) * H * D * elem_bytes
+    kv = 2.0 * float(ctx.to(torch.int64).sum()) * (H if H_kv is None else H_kv) * D * elem_bytes
     qo = 2.0 * B * H * D * elem_bytes
     return kv + qo + B * max_blocks * 4 + B * 4
 
@@ -212,7 +218,8 @@ def config_work(name: str, paged: Optional[PagedInputs] = None) -> float:
         return chunked_flops(cfg["B"], cfg["H"], cfg["Sq"], cfg["Skv"], cfg["D"])
     assert paged is not None
     return paged_bytes(paged.context_lens.cpu(), cfg["H"], cfg["D"],
-                       torch.finfo(cfg["dtype"]).bits // 8, paged.block_tables.shape[1])
+                       torch.finfo(cfg["dtype"]).bits // 8, paged.block_tables.shape[1],
+                       cfg.get("H_kv"))
 
 
 def default_scale(D: int) -> float:
