@@ -164,6 +164,23 @@ __device__ __forceinline__ void store_row(uint16_t* row, int g, const f32x16 (&a
     }
 }
 
+// Workgroup -> (tile, head) of a launch over n_heads x n_tiles. Workgroup i
+// runs on XCD i % 8; with n_heads a multiple of 8, XCD x takes heads x, x + 8,
+// ... one at a time, all tiles of a head before the next, so the workgroups
+// an XCD runs together share one or two heads' streamed tiles in its L2.
+// Otherwise: tile-major (each XCD cycles over all heads).
+__device__ __forceinline__ void grid_tile(int n_heads, int n_tiles, int& tile, int& head) {
+  const int i = blockIdx.x;
+  if (n_heads % 8 == 0) {
+    const int xcd = i % 8, local = i / 8;
+    tile = local % n_tiles;
+    head = (local / n_tiles) * 8 + xcd;
+  } else {
+    tile = i / n_heads;
+    head = i % n_heads;
+  }
+}
+
 // ---------------------------------------------------------------------------
 // dQ: a workgroup owns query rows [128 * qt, +128) of one (batch, head); wave
 // w rows +32w. Per KV tile: S^T = K Q^T and dP^T = V dO^T (K, V rows from LDS,
@@ -177,12 +194,10 @@ void fa_bwd_dq_kernel(BwdParams p) {
   // Stage s: K tile at [2s], V tile at [2s + 1].
   __shared__ __align__(1024) uint16_t lds[4 * TILE];
 
-  // Grid order: q-tile major, last (under a causal mask the longest) tiles
-  // first; workgroup i runs on XCD i % 8, so with B * H a multiple of 8 every
-  // tile of a head shares one XCD's L2 for its K and V.
   const int n_qt = (p.Sq + kBwdOwn - 1) / kBwdOwn;
-  const int qt = n_qt - 1 - (int)(blockIdx.x / (p.B * p.H));
-  const int bh = blockIdx.x % (p.B * p.H);
+  int qt, bh;
+  grid_tile(p.B * p.H, n_qt, qt, bh);
+  qt = n_qt - 1 - qt;  // last (under a causal mask the longest) tiles first
   const int b = bh / p.H, h = bh % p.H;
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int j = lane & 31, g = lane >> 5;
@@ -323,10 +338,9 @@ void fa_bwd_dkdv_kernel(BwdParams p) {
   __shared__ __align__(16) float lse_lds[2][kBwdTile];
   __shared__ __align__(16) float dvc_lds[2][kBwdTile];
 
-  // Grid order: key-tile major, first (under a causal mask the longest) tiles
-  // first, every tile of a K/V head on one XCD when B * H_kv is a multiple of 8.
-  const int kt = (int)(blockIdx.x / (p.B * p.H_kv));
-  const int bhk = blockIdx.x % (p.B * p.H_kv);  // (batch, K/V head)
+  const int n_kt = (p.Sk + kBwdOwn - 1) / kBwdOwn;
+  int kt, bhk;  // key tile (first, under a causal mask the longest, first), (batch, K/V head)
+  grid_tile(p.B * p.H_kv, n_kt, kt, bhk);
   const int b = bhk / p.H_kv, hk = bhk % p.H_kv;
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int j = lane & 31, g = lane >> 5;
