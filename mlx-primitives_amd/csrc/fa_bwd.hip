@@ -44,17 +44,18 @@ __device__ __forceinline__ int swz(int r) {
   }
 }
 
-// DMA of 64 rows of a 16-bit (rows, D) slice into a swizzled LDS tile. A DMA
-// instruction fills 1 KB of LDS (RPD rows); wave w issues the blocks w,
-// w + 4, ... . Lane l lands at slot l % CPR of row l / CPR of its block, so it
+// DMA of ROWS (64 by default) rows of a 16-bit (rows, D) slice into a swizzled
+// LDS tile. A DMA instruction fills 1 KB of LDS (RPD rows); wave w issues the
+// blocks w, w + 4, ... . Lane l lands at slot l % CPR of row l / CPR of its block, so it
 // loads logical chunk (l % CPR) ^ swz(row); the swizzle only depends on the
 // low 4 row bits, which are the same in all of a lane's blocks. Rows past the
 // slice end re-read its last row (callers mask them or weight them by 0).
-template <int D>
+template <int D, int ROWS = kBwdTile>
 struct TileDma {
   static constexpr int CPR = D / 8;                            // 16-byte chunks per row
   static constexpr int RPD = 64 / CPR;                         // rows per DMA (1 KB)
-  static constexpr int NDMA = kBwdTile / (RPD * kBwdWaves);    // DMAs per wave per tile
+  static constexpr int NDMA = ROWS / (RPD * kBwdWaves);        // DMAs per wave per tile
+  static_assert(NDMA * RPD * kBwdWaves == ROWS, "whole DMA rounds per tile");
   int row_bytes, lrow, lchunk, voff;
   u32 lds_off;
   __device__ __forceinline__ void init(int64_t row_stride, int wave, int lane) {
@@ -64,11 +65,11 @@ struct TileDma {
     voff = lrow * row_bytes + lchunk * 16;
     lds_off = (u32)wave * 1024u;
   }
-  // Rows row0 .. row0 + 63 of the slice at base (rows rows) into the LDS tile at lds.
+  // Rows row0 .. row0 + ROWS - 1 of the slice at base (rows rows) into the LDS tile at lds.
   __device__ __forceinline__ void load(const void* base, u32 lds, int row0, int rows) const {
     const u32x4 rs = buffer_desc(base);
     const int so = row0 * row_bytes;
-    if (row0 + kBwdTile <= rows) {
+    if (row0 + ROWS <= rows) {
 #pragma unroll
       for (int r = 0; r < NDMA; ++r)
         dma16(rs, lds + lds_off + r * kBwdWaves * 1024u, voff,
@@ -502,6 +503,185 @@ void fa_bwd_dkdv_kernel(BwdParams p) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// dK and dV in one pass at D = 128. fa_bwd_dkdv_kernel holds both accumulator
+// sets next to the wave's K and V rows only at D = 64; here the workgroup's
+// 128 K rows sit in LDS (read as the B operand of S = Q K^T), the wave's V
+// rows stay in registers, and Q / dO stream in 32-row tiles, two stages:
+// 32 KB of K + 32 KB of stages (two workgroups per CU) and two waves per SIMD.
+// Per tile: S and dP once, P and dS packed as B operands, then dV^T += dO^T P
+// and dK^T += Q^T dS (S is computed twice per backward instead of three times).
+// ---------------------------------------------------------------------------
+constexpr int kFusedTile = 32;
+
+template <bool BF16>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void fa_bwd_dkdv_fused_kernel(BwdParams p) {
+  constexpr int D = 128, NKS = D / 16, NDB = D / 32, TILE = kFusedTile * D;
+  __shared__ __align__(1024) uint16_t ktile[kBwdOwn * D];
+  // Stage s: Q tile at [2s], dO tile at [2s + 1].
+  __shared__ __align__(1024) uint16_t lds[4 * TILE];
+  __shared__ __align__(16) float lse_lds[2][kFusedTile];
+  __shared__ __align__(16) float dvc_lds[2][kFusedTile];
+  static_assert(sizeof(ktile) + sizeof(lds) + sizeof(lse_lds) + sizeof(dvc_lds) <= 80 * 1024,
+                "two workgroups per CU");
+
+  const int n_kt = (p.Sk + kBwdOwn - 1) / kBwdOwn;
+  int kt, bhk;  // key tile (first, under a causal mask the longest, first), (batch, K/V head)
+  grid_tile(p.B * p.H_kv, n_kt, kt, bhk);
+  const int b = bhk / p.H_kv, hk = bhk % p.H_kv;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int j = lane & 31, g = lane >> 5;
+  const int k0 = kt * kBwdOwn, wk0 = k0 + wave * 32, mykey = wk0 + j;
+  const int krow = min(mykey, p.Sk - 1);
+  const int q_first = p.win_right >= 0 ? mykey - p.win_right : -(1 << 30);
+  const int q_last = p.win_left >= 0 ? mykey + p.win_left : (1 << 30);
+
+  const uint16_t* K = (const uint16_t*)p.k + b * p.k_sb + hk * p.k_sh;
+  const uint16_t* V = (const uint16_t*)p.v + b * p.v_sb + hk * p.v_sh;
+  u32x4 vf[NKS];
+  load_row_frags<NKS>(V + (int64_t)krow * p.v_ss, g, vf);
+  // B operand of S: K row r = 32 wave + j (the wave's key j), k-group g of
+  // step ks, at chunk (2 ks + g) ^ swz(r) = (2 ks ^ km) + kodd (computed per
+  // read: an address array would push the kernel past 256 registers).
+  const int kswz = swz<D>(32 * wave + j);
+  const int kbase = (32 * wave + j) * D + 8 * ((g ^ kswz) & 1), km = kswz & 14;
+
+  const int k_last = min(k0 + kBwdOwn, p.Sk) - 1;
+  const int q_lo = p.win_right >= 0 ? max(0, k0 - p.win_right) : 0;
+  const int q_hi = p.win_left >= 0 ? min(p.Sq, k_last + p.win_left + 1) : p.Sq;
+  const int t0 = q_lo / kFusedTile;
+  const int n_t = q_hi > q_lo ? (q_hi - 1) / kFusedTile - t0 + 1 : 0;
+  const int n_steps = n_t * p.kv_group;
+
+  Addr<D> ad;
+  ad.init(lane);
+  TileDma<D, kBwdOwn> kd;
+  kd.init(p.k_ss, wave, lane);
+  TileDma<D, kFusedTile> qd, dd;
+  qd.init(p.q_ss, wave, lane);
+  dd.init(p.do_ss, wave, lane);
+  const u32 lbase = lds_addr(lds);
+  f32x16 dk[NDB], dv[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) {
+    dk[db] = (f32x16){};
+    dv[db] = (f32x16){};
+  }
+
+  float lse_r = 0.f, dvc_r = 0.f;  // row threadIdx.x of the tile in flight (first 32 threads)
+  auto load = [&](int u, int S) __attribute__((always_inline)) {
+    const int h = hk * p.kv_group + u / n_t;
+    const int row0 = (t0 + u % n_t) * kFusedTile;
+    qd.load((const uint16_t*)p.q + b * p.q_sb + h * p.q_sh, lbase + (2 * S) * TILE * 2, row0,
+            p.Sq);
+    dd.load((const uint16_t*)p.dout + b * p.do_sb + h * p.do_sh,
+            lbase + (2 * S + 1) * TILE * 2, row0, p.Sq);
+    if (threadIdx.x < kFusedTile) {
+      const int r = row0 + threadIdx.x;
+      const int64_t rix = ((int64_t)b * p.H + h) * p.Sq + r;
+      lse_r = r < p.Sq ? p.lse[rix] : INFINITY;
+      dvc_r = r < p.Sq ? p.dvec[rix] : 0.f;
+    }
+  };
+  auto store_vec = [&](int S) __attribute__((always_inline)) {
+    if (threadIdx.x < kFusedTile) {
+      lse_lds[S][threadIdx.x] = lse_r;
+      dvc_lds[S][threadIdx.x] = dvc_r;
+    }
+  };
+  if (n_steps > 0) {
+    wait_all();  // V fragments landed before the first DMA
+    kd.load(K, lds_addr(ktile), k0, p.Sk);
+    load(0, 0);
+    wait_all();
+    store_vec(0);
+    stage_barrier();
+  }
+  for (int u = 0; u < n_steps; ++u) {
+    const int S = u & 1;
+    if (u + 1 < n_steps) load(u + 1, S ^ 1);
+    const int qr0 = (t0 + u % n_t) * kFusedTile;
+    const bool skip = wk0 >= p.Sk ||
+                      (p.win_right >= 0 && wk0 > qr0 + kFusedTile - 1 + p.win_right) ||
+                      (p.win_left >= 0 && wk0 + 31 < qr0 - p.win_left);
+    const bool full = (p.win_right < 0 || wk0 + 31 <= qr0 + p.win_right) &&
+                      (p.win_left < 0 || wk0 >= qr0 + kFusedTile - 1 - p.win_left);
+    if (!skip) {
+      const uint16_t* Qt = lds + 2 * S * TILE;
+      const uint16_t* Dt = Qt + TILE;
+      const float* lsv = lse_lds[S];
+      const float* dvv = dvc_lds[S];
+      // S and dP of the tile's 32 query rows (element 8h + i: query qr0 + 16h + 8g + i).
+      f32x16 sb = {}, dpb = {};
+      // (opaque copies: the K addresses are recomputed every step instead of
+      // being hoisted into eight loop-long registers)
+      int kb = kbase, kx = km;
+      asm volatile("" : "+v"(kb), "+v"(kx));
+#pragma unroll
+      for (int kk = 0; kk < NKS; ++kk) {
+        const u32x4 qa = *(const u32x4*)(Qt + ad.row[kk]);
+        const u32x4 ka = *(const u32x4*)(ktile + kb + 8 * ((2 * kk) ^ kx));
+        sb = mfma32x32x16<BF16>(qa, ka, sb);
+      }
+#pragma unroll
+      for (int kk = 0; kk < NKS; ++kk) {
+        const u32x4 da = *(const u32x4*)(Dt + ad.row[kk]);
+        dpb = mfma32x32x16<BF16>(da, vf[kk], dpb);
+      }
+      if (!full) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int q = qr0 + 16 * (e >> 3) + 8 * g + (e & 7);
+          sb[e] = (q >= q_first) & (q <= q_last) ? sb[e] : -INFINITY;
+        }
+      }
+      u32x4 pp[2], dsp[2];
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const int r8 = 16 * hh + 8 * g;
+        const f32x4 l0 = *(const f32x4*)(lsv + r8);
+        const f32x4 l1 = *(const f32x4*)(lsv + r8 + 4);
+        const f32x4 d0 = *(const f32x4*)(dvv + r8);
+        const f32x4 d1 = *(const f32x4*)(dvv + r8 + 4);
+#pragma unroll
+        for (int e2 = 0; e2 < 4; ++e2) {
+          const int e = 8 * hh + 2 * e2;
+          const float lv0 = e2 < 2 ? l0[2 * e2] : l1[2 * e2 - 4];
+          const float lv1 = e2 < 2 ? l0[2 * e2 + 1] : l1[2 * e2 - 3];
+          const float dv0 = e2 < 2 ? d0[2 * e2] : d1[2 * e2 - 4];
+          const float dv1 = e2 < 2 ? d0[2 * e2 + 1] : d1[2 * e2 - 3];
+          const float p0 = fast_exp2(sb[e] * p.c - lv0);
+          const float p1 = fast_exp2(sb[e + 1] * p.c - lv1);
+          pp[hh][e2] = pack2<BF16>(p0, p1);
+          dsp[hh][e2] = pack2<BF16>(p0 * (dpb[e] - dv0), p1 * (dpb[e + 1] - dv1));
+        }
+      }
+      // dV^T += dO^T P and dK^T += Q^T dS (transposing reads of the tiles).
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          const u32x2 dlo = lds_read_tr16(Dt + ad.tr[db][0] + 16 * hh * D);
+          const u32x2 dhi = lds_read_tr16(Dt + ad.tr[db][1] + 16 * hh * D);
+          dv[db] = mfma32x32x16<BF16>((u32x4){dlo[0], dlo[1], dhi[0], dhi[1]}, pp[hh], dv[db]);
+          const u32x2 qlo = lds_read_tr16(Qt + ad.tr[db][0] + 16 * hh * D);
+          const u32x2 qhi = lds_read_tr16(Qt + ad.tr[db][1] + 16 * hh * D);
+          dk[db] = mfma32x32x16<BF16>((u32x4){qlo[0], qlo[1], qhi[0], qhi[1]}, dsp[hh], dk[db]);
+        }
+    }
+    wait_all();
+    if (u + 1 < n_steps) store_vec(S ^ 1);
+    stage_barrier();
+  }
+  if (mykey < p.Sk) {
+    store_row<NDB, BF16>((uint16_t*)p.dk + b * p.dk_sb + hk * p.dk_sh + (int64_t)mykey * p.dk_ss,
+                         g, dk, p.scale);
+    store_row<NDB, BF16>((uint16_t*)p.dv + b * p.dv_sb + hk * p.dv_sh + (int64_t)mykey * p.dv_ss,
+                         g, dv, 1.f);
+  }
+}
+
 template <int D, bool BF16>
 hipError_t launch_bwd(const BwdParams& p, hipStream_t st) {
   const int64_t rows = (int64_t)p.B * p.H * p.Sq;
@@ -511,8 +691,7 @@ hipError_t launch_bwd(const BwdParams& p, hipStream_t st) {
   hipLaunchKernelGGL((fa_bwd_dq_kernel<D, BF16>), dim3(p.B * p.H * n_qt), dim3(256), 0, st, p);
   const dim3 grid_kv(p.B * p.H_kv * n_kt);
   if constexpr (D == 128) {
-    hipLaunchKernelGGL((fa_bwd_dkdv_kernel<D, BF16, kOnlyK>), grid_kv, dim3(256), 0, st, p);
-    hipLaunchKernelGGL((fa_bwd_dkdv_kernel<D, BF16, kOnlyV>), grid_kv, dim3(256), 0, st, p);
+    hipLaunchKernelGGL((fa_bwd_dkdv_fused_kernel<BF16>), grid_kv, dim3(256), 0, st, p);
   } else {
     hipLaunchKernelGGL((fa_bwd_dkdv_kernel<D, BF16, kBoth>), grid_kv, dim3(256), 0, st, p);
   }
