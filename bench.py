@@ -56,8 +56,7 @@ PAGED_KERNELS = "paged_decode_part_kernel + paged_decode_merge_kernel"
 GQA_KERNELS = "paged_decode_gqa_kernel + paged_decode_merge_kernel"
 PREFILL_KERNEL = "fa_fwd16_kernel<128,128,8,bf16,paged>"
 APPEND_KERNEL = "kv_append_kernel (+ the 12-byte fill that clears the error words)"
-BWD_KERNELS = ("fa_bwd_dvec_kernel + fa_bwd_dq_kernel<128,bf16> + fa_bwd_dkdv_kernel<128,bf16,K> "
-               "+ fa_bwd_dkdv_kernel<128,bf16,V>")
+BWD_KERNELS = "fa_bwd_dq_kernel<128,bf16> (+ Dvec) + fa_bwd_dkdv_fused_kernel<bf16>"
 
 
 def measured_traffic(key: str):

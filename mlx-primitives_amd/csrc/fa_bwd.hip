@@ -5,15 +5,17 @@
 // (attention/flash.py:52-254; the reference differentiates its tiled path with
 // mx.grad, tests/attention/test_flash.py:338-362). With the forward's row
 // log-sum-exp lse (log2 units), P = exp2(s * c - lse), c = scale * log2(e):
-//   Dvec_i = sum_d dO[i, d] * O[i, d]                 (fa_bwd_dvec_kernel)
+//   Dvec_i = sum_d dO[i, d] * O[i, d]                 (fa_bwd_dq_kernel)
 //   dP = dO V^T,  dS = P * (dP - Dvec_i)
 //   dQ = scale * dS K                                 (fa_bwd_dq_kernel)
-//   dV = P^T dO,  dK = scale * dS^T Q                 (fa_bwd_dkdv_kernel)
+//   dV = P^T dO,  dK = scale * dS^T Q                 (fa_bwd_dkdv_kernel,
+//                                                      fa_bwd_dkdv_fused_kernel)
 // Two MFMA kernels, no atomics: dQ is query-parallel (each workgroup owns 128
-// query rows and streams K and V), dK/dV key-parallel (each workgroup owns 128
-// keys and streams Q and dO). Both recompute S and dP; tiles of 64 rows go
-// from HBM straight into LDS (buffer_load ... lds), double buffered: the tile
-// after the current one is in flight while the current one is computed.
+// query rows and streams K and V; it also writes Dvec), dK/dV key-parallel
+// (each workgroup owns 128 keys and streams Q and dO). Both recompute S and
+// dP; tiles go from HBM straight into LDS (buffer_load ... lds), double
+// buffered: the tile after the current one is in flight while the current one
+// is computed.
 //
 // MFMA 32x32x16 layouts (lane = j + 32*g, j in [0,32)): A (32 x 16) lane holds
 // row j, k-group g (8 values); B (16 x 32) column j, k-group g; C (32 x 32)
@@ -87,33 +89,6 @@ struct TileDma {
 // s_waitcnt vmcnt(0) lgkmcnt(0): every load and LDS access of this wave done.
 __device__ __forceinline__ void wait_all() { __builtin_amdgcn_s_waitcnt(0x0070); }
 
-// Dvec = rowsum(dO * O) in float32: D / 8 lanes per row, 8 elements each.
-template <int D, bool BF16>
-__global__ __launch_bounds__(256) void fa_bwd_dvec_kernel(BwdParams p) {
-  constexpr int LPR = D / 8;  // lanes per row
-  const int64_t rows = (int64_t)p.B * p.H * p.Sq;
-  const int64_t row = ((int64_t)blockIdx.x * 256 + threadIdx.x) / LPR;
-  const int l = threadIdx.x % LPR;
-  float acc = 0.f;
-  if (row < rows) {
-    const int i = (int)(row % p.Sq);
-    const int64_t bh = row / p.Sq;
-    const int b = (int)(bh / p.H), h = (int)(bh % p.H);
-    const uint16_t* o = (const uint16_t*)p.o + b * p.o_sb + h * p.o_sh + (int64_t)i * p.o_ss;
-    const uint16_t* d = (const uint16_t*)p.dout + b * p.do_sb + h * p.do_sh + (int64_t)i * p.do_ss;
-    const u32x4 ov = *(const u32x4*)(o + 8 * l);
-    const u32x4 dv = *(const u32x4*)(d + 8 * l);
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      acc += h2f<BF16>((uint16_t)(ov[w] & 0xffffu)) * h2f<BF16>((uint16_t)(dv[w] & 0xffffu));
-      acc += h2f<BF16>((uint16_t)(ov[w] >> 16)) * h2f<BF16>((uint16_t)(dv[w] >> 16));
-    }
-  }
-#pragma unroll
-  for (int off = LPR / 2; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 64);
-  if (row < rows && l == 0) p.dvec[row] = acc;
-}
-
 // Per-lane LDS element offsets into a swizzled (64, D) tile. row[ks]: A
 // operand rows 32*nb + perm(j), k-step ks (add nb * 32 * D). tr[db][hf]: the
 // transposing read for A = X^T over rows 16*sl + 8g + 4hf + s/4, columns
@@ -186,7 +161,10 @@ __device__ __forceinline__ void grid_tile(int n_heads, int n_tiles, int& tile, i
 // dQ: a workgroup owns query rows [128 * qt, +128) of one (batch, head); wave
 // w rows +32w. Per KV tile: S^T = K Q^T and dP^T = V dO^T (K, V rows from LDS,
 // Q, dO in registers), dS^T = P^T * (dP^T - Dvec), dQ^T += K^T dS^T. Two
-// workgroups per CU (two waves per SIMD) hide each other's VALU phases.
+// workgroups per CU (two waves per SIMD) hide each other's VALU phases. The
+// kernel also forms Dvec = rowsum(dO * O) of its rows in float32 (from the dO
+// fragments it holds and the O row) and writes it for the dK/dV kernel that
+// runs after it.
 // ---------------------------------------------------------------------------
 template <int D, bool BF16>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
@@ -215,7 +193,24 @@ void fa_bwd_dq_kernel(BwdParams p) {
   load_row_frags<NKS>(dO + (int64_t)qrow * p.do_ss, g, df);
   const int64_t rix = (int64_t)bh * p.Sq + qrow;
   const float lse = myq < p.Sq ? p.lse[rix] : INFINITY;
-  const float dvc = p.dvec[rix];
+  float dvc;
+  {
+    // This lane's half of the row (dims 16 ks + 8 g + 0..7), then the pair sum.
+    u32x4 of[NKS];
+    load_row_frags<NKS>((const uint16_t*)p.o + b * p.o_sb + h * p.o_sh + (int64_t)qrow * p.o_ss,
+                        g, of);
+    float part = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks)
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        part += h2f<BF16>((uint16_t)(of[ks][w] & 0xffffu)) *
+                h2f<BF16>((uint16_t)(df[ks][w] & 0xffffu));
+        part += h2f<BF16>((uint16_t)(of[ks][w] >> 16)) * h2f<BF16>((uint16_t)(df[ks][w] >> 16));
+      }
+    dvc = pair_sum32(part);
+    if (g == 0 && myq < p.Sq) p.dvec[rix] = dvc;
+  }
   // Keys this row sees: [kv_first, kv_last] (rows past Sq have lse = +inf, so
   // their probabilities vanish without a mask).
   const int kv_first = p.win_left >= 0 ? myq - p.win_left : -(1 << 30);
@@ -554,8 +549,24 @@ void fa_bwd_dkdv_fused_kernel(BwdParams p) {
   const int n_t = q_hi > q_lo ? (q_hi - 1) / kFusedTile - t0 + 1 : 0;
   const int n_steps = n_t * p.kv_group;
 
-  Addr<D> ad;
-  ad.init(lane);
+  // Row operands (A of S and dP): query row perm(j) of the tile, k-group g of
+  // step kk, at element rbase + ((16 kk) ^ rx). Transposing reads (A of dV^T
+  // and dK^T) for 32-dim block db and row half hf at trb[hf] + ((32 db) ^ tx).
+  // Two bases and a mask per family instead of an address per step keep the
+  // registers free for operands in flight.
+  const int perm = (j & ~12) | ((j & 4) << 1) | ((j & 8) >> 1);
+  const int rsw = swz<D>(perm);
+  const int rbase = perm * D + 8 * ((g ^ rsw) & 1), rx = 16 * (rsw >> 1);
+  const int ts = lane & 15, thalf = (lane >> 4) & 1;
+  const int tx = 32 * (ts >> 2);
+  int trb[2];
+#pragma unroll
+  for (int hf = 0; hf < 2; ++hf)
+    trb[hf] = (8 * g + 4 * hf + (ts >> 2)) * D +
+              8 * ((2 * thalf + ((ts & 3) >> 1)) ^ (2 * g + hf)) + 4 * (ts & 1);
+  // Visible query rows of this key: q - q_first <= span as unsigned.
+  const unsigned span = (unsigned)q_last - (unsigned)q_first;
+
   TileDma<D, kBwdOwn> kd;
   kd.init(p.k_ss, wave, lane);
   TileDma<D, kFusedTile> qd, dd;
@@ -570,18 +581,25 @@ void fa_bwd_dkdv_fused_kernel(BwdParams p) {
   }
 
   float lse_r = 0.f, dvc_r = 0.f;  // row threadIdx.x of the tile in flight (first 32 threads)
-  auto load = [&](int u, int S) __attribute__((always_inline)) {
-    const int h = hk * p.kv_group + u / n_t;
-    const int row0 = (t0 + u % n_t) * kFusedTile;
-    qd.load((const uint16_t*)p.q + b * p.q_sb + h * p.q_sh, lbase + (2 * S) * TILE * 2, row0,
+  // Step u covers query tile t0 + u % n_t of head hk * kv_group + u / n_t; the
+  // pair is stepped, not divided, for the tile being loaded (lt, lh) and the
+  // tile being computed (ct).
+  int lt = 0, lh = hk * p.kv_group, ct = 0;
+  auto load = [&](int S) __attribute__((always_inline)) {
+    const int row0 = (t0 + lt) * kFusedTile;
+    qd.load((const uint16_t*)p.q + b * p.q_sb + lh * p.q_sh, lbase + (2 * S) * TILE * 2, row0,
             p.Sq);
-    dd.load((const uint16_t*)p.dout + b * p.do_sb + h * p.do_sh,
+    dd.load((const uint16_t*)p.dout + b * p.do_sb + lh * p.do_sh,
             lbase + (2 * S + 1) * TILE * 2, row0, p.Sq);
     if (threadIdx.x < kFusedTile) {
       const int r = row0 + threadIdx.x;
-      const int64_t rix = ((int64_t)b * p.H + h) * p.Sq + r;
+      const int64_t rix = ((int64_t)b * p.H + lh) * p.Sq + r;
       lse_r = r < p.Sq ? p.lse[rix] : INFINITY;
       dvc_r = r < p.Sq ? p.dvec[rix] : 0.f;
+    }
+    if (++lt == n_t) {
+      lt = 0;
+      ++lh;
     }
   };
   auto store_vec = [&](int S) __attribute__((always_inline)) {
@@ -593,48 +611,49 @@ void fa_bwd_dkdv_fused_kernel(BwdParams p) {
   if (n_steps > 0) {
     wait_all();  // V fragments landed before the first DMA
     kd.load(K, lds_addr(ktile), k0, p.Sk);
-    load(0, 0);
+    load(0);
     wait_all();
     store_vec(0);
     stage_barrier();
   }
   for (int u = 0; u < n_steps; ++u) {
     const int S = u & 1;
-    if (u + 1 < n_steps) load(u + 1, S ^ 1);
-    const int qr0 = (t0 + u % n_t) * kFusedTile;
+    if (u + 1 < n_steps) load(S ^ 1);
+    const int qr0 = (t0 + ct) * kFusedTile;
+    if (++ct == n_t) ct = 0;
     const bool skip = wk0 >= p.Sk ||
                       (p.win_right >= 0 && wk0 > qr0 + kFusedTile - 1 + p.win_right) ||
                       (p.win_left >= 0 && wk0 + 31 < qr0 - p.win_left);
     const bool full = (p.win_right < 0 || wk0 + 31 <= qr0 + p.win_right) &&
                       (p.win_left < 0 || wk0 >= qr0 + kFusedTile - 1 - p.win_left);
     if (!skip) {
-      const uint16_t* Qt = lds + 2 * S * TILE;
-      const uint16_t* Dt = Qt + TILE;
       const float* lsv = lse_lds[S];
       const float* dvv = dvc_lds[S];
+      // (opaque copies: the addresses are recomputed every step instead of
+      // being hoisted into loop-long registers)
+      int kb = kbase, kx = km, rb = rbase + 2 * S * TILE, rxs = rx, t0b = trb[0] + 2 * S * TILE,
+          t1b = trb[1] + 2 * S * TILE, txs = tx;
+      asm volatile("" : "+v"(kb), "+v"(kx), "+v"(rb), "+v"(rxs), "+v"(t0b), "+v"(t1b), "+v"(txs));
       // S and dP of the tile's 32 query rows (element 8h + i: query qr0 + 16h + 8g + i).
+      // The runs of products go at raised wave priority so that the other
+      // wave on the SIMD fills the gaps between them rather than the runs.
+      __builtin_amdgcn_s_setprio(1);
       f32x16 sb = {}, dpb = {};
-      // (opaque copies: the K addresses are recomputed every step instead of
-      // being hoisted into eight loop-long registers)
-      int kb = kbase, kx = km;
-      asm volatile("" : "+v"(kb), "+v"(kx));
 #pragma unroll
       for (int kk = 0; kk < NKS; ++kk) {
-        const u32x4 qa = *(const u32x4*)(Qt + ad.row[kk]);
+        const int ro = rb + ((16 * kk) ^ rxs);
+        const u32x4 qa = *(const u32x4*)(lds + ro);
         const u32x4 ka = *(const u32x4*)(ktile + kb + 8 * ((2 * kk) ^ kx));
         sb = mfma32x32x16<BF16>(qa, ka, sb);
-      }
-#pragma unroll
-      for (int kk = 0; kk < NKS; ++kk) {
-        const u32x4 da = *(const u32x4*)(Dt + ad.row[kk]);
+        const u32x4 da = *(const u32x4*)(lds + ro + TILE);
         dpb = mfma32x32x16<BF16>(da, vf[kk], dpb);
       }
+      __builtin_amdgcn_s_setprio(0);
       if (!full) {
+        const int qd0 = qr0 + 8 * g - q_first;
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int q = qr0 + 16 * (e >> 3) + 8 * g + (e & 7);
-          sb[e] = (q >= q_first) & (q <= q_last) ? sb[e] : -INFINITY;
-        }
+        for (int e = 0; e < 16; ++e)
+          sb[e] = (unsigned)(qd0 + 16 * (e >> 3) + (e & 7)) <= span ? sb[e] : -INFINITY;
       }
       u32x4 pp[2], dsp[2];
 #pragma unroll
@@ -658,17 +677,21 @@ void fa_bwd_dkdv_fused_kernel(BwdParams p) {
         }
       }
       // dV^T += dO^T P and dK^T += Q^T dS (transposing reads of the tiles).
+      __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int db = 0; db < NDB; ++db)
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
-          const u32x2 dlo = lds_read_tr16(Dt + ad.tr[db][0] + 16 * hh * D);
-          const u32x2 dhi = lds_read_tr16(Dt + ad.tr[db][1] + 16 * hh * D);
+          const int o0 = t0b + ((32 * db) ^ txs) + 16 * hh * D;
+          const int o1 = t1b + ((32 * db) ^ txs) + 16 * hh * D;
+          const u32x2 dlo = lds_read_tr16(lds + o0 + TILE);
+          const u32x2 dhi = lds_read_tr16(lds + o1 + TILE);
           dv[db] = mfma32x32x16<BF16>((u32x4){dlo[0], dlo[1], dhi[0], dhi[1]}, pp[hh], dv[db]);
-          const u32x2 qlo = lds_read_tr16(Qt + ad.tr[db][0] + 16 * hh * D);
-          const u32x2 qhi = lds_read_tr16(Qt + ad.tr[db][1] + 16 * hh * D);
+          const u32x2 qlo = lds_read_tr16(lds + o0);
+          const u32x2 qhi = lds_read_tr16(lds + o1);
           dk[db] = mfma32x32x16<BF16>((u32x4){qlo[0], qlo[1], qhi[0], qhi[1]}, dsp[hh], dk[db]);
         }
+      __builtin_amdgcn_s_setprio(0);
     }
     wait_all();
     if (u + 1 < n_steps) store_vec(S ^ 1);
@@ -684,9 +707,7 @@ void fa_bwd_dkdv_fused_kernel(BwdParams p) {
 
 template <int D, bool BF16>
 hipError_t launch_bwd(const BwdParams& p, hipStream_t st) {
-  const int64_t rows = (int64_t)p.B * p.H * p.Sq;
-  hipLaunchKernelGGL((fa_bwd_dvec_kernel<D, BF16>),
-                     dim3((unsigned)((rows * (D / 8) + 255) / 256)), dim3(256), 0, st, p);
+  // dQ (which also writes Dvec) before dK / dV, which reads it.
   const int n_qt = (p.Sq + kBwdOwn - 1) / kBwdOwn, n_kt = (p.Sk + kBwdOwn - 1) / kBwdOwn;
   hipLaunchKernelGGL((fa_bwd_dq_kernel<D, BF16>), dim3(p.B * p.H * n_qt), dim3(256), 0, st, p);
   const dim3 grid_kv(p.B * p.H_kv * n_kt);
