@@ -174,141 +174,149 @@ void fa_bwd_dq_kernel(BwdParams p) {
   __shared__ __align__(1024) uint16_t lds[4 * TILE];
 
   const int n_qt = (p.Sq + kBwdOwn - 1) / kBwdOwn;
-  int qt, bh;
-  grid_tile(p.B * p.H, n_qt, qt, bh);
-  qt = n_qt - 1 - qt;  // last (under a causal mask the longest) tiles first
+  // A workgroup runs query tiles n_qt - 1 - pt and pt, the longer (under a
+  // causal mask, the last) first: their key-tile counts add up to the same
+  // total for every pair, so all workgroups carry equal work.
+  const int n_pair = (n_qt + 1) / 2;
+  int pt, bh;
+  grid_tile(p.B * p.H, n_pair, pt, bh);
   const int b = bh / p.H, h = bh % p.H;
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int j = lane & 31, g = lane >> 5;
-  const int q0 = qt * kBwdOwn, wq0 = q0 + wave * 32, myq = wq0 + j;
-  const int qrow = min(myq, p.Sq - 1);
 
   const int kvh = h / p.kv_group;
   const uint16_t* Q = (const uint16_t*)p.q + b * p.q_sb + h * p.q_sh;
   const uint16_t* K = (const uint16_t*)p.k + b * p.k_sb + kvh * p.k_sh;
   const uint16_t* V = (const uint16_t*)p.v + b * p.v_sb + kvh * p.v_sh;
   const uint16_t* dO = (const uint16_t*)p.dout + b * p.do_sb + h * p.do_sh;
-  u32x4 qf[NKS], df[NKS];
-  load_row_frags<NKS>(Q + (int64_t)qrow * p.q_ss, g, qf);
-  load_row_frags<NKS>(dO + (int64_t)qrow * p.do_ss, g, df);
-  const int64_t rix = (int64_t)bh * p.Sq + qrow;
-  const float lse = myq < p.Sq ? p.lse[rix] : INFINITY;
-  float dvc;
-  {
-    // This lane's half of the row (dims 16 ks + 8 g + 0..7), then the pair sum.
-    u32x4 of[NKS];
-    load_row_frags<NKS>((const uint16_t*)p.o + b * p.o_sb + h * p.o_sh + (int64_t)qrow * p.o_ss,
-                        g, of);
-    float part = 0.f;
-#pragma unroll
-    for (int ks = 0; ks < NKS; ++ks)
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        part += h2f<BF16>((uint16_t)(of[ks][w] & 0xffffu)) *
-                h2f<BF16>((uint16_t)(df[ks][w] & 0xffffu));
-        part += h2f<BF16>((uint16_t)(of[ks][w] >> 16)) * h2f<BF16>((uint16_t)(df[ks][w] >> 16));
-      }
-    dvc = pair_sum32(part);
-    if (g == 0 && myq < p.Sq) p.dvec[rix] = dvc;
-  }
-  // Keys this row sees: [kv_first, kv_last] (rows past Sq have lse = +inf, so
-  // their probabilities vanish without a mask).
-  const int kv_first = p.win_left >= 0 ? myq - p.win_left : -(1 << 30);
-  const int kv_last = min(p.win_right >= 0 ? myq + p.win_right : (1 << 30), p.Sk - 1);
-
-  // KV range of this workgroup's rows.
-  const int q_last = min(q0 + kBwdOwn, p.Sq) - 1;
-  const int kv_lo = p.win_left >= 0 ? max(0, q0 - p.win_left) : 0;
-  const int kv_hi = p.win_right >= 0 ? min(p.Sk, q_last + p.win_right + 1) : p.Sk;
-  const int t0 = kv_lo / kBwdTile;
-  const int n_t = kv_hi > kv_lo ? (kv_hi - 1) / kBwdTile - t0 + 1 : 0;
-
   Addr<D> ad;
   ad.init(lane);
   TileDma<D> kd, vd;
   kd.init(p.k_ss, wave, lane);
   vd.init(p.v_ss, wave, lane);
   const u32 lbase = lds_addr(lds);
-  f32x16 dq[NDB];
-#pragma unroll
-  for (int db = 0; db < NDB; ++db) dq[db] = (f32x16){};
 
-  auto load = [&](int t, int S) __attribute__((always_inline)) {
-    const int kv0 = (t0 + t) * kBwdTile;
-    kd.load(K, lbase + (2 * S) * TILE * 2, kv0, p.Sk);
-    vd.load(V, lbase + (2 * S + 1) * TILE * 2, kv0, p.Sk);
-  };
-  if (n_t > 0) {
-    wait_all();  // Q, dO fragments, lse and Dvec landed before the first DMA
-    load(0, 0);
-    wait_all();
-    stage_barrier();
-  }
-  // Step t computes stage t % 2 while tile t + 1 lands in the other stage
-  // (whose previous tile every wave finished before the last barrier).
-  for (int t = 0; t < n_t; ++t) {
-    const int S = t & 1;
-    if (t + 1 < n_t) load(t + 1, S ^ 1);
-    const int kv0 = (t0 + t) * kBwdTile;
-    // Wave-level skip of tiles outside every row's window; tiles inside every
-    // row's window and below Sk need no mask.
-    const bool skip = wq0 >= p.Sq ||
-                      (p.win_right >= 0 && kv0 > wq0 + 31 + p.win_right) ||
-                      (p.win_left >= 0 && kv0 + kBwdTile - 1 < wq0 - p.win_left);
-    const bool full = kv0 + kBwdTile <= p.Sk &&
-                      (p.win_right < 0 || kv0 + kBwdTile - 1 <= wq0 + p.win_right) &&
-                      (p.win_left < 0 || kv0 >= wq0 + 31 - p.win_left);
-    if (!skip) {
-      const uint16_t* Kt = lds + 2 * S * TILE;
-      const uint16_t* Vt = Kt + TILE;
-      // One 32-key block at a time: S^T and dP^T, then dS^T, then its dQ^T terms.
+  for (int pass = 0; pass < 2; ++pass) {
+    const int qt = pass == 0 ? n_qt - 1 - pt : pt;
+    if (pass == 1 && qt == n_qt - 1 - pt) break;  // odd n_qt: the middle tile runs alone
+    const int q0 = qt * kBwdOwn, wq0 = q0 + wave * 32, myq = wq0 + j;
+    const int qrow = min(myq, p.Sq - 1);
+    u32x4 qf[NKS], df[NKS];
+    load_row_frags<NKS>(Q + (int64_t)qrow * p.q_ss, g, qf);
+    load_row_frags<NKS>(dO + (int64_t)qrow * p.do_ss, g, df);
+    const int64_t rix = (int64_t)bh * p.Sq + qrow;
+    const float lse = myq < p.Sq ? p.lse[rix] : INFINITY;
+    float dvc;
+    {
+      // This lane's half of the row (dims 16 ks + 8 g + 0..7), then the pair sum.
+      u32x4 of[NKS];
+      load_row_frags<NKS>((const uint16_t*)p.o + b * p.o_sb + h * p.o_sh + (int64_t)qrow * p.o_ss,
+                          g, of);
+      float part = 0.f;
 #pragma unroll
-      for (int nb = 0; nb < 2; ++nb) {
-        f32x16 sb = {}, dpb = {};
+      for (int ks = 0; ks < NKS; ++ks)
 #pragma unroll
-        for (int kk = 0; kk < NKS; ++kk) {
-          const u32x4 ka = *(const u32x4*)(Kt + nb * 32 * D + ad.row[kk]);
-          const u32x4 va = *(const u32x4*)(Vt + nb * 32 * D + ad.row[kk]);
-          sb = mfma32x32x16<BF16>(ka, qf[kk], sb);
-          dpb = mfma32x32x16<BF16>(va, df[kk], dpb);
+        for (int w = 0; w < 4; ++w) {
+          part += h2f<BF16>((uint16_t)(of[ks][w] & 0xffffu)) *
+                  h2f<BF16>((uint16_t)(df[ks][w] & 0xffffu));
+          part += h2f<BF16>((uint16_t)(of[ks][w] >> 16)) * h2f<BF16>((uint16_t)(df[ks][w] >> 16));
         }
-        // Element 8h + i of the block is key kv0 + 32nb + 16h + 8g + i.
-        if (!full) {
-#pragma unroll
-          for (int e = 0; e < 16; ++e) {
-            const int key = kv0 + nb * 32 + 16 * (e >> 3) + 8 * g + (e & 7);
-            sb[e] = (key >= kv_first) & (key <= kv_last) ? sb[e] : -INFINITY;
-          }
-        }
-        // dsp[hh]: dS^T of keys 32nb + 16hh + 8g + 0..7, the B operand of k-step 2nb + hh.
-        u32x4 dsp[2];
-#pragma unroll
-        for (int hh = 0; hh < 2; ++hh)
-#pragma unroll
-          for (int e2 = 0; e2 < 4; ++e2) {
-            const int e = 8 * hh + 2 * e2;
-            const float p0 = fast_exp2(sb[e] * p.c - lse);
-            const float p1 = fast_exp2(sb[e + 1] * p.c - lse);
-            dsp[hh][e2] = pack2<BF16>(p0 * (dpb[e] - dvc), p1 * (dpb[e + 1] - dvc));
-          }
-        // dQ^T += K^T dS^T (K^T through the transposing read of the K tile).
-#pragma unroll
-        for (int db = 0; db < NDB; ++db)
-#pragma unroll
-          for (int hh = 0; hh < 2; ++hh) {
-            const int sl = 2 * nb + hh;
-            const u32x2 lo = lds_read_tr16(Kt + ad.tr[db][0] + 16 * sl * D);
-            const u32x2 hi = lds_read_tr16(Kt + ad.tr[db][1] + 16 * sl * D);
-            dq[db] = mfma32x32x16<BF16>((u32x4){lo[0], lo[1], hi[0], hi[1]}, dsp[hh], dq[db]);
-          }
-      }
+      dvc = pair_sum32(part);
+      if (g == 0 && myq < p.Sq) p.dvec[rix] = dvc;
     }
-    wait_all();
-    stage_barrier();
+    // Keys this row sees: [kv_first, kv_last] (rows past Sq have lse = +inf, so
+    // their probabilities vanish without a mask).
+    const int kv_first = p.win_left >= 0 ? myq - p.win_left : -(1 << 30);
+    const int kv_last = min(p.win_right >= 0 ? myq + p.win_right : (1 << 30), p.Sk - 1);
+
+    // KV range of this workgroup's rows.
+    const int q_last = min(q0 + kBwdOwn, p.Sq) - 1;
+    const int kv_lo = p.win_left >= 0 ? max(0, q0 - p.win_left) : 0;
+    const int kv_hi = p.win_right >= 0 ? min(p.Sk, q_last + p.win_right + 1) : p.Sk;
+    const int t0 = kv_lo / kBwdTile;
+    const int n_t = kv_hi > kv_lo ? (kv_hi - 1) / kBwdTile - t0 + 1 : 0;
+
+    f32x16 dq[NDB];
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) dq[db] = (f32x16){};
+
+    auto load = [&](int t, int S) __attribute__((always_inline)) {
+      const int kv0 = (t0 + t) * kBwdTile;
+      kd.load(K, lbase + (2 * S) * TILE * 2, kv0, p.Sk);
+      vd.load(V, lbase + (2 * S + 1) * TILE * 2, kv0, p.Sk);
+    };
+    if (n_t > 0) {
+      wait_all();  // Q, dO fragments, lse and Dvec landed before the first DMA
+      load(0, 0);
+      wait_all();
+      stage_barrier();
+    }
+    // Step t computes stage t % 2 while tile t + 1 lands in the other stage
+    // (whose previous tile every wave finished before the last barrier).
+    for (int t = 0; t < n_t; ++t) {
+      const int S = t & 1;
+      if (t + 1 < n_t) load(t + 1, S ^ 1);
+      const int kv0 = (t0 + t) * kBwdTile;
+      // Wave-level skip of tiles outside every row's window; tiles inside every
+      // row's window and below Sk need no mask.
+      const bool skip = wq0 >= p.Sq ||
+                        (p.win_right >= 0 && kv0 > wq0 + 31 + p.win_right) ||
+                        (p.win_left >= 0 && kv0 + kBwdTile - 1 < wq0 - p.win_left);
+      const bool full = kv0 + kBwdTile <= p.Sk &&
+                        (p.win_right < 0 || kv0 + kBwdTile - 1 <= wq0 + p.win_right) &&
+                        (p.win_left < 0 || kv0 >= wq0 + 31 - p.win_left);
+      if (!skip) {
+        const uint16_t* Kt = lds + 2 * S * TILE;
+        const uint16_t* Vt = Kt + TILE;
+        // One 32-key block at a time: S^T and dP^T, then dS^T, then its dQ^T terms.
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) {
+          f32x16 sb = {}, dpb = {};
+#pragma unroll
+          for (int kk = 0; kk < NKS; ++kk) {
+            const u32x4 ka = *(const u32x4*)(Kt + nb * 32 * D + ad.row[kk]);
+            const u32x4 va = *(const u32x4*)(Vt + nb * 32 * D + ad.row[kk]);
+            sb = mfma32x32x16<BF16>(ka, qf[kk], sb);
+            dpb = mfma32x32x16<BF16>(va, df[kk], dpb);
+          }
+          // Element 8h + i of the block is key kv0 + 32nb + 16h + 8g + i.
+          if (!full) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+              const int key = kv0 + nb * 32 + 16 * (e >> 3) + 8 * g + (e & 7);
+              sb[e] = (key >= kv_first) & (key <= kv_last) ? sb[e] : -INFINITY;
+            }
+          }
+          // dsp[hh]: dS^T of keys 32nb + 16hh + 8g + 0..7, the B operand of k-step 2nb + hh.
+          u32x4 dsp[2];
+#pragma unroll
+          for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+            for (int e2 = 0; e2 < 4; ++e2) {
+              const int e = 8 * hh + 2 * e2;
+              const float p0 = fast_exp2(sb[e] * p.c - lse);
+              const float p1 = fast_exp2(sb[e + 1] * p.c - lse);
+              dsp[hh][e2] = pack2<BF16>(p0 * (dpb[e] - dvc), p1 * (dpb[e + 1] - dvc));
+            }
+          // dQ^T += K^T dS^T (K^T through the transposing read of the K tile).
+#pragma unroll
+          for (int db = 0; db < NDB; ++db)
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+              const int sl = 2 * nb + hh;
+              const u32x2 lo = lds_read_tr16(Kt + ad.tr[db][0] + 16 * sl * D);
+              const u32x2 hi = lds_read_tr16(Kt + ad.tr[db][1] + 16 * sl * D);
+              dq[db] = mfma32x32x16<BF16>((u32x4){lo[0], lo[1], hi[0], hi[1]}, dsp[hh], dq[db]);
+            }
+        }
+      }
+      wait_all();
+      stage_barrier();
+    }
+    if (myq < p.Sq)
+      store_row<NDB, BF16>((uint16_t*)p.dq + b * p.dq_sb + h * p.dq_sh + (int64_t)myq * p.dq_ss,
+                           g, dq, p.scale);
   }
-  if (myq < p.Sq)
-    store_row<NDB, BF16>((uint16_t*)p.dq + b * p.dq_sb + h * p.dq_sh + (int64_t)myq * p.dq_ss,
-                         g, dq, p.scale);
 }
 
 // ---------------------------------------------------------------------------
@@ -522,32 +530,24 @@ void fa_bwd_dkdv_fused_kernel(BwdParams p) {
                 "two workgroups per CU");
 
   const int n_kt = (p.Sk + kBwdOwn - 1) / kBwdOwn;
-  int kt, bhk;  // key tile (first, under a causal mask the longest, first), (batch, K/V head)
-  grid_tile(p.B * p.H_kv, n_kt, kt, bhk);
+  // A workgroup runs key tiles pt and n_kt - 1 - pt, the longer (under a
+  // causal mask, the first) first: their step counts add up to the same total
+  // for every pair, so all workgroups carry equal work and the launch ends
+  // without a tail of long tiles that started late.
+  const int n_pair = (n_kt + 1) / 2;
+  int pt, bhk;  // tile pair, (batch, K/V head)
+  grid_tile(p.B * p.H_kv, n_pair, pt, bhk);
   const int b = bhk / p.H_kv, hk = bhk % p.H_kv;
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int j = lane & 31, g = lane >> 5;
-  const int k0 = kt * kBwdOwn, wk0 = k0 + wave * 32, mykey = wk0 + j;
-  const int krow = min(mykey, p.Sk - 1);
-  const int q_first = p.win_right >= 0 ? mykey - p.win_right : -(1 << 30);
-  const int q_last = p.win_left >= 0 ? mykey + p.win_left : (1 << 30);
 
   const uint16_t* K = (const uint16_t*)p.k + b * p.k_sb + hk * p.k_sh;
   const uint16_t* V = (const uint16_t*)p.v + b * p.v_sb + hk * p.v_sh;
-  u32x4 vf[NKS];
-  load_row_frags<NKS>(V + (int64_t)krow * p.v_ss, g, vf);
   // B operand of S: K row r = 32 wave + j (the wave's key j), k-group g of
   // step ks, at chunk (2 ks + g) ^ swz(r) = (2 ks ^ km) + kodd (computed per
   // read: an address array would push the kernel past 256 registers).
   const int kswz = swz<D>(32 * wave + j);
   const int kbase = (32 * wave + j) * D + 8 * ((g ^ kswz) & 1), km = kswz & 14;
-
-  const int k_last = min(k0 + kBwdOwn, p.Sk) - 1;
-  const int q_lo = p.win_right >= 0 ? max(0, k0 - p.win_right) : 0;
-  const int q_hi = p.win_left >= 0 ? min(p.Sq, k_last + p.win_left + 1) : p.Sq;
-  const int t0 = q_lo / kFusedTile;
-  const int n_t = q_hi > q_lo ? (q_hi - 1) / kFusedTile - t0 + 1 : 0;
-  const int n_steps = n_t * p.kv_group;
 
   // Row operands (A of S and dP): query row perm(j) of the tile, k-group g of
   // step kk, at element rbase + ((16 kk) ^ rx). Transposing reads (A of dV^T
@@ -564,144 +564,162 @@ void fa_bwd_dkdv_fused_kernel(BwdParams p) {
   for (int hf = 0; hf < 2; ++hf)
     trb[hf] = (8 * g + 4 * hf + (ts >> 2)) * D +
               8 * ((2 * thalf + ((ts & 3) >> 1)) ^ (2 * g + hf)) + 4 * (ts & 1);
-  // Visible query rows of this key: q - q_first <= span as unsigned.
-  const unsigned span = (unsigned)q_last - (unsigned)q_first;
-
   TileDma<D, kBwdOwn> kd;
   kd.init(p.k_ss, wave, lane);
   TileDma<D, kFusedTile> qd, dd;
   qd.init(p.q_ss, wave, lane);
   dd.init(p.do_ss, wave, lane);
   const u32 lbase = lds_addr(lds);
-  f32x16 dk[NDB], dv[NDB];
-#pragma unroll
-  for (int db = 0; db < NDB; ++db) {
-    dk[db] = (f32x16){};
-    dv[db] = (f32x16){};
-  }
 
-  float lse_r = 0.f, dvc_r = 0.f;  // row threadIdx.x of the tile in flight (first 32 threads)
-  // Step u covers query tile t0 + u % n_t of head hk * kv_group + u / n_t; the
-  // pair is stepped, not divided, for the tile being loaded (lt, lh) and the
-  // tile being computed (ct).
-  int lt = 0, lh = hk * p.kv_group, ct = 0;
-  auto load = [&](int S) __attribute__((always_inline)) {
-    const int row0 = (t0 + lt) * kFusedTile;
-    qd.load((const uint16_t*)p.q + b * p.q_sb + lh * p.q_sh, lbase + (2 * S) * TILE * 2, row0,
-            p.Sq);
-    dd.load((const uint16_t*)p.dout + b * p.do_sb + lh * p.do_sh,
-            lbase + (2 * S + 1) * TILE * 2, row0, p.Sq);
-    if (threadIdx.x < kFusedTile) {
-      const int r = row0 + threadIdx.x;
-      const int64_t rix = ((int64_t)b * p.H + lh) * p.Sq + r;
-      lse_r = r < p.Sq ? p.lse[rix] : INFINITY;
-      dvc_r = r < p.Sq ? p.dvec[rix] : 0.f;
-    }
-    if (++lt == n_t) {
-      lt = 0;
-      ++lh;
-    }
-  };
-  auto store_vec = [&](int S) __attribute__((always_inline)) {
-    if (threadIdx.x < kFusedTile) {
-      lse_lds[S][threadIdx.x] = lse_r;
-      dvc_lds[S][threadIdx.x] = dvc_r;
-    }
-  };
-  if (n_steps > 0) {
-    wait_all();  // V fragments landed before the first DMA
-    kd.load(K, lds_addr(ktile), k0, p.Sk);
-    load(0);
-    wait_all();
-    store_vec(0);
-    stage_barrier();
-  }
-  for (int u = 0; u < n_steps; ++u) {
-    const int S = u & 1;
-    if (u + 1 < n_steps) load(S ^ 1);
-    const int qr0 = (t0 + ct) * kFusedTile;
-    if (++ct == n_t) ct = 0;
-    const bool skip = wk0 >= p.Sk ||
-                      (p.win_right >= 0 && wk0 > qr0 + kFusedTile - 1 + p.win_right) ||
-                      (p.win_left >= 0 && wk0 + 31 < qr0 - p.win_left);
-    const bool full = (p.win_right < 0 || wk0 + 31 <= qr0 + p.win_right) &&
-                      (p.win_left < 0 || wk0 >= qr0 + kFusedTile - 1 - p.win_left);
-    if (!skip) {
-      const float* lsv = lse_lds[S];
-      const float* dvv = dvc_lds[S];
-      // (opaque copies: the addresses are recomputed every step instead of
-      // being hoisted into loop-long registers)
-      int kb = kbase, kx = km, rb = rbase + 2 * S * TILE, rxs = rx, t0b = trb[0] + 2 * S * TILE,
-          t1b = trb[1] + 2 * S * TILE, txs = tx;
-      asm volatile("" : "+v"(kb), "+v"(kx), "+v"(rb), "+v"(rxs), "+v"(t0b), "+v"(t1b), "+v"(txs));
-      // S and dP of the tile's 32 query rows (element 8h + i: query qr0 + 16h + 8g + i).
-      // The runs of products go at raised wave priority so that the other
-      // wave on the SIMD fills the gaps between them rather than the runs.
-      __builtin_amdgcn_s_setprio(1);
-      f32x16 sb = {}, dpb = {};
+  for (int pass = 0; pass < 2; ++pass) {
+    const int kt = pass == 0 ? pt : n_kt - 1 - pt;
+    if (pass == 1 && kt == pt) break;  // odd n_kt: the middle tile runs alone
+    const int k0 = kt * kBwdOwn, wk0 = k0 + wave * 32, mykey = wk0 + j;
+    const int krow = min(mykey, p.Sk - 1);
+    const int q_first = p.win_right >= 0 ? mykey - p.win_right : -(1 << 30);
+    const int q_last = p.win_left >= 0 ? mykey + p.win_left : (1 << 30);
+    // Visible query rows of this key: q - q_first <= span as unsigned.
+    const unsigned span = (unsigned)q_last - (unsigned)q_first;
+    u32x4 vf[NKS];
+    load_row_frags<NKS>(V + (int64_t)krow * p.v_ss, g, vf);
+
+    const int k_last = min(k0 + kBwdOwn, p.Sk) - 1;
+    const int q_lo = p.win_right >= 0 ? max(0, k0 - p.win_right) : 0;
+    const int q_hi = p.win_left >= 0 ? min(p.Sq, k_last + p.win_left + 1) : p.Sq;
+    const int t0 = q_lo / kFusedTile;
+    const int n_t = q_hi > q_lo ? (q_hi - 1) / kFusedTile - t0 + 1 : 0;
+    const int n_steps = n_t * p.kv_group;
+
+    f32x16 dk[NDB], dv[NDB];
 #pragma unroll
-      for (int kk = 0; kk < NKS; ++kk) {
-        const int ro = rb + ((16 * kk) ^ rxs);
-        const u32x4 qa = *(const u32x4*)(lds + ro);
-        const u32x4 ka = *(const u32x4*)(ktile + kb + 8 * ((2 * kk) ^ kx));
-        sb = mfma32x32x16<BF16>(qa, ka, sb);
-        const u32x4 da = *(const u32x4*)(lds + ro + TILE);
-        dpb = mfma32x32x16<BF16>(da, vf[kk], dpb);
+    for (int db = 0; db < NDB; ++db) {
+      dk[db] = (f32x16){};
+      dv[db] = (f32x16){};
+    }
+
+    float lse_r = 0.f, dvc_r = 0.f;  // row threadIdx.x of the tile in flight (first 32 threads)
+    // Step u covers query tile t0 + u % n_t of head hk * kv_group + u / n_t; the
+    // pair is stepped, not divided, for the tile being loaded (lt, lh) and the
+    // tile being computed (ct).
+    int lt = 0, lh = hk * p.kv_group, ct = 0;
+    auto load = [&](int S) __attribute__((always_inline)) {
+      const int row0 = (t0 + lt) * kFusedTile;
+      qd.load((const uint16_t*)p.q + b * p.q_sb + lh * p.q_sh, lbase + (2 * S) * TILE * 2, row0,
+              p.Sq);
+      dd.load((const uint16_t*)p.dout + b * p.do_sb + lh * p.do_sh,
+              lbase + (2 * S + 1) * TILE * 2, row0, p.Sq);
+      if (threadIdx.x < kFusedTile) {
+        const int r = row0 + threadIdx.x;
+        const int64_t rix = ((int64_t)b * p.H + lh) * p.Sq + r;
+        lse_r = r < p.Sq ? p.lse[rix] : INFINITY;
+        dvc_r = r < p.Sq ? p.dvec[rix] : 0.f;
       }
-      __builtin_amdgcn_s_setprio(0);
-      if (!full) {
-        const int qd0 = qr0 + 8 * g - q_first;
-#pragma unroll
-        for (int e = 0; e < 16; ++e)
-          sb[e] = (unsigned)(qd0 + 16 * (e >> 3) + (e & 7)) <= span ? sb[e] : -INFINITY;
+      if (++lt == n_t) {
+        lt = 0;
+        ++lh;
       }
-      u32x4 pp[2], dsp[2];
+    };
+    auto store_vec = [&](int S) __attribute__((always_inline)) {
+      if (threadIdx.x < kFusedTile) {
+        lse_lds[S][threadIdx.x] = lse_r;
+        dvc_lds[S][threadIdx.x] = dvc_r;
+      }
+    };
+    if (n_steps > 0) {
+      wait_all();  // V fragments landed before the first DMA
+      kd.load(K, lds_addr(ktile), k0, p.Sk);
+      load(0);
+      wait_all();
+      store_vec(0);
+      stage_barrier();
+    }
+    for (int u = 0; u < n_steps; ++u) {
+      const int S = u & 1;
+      if (u + 1 < n_steps) load(S ^ 1);
+      const int qr0 = (t0 + ct) * kFusedTile;
+      if (++ct == n_t) ct = 0;
+      const bool skip = wk0 >= p.Sk ||
+                        (p.win_right >= 0 && wk0 > qr0 + kFusedTile - 1 + p.win_right) ||
+                        (p.win_left >= 0 && wk0 + 31 < qr0 - p.win_left);
+      const bool full = (p.win_right < 0 || wk0 + 31 <= qr0 + p.win_right) &&
+                        (p.win_left < 0 || wk0 >= qr0 + kFusedTile - 1 - p.win_left);
+      if (!skip) {
+        const float* lsv = lse_lds[S];
+        const float* dvv = dvc_lds[S];
+        // (opaque copies: the addresses are recomputed every step instead of
+        // being hoisted into loop-long registers)
+        int kb = kbase, kx = km, rb = rbase + 2 * S * TILE, rxs = rx, t0b = trb[0] + 2 * S * TILE,
+            t1b = trb[1] + 2 * S * TILE, txs = tx;
+        asm volatile("" : "+v"(kb), "+v"(kx), "+v"(rb), "+v"(rxs), "+v"(t0b), "+v"(t1b), "+v"(txs));
+        // S and dP of the tile's 32 query rows (element 8h + i: query qr0 + 16h + 8g + i).
+        // The runs of products go at raised wave priority so that the other
+        // wave on the SIMD fills the gaps between them rather than the runs.
+        __builtin_amdgcn_s_setprio(1);
+        f32x16 sb = {}, dpb = {};
 #pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        const int r8 = 16 * hh + 8 * g;
-        const f32x4 l0 = *(const f32x4*)(lsv + r8);
-        const f32x4 l1 = *(const f32x4*)(lsv + r8 + 4);
-        const f32x4 d0 = *(const f32x4*)(dvv + r8);
-        const f32x4 d1 = *(const f32x4*)(dvv + r8 + 4);
-#pragma unroll
-        for (int e2 = 0; e2 < 4; ++e2) {
-          const int e = 8 * hh + 2 * e2;
-          const float lv0 = e2 < 2 ? l0[2 * e2] : l1[2 * e2 - 4];
-          const float lv1 = e2 < 2 ? l0[2 * e2 + 1] : l1[2 * e2 - 3];
-          const float dv0 = e2 < 2 ? d0[2 * e2] : d1[2 * e2 - 4];
-          const float dv1 = e2 < 2 ? d0[2 * e2 + 1] : d1[2 * e2 - 3];
-          const float p0 = fast_exp2(sb[e] * p.c - lv0);
-          const float p1 = fast_exp2(sb[e + 1] * p.c - lv1);
-          pp[hh][e2] = pack2<BF16>(p0, p1);
-          dsp[hh][e2] = pack2<BF16>(p0 * (dpb[e] - dv0), p1 * (dpb[e + 1] - dv1));
+        for (int kk = 0; kk < NKS; ++kk) {
+          const int ro = rb + ((16 * kk) ^ rxs);
+          const u32x4 qa = *(const u32x4*)(lds + ro);
+          const u32x4 ka = *(const u32x4*)(ktile + kb + 8 * ((2 * kk) ^ kx));
+          sb = mfma32x32x16<BF16>(qa, ka, sb);
+          const u32x4 da = *(const u32x4*)(lds + ro + TILE);
+          dpb = mfma32x32x16<BF16>(da, vf[kk], dpb);
         }
-      }
-      // dV^T += dO^T P and dK^T += Q^T dS (transposing reads of the tiles).
-      __builtin_amdgcn_s_setprio(1);
+        __builtin_amdgcn_s_setprio(0);
+        if (!full) {
+          const int qd0 = qr0 + 8 * g - q_first;
 #pragma unroll
-      for (int db = 0; db < NDB; ++db)
+          for (int e = 0; e < 16; ++e)
+            sb[e] = (unsigned)(qd0 + 16 * (e >> 3) + (e & 7)) <= span ? sb[e] : -INFINITY;
+        }
+        u32x4 pp[2], dsp[2];
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
-          const int o0 = t0b + ((32 * db) ^ txs) + 16 * hh * D;
-          const int o1 = t1b + ((32 * db) ^ txs) + 16 * hh * D;
-          const u32x2 dlo = lds_read_tr16(lds + o0 + TILE);
-          const u32x2 dhi = lds_read_tr16(lds + o1 + TILE);
-          dv[db] = mfma32x32x16<BF16>((u32x4){dlo[0], dlo[1], dhi[0], dhi[1]}, pp[hh], dv[db]);
-          const u32x2 qlo = lds_read_tr16(lds + o0);
-          const u32x2 qhi = lds_read_tr16(lds + o1);
-          dk[db] = mfma32x32x16<BF16>((u32x4){qlo[0], qlo[1], qhi[0], qhi[1]}, dsp[hh], dk[db]);
+          const int r8 = 16 * hh + 8 * g;
+          const f32x4 l0 = *(const f32x4*)(lsv + r8);
+          const f32x4 l1 = *(const f32x4*)(lsv + r8 + 4);
+          const f32x4 d0 = *(const f32x4*)(dvv + r8);
+          const f32x4 d1 = *(const f32x4*)(dvv + r8 + 4);
+#pragma unroll
+          for (int e2 = 0; e2 < 4; ++e2) {
+            const int e = 8 * hh + 2 * e2;
+            const float lv0 = e2 < 2 ? l0[2 * e2] : l1[2 * e2 - 4];
+            const float lv1 = e2 < 2 ? l0[2 * e2 + 1] : l1[2 * e2 - 3];
+            const float dv0 = e2 < 2 ? d0[2 * e2] : d1[2 * e2 - 4];
+            const float dv1 = e2 < 2 ? d0[2 * e2 + 1] : d1[2 * e2 - 3];
+            const float p0 = fast_exp2(sb[e] * p.c - lv0);
+            const float p1 = fast_exp2(sb[e + 1] * p.c - lv1);
+            pp[hh][e2] = pack2<BF16>(p0, p1);
+            dsp[hh][e2] = pack2<BF16>(p0 * (dpb[e] - dv0), p1 * (dpb[e + 1] - dv1));
+          }
         }
-      __builtin_amdgcn_s_setprio(0);
+        // dV^T += dO^T P and dK^T += Q^T dS (transposing reads of the tiles).
+        __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+          for (int hh = 0; hh < 2; ++hh) {
+            const int o0 = t0b + ((32 * db) ^ txs) + 16 * hh * D;
+            const int o1 = t1b + ((32 * db) ^ txs) + 16 * hh * D;
+            const u32x2 dlo = lds_read_tr16(lds + o0 + TILE);
+            const u32x2 dhi = lds_read_tr16(lds + o1 + TILE);
+            dv[db] = mfma32x32x16<BF16>((u32x4){dlo[0], dlo[1], dhi[0], dhi[1]}, pp[hh], dv[db]);
+            const u32x2 qlo = lds_read_tr16(lds + o0);
+            const u32x2 qhi = lds_read_tr16(lds + o1);
+            dk[db] = mfma32x32x16<BF16>((u32x4){qlo[0], qlo[1], qhi[0], qhi[1]}, dsp[hh], dk[db]);
+          }
+        __builtin_amdgcn_s_setprio(0);
+      }
+      wait_all();
+      if (u + 1 < n_steps) store_vec(S ^ 1);
+      stage_barrier();
     }
-    wait_all();
-    if (u + 1 < n_steps) store_vec(S ^ 1);
-    stage_barrier();
-  }
-  if (mykey < p.Sk) {
-    store_row<NDB, BF16>((uint16_t*)p.dk + b * p.dk_sb + hk * p.dk_sh + (int64_t)mykey * p.dk_ss,
-                         g, dk, p.scale);
-    store_row<NDB, BF16>((uint16_t*)p.dv + b * p.dv_sb + hk * p.dv_sh + (int64_t)mykey * p.dv_ss,
-                         g, dv, 1.f);
+    if (mykey < p.Sk) {
+      store_row<NDB, BF16>((uint16_t*)p.dk + b * p.dk_sb + hk * p.dk_sh + (int64_t)mykey * p.dk_ss,
+                           g, dk, p.scale);
+      store_row<NDB, BF16>((uint16_t*)p.dv + b * p.dv_sb + hk * p.dv_sh + (int64_t)mykey * p.dv_ss,
+                           g, dv, 1.f);
+    }
   }
 }
 
@@ -709,10 +727,12 @@ template <int D, bool BF16>
 hipError_t launch_bwd(const BwdParams& p, hipStream_t st) {
   // dQ (which also writes Dvec) before dK / dV, which reads it.
   const int n_qt = (p.Sq + kBwdOwn - 1) / kBwdOwn, n_kt = (p.Sk + kBwdOwn - 1) / kBwdOwn;
-  hipLaunchKernelGGL((fa_bwd_dq_kernel<D, BF16>), dim3(p.B * p.H * n_qt), dim3(256), 0, st, p);
+  hipLaunchKernelGGL((fa_bwd_dq_kernel<D, BF16>), dim3(p.B * p.H * ((n_qt + 1) / 2)), dim3(256),
+                     0, st, p);
   const dim3 grid_kv(p.B * p.H_kv * n_kt);
   if constexpr (D == 128) {
-    hipLaunchKernelGGL((fa_bwd_dkdv_fused_kernel<BF16>), grid_kv, dim3(256), 0, st, p);
+    const dim3 grid_pairs(p.B * p.H_kv * ((n_kt + 1) / 2));
+    hipLaunchKernelGGL((fa_bwd_dkdv_fused_kernel<BF16>), grid_pairs, dim3(256), 0, st, p);
   } else {
     hipLaunchKernelGGL((fa_bwd_dkdv_kernel<D, BF16, kBoth>), grid_kv, dim3(256), 0, st, p);
   }
