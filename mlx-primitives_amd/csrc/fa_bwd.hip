@@ -89,6 +89,15 @@ struct TileDma {
 // s_waitcnt vmcnt(0) lgkmcnt(0): every load and LDS access of this wave done.
 __device__ __forceinline__ void wait_all() { __builtin_amdgcn_s_waitcnt(0x0070); }
 
+// One 4-byte-per-lane DMA: lane l's dword lands at LDS address lds_addr + 4 l.
+// Untracked by the compiler like dma16.
+__device__ __forceinline__ void dma4(u32x4 rsrc, unsigned lds_addr, int voff) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds"
+               :
+               : "s"(lds_addr), "v"(voff), "s"(rsrc)
+               : "memory", "m0");
+}
+
 // Per-lane LDS element offsets into a swizzled (64, D) tile. row[ks]: A
 // operand rows 32*nb + perm(j), k-step ks (add nb * 32 * D). tr[db][hf]: the
 // transposing read for A = X^T over rows 16*sl + 8g + 4hf + s/4, columns
@@ -272,6 +281,7 @@ void fa_bwd_dq_kernel(BwdParams p) {
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb) {
           f32x16 sb = {}, dpb = {};
+          __builtin_amdgcn_s_setprio(1);
 #pragma unroll
           for (int kk = 0; kk < NKS; ++kk) {
             const u32x4 ka = *(const u32x4*)(Kt + nb * 32 * D + ad.row[kk]);
@@ -279,6 +289,7 @@ void fa_bwd_dq_kernel(BwdParams p) {
             sb = mfma32x32x16<BF16>(ka, qf[kk], sb);
             dpb = mfma32x32x16<BF16>(va, df[kk], dpb);
           }
+          __builtin_amdgcn_s_setprio(0);
           // Element 8h + i of the block is key kv0 + 32nb + 16h + 8g + i.
           if (!full) {
 #pragma unroll
@@ -524,9 +535,10 @@ void fa_bwd_dkdv_fused_kernel(BwdParams p) {
   __shared__ __align__(1024) uint16_t ktile[kBwdOwn * D];
   // Stage s: Q tile at [2s], dO tile at [2s + 1].
   __shared__ __align__(1024) uint16_t lds[4 * TILE];
-  __shared__ __align__(16) float lse_lds[2][kFusedTile];
-  __shared__ __align__(16) float dvc_lds[2][kFusedTile];
-  static_assert(sizeof(ktile) + sizeof(lds) + sizeof(lse_lds) + sizeof(dvc_lds) <= 80 * 1024,
+  // Stage s: lse of the tile's rows at [s][0], Dvec at [s][1], one 64-lane DMA
+  // each (the second half holds the 32 rows after the tile, unused).
+  __shared__ __align__(16) float vec_lds[2][2][64];
+  static_assert(sizeof(ktile) + sizeof(lds) + sizeof(vec_lds) <= 80 * 1024,
                 "two workgroups per CU");
 
   const int n_kt = (p.Sk + kBwdOwn - 1) / kBwdOwn;
@@ -537,7 +549,9 @@ void fa_bwd_dkdv_fused_kernel(BwdParams p) {
   const int n_pair = (n_kt + 1) / 2;
   int pt, bhk;  // tile pair, (batch, K/V head)
   grid_tile(p.B * p.H_kv, n_pair, pt, bhk);
-  const int b = bhk / p.H_kv, hk = bhk % p.H_kv;
+  // (scalar: the lse / Dvec DMA descriptors are built from them)
+  const int b = __builtin_amdgcn_readfirstlane(bhk / p.H_kv);
+  const int hk = __builtin_amdgcn_readfirstlane(bhk % p.H_kv);
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int j = lane & 31, g = lane >> 5;
 
@@ -576,10 +590,14 @@ void fa_bwd_dkdv_fused_kernel(BwdParams p) {
     if (pass == 1 && kt == pt) break;  // odd n_kt: the middle tile runs alone
     const int k0 = kt * kBwdOwn, wk0 = k0 + wave * 32, mykey = wk0 + j;
     const int krow = min(mykey, p.Sk - 1);
-    const int q_first = p.win_right >= 0 ? mykey - p.win_right : -(1 << 30);
-    const int q_last = p.win_left >= 0 ? mykey + p.win_left : (1 << 30);
-    // Visible query rows of this key: q - q_first <= span as unsigned.
-    const unsigned span = (unsigned)q_last - (unsigned)q_first;
+    // Visible query rows of this key, cut at Sq (rows past it are clamped
+    // copies with a real row's lse): q - q_first <= span as unsigned (no row
+    // at all: q_first = 2^30, span 0).
+    const int q_lo_key = p.win_right >= 0 ? mykey - p.win_right : -(1 << 30);
+    const int q_last = min(p.win_left >= 0 ? mykey + p.win_left : (1 << 30), p.Sq - 1);
+    const bool no_row = q_last < q_lo_key;
+    const int q_first = no_row ? (1 << 30) : q_lo_key;
+    const unsigned span = no_row ? 0u : (unsigned)q_last - (unsigned)q_first;
     u32x4 vf[NKS];
     load_row_frags<NKS>(V + (int64_t)krow * p.v_ss, g, vf);
 
@@ -597,32 +615,24 @@ void fa_bwd_dkdv_fused_kernel(BwdParams p) {
       dv[db] = (f32x16){};
     }
 
-    float lse_r = 0.f, dvc_r = 0.f;  // row threadIdx.x of the tile in flight (first 32 threads)
     // Step u covers query tile t0 + u % n_t of head hk * kv_group + u / n_t; the
     // pair is stepped, not divided, for the tile being loaded (lt, lh) and the
-    // tile being computed (ct).
+    // tile being computed (ct). Waves 0 and 1 also bring the tile's lse and
+    // Dvec rows (clamped at Sq) into LDS.
     int lt = 0, lh = hk * p.kv_group, ct = 0;
     auto load = [&](int S) __attribute__((always_inline)) {
       const int row0 = (t0 + lt) * kFusedTile;
+      if (wave < 2) {
+        const float* src = (wave == 0 ? p.lse : p.dvec) + ((int64_t)b * p.H + lh) * p.Sq;
+        dma4(buffer_desc(src), lds_addr(vec_lds[S][wave]), min(row0 + lane, p.Sq - 1) * 4);
+      }
       qd.load((const uint16_t*)p.q + b * p.q_sb + lh * p.q_sh, lbase + (2 * S) * TILE * 2, row0,
               p.Sq);
       dd.load((const uint16_t*)p.dout + b * p.do_sb + lh * p.do_sh,
               lbase + (2 * S + 1) * TILE * 2, row0, p.Sq);
-      if (threadIdx.x < kFusedTile) {
-        const int r = row0 + threadIdx.x;
-        const int64_t rix = ((int64_t)b * p.H + lh) * p.Sq + r;
-        lse_r = r < p.Sq ? p.lse[rix] : INFINITY;
-        dvc_r = r < p.Sq ? p.dvec[rix] : 0.f;
-      }
       if (++lt == n_t) {
         lt = 0;
         ++lh;
-      }
-    };
-    auto store_vec = [&](int S) __attribute__((always_inline)) {
-      if (threadIdx.x < kFusedTile) {
-        lse_lds[S][threadIdx.x] = lse_r;
-        dvc_lds[S][threadIdx.x] = dvc_r;
       }
     };
     if (n_steps > 0) {
@@ -630,7 +640,6 @@ void fa_bwd_dkdv_fused_kernel(BwdParams p) {
       kd.load(K, lds_addr(ktile), k0, p.Sk);
       load(0);
       wait_all();
-      store_vec(0);
       stage_barrier();
     }
     for (int u = 0; u < n_steps; ++u) {
@@ -641,11 +650,12 @@ void fa_bwd_dkdv_fused_kernel(BwdParams p) {
       const bool skip = wk0 >= p.Sk ||
                         (p.win_right >= 0 && wk0 > qr0 + kFusedTile - 1 + p.win_right) ||
                         (p.win_left >= 0 && wk0 + 31 < qr0 - p.win_left);
-      const bool full = (p.win_right < 0 || wk0 + 31 <= qr0 + p.win_right) &&
+      const bool full = qr0 + kFusedTile <= p.Sq &&
+                        (p.win_right < 0 || wk0 + 31 <= qr0 + p.win_right) &&
                         (p.win_left < 0 || wk0 >= qr0 + kFusedTile - 1 - p.win_left);
       if (!skip) {
-        const float* lsv = lse_lds[S];
-        const float* dvv = dvc_lds[S];
+        const float* lsv = vec_lds[S][0];
+        const float* dvv = vec_lds[S][1];
         // (opaque copies: the addresses are recomputed every step instead of
         // being hoisted into loop-long registers)
         int kb = kbase, kx = km, rb = rbase + 2 * S * TILE, rxs = rx, t0b = trb[0] + 2 * S * TILE,
@@ -711,7 +721,6 @@ void fa_bwd_dkdv_fused_kernel(BwdParams p) {
         __builtin_amdgcn_s_setprio(0);
       }
       wait_all();
-      if (u + 1 < n_steps) store_vec(S ^ 1);
       stage_barrier();
     }
     if (mykey < p.Sk) {
