@@ -884,6 +884,16 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& pin, const Wor
   // tile_ok_next / tile_ok: every page a key of the staged / computed tile
   // lies in is valid (else compute_tile checks each key against the table).
   static_assert(!kScalarPages || NST == 2, "paged 128-key tiles use two stages");
+  int pg_idx[NDMA];
+  u32 pg_in[NDMA];
+  if constexpr (kScalarPages) {
+#pragma unroll
+    for (int r = 0; r < NDMA; ++r) {
+      const int row = RPD * wave + RSTEP * r;  // row of the tile instruction r starts at
+      pg_idx[r] = row >> p.bs_log2;
+      pg_in[r] = (u32)(row & ((1 << p.bs_log2) - 1)) * (u32)p.k_ss * 2u;
+    }
+  }
   int pg_cur = 0;
   bool tile_ok = true, tile_ok_next = true;
   auto fetch_pages = [&](int kv0) __attribute__((always_inline)) {
@@ -904,19 +914,16 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& pin, const Wor
         const int npg = ((min(kv0 + BN, p.Sk) - 1) >> p.bs_log2) - pg0 + 1;
         tile_ok_next = !__any((lane < npg) & ((pg_cur < 0) | (pg_cur >= p.num_blocks)));
       }
-      int pg_next[NDMA];
-#pragma unroll
-      for (int r = 0; r < NDMA; ++r)
-        pg_next[r] = __builtin_amdgcn_readlane(
-            pg_cur, ((kv0 + RPD * wave + RSTEP * r) >> p.bs_log2) - pg0);
       if ((!kChecked || tile_ok_next) && kv0 + BN <= p.Sk) {
         // Every row exists: the page part of the offset is uniform (row
         // RPD * wave + RSTEP * r of the tile, in the scalar offset); the lane
-        // part (row lr % RPD, chunk) is fixed.
+        // part (row lr % RPD, chunk) is fixed. The tile starts on a page
+        // boundary, so instruction r reads page entry pg_idx[r] at in-page
+        // byte offset pg_in[r], both fixed for the kernel.
+        const u32 pg_bytes = (u32)pg_cur * (row_bytes << p.bs_log2);
 #pragma unroll
         for (int r = 0; r < NDMA; ++r) {
-          const int row0 = kv0 + RPD * wave + RSTEP * r;
-          const u32 soff = (((u32)pg_next[r] << p.bs_log2) + (u32)(row0 & bmask)) * row_bytes;
+          const u32 soff = __builtin_amdgcn_readlane(pg_bytes, pg_idx[r]) + pg_in[r];
           dma16(krs, kdst + r * RSTEP * ROWB, klane, (int)soff);
           dma16(vrs, vdst + r * RSTEP * ROWB, vlane, (int)soff);
         }
@@ -924,7 +931,8 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& pin, const Wor
       }
 #pragma unroll
       for (int r = 0; r < NDMA; ++r) {
-        const int page = pg_next[r];
+        const int page = __builtin_amdgcn_readlane(
+            pg_cur, ((kv0 + RPD * wave + RSTEP * r) >> p.bs_log2) - pg0);
         const int pos = kv0 + lr + RSTEP * r;
         const bool ok = pos < p.Sk && page >= 0 && page < p.num_blocks;
         const u32 base = (((u32)page << p.bs_log2) + (u32)(pos & bmask)) * row_bytes;
@@ -1684,7 +1692,9 @@ struct Plan {
 // table a step ahead) when pages are a power of two of at least the 4 rows one
 // DMA instruction of a wave stages, and no ALiBi bias is given.
 bool paged_wide_tiles(int D, int dtype, int bs_log2, bool alibi) {
-  return MPX_FA_DIRECT && dtype != MPX_F32 && D == 128 && bs_log2 >= 2 && !alibi;
+  // Page sizes 4 .. 128 divide the tile: every tile starts on a page boundary.
+  return MPX_FA_DIRECT && dtype != MPX_F32 && D == 128 && bs_log2 >= 2 && bs_log2 <= 7 &&
+         !alibi;
 }
 
 // Keys per KV tile (the D = 32 16-bit kernels, and the paged ones at other
