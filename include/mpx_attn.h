@@ -180,6 +180,30 @@ int mpx_kv_append(const void* k, const void* v, void* k_pool, void* v_pool,
                   int dtype, int32_t* errors, void* stream);
 
 /*
+ * mpx_kv_append with each K row rotated to its position on the way into the
+ * pool (half-split RoPE over the contiguous (n_pos, D/2) cos / sin tables of
+ * cache_dtype, float32 arithmetic, one rounding: the same values as mpx_rope
+ * followed by mpx_kv_append); V rows are copied. errors holds 4 words: the 3
+ * of mpx_kv_append and [3] = 1 for a position at or past n_pos (token
+ * skipped). D must be a multiple of 16, rows 16-byte aligned.
+ *
+ * Replaces the K side of the reference's fused kernel, which rotates K at
+ * kv_offset + j every time it attends (mlx_primitives/kernels/
+ * fused_rope_attention.py:766-800, 939-987): a cache written through this
+ * entry point holds K already rotated, so the attention that reads it rotates
+ * only Q (mpx_rope_at, or Q-on-load in mpx_attn_fwd_rope). Together with
+ * KVCache._store_kv (mlx_primitives/cache/kv_cache.py:194-264) as in
+ * mpx_kv_append.
+ */
+int mpx_kv_append_rope(const void* k, const void* v, void* k_pool, void* v_pool,
+                       const int32_t* block_tables, const int32_t* start_pos,
+                       const int32_t* n_tokens, const int64_t* k_strides,
+                       const int64_t* v_strides, int B, int T, int H, int D, int num_blocks,
+                       int block_size, int max_blocks, int dtype, const void* cos_cache,
+                       const void* sin_cache, int n_pos, int cache_dtype, int32_t* errors,
+                       void* stream);
+
+/*
  * Grouped-query variants (no counterpart in the reference, whose flash_attention
  * rejects Hq != Hk at mlx_primitives/attention/flash.py:151-154 and whose paged
  * pools carry the query heads; an extension behind the Python flag enable_gqa):
@@ -231,6 +255,22 @@ int mpx_paged_prefill_gqa(const void* q, const void* k_pool, const void* v_pool,
 int mpx_rope(const void* x, void* out, const void* cos_cache, const void* sin_cache,
              const int64_t* x_strides, const int64_t* out_strides, int B, int S, int H, int D,
              int offset, int n_pos, int dtype, int cache_dtype, void* stream);
+
+/*
+ * mpx_rope with a position per sequence: row s of batch b is rotated to
+ * position positions[b] + s (positions: device int32 (B,)). Rows whose position
+ * falls outside [0, n_pos) are left unwritten and set errors[0] = 1 (device
+ * int32 word, cleared by the caller).
+ *
+ * Replaces rope(x, cos_cache, sin_cache, offset) (mlx_primitives/kernels/rope.py:451-497)
+ * applied to each sequence of a decode batch at its own offset, as a serving
+ * loop rotates every sequence's new query at the position it has reached
+ * (mlx_primitives/kernels/fused_rope_attention.py:766-800: q_offset per call).
+ */
+int mpx_rope_at(const void* x, void* out, const void* cos_cache, const void* sin_cache,
+                const int64_t* x_strides, const int64_t* out_strides, int B, int S, int H,
+                int D, const int32_t* positions, int n_pos, int dtype, int cache_dtype,
+                int32_t* errors, void* stream);
 
 /*
  * mpx_attn_fwd_gqa with Q rotated on load: query row i is rotated to position

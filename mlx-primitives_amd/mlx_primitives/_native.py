@@ -137,6 +137,20 @@ def load() -> ctypes.CDLL:
             ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
             ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
         ]
+        lib.mpx_rope_at.restype = ctypes.c_int
+        lib.mpx_rope_at.argtypes = [
+            ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, _i64p, _i64p,
+            ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_int,
+            ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p,
+        ]
+        lib.mpx_kv_append_rope.restype = ctypes.c_int
+        lib.mpx_kv_append_rope.argtypes = [
+            ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+            ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, _i64p, _i64p,
+            ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+            ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
+            ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p,
+        ]
         lib.mpx_kv_append.restype = ctypes.c_int
         lib.mpx_kv_append.argtypes = [
             ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
@@ -330,6 +344,39 @@ def kv_append(k: torch.Tensor, v: torch.Tensor, k_pool: torch.Tensor, v_pool: to
         _strides(k_strides), _strides(v_strides), B, T, H, D, num_blocks, block_size, max_blocks,
         dtype_code(k_pool.dtype), errors.data_ptr(), _stream_ptr(dev))
     _check(rc, "mpx_kv_append failed")
+
+
+def kv_append_rope(k: torch.Tensor, v: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
+                   block_tables: torch.Tensor, start_pos: torch.Tensor, n_tokens: torch.Tensor,
+                   errors: torch.Tensor, k_strides: Sequence[int], v_strides: Sequence[int],
+                   B: int, T: int, H: int, D: int, num_blocks: int, block_size: int,
+                   max_blocks: int, cos_cache: torch.Tensor, sin_cache: torch.Tensor) -> None:
+    """Enqueue mpx_kv_append_rope on the current stream (strides in (b, t, h) order)."""
+    lib = load()
+    dev = require_device(k, v, k_pool, v_pool, block_tables, start_pos, n_tokens, errors,
+                         cos_cache, sin_cache)
+    rc = lib.mpx_kv_append_rope(
+        k.data_ptr(), v.data_ptr(), k_pool.data_ptr(), v_pool.data_ptr(),
+        block_tables.data_ptr(), start_pos.data_ptr(), n_tokens.data_ptr(),
+        _strides(k_strides), _strides(v_strides), B, T, H, D, num_blocks, block_size, max_blocks,
+        dtype_code(k_pool.dtype), cos_cache.data_ptr(), sin_cache.data_ptr(),
+        cos_cache.shape[0], dtype_code(cos_cache.dtype), errors.data_ptr(), _stream_ptr(dev))
+    _check(rc, "mpx_kv_append_rope failed")
+
+
+def rope_at(x: torch.Tensor, out: torch.Tensor, cos_cache: torch.Tensor, sin_cache: torch.Tensor,
+            positions: torch.Tensor, errors: torch.Tensor) -> None:
+    """Enqueue mpx_rope_at on the current stream: row s of batch b at positions[b] + s."""
+    lib = load()
+    dev = require_device(x, out, cos_cache, sin_cache, positions, errors)
+    B, S, H, D = x.shape
+    rc = lib.mpx_rope_at(
+        x.data_ptr(), out.data_ptr(), cos_cache.data_ptr(), sin_cache.data_ptr(),
+        _strides((x.stride(0), x.stride(1), x.stride(2))),
+        _strides((out.stride(0), out.stride(1), out.stride(2))),
+        B, S, H, D, positions.data_ptr(), cos_cache.shape[0], dtype_code(x.dtype),
+        dtype_code(cos_cache.dtype), errors.data_ptr(), _stream_ptr(dev))
+    _check(rc, "mpx_rope_at failed")
 
 
 def rope(x: torch.Tensor, out: torch.Tensor, cos_cache: torch.Tensor, sin_cache: torch.Tensor,

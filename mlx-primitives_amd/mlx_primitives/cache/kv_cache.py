@@ -92,6 +92,13 @@ class CacheMemoryStats:
         return self.used_bytes / (1024 * 1024)
 
 
+def _check_rope_positions(rope: Tuple[torch.Tensor, torch.Tensor], end: int) -> None:
+    """Positions below `end` must have rows in the RoPE tables."""
+    if end > rope[0].shape[0]:
+        raise ValueError(f"RoPE position {end - 1} is past the cos/sin tables' "
+                         f"{rope[0].shape[0]} rows")
+
+
 class KVCache:
     """Per-layer paged K/V storage with sequences that grow, fork and shrink."""
 
@@ -145,7 +152,8 @@ class KVCache:
         return uid
 
     def _store_kv(self, user_seq_id: int, k: torch.Tensor, v: torch.Tensor, layer_idx: int,
-                  start_position: Optional[int] = None) -> None:
+                  start_position: Optional[int] = None,
+                  rope: Optional[Tuple[torch.Tensor, torch.Tensor]] = None) -> None:
         """Write k, v (seq_len, heads, dim) at write_start = start_position, or
         num_tokens - seq_len (the tokens extend_sequence just counted), page by
         page through the sequence's table (kv_cache.py:194-264): ValueError for
@@ -164,12 +172,14 @@ class KVCache:
         bs = self._config.block_size
         capacity = len(meta.block_table) * bs
         fit = max(0, min(seq_len, capacity - write_start))
+        if rope is not None:
+            _check_rope_positions(rope, write_start + fit)
         if fit > 0:
             pt.make_writable(lsid, write_start // bs, (write_start + fit - 1) // bs)
             table = pt.get_block_table_tensor([lsid])
             k_pool, v_pool = self._allocators[layer_idx].get_pools()
             kv_store.store_kv(k_pool, v_pool, table, k[:fit][None], v[:fit][None], write_start,
-                              check=False)
+                              check=False, rope=rope)
         if fit < seq_len:
             block_idx = (write_start + fit) // bs
             raise RuntimeError(
@@ -177,13 +187,20 @@ class KVCache:
                 f"Have {len(meta.block_table)} blocks for {meta.num_tokens} tokens.")
 
     def update(self, sequence_id: int, k: torch.Tensor, v: torch.Tensor, layer_idx: int,
-               position: Optional[int] = None) -> None:
+               position: Optional[int] = None, *,
+               rope: Optional[Tuple[torch.Tensor, torch.Tensor]] = None) -> None:
         """Append k, v (new_tokens, heads, dim) to a sequence, or with
         `position` truncate to it first and write there (speculative-decoding
-        rollback) (kv_cache.py:266-304)."""
+        rollback) (kv_cache.py:266-304).
+
+        rope (keyword-only extension): (cos_cache, sin_cache); K is stored
+        rotated to each token's position in the sequence (store_kv)."""
         lsid = self._layer_id(sequence_id, layer_idx)
         self._notify("on_access", sequence_id)
         pt = self._page_tables[layer_idx]
+        if rope is not None:
+            first = pt.get_sequence_metadata(lsid).num_tokens if position is None else position
+            _check_rope_positions(rope, first + k.shape[0])
         if position is None:
             if k.shape[0] == 0:
                 return
@@ -191,18 +208,20 @@ class KVCache:
         else:
             pt.truncate_sequence(lsid, position)
             pt.extend_sequence(lsid, k.shape[0])
-        self._store_kv(sequence_id, k, v, layer_idx)
+        self._store_kv(sequence_id, k, v, layer_idx, rope=rope)
 
     def update_batch(self, sequence_ids: Sequence[int], k: torch.Tensor, v: torch.Tensor,
                      layer_idx: int, num_tokens: Optional[Sequence[int]] = None,
-                     errors: Optional[torch.Tensor] = None) -> None:
+                     errors: Optional[torch.Tensor] = None,
+                     rope: Optional[Tuple[torch.Tensor, torch.Tensor]] = None) -> None:
         """Append to several sequences with one kernel launch (a serving step).
 
         k, v: (batch, T, heads, dim); num_tokens: tokens of each row to append
         (default T, ragged appends otherwise). Equivalent to calling update for
-        each sequence in turn; `errors` (int32 (3,), device) receives the
-        kernel's error words instead of a temporary (they stay zero: every
-        position written here was allocated just before)."""
+        each sequence in turn; `errors` (int32 (3,), device; (4,) with rope)
+        receives the kernel's error words instead of a temporary (they stay
+        zero: every position written here was allocated just before, and
+        checked against the rope tables). rope: as in update."""
         if k.ndim != 4 or v.shape != k.shape or k.shape[0] != len(sequence_ids):
             raise ValueError(f"k and v must be (len(sequence_ids), T, heads, dim), got "
                              f"{tuple(k.shape)} and {tuple(v.shape)}")
@@ -211,6 +230,10 @@ class KVCache:
             raise ValueError(f"num_tokens must give 0..{k.shape[1]} tokens per sequence")
         pt = self._page_tables[layer_idx]
         bs = self._config.block_size
+        if rope is not None:
+            _check_rope_positions(rope, max(
+                pt.get_sequence_metadata(self._layer_id(sid, layer_idx)).num_tokens + n
+                for sid, n in zip(sequence_ids, counts)))
         lsids, starts = [], []
         for sid, n in zip(sequence_ids, counts):
             lsid = self._layer_id(sid, layer_idx)
@@ -229,7 +252,7 @@ class KVCache:
         kv_store.store_kv(k_pool, v_pool, tables, k, v,
                           torch.tensor(starts, dtype=torch.int32).to(dev),
                           torch.tensor(counts, dtype=torch.int32).to(dev), check=False,
-                          errors=errors)
+                          errors=errors, rope=rope)
 
     def get_kv(self, sequence_id: int, layer_idx: int) -> Tuple[torch.Tensor, torch.Tensor]:
         """All cached K, V of a sequence, materialized (num_tokens, heads, dim)."""

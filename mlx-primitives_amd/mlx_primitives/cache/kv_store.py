@@ -11,7 +11,7 @@ owns, eviction, copy-on-write) stays with the caller.
 
 from __future__ import annotations
 
-from typing import Optional, Union
+from typing import Optional, Tuple, Union
 
 import torch
 
@@ -28,7 +28,10 @@ def _i32(x, device, n: int, what: str) -> torch.Tensor:
 
 
 def _raise_errors(flags) -> None:
-    neg, past, bad = (int(x) for x in flags)
+    neg, past, bad = (int(x) for x in flags[:3])
+    if len(flags) > 3 and int(flags[3]):
+        raise ValueError("RoPE position out of range: a token's position lies past the "
+                         "cos/sin tables")
     if neg:
         raise ValueError("Invalid write_start position: a start position is negative")
     if past:
@@ -48,6 +51,7 @@ def store_kv(
     num_tokens: Optional[Union[int, torch.Tensor]] = None,
     check: bool = True,
     errors: Optional[torch.Tensor] = None,
+    rope: Optional[Tuple[torch.Tensor, torch.Tensor]] = None,
 ) -> Optional[torch.Tensor]:
     """Write new tokens into their pages, in place.
 
@@ -69,6 +73,13 @@ def store_kv(
     (cleared by a fill kernel, then set by the append kernel), so that a call
     allocates nothing, e.g. inside a captured HIP graph; without it a
     temporary is allocated per call.
+
+    rope (keyword-only extension): (cos_cache, sin_cache) tables as built by
+    precompute_rope_cache, (positions, dim // 2). Each K token is stored
+    rotated to its position p (the values rope(k, cos, sin, p) gives, in the
+    same kernel that writes the pages), V as given, so attention over the
+    cache rotates only its queries. The error words are then 4, the fourth
+    set for a position at or past the tables' rows (ValueError with check).
     """
     if k.ndim == 3:
         k, v = k[None], v[None]
@@ -107,17 +118,35 @@ def store_kv(
             return x.contiguous()
         return x
     k, v = fit(k), fit(v)
+    n_err = 3 if rope is None else 4
+    if rope is not None:
+        cos_cache, sin_cache = rope
+        if (cos_cache.shape != sin_cache.shape or cos_cache.ndim != 2
+                or cos_cache.shape[1] != dim // 2):
+            raise ValueError(
+                f"rope cos/sin caches must both be (positions, {dim // 2}); got "
+                f"{tuple(cos_cache.shape)} and {tuple(sin_cache.shape)}")
+        if dim % 16:
+            raise NotImplementedError(
+                f"store_kv(rope=...): head_dim must be a multiple of 16, got {dim}")
+        _native.require_device(cos_cache, sin_cache)
+        cos_cache, sin_cache = cos_cache.contiguous(), sin_cache.contiguous()
     if errors is None:
-        errors = torch.zeros(3, dtype=torch.int32, device=dev)
+        errors = torch.zeros(n_err, dtype=torch.int32, device=dev)
     else:
-        if (errors.dtype != torch.int32 or errors.numel() != 3 or errors.device != dev
+        if (errors.dtype != torch.int32 or errors.numel() != n_err or errors.device != dev
                 or not errors.is_contiguous()):
-            raise ValueError("errors must be a contiguous int32 tensor of 3 entries on the "
-                             "pools' device")
+            raise ValueError(f"errors must be a contiguous int32 tensor of {n_err} entries on "
+                             "the pools' device")
         errors.zero_()
-    _native.kv_append(k, v, k_pool, v_pool, tables, starts, counts, errors, k.stride()[:3],
-                      v.stride()[:3], batch, T, heads, dim, num_blocks, block_size,
-                      tables.shape[1])
+    if rope is None:
+        _native.kv_append(k, v, k_pool, v_pool, tables, starts, counts, errors, k.stride()[:3],
+                          v.stride()[:3], batch, T, heads, dim, num_blocks, block_size,
+                          tables.shape[1])
+    else:
+        _native.kv_append_rope(k, v, k_pool, v_pool, tables, starts, counts, errors,
+                               k.stride()[:3], v.stride()[:3], batch, T, heads, dim, num_blocks,
+                               block_size, tables.shape[1], cos_cache, sin_cache)
     if not check:
         return errors
     _raise_errors(errors.tolist())

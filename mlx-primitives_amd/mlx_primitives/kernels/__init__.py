@@ -5,11 +5,12 @@ from mlx_primitives.kernels.fused_rope_attention import (
     fast_fused_rope_attention,
     fused_rope_attention,
 )
-from mlx_primitives.kernels.rope import precompute_rope_cache, rope
+from mlx_primitives.kernels.rope import precompute_rope_cache, rope, rope_at
 
 __all__ = [
     "precompute_rope_cache",
     "rope",
+    "rope_at",
     "fused_rope_attention",
     "fast_fused_rope_attention",
     "FusedRoPEFlashAttention",

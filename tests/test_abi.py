@@ -33,7 +33,8 @@ def test_header_declares_expected_entry_points():
         "mpx_paged_decode", "mpx_paged_decode_workspace_bytes", "mpx_paged_prefill",
         "mpx_paged_prefill_workspace_bytes", "mpx_kv_append", "mpx_rope", "mpx_attn_fwd_gqa",
         "mpx_paged_decode_gqa", "mpx_paged_prefill_gqa", "mpx_attn_fwd_lse", "mpx_attn_bwd",
-        "mpx_attn_bwd_workspace_bytes", "mpx_attn_fwd_rope", "mpx_paged_decode_noalloc"])
+        "mpx_attn_bwd_workspace_bytes", "mpx_attn_fwd_rope", "mpx_paged_decode_noalloc",
+        "mpx_rope_at", "mpx_kv_append_rope"])
 
 
 def test_library_exports_every_declared_symbol(lib):
@@ -146,6 +147,26 @@ def test_rope_validation(lib):
     assert _rope(lib, offset=3) == _native.MPX_EINVAL and b"exceed" in lib.mpx_last_error()
     assert _rope(lib, ptr=24) == _native.MPX_EINVAL and b"aligned" in lib.mpx_last_error()
     assert _rope(lib, S=0) == _native.MPX_OK and lib.mpx_last_error() == b""
+
+
+def test_rope_at_and_append_rope_validation(lib):
+    st = (ctypes.c_int64 * 3)(8 * 4 * 128, 4 * 128, 128)
+    rc = lib.mpx_rope_at(16, 16, 16, 16, st, st, 1, 8, 4, 72, 16, 8, 2, 2, 16, None)
+    assert rc == _native.MPX_EINVAL and b"multiple of 16" in lib.mpx_last_error()
+    rc = lib.mpx_rope_at(16, 16, 16, 16, st, st, 1, 8, 4, 128, None, 8, 2, 2, 16, None)
+    assert rc == _native.MPX_EINVAL and b"null" in lib.mpx_last_error()
+    rc = lib.mpx_rope_at(16, 16, 16, 16, st, st, 0, 8, 4, 128, None, 8, 2, 2, None, None)
+    assert rc == _native.MPX_OK
+    kst = (ctypes.c_int64 * 3)(8 * 4 * 128, 4 * 128, 128)
+    rc = lib.mpx_kv_append_rope(16, 16, 16, 16, 16, 16, 16, kst, kst, 1, 8, 4, 128, 4, 16, 4, 2,
+                                24, 16, 64, 2, 16, None)
+    assert rc == _native.MPX_EINVAL and b"aligned" in lib.mpx_last_error()
+    rc = lib.mpx_kv_append_rope(16, 16, 16, 16, 16, 16, 16, kst, kst, 1, 8, 4, 128, 4, 0, 4, 2,
+                                16, 16, 64, 2, 16, None)
+    assert rc == _native.MPX_EINVAL and b"block_size" in lib.mpx_last_error()
+    rc = lib.mpx_kv_append_rope(16, 16, 16, 16, 16, 16, 16, kst, kst, 1, 8, 4, 128, 4, 16, 4, 5,
+                                16, 16, 64, 2, 16, None)
+    assert rc == _native.MPX_EINVAL and b"dtype" in lib.mpx_last_error()
 
 
 def test_gqa_head_counts_validated(lib):
