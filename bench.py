@@ -566,6 +566,22 @@ def main() -> int:
     c_gbs = 4.0 * ainp.k.numel() * ainp.k.element_size() / (c_ev * 1e-3) / 1e9
     del kdst, vdst
     log(f"[bench] {aname}: device-to-device copy of the same bytes {c_gbs:.1f} GB/s")
+    # The same append with K rotated to each token's position on the way in
+    # (store_kv rope=...): the bytes above plus the cos / sin rows it reads.
+    from mlx_primitives.cache import store_kv
+    from mlx_primitives.kernels import precompute_rope_cache
+    aB, aT, _, aD = ainp.k.shape
+    rcos, rsin = precompute_rope_cache(aT, aD, device=dev)
+    rerr = torch.zeros(4, dtype=torch.int32, device=dev)
+    rcounts = torch.full((aB,), aT, dtype=torch.int32, device=dev)
+    arstep = lambda: store_kv(ainp.k_pool, ainp.v_pool, ainp.block_tables, ainp.k, ainp.v,
+                              ainp.start_pos, rcounts, check=False, errors=rerr,
+                              rope=(rcos, rsin))
+    _, ar_ev, _, _ = time_steps(arstep, args.steps, args.warmup)
+    if rerr.tolist() != [0, 0, 0, 0]:
+        raise RuntimeError(f"kv append with rope reported errors {rerr.tolist()}")
+    ar_gbs = abytes / (ar_ev * 1e-3) / 1e9
+    log(f"[bench] {aname}: with K rotated on the way in {ar_ev:.3f} ms -> {ar_gbs:.1f} GB/s")
 
     # ---- fused RoPE + flash, bf16 BSHD (rotation kernels + attention) ----------------
     rstep = rope_attention_step(dev)
@@ -702,6 +718,8 @@ def main() -> int:
                          "frac": a_gbs / PEAK_HBM_GBS, "traffic": measured_traffic(aname),
                          "kernel": APPEND_KERNEL, "traffic_unit": "bytes per launch"},
             "d2d_copy_same_bytes_gbs": c_gbs,
+            "with_rope": {"kernel": "kv_append_rope_kernel", "kernel_ms": ar_ev,
+                          "value": ar_gbs, "unit": "GB/s (same bytes as value)"},
             "cpu_baseline": acpu,
         },
         "sliding_window": {
@@ -748,6 +766,8 @@ def main() -> int:
             "kernel_ms_median": b_med, "kernel_ms_min": b_min, "flop_per_step": bflops,
             "roofline": {"bound": "mfma", "achieved": b_tf, "peak": PEAK_BF16_TFLOPS,
                          "unit": "TFLOP/s", "frac": b_tf / PEAK_BF16_TFLOPS,
+                         "traffic": measured_traffic("flash_backward_bf16"),
+                         "traffic_unit": "bytes per step (both kernels)",
                          "kernel": BWD_KERNELS,
                          "flop_convention": "2.5x forward (5 S^2*D products)"},
             "cpu_baseline": bcpu,
