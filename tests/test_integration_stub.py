@@ -35,7 +35,7 @@ def test_stub_loads_and_binds():
         ns["_raise"](-1)
     for fn in ("flash_attention_fwd", "paged_attention_decode", "paged_attention_prefill",
                "store_kv", "rope", "flash_attention_fwd_lse", "flash_attention_bwd",
-               "fused_rope_attention_fwd"):
+               "fused_rope_attention_fwd", "store_kv_rope", "rope_at"):
         assert callable(ns[fn]), fn
 
 
@@ -148,6 +148,42 @@ def test_stub_store_kv_matches_api(device):
     assert errors.tolist() == [0, 0, 0]
     assert torch.equal(pools[0], pools[2]) and torch.equal(pools[1], pools[3])
     assert pools[0].any()
+
+
+@pytest.mark.gpu
+def test_stub_store_kv_rope_and_rope_at_match_api(device):
+    from mlx_primitives.cache import store_kv
+    from mlx_primitives.kernels import precompute_rope_cache, rope_at
+
+    ns = stub_namespace()
+    g = torch.Generator().manual_seed(10)
+    B, T, H, D, bs, nb = 2, 21, 4, 128, 16, 8
+    k = torch.randn(B, T, H, D, generator=g).to(torch.bfloat16).to(device)
+    v = torch.randn(B, T, H, D, generator=g).to(torch.bfloat16).to(device)
+    cos, sin = precompute_rope_cache(64, D, device=device)
+    tables = torch.tensor([[6, 1, 3], [0, 5, 7]], dtype=torch.int32, device=device)
+    starts = torch.tensor([5, 16], dtype=torch.int32, device=device)
+    counts = torch.tensor([21, 9], dtype=torch.int32, device=device)
+    pools = [torch.zeros(nb, bs, H, D, dtype=torch.bfloat16, device=device) for _ in range(4)]
+    errors = torch.zeros(4, dtype=torch.int32, device=device)
+    stream = torch.cuda.current_stream().cuda_stream
+    ns["store_kv_rope"](k.data_ptr(), v.data_ptr(), pools[0].data_ptr(), pools[1].data_ptr(),
+                        tables.data_ptr(), starts.data_ptr(), counts.data_ptr(),
+                        errors.data_ptr(), B, T, H, D, nb, bs, 3, ns["BF16"], cos.data_ptr(),
+                        sin.data_ptr(), 64, ns["F32"], stream=stream)
+    store_kv(pools[2], pools[3], tables, k, v, starts, counts, rope=(cos, sin))
+    q = torch.randn(B, 1, H, D, generator=g).to(torch.bfloat16).to(device)
+    q_out = torch.empty_like(q)
+    pos = torch.tensor([25, 24], dtype=torch.int32, device=device)
+    err1 = torch.zeros(1, dtype=torch.int32, device=device)
+    ns["rope_at"](q.data_ptr(), q_out.data_ptr(), cos.data_ptr(), sin.data_ptr(),
+                  pos.data_ptr(), err1.data_ptr(), B, 1, H, D, 64, ns["BF16"], ns["F32"],
+                  stream=stream)
+    ref_q = rope_at(q, cos, sin, pos)
+    torch.cuda.synchronize()
+    assert errors.tolist() == [0, 0, 0, 0] and err1.item() == 0
+    assert torch.equal(pools[0], pools[2]) and torch.equal(pools[1], pools[3])
+    assert torch.equal(q_out, ref_q)
 
 
 @pytest.mark.gpu
