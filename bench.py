@@ -57,6 +57,10 @@ GQA_KERNELS = "paged_decode_gqa_kernel + paged_decode_merge_kernel"
 PREFILL_KERNEL = "fa_fwd16_kernel<128,128,8,bf16,paged>"
 APPEND_KERNEL = "kv_append_kernel (+ the 12-byte fill that clears the error words)"
 BWD_KERNELS = "fa_bwd_dq_kernel<128,bf16> (+ Dvec) + fa_bwd_dkdv_fused_kernel<bf16>"
+DROPOUT_P = 0.1
+DROPOUT_KERNEL = "fa_fwd16_drop_kernel<128,128,8,bf16>"
+DROPOUT_BWD_KERNELS = ("fa_bwd_dq_kernel<128,bf16,drop> (+ Dvec) + "
+                       "fa_bwd_dkdv_fused_kernel<bf16,drop>")
 
 
 def measured_traffic(key: str):
@@ -350,6 +354,52 @@ def bwd_step(dev):
     return (q, k, v, dout), fn
 
 
+def dropout_steps(dev, p: float):
+    """The headline attention with dropout_p = p: a no-grad forward step and
+    a backward step (the forward with its row log-sum-exp runs once). The
+    BHSD tensors are passed as their BSHD views (the API applies dropout to
+    BSHD); the kernels see the same strides either way."""
+    from mlx_primitives.attention import flash_attention
+
+    cfg = wl.CONFIGS["flash_bf16_bhsd"]
+    q, k, v = (x.requires_grad_(True) for x in wl.make_qkv(cfg, device=dev))
+    dout = wl.make_qkv(cfg, device=dev, seed=wl.SEED + 1)[0]
+    qs, ks, vs, ds = (x.transpose(1, 2) for x in (q, k, v, dout))
+    qn, kn, vn = (x.detach() for x in (qs, ks, vs))
+    fwd = lambda: flash_attention(qn, kn, vn, causal=True, dropout_p=p)
+    out = flash_attention(qs, ks, vs, causal=True, dropout_p=p)
+    bwd = lambda: torch.autograd.grad(out, (q, k, v), ds, retain_graph=True)
+    return fwd, bwd
+
+
+def cpu_baseline_dropout(cfg: dict, q, k, v, p: float, budget_s: float) -> dict:
+    """The dropout oracle (oracle/dropout.py: keep mask from the hash, dense
+    masked softmax) in float32 numpy on host cores, whole heads of the same
+    workload until ~budget_s of CPU work."""
+    from oracle import dropout as od
+
+    B, H, S, D = q.shape
+    scale = wl.default_scale(D)
+    t_total, done = 0.0, 0
+    for b in range(B):
+        for h in range(H):
+            xs = [x[b:b + 1, h:h + 1].float().cpu().numpy() for x in (q, k, v)]
+            t0 = time.perf_counter()
+            od.attention_dropout(*xs, scale, True, p, seed=12345 + done, layout="BHSD")
+            t_total += time.perf_counter() - t0
+            done += 1
+            if t_total >= budget_s:
+                break
+        if t_total >= budget_s:
+            break
+    flops = wl.flash_flops(1, done, S, D, True)
+    return {"value": flops / t_total / 1e12, "unit": "TFLOP/s", "cores": blas_threads(),
+            "kind": "port",
+            "sample": f"{done} of {B * H} (batch, head) pairs of the same workload, oracle "
+                      f"dropout forward (hash mask, dense softmax) in float32 numpy, "
+                      f"{t_total:.1f} s"}
+
+
 def prefill_step(dev):
     from mlx_primitives.cache import paged_attention
 
@@ -600,6 +650,18 @@ def main() -> int:
     log(f"[bench] flash_backward: {b_wall:.3f} ms/step wall, kernels {b_ev:.3f} ms -> "
         f"{b_tf:.1f} TFLOP/s")
 
+    # ---- the headline attention with dropout_p = 0.1, forward and backward ------------
+    d_fwd, d_bwd = dropout_steps(dev, DROPOUT_P)
+    log(f"[bench] flash_dropout: warmup {args.warmup}, steps {args.steps}")
+    df_wall, df_ev, df_min, df_med = time_steps(d_fwd, args.steps, args.warmup)
+    db_wall, db_ev, db_min, db_med = time_steps(d_bwd, args.steps, args.warmup)
+    del d_fwd, d_bwd
+    df_tf = flops / (df_ev * 1e-3) / 1e12
+    db_tf = bflops / (db_ev * 1e-3) / 1e12
+    log(f"[bench] flash_dropout: forward {df_ev:.3f} ms -> {df_tf:.1f} TFLOP/s "
+        f"({df_ev / ev_ms:.2f}x plain), backward {db_ev:.3f} ms -> {db_tf:.1f} TFLOP/s "
+        f"({db_ev / b_ev:.2f}x plain)")
+
     # ---- config 3: sliding window W=4096, config 5: chunked cross attention ------------
     wcfg = wl.CONFIGS["window_bf16_bshd"]
     (wq, wk, wv), wstep = window_step(dev)
@@ -626,7 +688,7 @@ def main() -> int:
     o_tf = oflops / (o_ev * 1e-3) / 1e12
     log(f"[bench] flash_fp32: kernel {o_ev:.4f} ms -> {o_tf:.1f} TFLOP/s")
 
-    cpu = pcpu = fcpu = acpu = bcpu = wcpu = kcpu = ocpu = None
+    cpu = pcpu = fcpu = acpu = bcpu = wcpu = kcpu = ocpu = dcpu = None
     if not args.no_cpu_baseline:
         log("[bench] cpu baselines (oracle restatement on host cores)")
         cpu = cpu_baseline_flash(cfg, q, k, v, args.cpu_budget)
@@ -638,6 +700,7 @@ def main() -> int:
         wcpu = cpu_baseline_window(wcfg, wq, wk, wv, args.cpu_budget)
         kcpu = cpu_baseline_chunked(ccfg, cq, ck, cv, args.cpu_budget)
         ocpu = cpu_baseline_tiled(wl.CONFIGS["flash_fp32_bshd"], oq, ok_, ov, args.cpu_budget)
+        dcpu = cpu_baseline_dropout(cfg, q, k, v, DROPOUT_P, args.cpu_budget)
     del wq, wk, wv, cq, ck, cv
 
     result = {
@@ -771,6 +834,22 @@ def main() -> int:
                          "kernel": BWD_KERNELS,
                          "flop_convention": "2.5x forward (5 S^2*D products)"},
             "cpu_baseline": bcpu,
+        },
+        "flash_dropout": {
+            "workload": f"flash_attention bf16 B=4 H=32 S=4096 D=128 causal (the headline "
+                        f"tensors as BSHD views), dropout_p={DROPOUT_P}, training: forward "
+                        f"(no grad) and backward (autograd.grad) with the hash keep mask",
+            "value": df_tf, "unit": "TFLOP/s", "ms_per_step": df_wall, "kernel_ms": df_ev,
+            "kernel_ms_median": df_med, "kernel_ms_min": df_min, "flop_per_step": flops,
+            "vs_plain_forward": df_ev / ev_ms,
+            "roofline": {"bound": "mfma", "achieved": df_tf, "peak": PEAK_BF16_TFLOPS,
+                         "unit": "TFLOP/s", "frac": df_tf / PEAK_BF16_TFLOPS,
+                         "kernel": DROPOUT_KERNEL, "traffic": None},
+            "backward": {"value": db_tf, "unit": "TFLOP/s", "ms_per_step": db_wall,
+                         "kernel_ms": db_ev, "kernel_ms_median": db_med, "kernel_ms_min": db_min,
+                         "flop_per_step": bflops, "frac": db_tf / PEAK_BF16_TFLOPS,
+                         "vs_plain_backward": db_ev / b_ev, "kernel": DROPOUT_BWD_KERNELS},
+            "cpu_baseline": dcpu,
         },
     }
     print(json.dumps(result), flush=True)

@@ -333,6 +333,49 @@ int mpx_attn_bwd(const void* q, const void* k, const void* v, const void* o, con
                  void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * Attention with dropout on the weights, forward and backward.
+ *
+ * Replaces the reference's training path with dropout_p > 0
+ * (mlx_primitives/attention/flash.py:202-205 -> _reference_flash_attention_with_dropout,
+ * flash.py:528-578; sliding_window.py:280-282, 564-625; chunked.py:109-110, 206-255):
+ * weights = softmax(scores) * keep / (1 - dropout_p), output = weights @ v, with
+ * keep ~ Bernoulli(1 - dropout_p) per (batch, head, query, key).
+ *
+ * Here the keep mask is never stored: it is a hash of (seed, row, key), so the
+ * backward regenerates the forward's mask from the same seed. Row r =
+ * (b * H + h) * Sq + q (mod 2^32), key k, pair m = k / 2:
+ *   bits = lowbias32((r * 0x9E3779B1 + seed_lo) ^ (m * 0x85EBCA77 + seed_hi))
+ * (lowbias32: x ^= x >> 16; x *= 0x7feb352d; x ^= x >> 15; x *= 0x846ca68b;
+ * x ^= x >> 16), seed_lo / seed_hi the low / high 32 bits of seed; key 2m reads
+ * the low 16 bits of bits, key 2m + 1 the high 16, and a key is kept when its
+ * 16 bits are >= round(dropout_p * 65536) (at most 65535): the keep
+ * probability is 1 - dropout_p to within 2^-17.
+ *
+ * mpx_attn_fwd_dropout is mpx_attn_fwd_lse with dropout_p in [0, 1) and the
+ * seed (lse may be NULL; its values, and so the backward's probabilities, are
+ * those of the undropped softmax). dropout_p = 0 is the plain forward.
+ * mpx_attn_bwd_dropout is mpx_attn_bwd of that forward: same arguments plus
+ * the forward's dropout_p and seed. Scope: D in {64, 128}, float32 / float16 /
+ * bfloat16, every mask and K/V head grouping of the plain kernels.
+ */
+int mpx_attn_fwd_dropout(const void* q, const void* k, const void* v, void* o, float* lse,
+                         const int64_t* q_strides, const int64_t* k_strides,
+                         const int64_t* v_strides, const int64_t* o_strides,
+                         int B, int H, int H_kv, int Sq, int Sk, int D, float scale, int causal,
+                         int window_left, int window_right, int dtype, float dropout_p,
+                         uint64_t seed, void* workspace, size_t workspace_bytes, void* stream);
+
+int mpx_attn_bwd_dropout(const void* q, const void* k, const void* v, const void* o,
+                         const void* dout, const float* lse, void* dq, void* dk, void* dv,
+                         const int64_t* q_strides, const int64_t* k_strides,
+                         const int64_t* v_strides, const int64_t* o_strides,
+                         const int64_t* do_strides, const int64_t* dq_strides,
+                         const int64_t* dk_strides, const int64_t* dv_strides,
+                         int B, int H, int H_kv, int Sq, int Sk, int D, float scale, int causal,
+                         int window_left, int window_right, int dtype, float dropout_p,
+                         uint64_t seed, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Paged-KV decode that allocates nothing: mpx_paged_decode_gqa without the
  * workspace arguments. It has no counterpart in the reference; it is for
  * callers that cannot allocate device memory (code under HIP graph capture,

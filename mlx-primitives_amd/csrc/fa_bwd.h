@@ -22,14 +22,19 @@ struct BwdParams {
   int B, H, H_kv, kv_group, Sq, Sk;  // K/V (and dK/dV) carry H_kv = H / kv_group heads
   int win_left, win_right;  // -1 = unbounded (causal: win_right = 0)
   float scale, c;           // c = scale * log2(e)
+  // Dropout of the forward (the DROP kernels only): keep threshold and seed
+  // words of the keep-mask hash, and the 1 / (1 - p) of the kept weights.
+  uint32_t drop_thresh, seed0, seed1;
+  float drop_scale;
 };
 
 constexpr int kBwdWaves = 4;    // waves per workgroup (one per SIMD)
 constexpr int kBwdOwn = 32 * kBwdWaves;  // rows (or keys) a workgroup owns
 constexpr int kBwdTile = 64;    // streamed rows per step
 
-// The float32 backward (rowsum, dQ, dK/dV kernels) for D in {64, 128},
-// enqueued on st; defined in fa_bwd32.hip.
-hipError_t launch_bwd32(const BwdParams& p, int D, hipStream_t st);
+// The float32 backward (rowsum, dQ, dK/dV kernels) for D in {64, 128}, with
+// the forward's dropout when drop is set, enqueued on st; defined in
+// fa_bwd32.hip.
+hipError_t launch_bwd32(const BwdParams& p, int D, bool drop, hipStream_t st);
 
 }  // namespace mpx

@@ -175,7 +175,7 @@ __device__ __forceinline__ void grid_tile(int n_heads, int n_tiles, int& tile, i
 // fragments it holds and the O row) and writes it for the dK/dV kernel that
 // runs after it.
 // ---------------------------------------------------------------------------
-template <int D, bool BF16>
+template <int D, bool BF16, bool DROP = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void fa_bwd_dq_kernel(BwdParams p) {
   constexpr int NKS = D / 16, NDB = D / 32, TILE = kBwdTile * D;
@@ -215,6 +215,8 @@ void fa_bwd_dq_kernel(BwdParams p) {
     load_row_frags<NKS>(dO + (int64_t)qrow * p.do_ss, g, df);
     const int64_t rix = (int64_t)bh * p.Sq + qrow;
     const float lse = myq < p.Sq ? p.lse[rix] : INFINITY;
+    // Dropout: this row's key of the forward's keep-mask hash.
+    const u32 drop_rk = DROP ? drop_row_key((u32)((int64_t)bh * p.Sq + myq), p.seed0) : 0u;
     float dvc;
     {
       // This lane's half of the row (dims 16 ks + 8 g + 0..7), then the pair sum.
@@ -299,7 +301,11 @@ void fa_bwd_dq_kernel(BwdParams p) {
             }
           }
           // dsp[hh]: dS^T of keys 32nb + 16hh + 8g + 0..7, the B operand of k-step 2nb + hh.
+          // Dropout: dS = P (dP keep / (1 - p) - Dvec); element pair e2 of half
+          // hh is the hash's key pair kv0 / 2 + 16 nb + 8 hh + 4 g + e2.
           u32x4 dsp[2];
+          const u32 pair0 =
+              DROP ? drop_pair_key((u32)(kv0 >> 1) + 16u * nb + 4u * g, p.seed1) : 0u;
 #pragma unroll
           for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
@@ -307,7 +313,14 @@ void fa_bwd_dq_kernel(BwdParams p) {
               const int e = 8 * hh + 2 * e2;
               const float p0 = fast_exp2(sb[e] * p.c - lse);
               const float p1 = fast_exp2(sb[e + 1] * p.c - lse);
-              dsp[hh][e2] = pack2<BF16>(p0 * (dpb[e] - dvc), p1 * (dpb[e + 1] - dvc));
+              if constexpr (DROP) {
+                const u32 bits = drop_bits(drop_rk, pair0 + (u32)(8 * hh + e2) * 0x85EBCA77u);
+                const float dp0 = (bits & 0xffffu) >= p.drop_thresh ? dpb[e] * p.drop_scale : 0.f;
+                const float dp1 = bits >= (p.drop_thresh << 16) ? dpb[e + 1] * p.drop_scale : 0.f;
+                dsp[hh][e2] = pack2<BF16>(p0 * (dp0 - dvc), p1 * (dp1 - dvc));
+              } else {
+                dsp[hh][e2] = pack2<BF16>(p0 * (dpb[e] - dvc), p1 * (dpb[e + 1] - dvc));
+              }
             }
           // dQ^T += K^T dS^T (K^T through the transposing read of the K tile).
 #pragma unroll
@@ -343,7 +356,7 @@ void fa_bwd_dq_kernel(BwdParams p) {
 // ---------------------------------------------------------------------------
 constexpr int kBoth = 0, kOnlyK = 1, kOnlyV = 2;
 
-template <int D, bool BF16, int MODE>
+template <int D, bool BF16, int MODE, bool DROP = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void fa_bwd_dkdv_kernel(BwdParams p) {
   constexpr bool WANT_K = MODE != kOnlyV, WANT_V = MODE != kOnlyK;
@@ -365,6 +378,11 @@ void fa_bwd_dkdv_kernel(BwdParams p) {
   // stored, and queries past Sq have lse = +inf).
   const int q_first = p.win_right >= 0 ? mykey - p.win_right : -(1 << 30);
   const int q_last = p.win_left >= 0 ? mykey + p.win_left : (1 << 30);
+  // Dropout: this key's pair key of the forward's keep-mask hash and the half
+  // of the hash that decides it.
+  const u32 drop_pk = DROP ? drop_pair_key((u32)mykey >> 1, p.seed1) : 0u;
+  const u32 drop_hm = (mykey & 1) ? 0xffff0000u : 0xffffu;
+  const u32 drop_ht = (mykey & 1) ? p.drop_thresh << 16 : p.drop_thresh;
 
   const uint16_t* K = (const uint16_t*)p.k + b * p.k_sb + hk * p.k_sh;
   const uint16_t* V = (const uint16_t*)p.v + b * p.v_sb + hk * p.v_sh;
@@ -429,6 +447,12 @@ void fa_bwd_dkdv_kernel(BwdParams p) {
     const int S = u & 1;
     if (u + 1 < n_steps) load(u + 1, S ^ 1);
     const int qr0 = (t0 + u % n_t) * kBwdTile;
+    // (dropout: row key of query qr0 + 8 g of this step's head)
+    const u32 drop_rk =
+        DROP ? drop_row_key((u32)(((int64_t)b * p.H + hk * p.kv_group + u / n_t) * p.Sq + qr0 +
+                                  8 * g),
+                            p.seed0)
+             : 0u;
     const bool skip = wk0 >= p.Sk ||
                       (p.win_right >= 0 && wk0 > qr0 + kBwdTile - 1 + p.win_right) ||
                       (p.win_left >= 0 && wk0 + 31 < qr0 - p.win_left);
@@ -476,9 +500,20 @@ void fa_bwd_dkdv_kernel(BwdParams p) {
             const float dv1 = e2 < 2 ? d0[2 * e2 + 1] : d1[2 * e2 - 3];
             const float p0 = fast_exp2(sb[e] * p.c - lv0);
             const float p1 = fast_exp2(sb[e + 1] * p.c - lv1);
-            if constexpr (WANT_V) pp[hh][e2] = pack2<BF16>(p0, p1);
-            if constexpr (WANT_K)
-              dsp[hh][e2] = pack2<BF16>(p0 * (dpb[e] - dv0), p1 * (dpb[e + 1] - dv1));
+            if constexpr (DROP) {
+              // Rows qr0 + r8 + 2 e2 + {0, 1}: row keys drop_rk + (32 nb + 16 hh + 2 e2 + {0, 1}) G.
+              const u32 rk0 = drop_rk + (u32)(32 * nb + 16 * hh + 2 * e2) * 0x9E3779B1u;
+              const bool k0 = drop_keep(drop_bits(rk0, drop_pk), drop_hm, drop_ht);
+              const bool k1 = drop_keep(drop_bits(rk0 + 0x9E3779B1u, drop_pk), drop_hm, drop_ht);
+              if constexpr (WANT_V) pp[hh][e2] = pack2<BF16>(k0 ? p0 : 0.f, k1 ? p1 : 0.f);
+              if constexpr (WANT_K)
+                dsp[hh][e2] = pack2<BF16>(p0 * ((k0 ? dpb[e] * p.drop_scale : 0.f) - dv0),
+                                          p1 * ((k1 ? dpb[e + 1] * p.drop_scale : 0.f) - dv1));
+            } else {
+              if constexpr (WANT_V) pp[hh][e2] = pack2<BF16>(p0, p1);
+              if constexpr (WANT_K)
+                dsp[hh][e2] = pack2<BF16>(p0 * (dpb[e] - dv0), p1 * (dpb[e + 1] - dv1));
+            }
           }
         }
         // dV^T += dO^T P and dK^T += Q^T dS (transposing reads of the tiles).
@@ -513,7 +548,8 @@ void fa_bwd_dkdv_kernel(BwdParams p) {
           p.scale);
     if constexpr (WANT_V)
       store_row<NDB, BF16>(
-          (uint16_t*)p.dv + b * p.dv_sb + hk * p.dv_sh + (int64_t)mykey * p.dv_ss, g, dv, 1.f);
+          (uint16_t*)p.dv + b * p.dv_sb + hk * p.dv_sh + (int64_t)mykey * p.dv_ss, g, dv,
+          DROP ? p.drop_scale : 1.f);
   }
 }
 
@@ -528,7 +564,7 @@ void fa_bwd_dkdv_kernel(BwdParams p) {
 // ---------------------------------------------------------------------------
 constexpr int kFusedTile = 32;
 
-template <bool BF16>
+template <bool BF16, bool DROP = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void fa_bwd_dkdv_fused_kernel(BwdParams p) {
   constexpr int D = 128, NKS = D / 16, NDB = D / 32, TILE = kFusedTile * D;
@@ -598,6 +634,11 @@ void fa_bwd_dkdv_fused_kernel(BwdParams p) {
     const bool no_row = q_last < q_lo_key;
     const int q_first = no_row ? (1 << 30) : q_lo_key;
     const unsigned span = no_row ? 0u : (unsigned)q_last - (unsigned)q_first;
+    // Dropout: this key's pair key of the forward's keep-mask hash and the
+    // half of the hash that decides it.
+    const u32 drop_pk = DROP ? drop_pair_key((u32)mykey >> 1, p.seed1) : 0u;
+    const u32 drop_hm = (mykey & 1) ? 0xffff0000u : 0xffffu;
+    const u32 drop_ht = (mykey & 1) ? p.drop_thresh << 16 : p.drop_thresh;
     u32x4 vf[NKS];
     load_row_frags<NKS>(V + (int64_t)krow * p.v_ss, g, vf);
 
@@ -619,7 +660,7 @@ void fa_bwd_dkdv_fused_kernel(BwdParams p) {
     // pair is stepped, not divided, for the tile being loaded (lt, lh) and the
     // tile being computed (ct). Waves 0 and 1 also bring the tile's lse and
     // Dvec rows (clamped at Sq) into LDS.
-    int lt = 0, lh = hk * p.kv_group, ct = 0;
+    int lt = 0, lh = hk * p.kv_group, ct = 0, ch = hk * p.kv_group;
     auto load = [&](int S) __attribute__((always_inline)) {
       const int row0 = (t0 + lt) * kFusedTile;
       if (wave < 2) {
@@ -646,7 +687,13 @@ void fa_bwd_dkdv_fused_kernel(BwdParams p) {
       const int S = u & 1;
       if (u + 1 < n_steps) load(S ^ 1);
       const int qr0 = (t0 + ct) * kFusedTile;
-      if (++ct == n_t) ct = 0;
+      // (dropout: row key of query qr0 + 8 g of this step's head ch)
+      const u32 drop_rk =
+          DROP ? drop_row_key((u32)(((int64_t)b * p.H + ch) * p.Sq + qr0 + 8 * g), p.seed0) : 0u;
+      if (++ct == n_t) {
+        ct = 0;
+        ++ch;
+      }
       const bool skip = wk0 >= p.Sk ||
                         (p.win_right >= 0 && wk0 > qr0 + kFusedTile - 1 + p.win_right) ||
                         (p.win_left >= 0 && wk0 + 31 < qr0 - p.win_left);
@@ -699,8 +746,18 @@ void fa_bwd_dkdv_fused_kernel(BwdParams p) {
             const float dv1 = e2 < 2 ? d0[2 * e2 + 1] : d1[2 * e2 - 3];
             const float p0 = fast_exp2(sb[e] * p.c - lv0);
             const float p1 = fast_exp2(sb[e + 1] * p.c - lv1);
-            pp[hh][e2] = pack2<BF16>(p0, p1);
-            dsp[hh][e2] = pack2<BF16>(p0 * (dpb[e] - dv0), p1 * (dpb[e + 1] - dv1));
+            if constexpr (DROP) {
+              // Rows qr0 + r8 + 2 e2 + {0, 1}: row keys drop_rk + (16 hh + 2 e2 + {0, 1}) G.
+              const u32 rk0 = drop_rk + (u32)(16 * hh + 2 * e2) * 0x9E3779B1u;
+              const bool k0 = drop_keep(drop_bits(rk0, drop_pk), drop_hm, drop_ht);
+              const bool k1 = drop_keep(drop_bits(rk0 + 0x9E3779B1u, drop_pk), drop_hm, drop_ht);
+              pp[hh][e2] = pack2<BF16>(k0 ? p0 : 0.f, k1 ? p1 : 0.f);
+              dsp[hh][e2] = pack2<BF16>(p0 * ((k0 ? dpb[e] * p.drop_scale : 0.f) - dv0),
+                                        p1 * ((k1 ? dpb[e + 1] * p.drop_scale : 0.f) - dv1));
+            } else {
+              pp[hh][e2] = pack2<BF16>(p0, p1);
+              dsp[hh][e2] = pack2<BF16>(p0 * (dpb[e] - dv0), p1 * (dpb[e + 1] - dv1));
+            }
           }
         }
         // dV^T += dO^T P and dK^T += Q^T dS (transposing reads of the tiles).
@@ -727,25 +784,30 @@ void fa_bwd_dkdv_fused_kernel(BwdParams p) {
       store_row<NDB, BF16>((uint16_t*)p.dk + b * p.dk_sb + hk * p.dk_sh + (int64_t)mykey * p.dk_ss,
                            g, dk, p.scale);
       store_row<NDB, BF16>((uint16_t*)p.dv + b * p.dv_sb + hk * p.dv_sh + (int64_t)mykey * p.dv_ss,
-                           g, dv, 1.f);
+                           g, dv, DROP ? p.drop_scale : 1.f);
     }
   }
 }
 
-template <int D, bool BF16>
+template <int D, bool BF16, bool DROP>
 hipError_t launch_bwd(const BwdParams& p, hipStream_t st) {
   // dQ (which also writes Dvec) before dK / dV, which reads it.
   const int n_qt = (p.Sq + kBwdOwn - 1) / kBwdOwn, n_kt = (p.Sk + kBwdOwn - 1) / kBwdOwn;
-  hipLaunchKernelGGL((fa_bwd_dq_kernel<D, BF16>), dim3(p.B * p.H * ((n_qt + 1) / 2)), dim3(256),
-                     0, st, p);
+  hipLaunchKernelGGL((fa_bwd_dq_kernel<D, BF16, DROP>), dim3(p.B * p.H * ((n_qt + 1) / 2)),
+                     dim3(256), 0, st, p);
   const dim3 grid_kv(p.B * p.H_kv * n_kt);
   if constexpr (D == 128) {
     const dim3 grid_pairs(p.B * p.H_kv * ((n_kt + 1) / 2));
-    hipLaunchKernelGGL((fa_bwd_dkdv_fused_kernel<BF16>), grid_pairs, dim3(256), 0, st, p);
+    hipLaunchKernelGGL((fa_bwd_dkdv_fused_kernel<BF16, DROP>), grid_pairs, dim3(256), 0, st, p);
   } else {
-    hipLaunchKernelGGL((fa_bwd_dkdv_kernel<D, BF16, kBoth>), grid_kv, dim3(256), 0, st, p);
+    hipLaunchKernelGGL((fa_bwd_dkdv_kernel<D, BF16, kBoth, DROP>), grid_kv, dim3(256), 0, st, p);
   }
   return hipGetLastError();
+}
+
+template <bool BF16, bool DROP>
+hipError_t launch_bwd_d(const BwdParams& p, int D, hipStream_t st) {
+  return D == 64 ? launch_bwd<64, BF16, DROP>(p, st) : launch_bwd<128, BF16, DROP>(p, st);
 }
 
 }  // namespace mpx
@@ -757,16 +819,17 @@ extern "C" size_t mpx_attn_bwd_workspace_bytes(int B, int H, int Sq) {
   return (size_t)B * H * Sq * sizeof(float);
 }
 
-extern "C" int mpx_attn_bwd(const void* q, const void* k, const void* v, const void* o,
-                            const void* dout, const float* lse, void* dq, void* dk, void* dv,
-                            const int64_t* q_strides, const int64_t* k_strides,
-                            const int64_t* v_strides, const int64_t* o_strides,
-                            const int64_t* do_strides, const int64_t* dq_strides,
-                            const int64_t* dk_strides, const int64_t* dv_strides, int B, int H,
-                            int H_kv, int Sq, int Sk, int D, float scale, int causal,
-                            int window_left, int window_right, int dtype, void* workspace,
-                            size_t workspace_bytes, void* stream) {
-  clear_error();
+static int attn_bwd_entry(const void* q, const void* k, const void* v, const void* o,
+                          const void* dout, const float* lse, void* dq, void* dk, void* dv,
+                          const int64_t* q_strides, const int64_t* k_strides,
+                          const int64_t* v_strides, const int64_t* o_strides,
+                          const int64_t* do_strides, const int64_t* dq_strides,
+                          const int64_t* dk_strides, const int64_t* dv_strides, int B, int H,
+                          int H_kv, int Sq, int Sk, int D, float scale, int causal,
+                          int window_left, int window_right, int dtype, float dropout_p,
+                          uint64_t seed, void* workspace, size_t workspace_bytes, void* stream) {
+  MPX_CHECK_ARG(dropout_p >= 0.f && dropout_p < 1.f,
+                "mpx_attn_bwd_dropout: dropout_p must be in [0, 1), got %g", (double)dropout_p);
   MPX_CHECK_ARG(dtype == MPX_F32 || dtype == MPX_F16 || dtype == MPX_BF16,
                 "mpx_attn_bwd: unknown dtype code %d", dtype);
   MPX_CHECK_ARG(B >= 0 && H >= 0 && Sq >= 0 && Sk >= 0, "mpx_attn_bwd: negative size");
@@ -825,14 +888,54 @@ extern "C" int mpx_attn_bwd(const void* q, const void* k, const void* v, const v
   p.win_right = causal ? 0 : (window_right < 0 ? -1 : window_right);
   p.scale = scale;
   p.c = scale * kLog2e;
+  const bool drop = dropout_p > 0.f;
+  if (drop) {
+    p.drop_thresh = drop_threshold(dropout_p);
+    p.seed0 = (uint32_t)seed;
+    p.seed1 = (uint32_t)(seed >> 32);
+    p.drop_scale = 1.f / (1.f - dropout_p);
+  }
   hipStream_t st = (hipStream_t)stream;
   hipError_t e;
   if (dtype == MPX_F32)
-    e = launch_bwd32(p, D, st);
+    e = launch_bwd32(p, D, drop, st);
   else if (dtype == MPX_BF16)
-    e = D == 64 ? launch_bwd<64, true>(p, st) : launch_bwd<128, true>(p, st);
+    e = drop ? launch_bwd_d<true, true>(p, D, st) : launch_bwd_d<true, false>(p, D, st);
   else
-    e = D == 64 ? launch_bwd<64, false>(p, st) : launch_bwd<128, false>(p, st);
+    e = drop ? launch_bwd_d<false, true>(p, D, st) : launch_bwd_d<false, false>(p, D, st);
   MPX_CHECK_HIP(e);
   return MPX_OK;
+}
+
+extern "C" int mpx_attn_bwd(const void* q, const void* k, const void* v, const void* o,
+                            const void* dout, const float* lse, void* dq, void* dk, void* dv,
+                            const int64_t* q_strides, const int64_t* k_strides,
+                            const int64_t* v_strides, const int64_t* o_strides,
+                            const int64_t* do_strides, const int64_t* dq_strides,
+                            const int64_t* dk_strides, const int64_t* dv_strides, int B, int H,
+                            int H_kv, int Sq, int Sk, int D, float scale, int causal,
+                            int window_left, int window_right, int dtype, void* workspace,
+                            size_t workspace_bytes, void* stream) {
+  clear_error();
+  return attn_bwd_entry(q, k, v, o, dout, lse, dq, dk, dv, q_strides, k_strides, v_strides,
+                        o_strides, do_strides, dq_strides, dk_strides, dv_strides, B, H, H_kv, Sq,
+                        Sk, D, scale, causal, window_left, window_right, dtype, 0.f, 0, workspace,
+                        workspace_bytes, stream);
+}
+
+extern "C" int mpx_attn_bwd_dropout(const void* q, const void* k, const void* v, const void* o,
+                                    const void* dout, const float* lse, void* dq, void* dk,
+                                    void* dv, const int64_t* q_strides,
+                                    const int64_t* k_strides, const int64_t* v_strides,
+                                    const int64_t* o_strides, const int64_t* do_strides,
+                                    const int64_t* dq_strides, const int64_t* dk_strides,
+                                    const int64_t* dv_strides, int B, int H, int H_kv, int Sq,
+                                    int Sk, int D, float scale, int causal, int window_left,
+                                    int window_right, int dtype, float dropout_p, uint64_t seed,
+                                    void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  return attn_bwd_entry(q, k, v, o, dout, lse, dq, dk, dv, q_strides, k_strides, v_strides,
+                        o_strides, do_strides, dq_strides, dk_strides, dv_strides, B, H, H_kv, Sq,
+                        Sk, D, scale, causal, window_left, window_right, dtype, dropout_p, seed,
+                        workspace, workspace_bytes, stream);
 }

@@ -102,7 +102,7 @@ __device__ __forceinline__ constexpr int crow(int e, int g) {
 // per 32-key tile: S^T = K Q^T, dP^T = V dO^T, dS^T = P^T (dP^T - Dvec),
 // dQ^T += K^T dS^T.
 // ---------------------------------------------------------------------------
-template <int D>
+template <int D, bool DROP = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void fa_bwd32_dq_kernel(BwdParams p) {
   constexpr int NQ4 = D / 8, NDB = D / 32, RS = D + 4, TILE = kB32Tile * RS;
@@ -128,6 +128,8 @@ void fa_bwd32_dq_kernel(BwdParams p) {
   const int64_t rix = (int64_t)bh * p.Sq + qrow;
   const float lse = myq < p.Sq ? p.lse[rix] : INFINITY;
   const float dvc = p.dvec[rix];
+  // Dropout: this row's key of the forward's keep-mask hash.
+  const u32 drop_rk = DROP ? drop_row_key((u32)((int64_t)bh * p.Sq + myq), p.seed0) : 0u;
   const int kv_first = p.win_left >= 0 ? myq - p.win_left : -(1 << 30);
   const int kv_last = min(p.win_right >= 0 ? myq + p.win_right : (1 << 30), p.Sk - 1);
 
@@ -184,6 +186,18 @@ void fa_bwd32_dq_kernel(BwdParams p) {
           sb[e] = (key >= kv_first) & (key <= kv_last) ? sb[e] : -INFINITY;
         }
       }
+      if constexpr (DROP) {
+        // dS = P (dP keep / (1 - p) - Dvec); elements 2 e2, 2 e2 + 1 hold keys
+        // kv0 + crow(2 e2, g) + {0, 1}, the hash's key pair
+        // kv0 / 2 + 4 (e2 / 2) + 2 g + e2 % 2.
+        const u32 pair0 = drop_pair_key((u32)(kv0 >> 1) + 2u * g, p.seed1);
+#pragma unroll
+        for (int e2 = 0; e2 < 8; ++e2) {
+          const u32 bits = drop_bits(drop_rk, pair0 + (u32)(4 * (e2 >> 1) + (e2 & 1)) * 0x85EBCA77u);
+          dpb[2 * e2] = (bits & 0xffffu) >= p.drop_thresh ? dpb[2 * e2] * p.drop_scale : 0.f;
+          dpb[2 * e2 + 1] = bits >= (p.drop_thresh << 16) ? dpb[2 * e2 + 1] * p.drop_scale : 0.f;
+        }
+      }
       f32x16 ds;
 #pragma unroll
       for (int e = 0; e < 16; ++e) ds[e] = fast_exp2(sb[e] * p.c - lse) * (dpb[e] - dvc);
@@ -212,7 +226,7 @@ void fa_bwd32_dq_kernel(BwdParams p) {
 // accumulator sets do not fit one wave's registers, so dK and dV run as two
 // kernels (the dV one recomputes S and needs neither dP nor V).
 // ---------------------------------------------------------------------------
-template <int D, bool WANT_K, bool WANT_V>
+template <int D, bool WANT_K, bool WANT_V, bool DROP = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void fa_bwd32_dkdv_kernel(BwdParams p) {
   constexpr int NQ4 = D / 8, NDB = D / 32, RS = D + 4, TILE = kB32Tile * RS;
@@ -229,6 +243,11 @@ void fa_bwd32_dkdv_kernel(BwdParams p) {
   const int krow = min(mykey, p.Sk - 1);
   const int q_first = p.win_right >= 0 ? mykey - p.win_right : -(1 << 30);
   const int q_last = p.win_left >= 0 ? mykey + p.win_left : (1 << 30);
+  // Dropout: this key's pair key of the forward's keep-mask hash and the half
+  // of the hash that decides it.
+  const u32 drop_pk = DROP ? drop_pair_key((u32)mykey >> 1, p.seed1) : 0u;
+  const u32 drop_hm = (mykey & 1) ? 0xffff0000u : 0xffffu;
+  const u32 drop_ht = (mykey & 1) ? p.drop_thresh << 16 : p.drop_thresh;
 
   const float* K = (const float*)p.k + b * p.k_sb + hk * p.k_sh;
   const float* V = (const float*)p.v + b * p.v_sb + hk * p.v_sh;
@@ -317,7 +336,17 @@ void fa_bwd32_dkdv_kernel(BwdParams p) {
         for (int i = 0; i < 4; ++i) {
           const int e = 4 * e4 + i;
           pr[e] = fast_exp2(sb[e] * p.c - lv[i]);
-          if constexpr (WANT_K) ds[e] = pr[e] * (dpb[e] - dv4[i]);
+          if constexpr (DROP) {
+            // Row qr0 + crow(e, g) of this step's head (u / n_t of the group).
+            const u32 rk = drop_row_key(
+                (u32)(((int64_t)b * p.H + hk * p.kv_group + u / n_t) * p.Sq + qr0 + crow(e, g)),
+                p.seed0);
+            const bool keep = drop_keep(drop_bits(rk, drop_pk), drop_hm, drop_ht);
+            if constexpr (WANT_K) ds[e] = pr[e] * ((keep ? dpb[e] * p.drop_scale : 0.f) - dv4[i]);
+            pr[e] = keep ? pr[e] : 0.f;
+          } else {
+            if constexpr (WANT_K) ds[e] = pr[e] * (dpb[e] - dv4[i]);
+          }
         }
       }
 #pragma unroll
@@ -338,29 +367,30 @@ void fa_bwd32_dkdv_kernel(BwdParams p) {
                        dk, p.scale);
     if constexpr (WANT_V)
       store_row32<NDB>((float*)p.dv + b * p.dv_sb + hk * p.dv_sh + (int64_t)mykey * p.dv_ss, g,
-                       dv, 1.f);
+                       dv, DROP ? p.drop_scale : 1.f);
   }
 }
 
-template <int D>
+template <int D, bool DROP>
 hipError_t launch_bwd32_d(const BwdParams& p, hipStream_t st) {
   const int64_t rows = (int64_t)p.B * p.H * p.Sq;
   hipLaunchKernelGGL((fa_bwd32_dvec_kernel<D>), dim3((unsigned)((rows * (D / 4) + 255) / 256)),
                      dim3(256), 0, st, p);
   const int n_qt = (p.Sq + kBwdOwn - 1) / kBwdOwn, n_kt = (p.Sk + kBwdOwn - 1) / kBwdOwn;
-  hipLaunchKernelGGL((fa_bwd32_dq_kernel<D>), dim3(p.B * p.H * n_qt), dim3(256), 0, st, p);
+  hipLaunchKernelGGL((fa_bwd32_dq_kernel<D, DROP>), dim3(p.B * p.H * n_qt), dim3(256), 0, st, p);
   const dim3 grid_kv(p.B * p.H_kv * n_kt);
   if constexpr (D == 128) {
-    hipLaunchKernelGGL((fa_bwd32_dkdv_kernel<D, true, false>), grid_kv, dim3(256), 0, st, p);
-    hipLaunchKernelGGL((fa_bwd32_dkdv_kernel<D, false, true>), grid_kv, dim3(256), 0, st, p);
+    hipLaunchKernelGGL((fa_bwd32_dkdv_kernel<D, true, false, DROP>), grid_kv, dim3(256), 0, st, p);
+    hipLaunchKernelGGL((fa_bwd32_dkdv_kernel<D, false, true, DROP>), grid_kv, dim3(256), 0, st, p);
   } else {
-    hipLaunchKernelGGL((fa_bwd32_dkdv_kernel<D, true, true>), grid_kv, dim3(256), 0, st, p);
+    hipLaunchKernelGGL((fa_bwd32_dkdv_kernel<D, true, true, DROP>), grid_kv, dim3(256), 0, st, p);
   }
   return hipGetLastError();
 }
 
-hipError_t launch_bwd32(const BwdParams& p, int D, hipStream_t st) {
-  return D == 64 ? launch_bwd32_d<64>(p, st) : launch_bwd32_d<128>(p, st);
+hipError_t launch_bwd32(const BwdParams& p, int D, bool drop, hipStream_t st) {
+  if (drop) return D == 64 ? launch_bwd32_d<64, true>(p, st) : launch_bwd32_d<128, true>(p, st);
+  return D == 64 ? launch_bwd32_d<64, false>(p, st) : launch_bwd32_d<128, false>(p, st);
 }
 
 }  // namespace mpx

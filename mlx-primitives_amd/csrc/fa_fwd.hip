@@ -69,6 +69,10 @@ struct FwdParams {
   int bs, bs_log2;      // page size in tokens; log2(bs) or -1 if not a power of 2
   int max_blocks, num_blocks;
   uint32_t pool_bytes;  // bytes of one pool from its base (bounds of the buffer loads)
+  // Dropout on the weights (the dropout kernels only): keep threshold and seed
+  // words of the keep-mask hash, and the 1 / (1 - p) of the kept weights.
+  uint32_t drop_thresh, seed0, seed1;
+  float drop_scale;
 };
 
 // Page-table slice of one work item staged in LDS (entries).
@@ -759,7 +763,7 @@ constexpr u32 kNoRowDirect = 0xFFFFFF00u;
 // consecutive rows x 4 consecutive chunks (V^T operands).
 __device__ __forceinline__ int swz64(int r) { return (((r >> 1) & 1) << 2) | ((r >> 2) & 3); }
 
-template <int D, int BN, int NW, bool BF16, int NST, bool PAGED>
+template <int D, int BN, int NW, bool BF16, int NST, bool PAGED, bool DROP = false>
 __device__ __forceinline__ void fa16_rows_direct(const FwdParams& pin, const WorkItem wi,
                                                  unsigned char* __restrict__ st0,
                                                  unsigned char* __restrict__ st1,
@@ -827,6 +831,9 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& pin, const Wor
 
   const int wq0 = q0 + wave * 32;
   const int myq = wq0 + j;
+  // Dropout: this row's key of the keep-mask hash.
+  const u32 drop_rk =
+      DROP ? drop_row_key((u32)(((int64_t)wi.b * p.H + wi.h) * p.Sq + myq), p.seed0) : 0u;
   u32x4 qreg[NKS];
   {
     const u32x4* src = (const u32x4*)(Qp + (int64_t)min(myq, p.Sq - 1) * p.q_ss);
@@ -1126,9 +1133,14 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& pin, const Wor
   // the exponentials of slice sl+1 run while the MFMAs of slice sl execute.
   // The row sum accumulates the packed (rounded) weights, the exact weights
   // the PV product uses. V^T operands come through the transposing read, one
-  // slice ahead of their MFMAs.
-  auto exp_pv = [&](const f32x16 (&s)[NB], const unsigned char* Vb) __attribute__((always_inline)) {
+  // slice ahead of their MFMAs. Dropout: the PV operand keeps the weights of
+  // the kept keys only (the row sum takes them all; 1 / (1 - p) is applied
+  // with the normalisation); element pair e2 of slice sl holds keys
+  // kv0 + 16 sl + 8 g + 2 e2 + {0, 1}, the hash's key pair kv0 / 2 + 8 sl + 4 g + e2.
+  auto exp_pv = [&](const f32x16 (&s)[NB], const unsigned char* Vb, int kv0)
+                    __attribute__((always_inline)) {
     float lsum[2] = {0.f, 0.f};
+    const u32 pair0 = DROP ? drop_pair_key((u32)(kv0 >> 1) + 4u * g, p.seed1) : 0u;
     auto vread = [&](int sl, u32x4 (&va)[NDB]) __attribute__((always_inline)) {
 #pragma unroll
       for (int db = 0; db < NDB; ++db) {
@@ -1148,7 +1160,11 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& pin, const Wor
         const float x0 = fast_exp2(s[nb][8 * hh + 2 * e2]);
         const float x1 = fast_exp2(s[nb][8 * hh + 2 * e2 + 1]);
         const u32 pk = pack2<BF16>(x0, x1);
-        pk4[e2] = pk;
+        if constexpr (DROP)
+          pk4[e2] = pk & drop_mask2(drop_bits(drop_rk, pair0 + (u32)(8 * sl + e2) * 0x85EBCA77u),
+                                    p.drop_thresh);
+        else
+          pk4[e2] = pk;
         lsum[e2 & 1] = dot2_sum<BF16>(pk, lsum[e2 & 1]);
       }
       if (sl + 1 < NSL) vread(sl + 1, vnext);
@@ -1196,7 +1212,7 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& pin, const Wor
     qk_mfma(Kb, s);
     qk_sched();
     max_rescale(s, kv0, full, pmask);
-    exp_pv(s, Kb + KBYTES);
+    exp_pv(s, Kb + KBYTES, kv0);
   };
 
   // Every tile is 2 * NDMA DMA instructions per wave (4 at D = 128, 2 at
@@ -1251,10 +1267,12 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& pin, const Wor
 
   const float l_tot = pair_sum32(l_run);
   const float f = m_max == -INFINITY ? 0.f : fast_exp2(m_run - m_max);
+  // (dropout: kept weights times 1 / (1 - p); the row sums stay unscaled)
+  const float fo = DROP ? f * p.drop_scale : f;
   if (p.num_splits == 1) {
     if (myq < p.Sq) {
       const float inv = m_max == -INFINITY ? (p.nan_empty ? __builtin_nanf("") : 0.f)
-                                           : f / (l_tot * f + p.eps);
+                                           : fo / (l_tot * f + p.eps);
       if (p.lse && g == 0)
         p.lse[((int64_t)wi.b * p.H + wi.h) * p.Sq + myq] =
             m_max == -INFINITY ? INFINITY : m_max + log2f(l_tot * f + p.eps);
@@ -1277,8 +1295,8 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& pin, const Wor
 #pragma unroll
       for (int e4 = 0; e4 < 4; ++e4) {
         const int d = db * 32 + 8 * e4 + 4 * g;
-        *(f32x4*)(wo + d) = (f32x4){o[db][4 * e4] * f, o[db][4 * e4 + 1] * f,
-                                    o[db][4 * e4 + 2] * f, o[db][4 * e4 + 3] * f};
+        *(f32x4*)(wo + d) = (f32x4){o[db][4 * e4] * fo, o[db][4 * e4 + 1] * fo,
+                                    o[db][4 * e4 + 2] * fo, o[db][4 * e4 + 3] * fo};
       }
     if (g == 0) {
       p.ws_ml[2 * row] = m_max;
@@ -1328,13 +1346,36 @@ void fa_fwd16_kernel(FwdParams p) {
   }
 }
 
+// The same with dropout on the weights (dense K/V, D = 64 or 128: the direct
+// kernels).
+template <int D, int BN, int NW, bool BF16>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(MPX_FA_WAVES_PER_EU)))
+void fa_fwd16_drop_kernel(FwdParams p) {
+  constexpr int kDStages = MPX_FA_DSTAGES > 0 ? MPX_FA_DSTAGES
+                                              : (131072 / (4 * BN * D) < 4 ? 131072 / (4 * BN * D) : 4);
+  static_assert(MPX_FA_DIRECT && (D == 128 || D == 64) && (BN == 64 || BN == 128) &&
+                    (NW == 8 || NW == 4) && kDStages * 2 * BN * 2 * D <= 131072,
+                "dropout runs on the direct kernels");
+  constexpr int kStageB = 2 * BN * 2 * D;
+  __shared__ __align__(16) unsigned char dst0[kStageB];
+  __shared__ __align__(16) unsigned char dst1[kStageB];
+  __shared__ __align__(16) unsigned char dst2[kDStages >= 3 ? kStageB : 16];
+  __shared__ __align__(16) unsigned char dst3[kDStages == 4 ? kStageB : 16];
+  const WorkSlot ws = decode_slot(p);
+  const int n_items = slot_items(p, ws);
+#pragma nounroll
+  for (int item = 0; item < n_items; ++item)
+    fa16_rows_direct<D, BN, NW, BF16, kDStages, false, true>(p, slot_item(p, ws, item), dst0, dst1,
+                                                             dst2, dst3, nullptr);
+}
+
 // ---------------------------------------------------------------------------
 // fp32 kernel: 32x32x2 f32 MFMA (true fp32 products, for fp32 parity).
 // S^T = K Q^T with k index (4-dim run) dims 8*(ks/4) + 4*g + ks%4; C element e
 // of lane (j, g) holds key 32*nb + 8*(e/4) + 4*g + e%4. PV step (nb, e) has
 // k = g <-> that key, so P^T needs no repacking and V stays row-major in LDS.
 // ---------------------------------------------------------------------------
-template <int D, int BN, int NW, bool PAGED>
+template <int D, int BN, int NW, bool PAGED, bool DROP = false>
 __global__ __launch_bounds__(64 * NW) void fa_fwd32_kernel(FwdParams pin) {
   constexpr int BM = 32 * NW, NT = 64 * NW;
   constexpr int KS = D + 4;  // conflict-free 16-byte reads along rows
@@ -1367,6 +1408,9 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd32_kernel(FwdParams pin) {
 
   const int wq0 = q0 + wave * 32;
   const int myq = wq0 + j;
+  // Dropout: this row's key of the keep-mask hash.
+  const u32 drop_rk =
+      DROP ? drop_row_key((u32)(((int64_t)wi.b * p.H + wi.h) * p.Sq + myq), p.seed0) : 0u;
   f32x4 qf[NQ4];
   if (myq < p.Sq) {
     const f32x4* src = (const f32x4*)(Qp + (int64_t)myq * p.q_ss);
@@ -1542,6 +1586,21 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd32_kernel(FwdParams pin) {
           lsum += x;
         }
       l_run += lsum;
+      if constexpr (DROP) {
+        // Keep mask on the PV operand: elements 2 e2, 2 e2 + 1 of block nb hold
+        // keys kv0 + 32 nb + 8 (e2 / 2) + 4 g + 2 (e2 % 2) + {0, 1}, the hash's
+        // key pair kv0 / 2 + 16 nb + 4 (e2 / 2) + 2 g + e2 % 2.
+        const u32 pair0 = drop_pair_key((u32)(kv0 >> 1) + 2u * g, p.seed1);
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+          for (int e2 = 0; e2 < 8; ++e2) {
+            const u32 bits =
+                drop_bits(drop_rk, pair0 + (u32)(16 * nb + 4 * (e2 >> 1) + (e2 & 1)) * 0x85EBCA77u);
+            if ((bits & 0xffffu) < p.drop_thresh) s[nb][2 * e2] = 0.f;
+            if (bits < (p.drop_thresh << 16)) s[nb][2 * e2 + 1] = 0.f;
+          }
+      }
 
 #pragma unroll
       for (int db = 0; db < NDB; ++db)
@@ -1560,10 +1619,12 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd32_kernel(FwdParams pin) {
 
   const float l_tot = pair_sum32(l_run);
   const float f = m_max == -INFINITY ? 0.f : fast_exp2(m_run - m_max);
+  // (dropout: kept weights times 1 / (1 - p); the row sums stay unscaled)
+  const float fo = DROP ? f * p.drop_scale : f;
   if (p.num_splits == 1) {
     if (myq < p.Sq) {
       const float inv = m_max == -INFINITY ? (p.nan_empty ? __builtin_nanf("") : 0.f)
-                                           : f / (l_tot * f + p.eps);
+                                           : fo / (l_tot * f + p.eps);
       if (p.lse && g == 0)
         p.lse[((int64_t)wi.b * p.H + wi.h) * p.Sq + myq] =
             m_max == -INFINITY ? INFINITY : m_max + log2f(l_tot * f + p.eps);
@@ -1585,8 +1646,8 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd32_kernel(FwdParams pin) {
 #pragma unroll
       for (int e4 = 0; e4 < 4; ++e4) {
         const int d = db * 32 + 8 * e4 + 4 * g;
-        *(f32x4*)(wo + d) = (f32x4){o[db][4 * e4] * f, o[db][4 * e4 + 1] * f,
-                                    o[db][4 * e4 + 2] * f, o[db][4 * e4 + 3] * f};
+        *(f32x4*)(wo + d) = (f32x4){o[db][4 * e4] * fo, o[db][4 * e4 + 1] * fo,
+                                    o[db][4 * e4 + 2] * fo, o[db][4 * e4 + 3] * fo};
       }
     if (g == 0) {
       p.ws_ml[2 * row] = m_max;
@@ -1792,10 +1853,33 @@ hipError_t dispatch_fwd(const FwdParams& p, int D, int dtype, int grid, hipStrea
   }
 }
 
-// Attention kernel(s) for a prepared FwdParams: the forward launch, then the
-// split merge when the plan splits the KV range.
+// The dropout kernels (dense K/V, D = 64 or 128).
+hipError_t dispatch_fwd_drop(const FwdParams& p, int D, int dtype, int grid, hipStream_t st) {
+#define MPX_DROP16(DD, BF)                                                                  \
+  hipLaunchKernelGGL((fa_fwd16_drop_kernel<DD, kBN16<false, DD>, kNumWaves16, BF>), dim3(grid), \
+                     dim3(64 * kNumWaves16), 0, st, p)
+  if (dtype == MPX_F32) {
+    if (D == 64)
+      hipLaunchKernelGGL((fa_fwd32_kernel<64, 64, kNumWaves32, false, true>), dim3(grid),
+                         dim3(64 * kNumWaves32), 0, st, p);
+    else
+      hipLaunchKernelGGL((fa_fwd32_kernel<128, 32, kNumWaves32, false, true>), dim3(grid),
+                         dim3(64 * kNumWaves32), 0, st, p);
+  } else if (dtype == MPX_BF16) {
+    if (D == 64) MPX_DROP16(64, true); else MPX_DROP16(128, true);
+  } else {
+    if (D == 64) MPX_DROP16(64, false); else MPX_DROP16(128, false);
+  }
+#undef MPX_DROP16
+  return hipGetLastError();
+}
+
+// Attention kernel(s) for a prepared FwdParams: the forward launch (with
+// dropout: the dropout kernels), then the split merge when the plan splits
+// the KV range.
 template <bool PAGED>
-int run_fwd(FwdParams& p, const Plan& pl, int D, int dtype, void* workspace, hipStream_t st) {
+int run_fwd(FwdParams& p, const Plan& pl, int D, int dtype, void* workspace, hipStream_t st,
+            bool drop = false) {
   p.ws_o = pl.splits > 1 ? (float*)workspace : nullptr;
   p.ws_ml = pl.splits > 1 ? (float*)workspace + (size_t)pl.splits * p.B * p.H * p.Sq * D : nullptr;
   p.win_left = pl.win_left; p.win_right = pl.win_right;
@@ -1803,7 +1887,10 @@ int run_fwd(FwdParams& p, const Plan& pl, int D, int dtype, void* workspace, hip
   p.n_slots = pl.n_slots; p.paired = pl.paired;
   const long grid_l = (long)p.B * p.H * pl.n_slots * pl.splits;
   MPX_CHECK_ARG(grid_l < (1L << 31), "attention: problem too large");
-  MPX_CHECK_HIP(dispatch_fwd<PAGED>(p, D, dtype, (int)grid_l, st));
+  if (!PAGED && drop)
+    MPX_CHECK_HIP(dispatch_fwd_drop(p, D, dtype, (int)grid_l, st));
+  else
+    MPX_CHECK_HIP(dispatch_fwd<PAGED>(p, D, dtype, (int)grid_l, st));
   if (pl.splits > 1) {
     const long threads = (long)p.B * p.H * p.Sq * (D / 4);
     const int blocks = (int)((threads + 255) / 256);
@@ -1875,6 +1962,9 @@ struct FwdExtras {
   const void* rope_cos = nullptr;
   const void* rope_sin = nullptr;
   int rope_offset = 0, rope_cdt = 0;
+  bool drop = false;  // dropout on the weights (the fields below)
+  uint32_t drop_thresh = 0, seed0 = 0, seed1 = 0;
+  float drop_scale = 1.f;
 };
 }  // namespace
 
@@ -1940,7 +2030,11 @@ static int attn_fwd_entry(const void* q, const void* k, const void* v, void* o,
   p.rope_sin = ex.rope_sin;
   p.rope_offset = ex.rope_offset;
   p.rope_cdt = ex.rope_cdt;
-  return run_fwd<false>(p, pl, D, dtype, workspace, (hipStream_t)stream);
+  p.drop_thresh = ex.drop_thresh;
+  p.seed0 = ex.seed0;
+  p.seed1 = ex.seed1;
+  p.drop_scale = ex.drop_scale;
+  return run_fwd<false>(p, pl, D, dtype, workspace, (hipStream_t)stream, ex.drop);
 }
 
 extern "C" int mpx_attn_fwd_lse(const void* q, const void* k, const void* v, void* o,
@@ -1952,6 +2046,35 @@ extern "C" int mpx_attn_fwd_lse(const void* q, const void* k, const void* v, voi
   clear_error();
   FwdExtras ex;
   ex.lse = lse;
+  return attn_fwd_entry(q, k, v, o, q_strides, k_strides, v_strides, o_strides, B, H, H_kv, Sq,
+                        Sk, D, scale, causal, window_left, window_right, dtype, workspace,
+                        workspace_bytes, stream, ex);
+}
+
+extern "C" int mpx_attn_fwd_dropout(const void* q, const void* k, const void* v, void* o,
+                                    float* lse, const int64_t* q_strides,
+                                    const int64_t* k_strides, const int64_t* v_strides,
+                                    const int64_t* o_strides, int B, int H, int H_kv, int Sq,
+                                    int Sk, int D, float scale, int causal, int window_left,
+                                    int window_right, int dtype, float dropout_p, uint64_t seed,
+                                    void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  MPX_CHECK_ARG(dropout_p >= 0.f && dropout_p < 1.f,
+                "mpx_attn_fwd_dropout: dropout_p must be in [0, 1), got %g", (double)dropout_p);
+  FwdExtras ex;
+  ex.lse = lse;
+  if (dropout_p > 0.f) {
+    if (D != 64 && D != 128) {
+      set_error("mpx_attn_fwd_dropout: head_dim %d not supported (dropout kernels exist for 64, "
+                "128)", D);
+      return MPX_EUNSUPPORTED;
+    }
+    ex.drop = true;
+    ex.drop_thresh = drop_threshold(dropout_p);
+    ex.seed0 = (uint32_t)seed;
+    ex.seed1 = (uint32_t)(seed >> 32);
+    ex.drop_scale = 1.f / (1.f - dropout_p);
+  }
   return attn_fwd_entry(q, k, v, o, q_strides, k_strides, v_strides, o_strides, B, H, H_kv, Sq,
                         Sk, D, scale, causal, window_left, window_right, dtype, workspace,
                         workspace_bytes, stream, ex);

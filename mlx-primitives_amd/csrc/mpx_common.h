@@ -142,6 +142,52 @@ __device__ __forceinline__ void rope_pair(float x1, float x2, float c, float s, 
   y2 = __builtin_fmaf(x1, s, x2 * c);
 }
 
+// ---- dropout on the attention weights ------------------------------------------
+// The keep mask is counter-based: a hash of (seed, row, key), so the backward
+// regenerates the forward's mask without storing it. Row r = (b * H + h) * Sq + q
+// (query head h, counted mod 2^32), key k. One 32-bit hash covers the key pair
+// (2m, 2m + 1): its low 16 bits decide key 2m, its high 16 bits key 2m + 1, and
+// a key is kept when its 16 bits are >= thresh = round(p * 65536) (at most
+// 65535), i.e. with probability 1 - thresh / 65536; kept weights are scaled by
+// 1 / (1 - p) (inverted dropout, attention/flash.py:570-574).
+//   bits(r, m) = lowbias32((r * 0x9E3779B1 + seed0) ^ (m * 0x85EBCA77 + seed1))
+// lowbias32 is C. Wellons' 32-bit integer hash (hash-prospector, 2018):
+//   x ^= x >> 16; x *= 0x7feb352d; x ^= x >> 15; x *= 0x846ca68b; x ^= x >> 16.
+// 0x9E3779B1 is the 32-bit golden-ratio multiplier, 0x85EBCA77 the second
+// xxHash32 prime; both are odd, so distinct rows (pairs) give distinct words.
+__device__ __forceinline__ u32 lowbias32(u32 x) {
+  x ^= x >> 16;
+  x *= 0x7feb352du;
+  x ^= x >> 15;
+  x *= 0x846ca68bu;
+  x ^= x >> 16;
+  return x;
+}
+__device__ __forceinline__ u32 drop_row_key(u32 row, u32 seed0) {
+  return row * 0x9E3779B1u + seed0;
+}
+__device__ __forceinline__ u32 drop_pair_key(u32 pair, u32 seed1) {
+  return pair * 0x85EBCA77u + seed1;
+}
+__device__ __forceinline__ u32 drop_bits(u32 row_key, u32 pair_key) {
+  return lowbias32(row_key ^ pair_key);
+}
+// 16-bit lane mask of a key pair's packed weights: 0xffff over each kept key.
+__device__ __forceinline__ u32 drop_mask2(u32 bits, u32 thresh) {
+  return ((bits & 0xffffu) >= thresh ? 0xffffu : 0u) | (bits >= (thresh << 16) ? 0xffff0000u : 0u);
+}
+// Keep test of one key of the pair: its half of the hash is selected by
+// (half_mask, half_thresh) = (0xffff, thresh) for key 2m, (0xffff0000,
+// thresh << 16) for key 2m + 1.
+__device__ __forceinline__ bool drop_keep(u32 bits, u32 half_mask, u32 half_thresh) {
+  return (bits & half_mask) >= half_thresh;
+}
+// Keep threshold for dropout probability p in [0, 1): round(p * 65536), at most 65535.
+inline u32 drop_threshold(float p) {
+  const double t = (double)p * 65536.0 + 0.5;
+  return t >= 65535.0 ? 65535u : (u32)t;
+}
+
 // ---- LDS staging helpers (gfx950) ---------------------------------------------
 
 // Compile-time integer tag (selects a register set in the unrolled loop).

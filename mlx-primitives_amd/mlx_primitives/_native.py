@@ -92,6 +92,14 @@ def load() -> ctypes.CDLL:
             ctypes.c_float, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
             ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
         ]
+        lib.mpx_attn_fwd_dropout.restype = ctypes.c_int
+        lib.mpx_attn_fwd_dropout.argtypes = [ctypes.c_void_p] * 5 + [_i64p] * 4 + [
+            ctypes.c_int] * 6 + [ctypes.c_float] + [ctypes.c_int] * 4 + [
+            ctypes.c_float, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+        lib.mpx_attn_bwd_dropout.restype = ctypes.c_int
+        lib.mpx_attn_bwd_dropout.argtypes = [ctypes.c_void_p] * 9 + [_i64p] * 8 + [
+            ctypes.c_int] * 6 + [ctypes.c_float] + [ctypes.c_int] * 4 + [
+            ctypes.c_float, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
         lib.mpx_attn_bwd_workspace_bytes.restype = ctypes.c_size_t
         lib.mpx_attn_bwd_workspace_bytes.argtypes = [ctypes.c_int] * 3
         lib.mpx_attn_fwd_workspace_bytes.restype = ctypes.c_size_t
@@ -222,12 +230,13 @@ def attn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor,
              o_strides: Sequence[int], B: int, H: int, Sq: int, Sk: int, D: int,
              scale: float, causal: bool, window_left: int = -1, window_right: int = -1,
              H_kv: Optional[int] = None, lse: Optional[torch.Tensor] = None,
-             q_rope: Optional[tuple] = None) -> None:
+             q_rope: Optional[tuple] = None, dropout: Optional[tuple] = None) -> None:
     """Enqueue mpx_attn_fwd_lse on the current stream (strides in (b, h, s) order;
     K/V carry H_kv heads, default H; lse: optional contiguous (B, H, Sq) float32
     that receives each row's base-2 log-sum-exp for the backward). With
     q_rope = (cos_cache, sin_cache, q_offset) the kernel rotates Q on load
-    (mpx_attn_fwd_rope)."""
+    (mpx_attn_fwd_rope); with dropout = (dropout_p, seed) the weights are
+    dropped by the counter-based keep mask (mpx_attn_fwd_dropout)."""
     lib = load()
     dev = require_device(q, k, v, o)
     code = dtype_code(q.dtype)
@@ -255,13 +264,17 @@ def attn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor,
     ws_bytes = int(lib.mpx_attn_fwd_workspace_bytes(
         B, H, Sq, Sk, D, int(causal), window_left, window_right, code))
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
-    rc = lib.mpx_attn_fwd_lse(
-        q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
-        lse.data_ptr() if lse is not None else None,
-        _strides(q_strides), _strides(k_strides), _strides(v_strides), _strides(o_strides),
-        B, H, H if H_kv is None else H_kv, Sq, Sk, D, float(scale), int(causal),
-        int(window_left), int(window_right), code,
-        ws.data_ptr() if ws is not None else None, ws_bytes, _stream_ptr(dev))
+    args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+            lse.data_ptr() if lse is not None else None,
+            _strides(q_strides), _strides(k_strides), _strides(v_strides), _strides(o_strides),
+            B, H, H if H_kv is None else H_kv, Sq, Sk, D, float(scale), int(causal),
+            int(window_left), int(window_right), code)
+    tail = (ws.data_ptr() if ws is not None else None, ws_bytes, _stream_ptr(dev))
+    if dropout is not None:
+        p, seed = dropout
+        rc = lib.mpx_attn_fwd_dropout(*args, float(p), int(seed) & (2**64 - 1), *tail)
+    else:
+        rc = lib.mpx_attn_fwd_lse(*args, *tail)
     _check(rc, "mpx_attn_fwd failed")
 
 
@@ -269,20 +282,26 @@ def attn_bwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor,
              dout: torch.Tensor, lse: torch.Tensor, dq: torch.Tensor, dk: torch.Tensor,
              dv: torch.Tensor, strides: Sequence[Sequence[int]], B: int, H: int, H_kv: int,
              Sq: int, Sk: int, D: int, scale: float, causal: bool, window_left: int = -1,
-             window_right: int = -1) -> None:
+             window_right: int = -1, dropout: Optional[tuple] = None) -> None:
     """Enqueue mpx_attn_bwd on the current stream. ``strides`` holds the (b, h, s)
-    element strides of q, k, v, o, dout, dq, dk, dv in that order."""
+    element strides of q, k, v, o, dout, dq, dk, dv in that order; dropout =
+    (dropout_p, seed) of the forward (mpx_attn_bwd_dropout)."""
     lib = load()
     dev = require_device(q, k, v, o, dout, lse, dq, dk, dv)
     code = dtype_code(q.dtype)
     ws_bytes = int(lib.mpx_attn_bwd_workspace_bytes(B, H, Sq))
     ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=dev)
-    rc = lib.mpx_attn_bwd(
-        q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), dout.data_ptr(),
-        lse.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
-        *[_strides(s) for s in strides],
-        B, H, H_kv, Sq, Sk, D, float(scale), int(causal), int(window_left), int(window_right),
-        code, ws.data_ptr(), ws_bytes, _stream_ptr(dev))
+    args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), dout.data_ptr(),
+            lse.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+            *[_strides(s) for s in strides],
+            B, H, H_kv, Sq, Sk, D, float(scale), int(causal), int(window_left),
+            int(window_right), code)
+    tail = (ws.data_ptr(), ws_bytes, _stream_ptr(dev))
+    if dropout is not None:
+        p, seed = dropout
+        rc = lib.mpx_attn_bwd_dropout(*args, float(p), int(seed) & (2**64 - 1), *tail)
+    else:
+        rc = lib.mpx_attn_bwd(*args, *tail)
     _check(rc, "mpx_attn_bwd failed")
 
 

@@ -60,22 +60,22 @@ class _FlashAttentionFn(torch.autograd.Function):
     autograd differentiates them."""
 
     @staticmethod
-    def forward(ctx, q, k, v, layout, scale, causal, window_left, window_right):
+    def forward(ctx, q, k, v, layout, scale, causal, window_left, window_right, dropout):
         B, H, H_kv, Sq, Sk, D = _dims(q, k, layout)
         o = torch.empty(q.shape, dtype=q.dtype, device=q.device)
         lse = torch.empty((B, H, Sq), dtype=torch.float32, device=q.device)
         _native.attn_fwd(q, k, v, o, _bhs(q, layout), _bhs(k, layout), _bhs(v, layout),
                          _bhs(o, layout), B, H, Sq, Sk, D, scale, causal, window_left,
-                         window_right, H_kv=H_kv, lse=lse)
+                         window_right, H_kv=H_kv, lse=lse, dropout=dropout)
         ctx.save_for_backward(q, k, v, o, lse)
-        ctx.cfg = (layout, scale, causal, window_left, window_right)
+        ctx.cfg = (layout, scale, causal, window_left, window_right, dropout)
         return o
 
     @staticmethod
     @torch.autograd.function.once_differentiable
     def backward(ctx, dout):
         q, k, v, o, lse = ctx.saved_tensors
-        layout, scale, causal, window_left, window_right = ctx.cfg
+        layout, scale, causal, window_left, window_right, dropout = ctx.cfg
         B, H, H_kv, Sq, Sk, D = _dims(q, k, layout)
         dout = _prepare(dout, D)
         dq = torch.empty(q.shape, dtype=q.dtype, device=q.device)
@@ -83,11 +83,24 @@ class _FlashAttentionFn(torch.autograd.Function):
         dv = torch.empty(v.shape, dtype=v.dtype, device=v.device)
         strides = [_bhs(x, layout) for x in (q, k, v, o, dout, dq, dk, dv)]
         _native.attn_bwd(q, k, v, o, dout, lse, dq, dk, dv, strides, B, H, H_kv, Sq, Sk, D,
-                         scale, causal, window_left, window_right)
-        return dq, dk, dv, None, None, None, None, None
+                         scale, causal, window_left, window_right, dropout=dropout)
+        return dq, dk, dv, None, None, None, None, None, None
 
 
-def _attention_with_grad(q, k, v, layout, scale, causal, window_left, window_right):
+def dropout_seed() -> int:
+    """A 64-bit seed for the dropout keep mask, drawn from torch's default
+    (CPU) generator, so torch.manual_seed makes the masks reproducible."""
+    lo, hi = torch.randint(0, 2**32, (2,), dtype=torch.int64).tolist()
+    return lo | (hi << 32)
+
+
+def check_dropout_p(dropout_p: float, name: str) -> None:
+    if not 0.0 <= dropout_p < 1.0:
+        raise ValueError(f"{name}: dropout_p must be in [0, 1), got {dropout_p}")
+
+
+def _attention_with_grad(q, k, v, layout, scale, causal, window_left, window_right,
+                         dropout=None):
     if not scale > 0:
         raise NotImplementedError(
             "mlx_primitives (MI355X build) differentiates attention with scale > 0 only "
@@ -95,35 +108,49 @@ def _attention_with_grad(q, k, v, layout, scale, causal, window_left, window_rig
     D = q.shape[-1]
     dk = 64 if D <= 64 else 128
     qk, kk, vk = (_prepare(x, dk) for x in (q, k, v))
-    o = _FlashAttentionFn.apply(qk, kk, vk, layout, scale, causal, window_left, window_right)
+    o = _FlashAttentionFn.apply(qk, kk, vk, layout, scale, causal, window_left, window_right,
+                                dropout)
     return o[..., :D].contiguous() if dk != D else o
 
 
 def run_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, layout: Layout,
                   scale: float, causal: bool, window_left: int = -1,
-                  window_right: int = -1, q_rope: Optional[tuple] = None) -> torch.Tensor:
+                  window_right: int = -1, q_rope: Optional[tuple] = None,
+                  dropout_p: float = 0.0, dropout_seed_value: Optional[int] = None
+                  ) -> torch.Tensor:
     """Attention forward on the GPU kernel; returns a new tensor shaped like q.
     When autograd tracks q, k or v, the result is differentiable through the
     gfx950 backward kernels. q_rope = (cos_cache, sin_cache, q_offset) rotates Q
-    inside the kernel (16-bit, D in 32/64/128, no gradients)."""
+    inside the kernel (16-bit, D in 32/64/128, no gradients). dropout_p > 0
+    drops attention weights by the kernels' counter-based keep mask, seeded by
+    dropout_seed_value or else a fresh dropout_seed(); the backward regenerates
+    the same mask."""
     _native.require_device(q, k, v)
     B, H, H_kv, Sq, Sk, D = _dims(q, k, layout)
     if q.numel() == 0:
         return torch.empty(q.shape, dtype=q.dtype, device=q.device)
     dk = kernel_head_dim(D)
+    dropout = None
+    if dropout_p > 0.0:
+        dropout = (float(dropout_p),
+                   dropout_seed() if dropout_seed_value is None else int(dropout_seed_value))
     if q_rope is not None:
-        if dk != D or q.dtype == torch.float32 or _needs_grad(q, k, v):
-            raise ValueError("in-kernel Q rotation needs 16-bit inputs, D in (32, 64, 128) "
-                             "and no gradients")
-    elif _needs_grad(q, k, v):
-        return _attention_with_grad(q, k, v, layout, scale, causal, window_left, window_right)
+        if dk != D or q.dtype == torch.float32 or _needs_grad(q, k, v) or dropout:
+            raise ValueError("in-kernel Q rotation needs 16-bit inputs, D in (32, 64, 128), "
+                             "no gradients and no dropout")
+    elif _needs_grad(q, k, v) or dropout:
+        if _needs_grad(q, k, v):
+            return _attention_with_grad(q, k, v, layout, scale, causal, window_left,
+                                        window_right, dropout)
+        # (the dropout kernels take D = 64 or 128)
+        dk = 64 if D <= 64 else 128
     qk, kk, vk = (_prepare(x, dk) for x in (q, k, v))
     out_shape = list(q.shape)
     out_shape[-1] = dk
     o = torch.empty(out_shape, dtype=q.dtype, device=q.device)
     _native.attn_fwd(qk, kk, vk, o, _bhs(qk, layout), _bhs(kk, layout), _bhs(vk, layout),
                      _bhs(o, layout), B, H, Sq, Sk, dk, scale, causal, window_left,
-                     window_right, H_kv=H_kv, q_rope=q_rope)
+                     window_right, H_kv=H_kv, q_rope=q_rope, dropout=dropout)
     if dk != D:
         o = o[..., :D].contiguous()
     return o

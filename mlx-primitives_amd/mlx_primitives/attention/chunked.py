@@ -16,7 +16,7 @@ from typing import Optional, Tuple
 
 import torch
 
-from mlx_primitives.attention._launch import run_attention
+from mlx_primitives.attention._launch import check_dropout_p, run_attention
 from mlx_primitives.constants import Layout
 
 
@@ -35,16 +35,14 @@ def chunked_cross_attention(
 
     causal masks kv_pos > q_pos on absolute positions (top-left), as the
     reference (chunked.py:149-154 via compute_chunk_attention). dropout_p > 0
-    in training raises NotImplementedError.
+    in training drops attention weights, kept ones scaled by 1 / (1 - dropout_p)
+    (chunked.py:109-110, 248-251), with the kernels' counter-based keep mask;
+    dropout_p must be in [0, 1).
     """
     if q.ndim != 4:
         raise ValueError(f"Expected 4D tensors (batch, seq, heads, dim), got {q.ndim}D")
     if scale is None:
         scale = 1.0 / math.sqrt(q.shape[-1])
-    if dropout_p > 0.0 and training:
-        raise NotImplementedError(
-            "chunked_cross_attention: dropout_p > 0 in training mode is not supported by "
-            "the MI355X kernels")
     if k.ndim != 4 or v.ndim != 4:
         raise ValueError("k and v must be 4D tensors (batch, seq_kv, heads, dim)")
     if k.shape != v.shape:
@@ -54,7 +52,9 @@ def chunked_cross_attention(
             f"q {tuple(q.shape)} and k {tuple(k.shape)} must agree on batch, heads and dim")
     if q.dtype != k.dtype or q.dtype != v.dtype:
         raise ValueError(f"Q/K/V dtype mismatch: Q={q.dtype}, K={k.dtype}, V={v.dtype}")
-    return run_attention(q, k, v, Layout.BSHD, scale, causal=causal)
+    drop = dropout_p if training and dropout_p > 0.0 else 0.0
+    check_dropout_p(drop, "chunked_cross_attention")
+    return run_attention(q, k, v, Layout.BSHD, scale, causal=causal, dropout_p=drop)
 
 
 class ChunkedCrossAttention:

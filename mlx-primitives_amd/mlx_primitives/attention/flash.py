@@ -19,7 +19,7 @@ from typing import Optional, Tuple, Union
 
 import torch
 
-from mlx_primitives.attention._launch import run_attention
+from mlx_primitives.attention._launch import check_dropout_p, run_attention
 from mlx_primitives.constants import Layout
 
 
@@ -97,10 +97,14 @@ def flash_attention(
         every key (utils/masking.py:52-56); otherwise it is the tiled path's
         top-left rule (kv <= q).
       block_q, block_kv, use_metal: accepted, no effect on the result.
-      dropout_p, training: dropout on the attention weights is not
-        implemented by the MI355X kernels (raises NotImplementedError when
-        dropout_p > 0 and training, BSHD; BHSD ignores dropout like the
-        reference's BHSD branch).
+      dropout_p, training: with dropout_p > 0 and training (BSHD), each
+        attention weight is dropped with probability dropout_p and the kept
+        ones scaled by 1 / (1 - dropout_p) (flash.py:202-205, 570-574). The
+        keep mask is a counter-based hash of (seed, batch, head, query, key)
+        evaluated inside the kernels (never stored); the seed comes from
+        torch's default generator, and the backward regenerates the same
+        mask. dropout_p must be in [0, 1). BHSD ignores dropout like the
+        reference's BHSD branch.
       layout: "BSHD" / "BHSD" or Layout.
       enable_gqa: keyword-only extension (the reference requires equal head
         counts, flash.py:151-154): K and V may carry H_kv heads, H a multiple
@@ -113,18 +117,18 @@ def flash_attention(
     head_dim = q.shape[-1]
     if scale is None:
         scale = 1.0 / math.sqrt(head_dim)
-    if layout == Layout.BSHD and dropout_p > 0.0 and training:
-        raise NotImplementedError(
-            "flash_attention: dropout_p > 0 in training mode is not supported by the "
-            "MI355X kernels")
+    # Dropout applies to BSHD in training; BHSD ignores it, as the reference's
+    # BHSD branch does (flash.py:161-191 returns before the dropout check).
+    drop = dropout_p if (layout == Layout.BSHD and training and dropout_p > 0.0) else 0.0
+    check_dropout_p(drop, "flash_attention")
     if causal:
         seq_q, seq_kv = ((q.shape[1], k.shape[1]) if layout == Layout.BSHD
                          else (q.shape[2], k.shape[2]))
         if seq_kv > seq_q:
             # bottom-right diagonal: j <= i + (Sk - Sq)
             return run_attention(q, k, v, layout, scale, causal=False,
-                                 window_right=seq_kv - seq_q)
-    return run_attention(q, k, v, layout, scale, causal=causal)
+                                 window_right=seq_kv - seq_q, dropout_p=drop)
+    return run_attention(q, k, v, layout, scale, causal=causal, dropout_p=drop)
 
 
 class FlashAttention:

@@ -16,7 +16,7 @@ from typing import Optional
 
 import torch
 
-from mlx_primitives.attention._launch import run_attention
+from mlx_primitives.attention._launch import check_dropout_p, run_attention
 from mlx_primitives.constants import Layout
 
 
@@ -36,17 +36,15 @@ def sliding_window_attention(
     q, k, v: (batch, seq, heads, dim) ROCm tensors of one dtype.
     window_size: one-sided window; query i sees keys [i - W, i] if causal,
       else [i - W, i + W].
-    scale defaults to 1/sqrt(dim); use_metal is accepted and has no effect;
-    dropout_p > 0 in training raises NotImplementedError.
+    scale defaults to 1/sqrt(dim); use_metal is accepted and has no effect.
+    dropout_p > 0 in training drops attention weights, kept ones scaled by
+    1 / (1 - dropout_p) (sliding_window.py:280-282, 617-620), with the kernels'
+    counter-based keep mask; dropout_p must be in [0, 1).
     """
     if q.ndim != 4:
         raise ValueError(f"Expected 4D tensors (batch, seq, heads, dim), got {q.ndim}D")
     if scale is None:
         scale = 1.0 / math.sqrt(q.shape[-1])
-    if dropout_p > 0.0 and training:
-        raise NotImplementedError(
-            "sliding_window_attention: dropout_p > 0 in training mode is not supported by "
-            "the MI355X kernels")
     if window_size < 0:
         raise ValueError(f"window_size must be non-negative, got {window_size}")
     if k.shape != q.shape or v.shape != q.shape:
@@ -55,9 +53,11 @@ def sliding_window_attention(
             f"{tuple(v.shape)}")
     if q.dtype != k.dtype or q.dtype != v.dtype:
         raise ValueError(f"Q/K/V dtype mismatch: Q={q.dtype}, K={k.dtype}, V={v.dtype}")
+    drop = dropout_p if training and dropout_p > 0.0 else 0.0
+    check_dropout_p(drop, "sliding_window_attention")
     window_right = -1 if causal else window_size
     return run_attention(q, k, v, Layout.BSHD, scale, causal=causal,
-                         window_left=window_size, window_right=window_right)
+                         window_left=window_size, window_right=window_right, dropout_p=drop)
 
 
 def create_sliding_window_mask(seq_len: int, window_size: int, causal: bool = True,

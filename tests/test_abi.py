@@ -34,7 +34,7 @@ def test_header_declares_expected_entry_points():
         "mpx_paged_prefill_workspace_bytes", "mpx_kv_append", "mpx_rope", "mpx_attn_fwd_gqa",
         "mpx_paged_decode_gqa", "mpx_paged_prefill_gqa", "mpx_attn_fwd_lse", "mpx_attn_bwd",
         "mpx_attn_bwd_workspace_bytes", "mpx_attn_fwd_rope", "mpx_paged_decode_noalloc",
-        "mpx_rope_at", "mpx_kv_append_rope"])
+        "mpx_rope_at", "mpx_kv_append_rope", "mpx_attn_fwd_dropout", "mpx_attn_bwd_dropout"])
 
 
 def test_library_exports_every_declared_symbol(lib):
@@ -232,3 +232,25 @@ def test_fwd_rope_validation(lib):
     assert _fwd_rope(lib, cos=None) == _native.MPX_EINVAL and b"null" in lib.mpx_last_error()
     assert _fwd_rope(lib, cos=24) == _native.MPX_EINVAL and b"aligned" in lib.mpx_last_error()
     assert _fwd_rope(lib, Sq=0, cos=None) == _native.MPX_OK
+
+
+def test_dropout_entries_validation(lib):
+    st = (ctypes.c_int64 * 3)(8 * 64, 8 * 64, 64)
+
+    def fwd(p=0.1, D=64, dtype=2, ptr=16, Sq=8):
+        return lib.mpx_attn_fwd_dropout(ptr, ptr, ptr, ptr, None, st, st, st, st, 1, 1, 1, Sq, 8,
+                                        D, 0.1, 1, -1, -1, dtype, p, 12345, None, 0, None)
+
+    def bwd(p=0.1, D=64, scale=0.1):
+        return lib.mpx_attn_bwd_dropout(*([16] * 9), *([st] * 8), 1, 1, 1, 8, 8, D, scale, 1, -1,
+                                        -1, 2, p, 12345, 16, 1 << 20, None)
+
+    for p in (1.0, -0.5, float("nan")):
+        assert fwd(p=p) == _native.MPX_EINVAL and b"dropout_p" in lib.mpx_last_error()
+        assert bwd(p=p) == _native.MPX_EINVAL and b"dropout_p" in lib.mpx_last_error()
+    assert fwd(D=32) == _native.MPX_EUNSUPPORTED and b"64, 128" in lib.mpx_last_error()
+    assert bwd(D=32) == _native.MPX_EUNSUPPORTED
+    assert fwd(dtype=6) == _native.MPX_EINVAL and b"dtype" in lib.mpx_last_error()
+    assert fwd(ptr=24) == _native.MPX_EINVAL and b"aligned" in lib.mpx_last_error()
+    assert bwd(scale=-1.0) == _native.MPX_EINVAL and b"positive" in lib.mpx_last_error()
+    assert fwd(Sq=0) == _native.MPX_OK  # empty problem: nothing enqueued

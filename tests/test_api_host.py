@@ -68,13 +68,20 @@ def test_no_cpu_fallback():
                         torch.ones(2, dtype=torch.int32))
 
 
-def test_dropout_not_silently_dropped():
+def test_dropout_validated_and_no_cpu_fallback():
     x = t(1, 8, 2, 64)
-    with pytest.raises(NotImplementedError):
+    with pytest.raises(ValueError, match="dropout_p"):
+        flash_attention(x, x, x, dropout_p=1.0)
+    with pytest.raises(ValueError, match="dropout_p"):
+        sliding_window_attention(x, x, x, 2, dropout_p=1.0)
+    with pytest.raises(ValueError, match="dropout_p"):
+        chunked_cross_attention(x, x, x, dropout_p=2.0)
+    # a valid rate runs on the GPU kernels only
+    with pytest.raises(RuntimeError, match="ROCm device tensors only"):
         flash_attention(x, x, x, dropout_p=0.1)
-    with pytest.raises(NotImplementedError):
+    with pytest.raises(RuntimeError, match="ROCm device tensors only"):
         sliding_window_attention(x, x, x, 2, dropout_p=0.1)
-    with pytest.raises(NotImplementedError):
+    with pytest.raises(RuntimeError, match="ROCm device tensors only"):
         chunked_cross_attention(x, x, x, dropout_p=0.1)
 
 

@@ -1,0 +1,254 @@
+"""GPU parity of attention with dropout (mpx_attn_fwd_dropout /
+mpx_attn_bwd_dropout through flash_attention, sliding_window_attention,
+chunked_cross_attention and autograd) against the CPU oracle
+(oracle/dropout.py) with the same seed.
+
+  * The keep mask bit for bit: with Q = 0 every visible key weighs the same
+    and V[k] = one-hot(k mod D) makes output column d count the kept visible
+    keys k = d (mod D): O[q, d] * n_visible(q) * (1 - p) is that count (an
+    integer: float32 / float16 exactly, bfloat16 to well under 0.5 for the
+    counts used), compared with the oracle's mask for every row, column,
+    batch and head, on the split-KV and the single-pass forward.
+  * The forward on random inputs: float32 rtol 1e-4 / atol 1e-5, 16-bit
+    max-abs 2e-2 against the float64 oracle (the plain forward's bars).
+  * The gradients: the plain backward's bars (tests/test_gpu_attention_bwd.py:
+    elementwise float32 1e-3 / 1e-4, float16 1e-2, bfloat16 1e-1; normwise
+    2e-5 / 2e-3 / 1.5e-2) scaled by 1 / (1 - p) for the kept weights' scale.
+  * The API: torch.manual_seed makes the mask reproducible, the measured
+    keep rate is 1 - p within 5 sigma, dropout_p = 0 or training=False is the
+    plain forward bit for bit (negative dropout_p too, as in the reference),
+    dropout_p >= 1 is a ValueError.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from mlx_primitives.attention import (chunked_cross_attention, flash_attention,
+                                      sliding_window_attention)
+from mlx_primitives.attention._launch import dropout_seed, run_attention
+from mlx_primitives.constants import Layout
+from oracle import dropout as od
+
+pytestmark = pytest.mark.gpu
+
+DTYPES = [torch.float32, torch.float16, torch.bfloat16]
+SEED = 0x9E3779B97F4A7C15
+GRAD_TOL = {torch.float32: (1e-3, 1e-4, 2e-5), torch.float16: (1e-2, 1e-2, 2e-3),
+            torch.bfloat16: (1e-1, 1e-1, 1.5e-2)}
+
+
+def rnd(shape, seed, dtype, mult=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(shape, generator=g) * mult).to(dtype)
+
+
+def visible(Sq, Sk, causal, wl=-1, wr=-1):
+    qi, ki = np.arange(Sq)[:, None], np.arange(Sk)[None, :]
+    vis = np.ones((Sq, Sk), dtype=bool)
+    if causal:
+        vis &= ki <= qi
+    if wl >= 0:
+        vis &= qi - ki <= wl
+    if wr >= 0 and not causal:
+        vis &= ki - qi <= wr
+    return vis
+
+
+def mask_counts(device, dtype, B, H, Sq, Sk, D, p, seed, causal, wl=-1, wr=-1):
+    """(measured, expected) kept-key counts per (b, h, q, residue d)."""
+    q = torch.zeros((B, Sq, H, D), dtype=dtype, device=device)
+    k = rnd((B, Sk, H, D), 1, dtype).to(device)
+    v = torch.zeros((B, Sk, H, D), dtype=dtype)
+    v[:, torch.arange(Sk), :, torch.arange(Sk) % D] = 1.0
+    v = v.to(device)
+    out = run_attention(q, k, v, Layout.BSHD, 1.0, causal, wl, wr, dropout_p=p,
+                        dropout_seed_value=seed)
+    torch.cuda.synchronize()
+    vis = visible(Sq, Sk, causal, wl, wr)
+    n = vis.sum(axis=1).astype(np.float64)  # (Sq,)
+    got = out.double().cpu().numpy().transpose(0, 2, 1, 3)  # (B, H, Sq, D)
+    measured = got * n[None, None, :, None] * (1.0 - p)
+    keep = od.keep_mask(B, H, Sq, Sk, p, seed) & vis[None, None]
+    onehot = (np.arange(Sk)[:, None] % D) == np.arange(D)[None, :]
+    expected = keep.astype(np.float64) @ onehot.astype(np.float64)
+    return measured, expected
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("causal", [False, True])
+def test_forward_keep_mask_bit_exact(device, dtype, D, causal):
+    # B * H * q-tiles well below the CU count: the split-KV path and its merge.
+    B, H, Sq, Sk, p = 2, 3, 200, 1024, 0.3
+    measured, expected = mask_counts(device, dtype, B, H, Sq, Sk, D, p, SEED, causal)
+    err = np.abs(measured - expected).max()
+    assert err < 0.25, err
+    assert np.array_equal(np.rint(measured), expected)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_forward_keep_mask_single_pass_and_window(device, dtype):
+    # Many (batch, head) rows: one pass per q-tile (no split), paired causal
+    # slots on the 16-bit kernel; then a sliding window.
+    B, H, Sq, Sk, D, p = 4, 64, 256, 256, 128, 0.5
+    measured, expected = mask_counts(device, dtype, B, H, Sq, Sk, D, p, 77, True)
+    assert np.array_equal(np.rint(measured), expected)
+    assert np.abs(measured - expected).max() < 0.25
+    measured, expected = mask_counts(device, dtype, 2, 4, 300, 300, 64, 0.2, 78, True, wl=37)
+    assert np.array_equal(np.rint(measured), expected)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("causal", [True, False])
+def test_forward_vs_oracle(device, dtype, D, causal):
+    B, S, H, p = 2, 333, 4, 0.25
+    q, k, v = (rnd((B, S, H, D), i, dtype) for i in range(3))
+    out = run_attention(q.to(device), k.to(device), v.to(device), Layout.BSHD,
+                        1 / math.sqrt(D), causal, dropout_p=p, dropout_seed_value=SEED + D)
+    torch.cuda.synchronize()
+    ref = od.attention_dropout(*(x.double().numpy() for x in (q, k, v)), 1 / math.sqrt(D),
+                               causal, p, SEED + D)
+    got = out.double().cpu().numpy()
+    assert np.isfinite(got).all()
+    if dtype == torch.float32:
+        np.testing.assert_allclose(got, ref, rtol=1e-4, atol=1e-5)
+    else:
+        assert np.abs(got - ref).max() <= 2e-2
+
+
+def check_grads(got, want, dtype, p):
+    rtol, atol, nrel = GRAD_TOL[dtype]
+    atol = atol / (1.0 - p)
+    for name, g, w in zip(("dq", "dk", "dv"), got, want):
+        assert g.dtype == dtype and tuple(g.shape) == w.shape, name
+        gn = g.double().cpu().numpy()
+        assert np.isfinite(gn).all(), name
+        np.testing.assert_allclose(gn, w, rtol=rtol, atol=atol, err_msg=name)
+        rms = np.linalg.norm(w) / math.sqrt(w.size)
+        if rms > atol:
+            err = np.linalg.norm(gn - w) / np.linalg.norm(w)
+            assert err <= nrel, f"{name}: normwise relative error {err:.3e} > {nrel}"
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("causal,wl,H_kv", [(True, -1, 4), (False, -1, 4), (True, 50, 4),
+                                            (True, -1, 2)])
+def test_grad_vs_oracle(device, dtype, D, causal, wl, H_kv):
+    B, Sq, Sk, H, p, seed = 2, 300, 300, 4, 0.2, SEED ^ (D * 31 + H_kv)
+    scale = 1 / math.sqrt(D)
+    q = rnd((B, Sq, H, D), 10, dtype)
+    k = rnd((B, Sk, H_kv, D), 11, dtype)
+    v = rnd((B, Sk, H_kv, D), 12, dtype)
+    do = rnd((B, Sq, H, D), 13, dtype)
+    qd, kd, vd = (x.to(device).requires_grad_(True) for x in (q, k, v))
+    out = run_attention(qd, kd, vd, Layout.BSHD, scale, causal, wl, -1, dropout_p=p,
+                        dropout_seed_value=seed)
+    out.backward(do.to(device))
+    torch.cuda.synchronize()
+    a = lambda x: x.double().numpy()
+    ref_o = od.attention_dropout(a(q), a(k), a(v), scale, causal, p, seed, wl)
+    got_o = out.detach().double().cpu().numpy()
+    if dtype == torch.float32:
+        np.testing.assert_allclose(got_o, ref_o, rtol=1e-4, atol=1e-5)
+    else:
+        assert np.abs(got_o - ref_o).max() <= 2e-2
+    want = od.attention_dropout_grad(a(q), a(k), a(v), a(do), scale, causal, p, seed, wl)
+    check_grads((qd.grad, kd.grad, vd.grad), want, dtype, p)
+
+
+def test_api_seed_reproducible_and_keep_rate(device):
+    B, S, H, D, p = 2, 512, 8, 64, 0.4
+    q, k, v = (rnd((B, S, H, D), 20 + i, torch.bfloat16).to(device) for i in range(3))
+    torch.manual_seed(5)
+    a = flash_attention(q, k, v, causal=True, dropout_p=p)
+    torch.manual_seed(5)
+    b = flash_attention(q, k, v, causal=True, dropout_p=p)
+    torch.manual_seed(5)
+    seed = dropout_seed()
+    c = run_attention(q, k, v, Layout.BSHD, 1 / math.sqrt(D), True, dropout_p=p,
+                      dropout_seed_value=seed)
+    torch.manual_seed(6)
+    d = flash_attention(q, k, v, causal=True, dropout_p=p)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b) and torch.equal(a, c)
+    assert not torch.equal(a, d)
+    # keep rate of the API's mask, counted through the kernel (non-causal)
+    measured, expected = mask_counts(device, torch.float32, 1, 8, 64, 1024, 64, p, seed, False)
+    assert np.array_equal(np.rint(measured), expected)
+    kept, total = expected.sum(), 8 * 64 * 1024
+    qk = 1 - od.threshold(p) / 65536
+    assert abs(kept / total - qk) <= 5 * math.sqrt(qk * (1 - qk) / total)
+
+
+def test_no_dropout_is_plain_forward(device):
+    q, k, v = (rnd((2, 100, 4, 64), 30 + i, torch.float16).to(device) for i in range(3))
+    plain = flash_attention(q, k, v, causal=True)
+    assert torch.equal(flash_attention(q, k, v, causal=True, dropout_p=0.3, training=False),
+                       plain)
+    assert torch.equal(flash_attention(q, k, v, causal=True, dropout_p=0.0), plain)
+    # BHSD ignores dropout, as the reference's BHSD branch
+    qb, kb, vb = (x.transpose(1, 2) for x in (q, k, v))
+    assert torch.equal(flash_attention(qb, kb, vb, causal=True, dropout_p=0.3, layout="BHSD"),
+                       plain.transpose(1, 2))
+    with pytest.raises(ValueError, match="dropout_p"):
+        flash_attention(q, k, v, dropout_p=1.0)
+    with pytest.raises(ValueError, match="dropout_p"):
+        sliding_window_attention(q, k, v, 8, dropout_p=1.0)
+    with pytest.raises(ValueError, match="dropout_p"):
+        chunked_cross_attention(q, k, v, dropout_p=1.5)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_sliding_window_and_chunked_api(device, dtype):
+    B, S, H, D, p = 2, 257, 4, 32, 0.15
+    q, k, v = (rnd((B, S, H, D), 40 + i, dtype) for i in range(3))
+    kl, vl = rnd((B, 700, H, D), 43, dtype), rnd((B, 700, H, D), 44, dtype)
+    a = lambda x: x.double().numpy()
+    scale = 1 / math.sqrt(D)
+    cases = [
+        (lambda: sliding_window_attention(q.to(device), k.to(device), v.to(device), 20,
+                                          dropout_p=p),
+         lambda s: od.attention_dropout(a(q), a(k), a(v), scale, True, p, s, 20)),
+        (lambda: sliding_window_attention(q.to(device), k.to(device), v.to(device), 20,
+                                          causal=False, dropout_p=p),
+         lambda s: od.attention_dropout(a(q), a(k), a(v), scale, False, p, s, 20, 20)),
+        (lambda: chunked_cross_attention(q.to(device), kl.to(device), vl.to(device),
+                                         chunk_size=128, dropout_p=p),
+         lambda s: od.attention_dropout(a(q), a(kl), a(vl), scale, False, p, s)),
+        (lambda: chunked_cross_attention(q.to(device), kl.to(device), vl.to(device),
+                                         causal=True, dropout_p=p),
+         lambda s: od.attention_dropout(a(q), a(kl), a(vl), scale, True, p, s)),
+    ]
+    for i, (run, ref) in enumerate(cases):
+        torch.manual_seed(100 + i)
+        out = run()
+        torch.manual_seed(100 + i)
+        want = ref(dropout_seed())
+        torch.cuda.synchronize()
+        got = out.double().cpu().numpy()
+        assert got.shape == want.shape
+        if dtype == torch.float32:
+            np.testing.assert_allclose(got, want, rtol=1e-4, atol=1e-5, err_msg=str(i))
+        else:
+            assert np.abs(got - want).max() <= 2e-2, i
+
+
+def test_chunked_grad_with_dropout(device):
+    B, Sq, Sk, H, D, p = 1, 130, 400, 2, 128, 0.3
+    q, k, v, do = (rnd(s, 50 + i, torch.float16) for i, s in
+                   enumerate([(B, Sq, H, D), (B, Sk, H, D), (B, Sk, H, D), (B, Sq, H, D)]))
+    qd, kd, vd = (x.to(device).requires_grad_(True) for x in (q, k, v))
+    torch.manual_seed(9)
+    out = chunked_cross_attention(qd, kd, vd, dropout_p=p)
+    out.backward(do.to(device))
+    torch.cuda.synchronize()
+    torch.manual_seed(9)
+    seed = dropout_seed()
+    a = lambda x: x.double().numpy()
+    want = od.attention_dropout_grad(a(q), a(k), a(v), a(do), 1 / math.sqrt(D), False, p, seed)
+    check_grads((qd.grad, kd.grad, vd.grad), want, torch.float16, p)
