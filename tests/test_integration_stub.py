@@ -35,7 +35,8 @@ def test_stub_loads_and_binds():
         ns["_raise"](-1)
     for fn in ("flash_attention_fwd", "paged_attention_decode", "paged_attention_prefill",
                "store_kv", "rope", "flash_attention_fwd_lse", "flash_attention_bwd",
-               "fused_rope_attention_fwd", "store_kv_rope", "rope_at"):
+               "fused_rope_attention_fwd", "store_kv_rope", "rope_at",
+               "flash_attention_dropout_fwd", "flash_attention_dropout_bwd"):
         assert callable(ns[fn]), fn
 
 
@@ -269,3 +270,41 @@ def test_stub_fused_rope_matches_api(device):
                                kv_offset=q_off, causal=True)
     torch.cuda.synchronize()
     assert torch.equal(o, ref)
+
+
+@pytest.mark.gpu
+def test_stub_dropout_matches_api(device):
+    from mlx_primitives.attention._launch import run_attention
+    from mlx_primitives.constants import Layout
+
+    ns = stub_namespace()
+    g = torch.Generator().manual_seed(11)
+    B, H, S, D, p, seed = 2, 4, 260, 64, 0.2, 0xDEADBEEF12345678
+    q, k, v, do = (torch.randn((B, S, H, D), generator=g).to(torch.float16).to(device)
+                   for _ in range(4))
+    bufs = []
+
+    def alloc(n):
+        bufs.append(torch.empty(n, dtype=torch.uint8, device=device))
+        return bufs[-1].data_ptr()
+
+    st = torch.cuda.current_stream().cuda_stream
+    o = torch.empty_like(q)
+    lse = torch.empty(B, H, S, dtype=torch.float32, device=device)
+    ns["flash_attention_dropout_fwd"](q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+                                      lse.data_ptr(), B, H, S, S, D, "BSHD", ns["F16"],
+                                      1 / math.sqrt(D), 1, p, seed, alloc=alloc, stream=st)
+    dq, dk, dv = (torch.empty_like(x) for x in (q, k, v))
+    ns["flash_attention_dropout_bwd"](q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+                                      do.data_ptr(), lse.data_ptr(), dq.data_ptr(),
+                                      dk.data_ptr(), dv.data_ptr(), B, H, S, S, D, "BSHD",
+                                      ns["F16"], 1 / math.sqrt(D), 1, p, seed, alloc=alloc,
+                                      stream=st)
+    qg, kg, vg = (x.clone().requires_grad_(True) for x in (q, k, v))
+    out = run_attention(qg, kg, vg, Layout.BSHD, 1 / math.sqrt(D), True, dropout_p=p,
+                        dropout_seed_value=seed)
+    out.backward(do)
+    torch.cuda.synchronize()
+    assert torch.equal(o, out.detach())
+    for mine, ref in ((dq, qg.grad), (dk, kg.grad), (dv, vg.grad)):
+        assert torch.equal(mine, ref)
