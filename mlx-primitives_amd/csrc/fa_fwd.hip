@@ -380,7 +380,8 @@ __device__ __forceinline__ void fa16_rows(const FwdParams& pin, const WorkItem w
   // so a load has two tile times to arrive.
   // (The paged variant prefetches one tile ahead: its page lookups need the
   // registers of the second set.)
-  constexpr int NSET = PAGED ? 1 : MPX_FA_DEPTH;
+  // (D = 256: one set too, for registers)
+  constexpr int NSET = (PAGED || D > 128) ? 1 : MPX_FA_DEPTH;
   u32x4 kbuf[NSET][K_PER_T];
   u32x4 vbuf[NSET][V_PER_T][2];
   // Rows of a staged tile at or past v_rows are zeroed when V is stored (BN
@@ -1369,6 +1370,25 @@ void fa_fwd16_drop_kernel(FwdParams p) {
                                                              dst2, dst3, nullptr);
 }
 
+// Head dims 129 .. 256 (zero-padded to 256): the register-staged rows with
+// 32-key tiles and four waves of one wave per SIMD. The Q fragments (64
+// registers), the O accumulators (128) and two sets of staged tile loads (64)
+// do not fit the 256 registers of two waves per SIMD.
+constexpr int kNumWavesWide = 4;
+template <int D, int BN, int NW, bool BF16>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void fa_fwd16_wide_kernel(FwdParams p) {
+  constexpr int kLdsBytes = kFa16Stages * fa16_stage_elems<D, BN>() * 2;
+  static_assert(kLdsBytes <= 131072, "LDS budget");
+  __shared__ __align__(16) uint16_t smem[kLdsBytes / 2];
+  const WorkSlot ws = decode_slot(p);
+  const int n_items = slot_items(p, ws);
+  // Every item ends with a barrier after its last LDS read.
+#pragma nounroll
+  for (int item = 0; item < n_items; ++item)
+    fa16_rows<D, BN, NW, BF16, false>(p, slot_item(p, ws, item), smem, nullptr);
+}
+
 // ---------------------------------------------------------------------------
 // fp32 kernel: 32x32x2 f32 MFMA (true fp32 products, for fp32 parity).
 // S^T = K Q^T with k index (4-dim run) dims 8*(ks/4) + 4*g + ks%4; C element e
@@ -1386,9 +1406,13 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd32_kernel(FwdParams pin) {
   constexpr int CHUNKS = BN * CPR;
   constexpr int PER_T = (CHUNKS + NT - 1) / NT;
   static_assert(D % 32 == 0 && BN % 32 == 0, "tile shape");
-  static_assert(2 * STAGE * 4 <= 131072, "LDS budget");
+  // D = 256: one LDS stage (two do not fit 128 KB); the next tile is loaded
+  // once every wave has finished reading the current one (not under the
+  // compute: its registers would spill).
+  constexpr int NSTG = D > 128 ? 1 : 2;
+  static_assert(NSTG * STAGE * 4 <= 131072, "LDS budget");
 
-  __shared__ __align__(16) float smem[2 * STAGE];
+  __shared__ __align__(16) float smem[NSTG * STAGE];
   __shared__ int pages[PAGED ? kMaxItemPages : 1];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -1504,10 +1528,10 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd32_kernel(FwdParams pin) {
   __syncthreads();
 
   for (int t = t_begin; t < t_end; ++t) {
-    const int stage = (t - t_begin) & 1;
+    const int stage = NSTG == 1 ? 0 : (t - t_begin) & 1;
     const int kv0 = kv_lo + t * BN;
     const bool has_next = t + 1 < t_end;
-    if (has_next) load_tile(kv0 + BN);
+    if (NSTG == 2 && has_next) load_tile(kv0 + BN);
 
     bool skip, full;
     classify_tile<BN>(p, kv0, wq0, wq0 + 31, skip, full);
@@ -1613,7 +1637,13 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd32_kernel(FwdParams pin) {
           }
     }
 
-    if (has_next) store_tile(stage ^ 1);
+    if (has_next) {
+      if constexpr (NSTG == 1) {
+        __syncthreads();
+        load_tile(kv0 + BN);
+      }
+      store_tile(NSTG == 1 ? 0 : stage ^ 1);
+    }
     __syncthreads();
   }
 
@@ -1763,6 +1793,7 @@ bool paged_wide_tiles(int D, int dtype, int bs_log2, bool alibi) {
 int tile_n(int D, int dtype, bool paged = false, int bs_log2 = -1, bool alibi = false) {
   if (dtype == MPX_F32) return D > 64 ? 32 : 64;
   if (paged) return paged_wide_tiles(D, dtype, bs_log2, alibi) ? 128 : 64;
+  if (D > 128) return 32;
   return D < 64 || !MPX_FA_DIRECT ? 64 : MPX_FA_BN16;
 }
 
@@ -1770,7 +1801,7 @@ Plan make_plan(int B, int H, int Sq, int Sk, int D, int causal, int window_left,
                int window_right, int dtype, int max_tiles_per_split = 1 << 30,
                bool paged = false, int bs_log2 = -1, bool alibi = false) {
   Plan pl;
-  pl.BM = 32 * (dtype == MPX_F32 ? kNumWaves32 : kNumWaves16);
+  pl.BM = 32 * (dtype == MPX_F32 ? kNumWaves32 : (D > 128 ? kNumWavesWide : kNumWaves16));
   pl.BN = tile_n(D, dtype, paged, bs_log2, alibi);
   pl.win_left = window_left < 0 ? -1 : window_left;
   pl.win_right = causal ? 0 : (window_right < 0 ? -1 : window_right);
@@ -1826,6 +1857,18 @@ constexpr int kBN16 = PAGED || D < 64 || !MPX_FA_DIRECT ? 64 : MPX_FA_BN16;
 
 template <bool PAGED>
 hipError_t dispatch_fwd(const FwdParams& p, int D, int dtype, int grid, hipStream_t st) {
+  if constexpr (!PAGED) {
+    if (D == 256) {
+      if (dtype == MPX_F32) return launch_fwd<256, 32, true, false, false>(p, grid, st);
+      if (dtype == MPX_BF16)
+        hipLaunchKernelGGL((fa_fwd16_wide_kernel<256, 32, kNumWavesWide, true>), dim3(grid),
+                           dim3(64 * kNumWavesWide), 0, st, p);
+      else
+        hipLaunchKernelGGL((fa_fwd16_wide_kernel<256, 32, kNumWavesWide, false>), dim3(grid),
+                           dim3(64 * kNumWavesWide), 0, st, p);
+      return hipGetLastError();
+    }
+  }
   if constexpr (PAGED) {
     if (paged_wide_tiles(D, dtype, p.bs_log2, p.slopes != nullptr)) {
       return dtype == MPX_BF16 ? launch_fwd<128, 128, false, true, true>(p, grid, st)
@@ -1979,8 +2022,8 @@ static int attn_fwd_entry(const void* q, const void* k, const void* v, void* o,
   MPX_CHECK_ARG(B >= 0 && H >= 0 && Sq >= 0 && Sk >= 0, "mpx_attn_fwd: negative size");
   MPX_CHECK_ARG(H_kv > 0 ? H % H_kv == 0 : H == 0,
                 "mpx_attn_fwd: %d query heads are not a multiple of %d K/V heads", H, H_kv);
-  if (D != 32 && D != 64 && D != 128) {
-    set_error("mpx_attn_fwd: head_dim %d not supported (kernels exist for 32, 64, 128)", D);
+  if (D != 32 && D != 64 && D != 128 && D != 256) {
+    set_error("mpx_attn_fwd: head_dim %d not supported (kernels exist for 32, 64, 128, 256)", D);
     return MPX_EUNSUPPORTED;
   }
   MPX_CHECK_ARG(std::isfinite(scale), "mpx_attn_fwd: scale must be finite");
@@ -2091,6 +2134,10 @@ extern "C" int mpx_attn_fwd_rope(const void* q, const void* k, const void* v, vo
   clear_error();
   if (dtype == MPX_F32) {
     set_error("mpx_attn_fwd_rope: Q is rotated on load by the 16-bit kernels only");
+    return MPX_EUNSUPPORTED;
+  }
+  if (D > 128) {
+    set_error("mpx_attn_fwd_rope: head_dim %d not supported (32, 64, 128)", D);
     return MPX_EUNSUPPORTED;
   }
   MPX_CHECK_ARG(cache_dtype == MPX_F32 || cache_dtype == MPX_F16 || cache_dtype == MPX_BF16,

@@ -16,15 +16,19 @@ import torch.nn.functional as F
 from mlx_primitives import _native
 from mlx_primitives.constants import METAL_ATTENTION_MAX_HEAD_DIM, Layout
 
-_KERNEL_HEAD_DIMS = (32, 64, 128)
+# Head dims of the forward kernels (flash, sliding-window, chunked); the paged
+# kernels, the backward and dropout stop at METAL_ATTENTION_MAX_HEAD_DIM (128).
+_KERNEL_HEAD_DIMS = (32, 64, 128, 256)
+MAX_HEAD_DIM = _KERNEL_HEAD_DIMS[-1]
 
 
-def kernel_head_dim(dim: int) -> int:
+def kernel_head_dim(dim: int, limit: int = MAX_HEAD_DIM, what: str = "attention") -> int:
+    """Smallest kernel head dim >= dim (inputs are zero-padded to it)."""
     for d in _KERNEL_HEAD_DIMS:
-        if dim <= d:
+        if dim <= d <= limit:
             return d
     raise NotImplementedError(
-        f"head_dim={dim} exceeds the MI355X kernel limit of {METAL_ATTENTION_MAX_HEAD_DIM}")
+        f"head_dim={dim} exceeds the MI355X {what} kernels' limit of {limit}")
 
 
 def _prepare(x: torch.Tensor, dk: int) -> torch.Tensor:
@@ -106,6 +110,8 @@ def _attention_with_grad(q, k, v, layout, scale, causal, window_left, window_rig
             "mlx_primitives (MI355X build) differentiates attention with scale > 0 only "
             f"(got scale={scale}); run it under torch.no_grad()")
     D = q.shape[-1]
+    kernel_head_dim(D, METAL_ATTENTION_MAX_HEAD_DIM,
+                    "backward" if dropout is None else "dropout")
     dk = 64 if D <= 64 else 128
     qk, kk, vk = (_prepare(x, dk) for x in (q, k, v))
     o = _FlashAttentionFn.apply(qk, kk, vk, layout, scale, causal, window_left, window_right,
@@ -143,6 +149,7 @@ def run_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, layout: Lay
             return _attention_with_grad(q, k, v, layout, scale, causal, window_left,
                                         window_right, dropout)
         # (the dropout kernels take D = 64 or 128)
+        kernel_head_dim(D, METAL_ATTENTION_MAX_HEAD_DIM, "dropout")
         dk = 64 if D <= 64 else 128
     qk, kk, vk = (_prepare(x, dk) for x in (q, k, v))
     out_shape = list(q.shape)

@@ -118,10 +118,58 @@ def test_flash_padded_head_dims(device, D):
     check(out, oa.flash_attention(qn, kn, vn, causal=True), torch.float32)
 
 
-def test_flash_head_dim_over_128_unsupported(device):
-    x = torch.zeros(1, 8, 1, 160, device=device)
-    with pytest.raises(NotImplementedError):
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("layout", ["BSHD", "BHSD"])
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("D", [160, 256])
+def test_flash_head_dims_above_128(device, dtype, layout, causal, D):
+    # Head dims 129 .. 256 run on the D = 256 kernels (inputs zero-padded);
+    # B * H * q-tiles below the CU count: the split-KV path.
+    B, S, H = 2, 300, 3
+    shape = (B, S, H, D) if layout == "BSHD" else (B, H, S, D)
+    (q, k, v), (qn, kn, vn) = inputs([shape] * 3, dtype, D + S, device)
+    out = flash_attention(q, k, v, causal=causal, layout=layout)
+    check(out, oa.flash_attention(qn, kn, vn, causal=causal, layout=layout), dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_flash_head_dim_256_single_pass_paired(device, dtype):
+    # 4 x 64 (batch, head) pairs x 4 q-tiles: no split; the 16-bit causal
+    # launch pairs q-tiles.
+    (q, k, v), (qn, kn, vn) = inputs([(4, 64, 512, 256)] * 3, dtype, 5, device)
+    out = flash_attention(q, k, v, causal=True, layout="BHSD")
+    sel = [0, 31, 63]
+    ref = oa.flash_attention(qn[:1, sel], kn[:1, sel], vn[:1, sel], causal=True, layout="BHSD")
+    check(out[:1, sel], ref, dtype)
+
+
+def test_head_dim_256_window_and_chunked(device):
+    (q, k, v), (qn, kn, vn) = inputs([(2, 333, 2, 256)] * 3, torch.float16, 17, device)
+    check(sliding_window_attention(q, k, v, 40),
+          oa.sliding_window_attention(qn, kn, vn, 40, causal=True), torch.float16)
+    check(sliding_window_attention(q, k, v, 40, causal=False),
+          oa.sliding_window_attention(qn, kn, vn, 40, causal=False), torch.float16)
+    (q, k, v), (qn, kn, vn) = inputs([(1, 64, 2, 200), (1, 3000, 2, 200), (1, 3000, 2, 200)],
+                                     torch.bfloat16, 18, device)
+    check(chunked_cross_attention(q, k, v, chunk_size=512),
+          oa.chunked_cross_attention(qn, kn, vn, chunk_size=512), torch.bfloat16)
+
+
+def test_head_dim_limits(device):
+    x = torch.zeros(1, 8, 1, 264, device=device)
+    with pytest.raises(NotImplementedError, match="256"):
         flash_attention(x, x, x)
+    y = torch.zeros(1, 8, 1, 160, device=device, requires_grad=True)
+    with pytest.raises(NotImplementedError, match="backward.*128"):
+        flash_attention(y, y, y)
+    with pytest.raises(NotImplementedError, match="dropout.*128"):
+        flash_attention(y.detach(), y.detach(), y.detach(), dropout_p=0.1)
+    from mlx_primitives.cache import paged_attention
+    q = torch.zeros(2, 1, 2, 160, device=device)
+    pool = torch.zeros(4, 16, 2, 160, device=device)
+    with pytest.raises(NotImplementedError, match="paged attention.*128"):
+        paged_attention(q, pool, pool, torch.zeros(2, 1, dtype=torch.int32, device=device),
+                        torch.ones(2, dtype=torch.int32, device=device))
 
 
 @pytest.mark.parametrize("scale", [0.05, 1.0, -0.3])
