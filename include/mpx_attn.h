@@ -26,7 +26,7 @@ extern "C" {
 
 #define MPX_OK 0
 #define MPX_EINVAL (-1)       /* bad argument: the Python layer raises ValueError */
-#define MPX_EUNSUPPORTED (-2) /* valid but not implemented (e.g. head_dim > 128) */
+#define MPX_EUNSUPPORTED (-2) /* valid but not implemented (e.g. head_dim > 256) */
 #define MPX_EHIP (-3)         /* a HIP launch/runtime call failed: RuntimeError */
 
 #define MPX_F32 0
@@ -64,8 +64,8 @@ const char* mpx_last_error(void);
  * Sliding-window semantics of the reference (|q-kv| <= W, plus kv <= q when
  * causal) are window_left = W with causal = 1, or window_left = window_right = W.
  *
- * Supported: D <= 128 (kernels are built for D in {32, 64, 128}; pass D as
- * one of those, zero-padded by the caller otherwise), dtype f32/f16/bf16,
+ * Supported: D <= 256 (kernels are built for D in {32, 64, 128, 256}; pass D
+ * as one of those, zero-padded by the caller otherwise), dtype f32/f16/bf16,
  * 16-byte aligned base pointers and seq strides that are multiples of 8
  * elements (4 for f32).
  *
@@ -310,7 +310,8 @@ int mpx_attn_fwd_rope(const void* q, const void* k, const void* v, void* o,
  * sums over its group of query heads). All tensors use {batch, head, seq}
  * element strides like mpx_attn_fwd, D contiguous; dq, dk, dv must not
  * overlap the inputs. Masks (causal, windows) are those of the forward call.
- * Scope: dtype float32 / float16 / bfloat16, D in {64, 128}, scale > 0.
+ * Scope: dtype float32 / float16 / bfloat16, D in {64, 128} (and 256 for
+ * float16 / bfloat16), scale > 0.
  * Workspace: mpx_attn_bwd_workspace_bytes(B, H, Sq) bytes, 16-byte aligned
  * (per-row rowsum(dout * o)).
  */

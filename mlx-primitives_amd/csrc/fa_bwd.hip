@@ -41,6 +41,11 @@ template <int D>
 __device__ __forceinline__ int swz(int r) {
   if constexpr (D == 128) {
     return ((r & 3) << 2) | ((r >> 2) & 3);
+  } else if constexpr (D == 256) {
+    // 512-byte rows: a DMA block is 2 rows and a wave's blocks are 8 rows
+    // apart, so the swizzle may use row bits 0-2 only (row operand reads of 16
+    // rows then pair up on 8 bank groups).
+    return ((r & 3) << 2) | ((r >> 2) & 1);
   } else {
     return (((r >> 1) & 1) << 2) | ((r >> 2) & 3);
   }
@@ -50,7 +55,7 @@ __device__ __forceinline__ int swz(int r) {
 // LDS tile. A DMA instruction fills 1 KB of LDS (RPD rows); wave w issues the
 // blocks w, w + 4, ... . Lane l lands at slot l % CPR of row l / CPR of its block, so it
 // loads logical chunk (l % CPR) ^ swz(row); the swizzle only depends on the
-// low 4 row bits, which are the same in all of a lane's blocks. Rows past the
+// low 4 row bits (3 at D = 256), which are the same in all of a lane's blocks. Rows past the
 // slice end re-read its last row (callers mask them or weight them by 0).
 template <int D, int ROWS = kBwdTile>
 struct TileDma {
@@ -176,7 +181,8 @@ __device__ __forceinline__ void grid_tile(int n_heads, int n_tiles, int& tile, i
 // runs after it.
 // ---------------------------------------------------------------------------
 template <int D, bool BF16, bool DROP = false>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+__global__ __launch_bounds__(256)
+__attribute__((amdgpu_waves_per_eu(D > 128 ? 1 : 2, D > 128 ? 1 : 2)))
 void fa_bwd_dq_kernel(BwdParams p) {
   constexpr int NKS = D / 16, NDB = D / 32, TILE = kBwdTile * D;
   // Stage s: K tile at [2s], V tile at [2s + 1].
@@ -357,14 +363,18 @@ void fa_bwd_dq_kernel(BwdParams p) {
 constexpr int kBoth = 0, kOnlyK = 1, kOnlyV = 2;
 
 template <int D, bool BF16, int MODE, bool DROP = false>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+__global__ __launch_bounds__(256)
+__attribute__((amdgpu_waves_per_eu(D > 128 ? 1 : 2, D > 128 ? 1 : 2)))
 void fa_bwd_dkdv_kernel(BwdParams p) {
   constexpr bool WANT_K = MODE != kOnlyV, WANT_V = MODE != kOnlyK;
-  constexpr int NKS = D / 16, NDB = D / 32, TILE = kBwdTile * D;
+  // Streamed Q / dO rows per step: 64, or 32 at D = 256 (four 64-row tiles of
+  // 512-byte rows would fill 128 KB of LDS). NBLK 32-row blocks per step.
+  constexpr int ROWS = D > 128 ? 32 : kBwdTile, NBLK = ROWS / 32;
+  constexpr int NKS = D / 16, NDB = D / 32, TILE = ROWS * D;
   // Stage s: Q tile at [2s], dO tile at [2s + 1].
   __shared__ __align__(1024) uint16_t lds[4 * TILE];
-  __shared__ __align__(16) float lse_lds[2][kBwdTile];
-  __shared__ __align__(16) float dvc_lds[2][kBwdTile];
+  __shared__ __align__(16) float lse_lds[2][ROWS];
+  __shared__ __align__(16) float dvc_lds[2][ROWS];
 
   const int n_kt = (p.Sk + kBwdOwn - 1) / kBwdOwn;
   int kt, bhk;  // key tile (first, under a causal mask the longest, first), (batch, K/V head)
@@ -395,13 +405,13 @@ void fa_bwd_dkdv_kernel(BwdParams p) {
   const int k_last = min(k0 + kBwdOwn, p.Sk) - 1;
   const int q_lo = p.win_right >= 0 ? max(0, k0 - p.win_right) : 0;
   const int q_hi = p.win_left >= 0 ? min(p.Sq, k_last + p.win_left + 1) : p.Sq;
-  const int t0 = q_lo / kBwdTile;
-  const int n_t = q_hi > q_lo ? (q_hi - 1) / kBwdTile - t0 + 1 : 0;
+  const int t0 = q_lo / ROWS;
+  const int n_t = q_hi > q_lo ? (q_hi - 1) / ROWS - t0 + 1 : 0;
   const int n_steps = n_t * p.kv_group;
 
   Addr<D> ad;
   ad.init(lane);
-  TileDma<D> qd, dd;
+  TileDma<D, ROWS> qd, dd;
   qd.init(p.q_ss, wave, lane);
   dd.init(p.do_ss, wave, lane);
   const u32 lbase = lds_addr(lds);
@@ -416,12 +426,12 @@ void fa_bwd_dkdv_kernel(BwdParams p) {
   // Step u's Q and dO tiles into stage S by DMA, its lse and Dvec rows into registers.
   auto load = [&](int u, int S) __attribute__((always_inline)) {
     const int h = hk * p.kv_group + u / n_t;
-    const int row0 = (t0 + u % n_t) * kBwdTile;
+    const int row0 = (t0 + u % n_t) * ROWS;
     qd.load((const uint16_t*)p.q + b * p.q_sb + h * p.q_sh, lbase + (2 * S) * TILE * 2, row0,
             p.Sq);
     dd.load((const uint16_t*)p.dout + b * p.do_sb + h * p.do_sh,
             lbase + (2 * S + 1) * TILE * 2, row0, p.Sq);
-    if (threadIdx.x < kBwdTile) {
+    if (threadIdx.x < ROWS) {
       const int r = row0 + threadIdx.x;
       const int64_t rix = ((int64_t)b * p.H + h) * p.Sq + r;
       lse_r = r < p.Sq ? p.lse[rix] : INFINITY;
@@ -429,7 +439,7 @@ void fa_bwd_dkdv_kernel(BwdParams p) {
     }
   };
   auto store_vec = [&](int S) __attribute__((always_inline)) {
-    if (threadIdx.x < kBwdTile) {
+    if (threadIdx.x < ROWS) {
       lse_lds[S][threadIdx.x] = lse_r;
       dvc_lds[S][threadIdx.x] = dvc_r;
     }
@@ -446,7 +456,7 @@ void fa_bwd_dkdv_kernel(BwdParams p) {
   for (int u = 0; u < n_steps; ++u) {
     const int S = u & 1;
     if (u + 1 < n_steps) load(u + 1, S ^ 1);
-    const int qr0 = (t0 + u % n_t) * kBwdTile;
+    const int qr0 = (t0 + u % n_t) * ROWS;
     // (dropout: row key of query qr0 + 8 g of this step's head)
     const u32 drop_rk =
         DROP ? drop_row_key((u32)(((int64_t)b * p.H + hk * p.kv_group + u / n_t) * p.Sq + qr0 +
@@ -454,10 +464,10 @@ void fa_bwd_dkdv_kernel(BwdParams p) {
                             p.seed0)
              : 0u;
     const bool skip = wk0 >= p.Sk ||
-                      (p.win_right >= 0 && wk0 > qr0 + kBwdTile - 1 + p.win_right) ||
+                      (p.win_right >= 0 && wk0 > qr0 + ROWS - 1 + p.win_right) ||
                       (p.win_left >= 0 && wk0 + 31 < qr0 - p.win_left);
     const bool full = (p.win_right < 0 || wk0 + 31 <= qr0 + p.win_right) &&
-                      (p.win_left < 0 || wk0 >= qr0 + kBwdTile - 1 - p.win_left);
+                      (p.win_left < 0 || wk0 >= qr0 + ROWS - 1 - p.win_left);
     if (!skip) {
       const uint16_t* Qt = lds + 2 * S * TILE;
       const uint16_t* Dt = Qt + TILE;
@@ -467,7 +477,7 @@ void fa_bwd_dkdv_kernel(BwdParams p) {
       // qr0 + 32nb + 16h + 8g + i): S and dP, then P and dS packed as the B
       // operands of k-steps 2nb, 2nb + 1, then their dV^T and dK^T terms.
 #pragma unroll
-      for (int nb = 0; nb < 2; ++nb) {
+      for (int nb = 0; nb < NBLK; ++nb) {
         f32x16 sb = {}, dpb = {};
 #pragma unroll
         for (int kk = 0; kk < NKS; ++kk) {
@@ -799,7 +809,7 @@ hipError_t launch_bwd(const BwdParams& p, hipStream_t st) {
   if constexpr (D == 128) {
     const dim3 grid_pairs(p.B * p.H_kv * ((n_kt + 1) / 2));
     hipLaunchKernelGGL((fa_bwd_dkdv_fused_kernel<BF16, DROP>), grid_pairs, dim3(256), 0, st, p);
-  } else {
+  } else {  // D = 64, and D = 256 (one wave per SIMD)
     hipLaunchKernelGGL((fa_bwd_dkdv_kernel<D, BF16, kBoth, DROP>), grid_kv, dim3(256), 0, st, p);
   }
   return hipGetLastError();
@@ -807,7 +817,11 @@ hipError_t launch_bwd(const BwdParams& p, hipStream_t st) {
 
 template <bool BF16, bool DROP>
 hipError_t launch_bwd_d(const BwdParams& p, int D, hipStream_t st) {
-  return D == 64 ? launch_bwd<64, BF16, DROP>(p, st) : launch_bwd<128, BF16, DROP>(p, st);
+  if (D == 64) return launch_bwd<64, BF16, DROP>(p, st);
+  if constexpr (!DROP) {
+    if (D == 256) return launch_bwd<256, BF16, false>(p, st);
+  }
+  return launch_bwd<128, BF16, DROP>(p, st);
 }
 
 }  // namespace mpx
@@ -835,8 +849,9 @@ static int attn_bwd_entry(const void* q, const void* k, const void* v, const voi
   MPX_CHECK_ARG(B >= 0 && H >= 0 && Sq >= 0 && Sk >= 0, "mpx_attn_bwd: negative size");
   MPX_CHECK_ARG(H_kv > 0 ? H % H_kv == 0 : H == 0,
                 "mpx_attn_bwd: %d query heads are not a multiple of %d K/V heads", H, H_kv);
-  if (D != 64 && D != 128) {
-    set_error("mpx_attn_bwd: head_dim %d not supported (backward kernels exist for 64, 128)", D);
+  if (D != 64 && D != 128 && !(D == 256 && dtype != MPX_F32 && dropout_p == 0.f)) {
+    set_error("mpx_attn_bwd: head_dim %d not supported (backward kernels exist for 64, 128, "
+              "and 256 for 16-bit types without dropout)", D);
     return MPX_EUNSUPPORTED;
   }
   MPX_CHECK_ARG(std::isfinite(scale) && scale > 0.f, "mpx_attn_bwd: scale must be positive");

@@ -110,9 +110,14 @@ def _attention_with_grad(q, k, v, layout, scale, causal, window_left, window_rig
             "mlx_primitives (MI355X build) differentiates attention with scale > 0 only "
             f"(got scale={scale}); run it under torch.no_grad()")
     D = q.shape[-1]
-    kernel_head_dim(D, METAL_ATTENTION_MAX_HEAD_DIM,
-                    "backward" if dropout is None else "dropout")
-    dk = 64 if D <= 64 else 128
+    # Backward kernels: D = 64, 128, and 256 for 16-bit types without dropout.
+    if dropout is not None:
+        kernel_head_dim(D, METAL_ATTENTION_MAX_HEAD_DIM, "dropout")
+    elif q.dtype == torch.float32:
+        kernel_head_dim(D, METAL_ATTENTION_MAX_HEAD_DIM, "float32 backward")
+    else:
+        kernel_head_dim(D, MAX_HEAD_DIM, "backward")
+    dk = 64 if D <= 64 else (128 if D <= 128 else 256)
     qk, kk, vk = (_prepare(x, dk) for x in (q, k, v))
     o = _FlashAttentionFn.apply(qk, kk, vk, layout, scale, causal, window_left, window_right,
                                 dropout)

@@ -75,6 +75,38 @@ def test_flash_grad(device, dtype, layout, D, causal):
     check_grads(g, q, k, v, d, dtype, scale, causal, layout=layout)
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("layout", ["BSHD", "BHSD"])
+@pytest.mark.parametrize("D", [160, 256])
+@pytest.mark.parametrize("causal", [True, False])
+def test_flash_grad_head_dims_above_128(device, dtype, layout, D, causal):
+    # 16-bit head dims 129 .. 256: the D = 256 backward kernels (one wave per
+    # SIMD, 32-row streamed tiles in dK / dV), inputs zero-padded.
+    B, S, H = 2, 200, 3
+    shape = (B, S, H, D) if layout == "BSHD" else (B, H, S, D)
+    q, k, v, dout = (rnd(shape, 70 + i, dtype) for i in range(4))
+    scale = 1 / math.sqrt(D)
+    got = run_grads(lambda a, b, c: flash_attention(a, b, c, causal=causal, layout=layout),
+                    device, q, k, v, dout)[1:]
+    check_grads(got, q, k, v, dout, dtype, scale, causal, layout=layout)
+
+
+@pytest.mark.parametrize("W,H,H_kv", [(33, 4, 4), (-1, 8, 2)])
+def test_head_dim_256_grad_window_gqa(device, W, H, H_kv):
+    # D = 256 gradients under a sliding window (W = 33) and with grouped K/V
+    # heads (8 query heads over 2).
+    dtype, B, Sq, Sk, D = torch.bfloat16, 2, 300, 300, 256
+    q = rnd((B, Sq, H, D), 80, dtype)
+    k, v = rnd((B, Sk, H_kv, D), 81, dtype), rnd((B, Sk, H_kv, D), 82, dtype)
+    dout = rnd((B, Sq, H, D), 83, dtype)
+    if W >= 0:
+        fn = lambda a, b, c: sliding_window_attention(a, b, c, W)
+    else:
+        fn = lambda a, b, c: flash_attention(a, b, c, causal=True, enable_gqa=True)
+    got = run_grads(fn, device, q, k, v, dout)[1:]
+    check_grads(got, q, k, v, dout, dtype, 1 / math.sqrt(D), True, W)
+
+
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("Sq,Sk,causal", [(77, 300, False), (300, 77, False), (77, 300, True),
                                           (300, 77, True), (1, 129, False), (129, 1, True)])
