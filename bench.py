@@ -20,7 +20,7 @@ path (32x32 blocks) on host cores.
 
 Prints ONE JSON line. Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 
-`--only flash|fp32|window|chunked|paged|gqa|prefill|append|rope|bwd|copy` runs a single leg
+`--only flash|fp32|window|chunked|paged|gqa|prefill|append|rope|bwd|dropout|d256|copy` runs a single leg
 (no CPU baseline) for profiler passes; `copy` streams a 1 GiB float32 buffer through an elementwise kernel,
 the known-size reference for scaling the HBM byte counters. The HBM traffic
 per launch measured by those passes (rocprofv3 FETCH_SIZE / WRITE_SIZE) is read
@@ -372,6 +372,22 @@ def dropout_steps(dev, p: float):
     return fwd, bwd
 
 
+D256_SHAPE = (2, 16, 4096, 256)  # (B, H, S, D), bf16 BHSD causal
+
+
+def d256_step(dev):
+    """flash_attention at head dim 256 (bf16 BHSD causal, D256_SHAPE): the
+    D = 256 kernel. Returns (step, FLOP per step)."""
+    from mlx_primitives.attention import flash_attention
+
+    B, H, S, D = D256_SHAPE
+    g = torch.Generator(device=dev).manual_seed(wl.SEED)
+    q, k, v = (torch.randn(D256_SHAPE, generator=g, device=dev).to(torch.bfloat16)
+               for _ in range(3))
+    return (lambda: flash_attention(q, k, v, causal=True, layout="BHSD"),
+            wl.flash_flops(B, H, S, D, True))
+
+
 def cpu_baseline_dropout(cfg: dict, q, k, v, p: float, budget_s: float) -> dict:
     """The dropout oracle (oracle/dropout.py: keep mask from the hash, dense
     masked softmax) in float32 numpy on host cores, whole heads of the same
@@ -500,6 +516,13 @@ def run_one_leg(args) -> int:
     elif args.only == "bwd":
         _, fn = bwd_step(dev)
         work, unit = 2.5 * wl.config_work("flash_bf16_bhsd"), "flop"
+    elif args.only == "dropout":
+        d_fwd, d_bwd = dropout_steps(dev, DROPOUT_P)
+        fn = lambda: (d_fwd(), d_bwd())
+        work, unit = 3.5 * wl.config_work("flash_bf16_bhsd"), "flop"
+    elif args.only == "d256":
+        fn, work = d256_step(dev)
+        unit = "flop"
     else:
         from mlx_primitives.cache import paged_attention
 
@@ -532,7 +555,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only",
                     choices=["flash", "fp32", "window", "chunked", "paged", "gqa", "prefill",
-                             "append", "rope", "bwd", "copy"],
+                             "append", "rope", "bwd", "dropout", "d256", "copy"],
                     default=None,
                     help="run one leg only (profiler passes); prints that leg's timing")
     ap.add_argument("--settle", type=float, default=0.0,
@@ -661,6 +684,14 @@ def main() -> int:
     log(f"[bench] flash_dropout: forward {df_ev:.3f} ms -> {df_tf:.1f} TFLOP/s "
         f"({df_ev / ev_ms:.2f}x plain), backward {db_ev:.3f} ms -> {db_tf:.1f} TFLOP/s "
         f"({db_ev / b_ev:.2f}x plain)")
+
+    # ---- head dim 256 (the D = 256 kernel), bf16 BHSD causal ----------------------------
+    h_fn, hflops = d256_step(dev)
+    log(f"[bench] flash_d256: warmup {args.warmup}, steps {args.steps}")
+    h_wall, h_ev, h_min, h_med = time_steps(h_fn, args.steps, args.warmup)
+    del h_fn
+    h_tf = hflops / (h_ev * 1e-3) / 1e12
+    log(f"[bench] flash_d256: {h_wall:.3f} ms/step wall, kernel {h_ev:.3f} ms -> {h_tf:.1f} TFLOP/s")
 
     # ---- config 3: sliding window W=4096, config 5: chunked cross attention ------------
     wcfg = wl.CONFIGS["window_bf16_bshd"]
@@ -834,6 +865,15 @@ def main() -> int:
                          "kernel": BWD_KERNELS,
                          "flop_convention": "2.5x forward (5 S^2*D products)"},
             "cpu_baseline": bcpu,
+        },
+        "flash_d256": {
+            "workload": f"flash_attention bf16 BHSD {D256_SHAPE} (B, H, S, D) causal: head dim "
+                        f"256 (no BASELINE config; the reference's routes take any D)",
+            "value": h_tf, "unit": "TFLOP/s", "ms_per_step": h_wall, "kernel_ms": h_ev,
+            "kernel_ms_median": h_med, "kernel_ms_min": h_min, "flop_per_step": hflops,
+            "roofline": {"bound": "mfma", "achieved": h_tf, "peak": PEAK_BF16_TFLOPS,
+                         "unit": "TFLOP/s", "frac": h_tf / PEAK_BF16_TFLOPS,
+                         "kernel": "fa_fwd16_wide_kernel<256,32,4,bf16>", "traffic": None},
         },
         "flash_dropout": {
             "workload": f"flash_attention bf16 B=4 H=32 S=4096 D=128 causal (the headline "
