@@ -99,7 +99,7 @@ size_t mpx_attn_fwd_workspace_bytes(int B, int H, int Sq, int Sk, int D, int cau
  *   o             (B, H, D) via o_strides
  *
  * D is the head dim of q, the pools and o: any multiple of 8 elements (16-bit
- * dtypes) or 4 (float32) up to 128, read in place (no padded copy of the
+ * dtypes) or 4 (float32) up to 256, read in place (no padded copy of the
  * pools). Token t of sequence b is valid iff t < context_lens[b] and
  * 0 <= block_tables[b, t / block_size] < num_blocks; the softmax runs over
  * valid tokens only (exact, no epsilon). A sequence with no valid token gets
@@ -135,7 +135,7 @@ size_t mpx_paged_decode_workspace_bytes(int B, int H, int D, int block_size, int
  * causal != 0 it sees kv_pos <= i. Token t of sequence b is valid iff
  * t < context_lens[b] and 0 <= block_tables[b, t / block_size] < num_blocks.
  * Exact softmax over the valid, unmasked tokens; a query row with none gets
- * NaN (the reference's softmax over an all -inf row). D in {32, 64, 128};
+ * NaN (the reference's softmax over an all -inf row). D in {32, 64, 128, 256};
  * 16-bit pools must be below 4 GiB each (MPX_EUNSUPPORTED otherwise).
  */
 int mpx_paged_prefill(const void* q, const void* k_pool, const void* v_pool,

@@ -1372,21 +1372,23 @@ void fa_fwd16_drop_kernel(FwdParams p) {
 
 // Head dims 129 .. 256 (zero-padded to 256): the register-staged rows with
 // 32-key tiles and four waves of one wave per SIMD. The Q fragments (64
-// registers), the O accumulators (128) and two sets of staged tile loads (64)
-// do not fit the 256 registers of two waves per SIMD.
+// registers), the O accumulators (128) and the staged tile loads do not fit
+// the 256 registers of two waves per SIMD. PAGED: K/V through the page table
+// (prefill over a paged cache), as the 64-key paged kernels.
 constexpr int kNumWavesWide = 4;
-template <int D, int BN, int NW, bool BF16>
+template <int D, int BN, int NW, bool BF16, bool PAGED = false>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void fa_fwd16_wide_kernel(FwdParams p) {
   constexpr int kLdsBytes = kFa16Stages * fa16_stage_elems<D, BN>() * 2;
-  static_assert(kLdsBytes <= 131072, "LDS budget");
+  static_assert(kLdsBytes + (PAGED ? kMaxItemPages * 4 : 0) <= 131072, "LDS budget");
   __shared__ __align__(16) uint16_t smem[kLdsBytes / 2];
+  __shared__ int pages[PAGED ? kMaxItemPages : 1];
   const WorkSlot ws = decode_slot(p);
   const int n_items = slot_items(p, ws);
   // Every item ends with a barrier after its last LDS read.
 #pragma nounroll
   for (int item = 0; item < n_items; ++item)
-    fa16_rows<D, BN, NW, BF16, false>(p, slot_item(p, ws, item), smem, nullptr);
+    fa16_rows<D, BN, NW, BF16, PAGED>(p, slot_item(p, ws, item), smem, pages);
 }
 
 // ---------------------------------------------------------------------------
@@ -1792,8 +1794,8 @@ bool paged_wide_tiles(int D, int dtype, int bs_log2, bool alibi) {
 // page sizes, take 64).
 int tile_n(int D, int dtype, bool paged = false, int bs_log2 = -1, bool alibi = false) {
   if (dtype == MPX_F32) return D > 64 ? 32 : 64;
-  if (paged) return paged_wide_tiles(D, dtype, bs_log2, alibi) ? 128 : 64;
   if (D > 128) return 32;
+  if (paged) return paged_wide_tiles(D, dtype, bs_log2, alibi) ? 128 : 64;
   return D < 64 || !MPX_FA_DIRECT ? 64 : MPX_FA_BN16;
 }
 
@@ -1857,17 +1859,15 @@ constexpr int kBN16 = PAGED || D < 64 || !MPX_FA_DIRECT ? 64 : MPX_FA_BN16;
 
 template <bool PAGED>
 hipError_t dispatch_fwd(const FwdParams& p, int D, int dtype, int grid, hipStream_t st) {
-  if constexpr (!PAGED) {
-    if (D == 256) {
-      if (dtype == MPX_F32) return launch_fwd<256, 32, true, false, false>(p, grid, st);
-      if (dtype == MPX_BF16)
-        hipLaunchKernelGGL((fa_fwd16_wide_kernel<256, 32, kNumWavesWide, true>), dim3(grid),
-                           dim3(64 * kNumWavesWide), 0, st, p);
-      else
-        hipLaunchKernelGGL((fa_fwd16_wide_kernel<256, 32, kNumWavesWide, false>), dim3(grid),
-                           dim3(64 * kNumWavesWide), 0, st, p);
-      return hipGetLastError();
-    }
+  if (D == 256) {
+    if (dtype == MPX_F32) return launch_fwd<256, 32, true, false, PAGED>(p, grid, st);
+    if (dtype == MPX_BF16)
+      hipLaunchKernelGGL((fa_fwd16_wide_kernel<256, 32, kNumWavesWide, true, PAGED>), dim3(grid),
+                         dim3(64 * kNumWavesWide), 0, st, p);
+    else
+      hipLaunchKernelGGL((fa_fwd16_wide_kernel<256, 32, kNumWavesWide, false, PAGED>), dim3(grid),
+                         dim3(64 * kNumWavesWide), 0, st, p);
+    return hipGetLastError();
   }
   if constexpr (PAGED) {
     if (paged_wide_tiles(D, dtype, p.bs_log2, p.slopes != nullptr)) {
@@ -2214,8 +2214,9 @@ extern "C" int mpx_paged_prefill_gqa(const void* q, const void* k_pool, const vo
   MPX_CHECK_ARG(block_size > 0, "mpx_paged_prefill: block_size must be positive");
   MPX_CHECK_ARG(H_kv > 0 ? H % H_kv == 0 : H == 0,
                 "mpx_paged_prefill: %d query heads are not a multiple of %d K/V heads", H, H_kv);
-  if (D != 32 && D != 64 && D != 128) {
-    set_error("mpx_paged_prefill: head_dim %d not supported (kernels exist for 32, 64, 128)", D);
+  if (D != 32 && D != 64 && D != 128 && D != 256) {
+    set_error("mpx_paged_prefill: head_dim %d not supported (kernels exist for 32, 64, 128, "
+              "256)", D);
     return MPX_EUNSUPPORTED;
   }
   MPX_CHECK_ARG(std::isfinite(scale), "mpx_paged_prefill: scale must be finite");

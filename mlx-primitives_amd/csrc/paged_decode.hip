@@ -230,7 +230,8 @@ __global__ __launch_bounds__(64 * kHeadsPerWG<NT>) void paged_decode_part_kernel
 // (sequence, head): lane i takes the (m, l) of partition i and its weight
 // 2^(m_i - M), lane l accumulates dims 2l, 2l+1 over the partitions (16
 // partition rows in flight, each a coalesced 2 D-float read). D is the kernel
-// head dim (the partials' row length); dp <= D columns are written.
+// head dim (the partials' row length); dp <= D columns are written. Head dims
+// above 128 take one workgroup per 128 dims (blockIdx.y).
 template <int DT>
 __global__ __launch_bounds__(64) void paged_decode_merge_kernel(DecodeParams p, int D) {
   const int bh = blockIdx.x;
@@ -239,7 +240,7 @@ __global__ __launch_bounds__(64) void paged_decode_merge_kernel(DecodeParams p, 
   const int ctx = max(0, min(p.cl[b], p.max_blocks * p.bs));
   const int nparts = (ctx + kPart - 1) / kPart;
   const int64_t base = (int64_t)bh * p.max_parts;
-  const int d = 2 * lane;
+  const int d = 2 * lane + 128 * (int)blockIdx.y;
   const bool dl = d < D;
   // Online over chunks of 64 partitions (one chunk up to 32768 tokens): a
   // chunk's (m, l) and its first 16 partition rows are requested together.
@@ -518,8 +519,13 @@ int max_parts_for(int block_size, int max_blocks) {
   return (int)((tokens + kPart - 1) / kPart);
 }
 
-// Kernel head dim serving pools of head dim D (<= 128): 32, 64 or 128.
-int kernel_dim(int D) { return D <= 32 ? 32 : D <= 64 ? 64 : 128; }
+// Kernel head dim serving pools of head dim D (<= 256): 32, 64, 128 or 256.
+int kernel_dim(int D) { return D <= 32 ? 32 : D <= 64 ? 64 : D <= 128 ? 128 : 256; }
+
+// Merge workgroups per (sequence, head): one per 128 dims.
+dim3 merge_grid(const DecodeParams& p, int D) {
+  return dim3(p.B * p.H, D > 128 ? D / 128 : 1);
+}
 
 // The grouped-query MFMA kernel serves 16-bit pools of head dim 128 with 2 to
 // 16 query heads per K/V head and pools below 4 GiB - 256 bytes
@@ -536,7 +542,7 @@ hipError_t launch_decode(const DecodeParams& p, hipStream_t st) {
                          0, st, p);
       hipError_t e = hipGetLastError();
       if (e != hipSuccess) return e;
-      hipLaunchKernelGGL(paged_decode_merge_kernel<DT>, dim3(p.B * p.H), dim3(64), 0, st, p, D);
+      hipLaunchKernelGGL(paged_decode_merge_kernel<DT>, merge_grid(p, D), dim3(64), 0, st, p, D);
       return hipGetLastError();
     }
   }
@@ -551,7 +557,7 @@ hipError_t launch_decode(const DecodeParams& p, hipStream_t st) {
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(paged_decode_merge_kernel<DT>, dim3(p.B * p.H), dim3(64), 0, st, p, D);
+  hipLaunchKernelGGL(paged_decode_merge_kernel<DT>, merge_grid(p, D), dim3(64), 0, st, p, D);
   return hipGetLastError();
 }
 
@@ -560,6 +566,7 @@ hipError_t dispatch_decode_d(const DecodeParams& p, int D, hipStream_t st) {
   switch (D) {
     case 32: return launch_decode<32, DT>(p, st);
     case 64: return launch_decode<64, DT>(p, st);
+    case 256: return launch_decode<256, DT>(p, st);
     default: return launch_decode<128, DT>(p, st);
   }
 }
@@ -586,8 +593,8 @@ int paged_decode_run(const void* q, const void* k_pool, const void* v_pool,
                 "%s: %d query heads are not a multiple of %d K/V heads", who, H, H_kv);
   MPX_CHECK_ARG(block_size > 0, "%s: block_size must be positive", who);
   const int vec = dtype == MPX_F32 ? 4 : 8;
-  if (D <= 0 || D > 128 || D % vec != 0) {
-    set_error("%s: head_dim %d not supported (a multiple of %d elements up to 128)", who, D,
+  if (D <= 0 || D > 256 || D % vec != 0) {
+    set_error("%s: head_dim %d not supported (a multiple of %d elements up to 256)", who, D,
               vec);
     return MPX_EUNSUPPORTED;
   }

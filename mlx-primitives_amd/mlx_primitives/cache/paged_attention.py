@@ -18,7 +18,6 @@ import torch
 
 from mlx_primitives import _native
 from mlx_primitives.attention._launch import kernel_head_dim
-from mlx_primitives.constants import METAL_ATTENTION_MAX_HEAD_DIM
 
 
 def get_alibi_slopes(num_heads: int, device=None) -> torch.Tensor:
@@ -99,7 +98,7 @@ def paged_attention(
         alibi_slopes = alibi_slopes.to(device=q.device, dtype=torch.float32).contiguous()
         if alibi_slopes.numel() != heads:
             raise ValueError(f"alibi_slopes must have {heads} entries, got {alibi_slopes.numel()}")
-    dk = kernel_head_dim(dim, METAL_ATTENTION_MAX_HEAD_DIM, "paged attention")
+    dk = kernel_head_dim(dim, what="paged attention")
     vec = 4 if q.dtype == torch.float32 else 8
     if dk != dim and not (seq_q == 1 and dim % vec == 0):
         # The decode kernel reads pools of any head dim that is a multiple of

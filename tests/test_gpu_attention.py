@@ -165,9 +165,9 @@ def test_head_dim_limits(device):
     with pytest.raises(NotImplementedError, match="dropout.*128"):
         flash_attention(y.detach(), y.detach(), y.detach(), dropout_p=0.1)
     from mlx_primitives.cache import paged_attention
-    q = torch.zeros(2, 1, 2, 160, device=device)
-    pool = torch.zeros(4, 16, 2, 160, device=device)
-    with pytest.raises(NotImplementedError, match="paged attention.*128"):
+    q = torch.zeros(2, 1, 2, 264, device=device)
+    pool = torch.zeros(4, 16, 2, 264, device=device)
+    with pytest.raises(NotImplementedError, match="paged attention.*256"):
         paged_attention(q, pool, pool, torch.zeros(2, 1, dtype=torch.int32, device=device),
                         torch.ones(2, dtype=torch.int32, device=device))
 

@@ -70,7 +70,7 @@ def test_reference_small_cases(device, lens, tables, nb):
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("bs", [1, 8, 16, 32, 128])
-@pytest.mark.parametrize("D", [32, 64, 128])
+@pytest.mark.parametrize("D", [32, 64, 128, 256])
 def test_random_tables(device, dtype, bs, D):
     rng = np.random.default_rng(bs * 1000 + D)
     B, H = 5, 6  # three workgroups of 2 heads; not a multiple of the grouped launch's 4
@@ -111,7 +111,9 @@ def test_odd_head_counts(device, dtype, H, alibi):
 @pytest.mark.parametrize("dtype,D", [(torch.float16, 80), (torch.bfloat16, 96),
                                      (torch.bfloat16, 48), (torch.float32, 100),
                                      (torch.float32, 20), (torch.float16, 8),
-                                     (torch.bfloat16, 100), (torch.float16, 30)])
+                                     (torch.bfloat16, 100), (torch.float16, 30),
+                                     (torch.bfloat16, 200), (torch.float32, 136),
+                                     (torch.float16, 150)])
 def test_unpadded_head_dims(device, dtype, D):
     # Head dims that are multiples of the 16-byte vector are read in place by
     # the decode kernel; others copy only the referenced pages, padded.

@@ -81,7 +81,7 @@ def random_tables(rng, lens, bs, extra=3, holes=True):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
-@pytest.mark.parametrize("D", [32, 64, 128])
+@pytest.mark.parametrize("D", [32, 64, 128, 256, 200])
 @pytest.mark.parametrize("causal", [True, False])
 def test_random_tables(device, dtype, D, causal):
     rng = np.random.default_rng(D * 7 + int(causal))
@@ -104,7 +104,8 @@ def test_block_sizes(device, bs):
 
 
 @pytest.mark.parametrize("dtype,D", [(torch.bfloat16, 128), (torch.float16, 64),
-                                     (torch.float32, 128)])
+                                     (torch.float32, 128), (torch.bfloat16, 256),
+                                     (torch.float32, 256)])
 def test_split_kv_long_context(device, dtype, D):
     # few query tiles over a long table: the kv range is split across workgroups
     # and merged (the workspace path)
