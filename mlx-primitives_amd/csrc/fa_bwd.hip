@@ -818,9 +818,7 @@ hipError_t launch_bwd(const BwdParams& p, hipStream_t st) {
 template <bool BF16, bool DROP>
 hipError_t launch_bwd_d(const BwdParams& p, int D, hipStream_t st) {
   if (D == 64) return launch_bwd<64, BF16, DROP>(p, st);
-  if constexpr (!DROP) {
-    if (D == 256) return launch_bwd<256, BF16, false>(p, st);
-  }
+  if (D == 256) return launch_bwd<256, BF16, DROP>(p, st);
   return launch_bwd<128, BF16, DROP>(p, st);
 }
 
@@ -849,9 +847,9 @@ static int attn_bwd_entry(const void* q, const void* k, const void* v, const voi
   MPX_CHECK_ARG(B >= 0 && H >= 0 && Sq >= 0 && Sk >= 0, "mpx_attn_bwd: negative size");
   MPX_CHECK_ARG(H_kv > 0 ? H % H_kv == 0 : H == 0,
                 "mpx_attn_bwd: %d query heads are not a multiple of %d K/V heads", H, H_kv);
-  if (D != 64 && D != 128 && !(D == 256 && dtype != MPX_F32 && dropout_p == 0.f)) {
+  if (D != 64 && D != 128 && !(D == 256 && dtype != MPX_F32)) {
     set_error("mpx_attn_bwd: head_dim %d not supported (backward kernels exist for 64, 128, "
-              "and 256 for 16-bit types without dropout)", D);
+              "and 256 for 16-bit types)", D);
     return MPX_EUNSUPPORTED;
   }
   MPX_CHECK_ARG(std::isfinite(scale) && scale > 0.f, "mpx_attn_bwd: scale must be positive");

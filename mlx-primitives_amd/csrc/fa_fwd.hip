@@ -271,7 +271,7 @@ constexpr int fa16_stage_elems() {
 // Query rows [32*NW*wi.qt, +32*NW) of one (batch, head) against its KV range.
 // PAGED: K/V rows come from pools through the page table (prefill over a
 // paged cache); invalid rows load as zeros and are masked.
-template <int D, int BN, int NW, bool BF16, bool PAGED>
+template <int D, int BN, int NW, bool BF16, bool PAGED, bool DROP = false>
 __device__ __forceinline__ void fa16_rows(const FwdParams& pin, const WorkItem wi,
                                           uint16_t* __restrict__ smem, int* __restrict__ pages) {
   FwdParams p = pin;
@@ -348,6 +348,9 @@ __device__ __forceinline__ void fa16_rows(const FwdParams& pin, const WorkItem w
   // Rows past Sq read the last row (never stored).
   const int wq0 = q0 + wave * 32;
   const int myq = wq0 + j;
+  // Dropout: this row's key of the keep-mask hash.
+  const u32 drop_rk =
+      DROP ? drop_row_key((u32)(((int64_t)wi.b * p.H + wi.h) * p.Sq + myq), p.seed0) : 0u;
   u32x4 qreg[NKS];
   {
     const u32x4* src = (const u32x4*)(Qp + (int64_t)min(myq, p.Sq - 1) * p.q_ss);
@@ -598,6 +601,11 @@ __device__ __forceinline__ void fa16_rows(const FwdParams& pin, const WorkItem w
 
     // P = exp2(s*c - m), packed to 16 bits; the row sum accumulates the
     // packed (rounded) weights, the exact weights the PV product uses.
+    // Dropout: the PV operand keeps the kept keys' weights only (the row sum
+    // takes them all); element pair e2 of half hh of block nb holds keys
+    // kv0 + 32 nb + 16 hh + 8 g + 2 e2 + {0, 1}, the hash's key pair
+    // kv0 / 2 + 16 nb + 8 hh + 4 g + e2.
+    const u32 pair0 = DROP ? drop_pair_key((u32)(kv0 >> 1) + 4u * g, p.seed1) : 0u;
     float lsum = 0.f;
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb)
@@ -608,7 +616,13 @@ __device__ __forceinline__ void fa16_rows(const FwdParams& pin, const WorkItem w
           const float x0 = fast_exp2(s[nb][8 * hh + 2 * e2] * c - msub);
           const float x1 = fast_exp2(s[nb][8 * hh + 2 * e2 + 1] * c - msub);
           const u32 pk = pack2<BF16>(x0, x1);
-          pop[2 * nb + hh][e2] = pk;
+          if constexpr (DROP)
+            pop[2 * nb + hh][e2] =
+                pk & drop_mask2(drop_bits(drop_rk, pair0 + (u32)(16 * nb + 8 * hh + e2) *
+                                                               0x85EBCA77u),
+                                p.drop_thresh);
+          else
+            pop[2 * nb + hh][e2] = pk;
           lsum = dot2_sum<BF16>(pk, lsum);
         }
     l_run += lsum;
@@ -694,10 +708,12 @@ __device__ __forceinline__ void fa16_rows(const FwdParams& pin, const WorkItem w
   // Epilogue: move o and l to the true max, then normalise (or emit partials).
   const float l_tot = pair_sum32(l_run);
   const float f = m_max == -INFINITY ? 0.f : fast_exp2(m_run - m_max);
+  // (dropout: kept weights times 1 / (1 - p); the row sums stay unscaled)
+  const float fo = DROP ? f * p.drop_scale : f;
   if (p.num_splits == 1) {
     if (myq < p.Sq) {
       const float inv = m_max == -INFINITY ? (p.nan_empty ? __builtin_nanf("") : 0.f)
-                                           : f / (l_tot * f + p.eps);
+                                           : fo / (l_tot * f + p.eps);
       if (p.lse && g == 0)
         p.lse[((int64_t)wi.b * p.H + wi.h) * p.Sq + myq] =
             m_max == -INFINITY ? INFINITY : m_max + log2f(l_tot * f + p.eps);
@@ -720,8 +736,8 @@ __device__ __forceinline__ void fa16_rows(const FwdParams& pin, const WorkItem w
 #pragma unroll
       for (int e4 = 0; e4 < 4; ++e4) {
         const int d = db * 32 + 8 * e4 + 4 * g;
-        *(f32x4*)(wo + d) = (f32x4){o[db][4 * e4] * f, o[db][4 * e4 + 1] * f,
-                                    o[db][4 * e4 + 2] * f, o[db][4 * e4 + 3] * f};
+        *(f32x4*)(wo + d) = (f32x4){o[db][4 * e4] * fo, o[db][4 * e4 + 1] * fo,
+                                    o[db][4 * e4 + 2] * fo, o[db][4 * e4 + 3] * fo};
       }
     if (g == 0) {
       p.ws_ml[2 * row] = m_max;
@@ -1376,7 +1392,7 @@ void fa_fwd16_drop_kernel(FwdParams p) {
 // the 256 registers of two waves per SIMD. PAGED: K/V through the page table
 // (prefill over a paged cache), as the 64-key paged kernels.
 constexpr int kNumWavesWide = 4;
-template <int D, int BN, int NW, bool BF16, bool PAGED = false>
+template <int D, int BN, int NW, bool BF16, bool PAGED = false, bool DROP = false>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void fa_fwd16_wide_kernel(FwdParams p) {
   constexpr int kLdsBytes = kFa16Stages * fa16_stage_elems<D, BN>() * 2;
@@ -1388,7 +1404,7 @@ void fa_fwd16_wide_kernel(FwdParams p) {
   // Every item ends with a barrier after its last LDS read.
 #pragma nounroll
   for (int item = 0; item < n_items; ++item)
-    fa16_rows<D, BN, NW, BF16, PAGED>(p, slot_item(p, ws, item), smem, pages);
+    fa16_rows<D, BN, NW, BF16, PAGED, DROP>(p, slot_item(p, ws, item), smem, pages);
 }
 
 // ---------------------------------------------------------------------------
@@ -1896,11 +1912,23 @@ hipError_t dispatch_fwd(const FwdParams& p, int D, int dtype, int grid, hipStrea
   }
 }
 
-// The dropout kernels (dense K/V, D = 64 or 128).
+// The dropout kernels (dense K/V, D = 64, 128 or 256).
 hipError_t dispatch_fwd_drop(const FwdParams& p, int D, int dtype, int grid, hipStream_t st) {
 #define MPX_DROP16(DD, BF)                                                                  \
   hipLaunchKernelGGL((fa_fwd16_drop_kernel<DD, kBN16<false, DD>, kNumWaves16, BF>), dim3(grid), \
                      dim3(64 * kNumWaves16), 0, st, p)
+  if (D == 256) {
+    if (dtype == MPX_F32)
+      hipLaunchKernelGGL((fa_fwd32_kernel<256, 32, kNumWaves32, false, true>), dim3(grid),
+                         dim3(64 * kNumWaves32), 0, st, p);
+    else if (dtype == MPX_BF16)
+      hipLaunchKernelGGL((fa_fwd16_wide_kernel<256, 32, kNumWavesWide, true, false, true>),
+                         dim3(grid), dim3(64 * kNumWavesWide), 0, st, p);
+    else
+      hipLaunchKernelGGL((fa_fwd16_wide_kernel<256, 32, kNumWavesWide, false, false, true>),
+                         dim3(grid), dim3(64 * kNumWavesWide), 0, st, p);
+    return hipGetLastError();
+  }
   if (dtype == MPX_F32) {
     if (D == 64)
       hipLaunchKernelGGL((fa_fwd32_kernel<64, 64, kNumWaves32, false, true>), dim3(grid),
@@ -2107,9 +2135,9 @@ extern "C" int mpx_attn_fwd_dropout(const void* q, const void* k, const void* v,
   FwdExtras ex;
   ex.lse = lse;
   if (dropout_p > 0.f) {
-    if (D != 64 && D != 128) {
+    if (D != 64 && D != 128 && D != 256) {
       set_error("mpx_attn_fwd_dropout: head_dim %d not supported (dropout kernels exist for 64, "
-                "128)", D);
+                "128, 256)", D);
       return MPX_EUNSUPPORTED;
     }
     ex.drop = true;

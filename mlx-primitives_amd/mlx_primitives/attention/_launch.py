@@ -16,8 +16,8 @@ import torch.nn.functional as F
 from mlx_primitives import _native
 from mlx_primitives.constants import METAL_ATTENTION_MAX_HEAD_DIM, Layout
 
-# Head dims of the forward kernels (flash, sliding-window, chunked); the paged
-# kernels, the backward and dropout stop at METAL_ATTENTION_MAX_HEAD_DIM (128).
+# Head dims of the kernels (forward, paged, dropout, 16-bit backward); the
+# float32 backward stops at METAL_ATTENTION_MAX_HEAD_DIM (128).
 _KERNEL_HEAD_DIMS = (32, 64, 128, 256)
 MAX_HEAD_DIM = _KERNEL_HEAD_DIMS[-1]
 
@@ -110,10 +110,8 @@ def _attention_with_grad(q, k, v, layout, scale, causal, window_left, window_rig
             "mlx_primitives (MI355X build) differentiates attention with scale > 0 only "
             f"(got scale={scale}); run it under torch.no_grad()")
     D = q.shape[-1]
-    # Backward kernels: D = 64, 128, and 256 for 16-bit types without dropout.
-    if dropout is not None:
-        kernel_head_dim(D, METAL_ATTENTION_MAX_HEAD_DIM, "dropout")
-    elif q.dtype == torch.float32:
+    # Backward kernels: D = 64, 128, and 256 for the 16-bit types.
+    if q.dtype == torch.float32:
         kernel_head_dim(D, METAL_ATTENTION_MAX_HEAD_DIM, "float32 backward")
     else:
         kernel_head_dim(D, MAX_HEAD_DIM, "backward")
@@ -153,9 +151,8 @@ def run_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, layout: Lay
         if _needs_grad(q, k, v):
             return _attention_with_grad(q, k, v, layout, scale, causal, window_left,
                                         window_right, dropout)
-        # (the dropout kernels take D = 64 or 128)
-        kernel_head_dim(D, METAL_ATTENTION_MAX_HEAD_DIM, "dropout")
-        dk = 64 if D <= 64 else 128
+        # (the dropout kernels take D = 64, 128 or 256)
+        dk = 64 if D <= 64 else (128 if D <= 128 else 256)
     qk, kk, vk = (_prepare(x, dk) for x in (q, k, v))
     out_shape = list(q.shape)
     out_shape[-1] = dk

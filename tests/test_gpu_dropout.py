@@ -78,7 +78,7 @@ def mask_counts(device, dtype, B, H, Sq, Sk, D, p, seed, causal, wl=-1, wr=-1):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
-@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("D", [64, 128, 256])
 @pytest.mark.parametrize("causal", [False, True])
 def test_forward_keep_mask_bit_exact(device, dtype, D, causal):
     # B * H * q-tiles well below the CU count: the split-KV path and its merge.
@@ -134,8 +134,8 @@ def check_grads(got, want, dtype, p):
             assert err <= nrel, f"{name}: normwise relative error {err:.3e} > {nrel}"
 
 
-@pytest.mark.parametrize("dtype", DTYPES)
-@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("dtype,D", [(dt, d) for dt in DTYPES for d in (64, 128)] +
+                         [(torch.float16, 256), (torch.bfloat16, 256)])
 @pytest.mark.parametrize("causal,wl,H_kv", [(True, -1, 4), (False, -1, 4), (True, 50, 4),
                                             (True, -1, 2)])
 def test_grad_vs_oracle(device, dtype, D, causal, wl, H_kv):
