@@ -310,8 +310,7 @@ int mpx_attn_fwd_rope(const void* q, const void* k, const void* v, void* o,
  * sums over its group of query heads). All tensors use {batch, head, seq}
  * element strides like mpx_attn_fwd, D contiguous; dq, dk, dv must not
  * overlap the inputs. Masks (causal, windows) are those of the forward call.
- * Scope: dtype float32 / float16 / bfloat16, D in {64, 128} (and 256 for
- * float16 / bfloat16), scale > 0.
+ * Scope: dtype float32 / float16 / bfloat16, D in {64, 128, 256}, scale > 0.
  * Workspace: mpx_attn_bwd_workspace_bytes(B, H, Sq) bytes, 16-byte aligned
  * (per-row rowsum(dout * o)).
  */
@@ -356,9 +355,8 @@ int mpx_attn_bwd(const void* q, const void* k, const void* v, const void* o, con
  * seed (lse may be NULL; its values, and so the backward's probabilities, are
  * those of the undropped softmax). dropout_p = 0 is the plain forward.
  * mpx_attn_bwd_dropout is mpx_attn_bwd of that forward: same arguments plus
- * the forward's dropout_p and seed. Scope: D in {64, 128, 256} (the backward
- * at 256 for float16 / bfloat16 only), float32 / float16 / bfloat16, every
- * mask and K/V head grouping of the plain kernels.
+ * the forward's dropout_p and seed. Scope: D in {64, 128, 256}, float32 /
+ * float16 / bfloat16, every mask and K/V head grouping of the plain kernels.
  */
 int mpx_attn_fwd_dropout(const void* q, const void* k, const void* v, void* o, float* lse,
                          const int64_t* q_strides, const int64_t* k_strides,

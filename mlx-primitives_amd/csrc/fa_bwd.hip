@@ -847,9 +847,9 @@ static int attn_bwd_entry(const void* q, const void* k, const void* v, const voi
   MPX_CHECK_ARG(B >= 0 && H >= 0 && Sq >= 0 && Sk >= 0, "mpx_attn_bwd: negative size");
   MPX_CHECK_ARG(H_kv > 0 ? H % H_kv == 0 : H == 0,
                 "mpx_attn_bwd: %d query heads are not a multiple of %d K/V heads", H, H_kv);
-  if (D != 64 && D != 128 && !(D == 256 && dtype != MPX_F32)) {
+  if (D != 64 && D != 128 && D != 256) {
     set_error("mpx_attn_bwd: head_dim %d not supported (backward kernels exist for 64, 128, "
-              "and 256 for 16-bit types)", D);
+              "256)", D);
     return MPX_EUNSUPPORTED;
   }
   MPX_CHECK_ARG(std::isfinite(scale) && scale > 0.f, "mpx_attn_bwd: scale must be positive");

@@ -106,7 +106,10 @@ template <int D, bool DROP = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void fa_bwd32_dq_kernel(BwdParams p) {
   constexpr int NQ4 = D / 8, NDB = D / 32, RS = D + 4, TILE = kB32Tile * RS;
-  __shared__ __align__(16) float lds[2][2][TILE];  // [stage][K, V]
+  // D = 256: one LDS stage (two would be 133 KB); the next tile is loaded
+  // after the barrier that ends the current one.
+  constexpr int NSTG = D > 128 ? 1 : 2;
+  __shared__ __align__(16) float lds[NSTG][2][TILE];  // [stage][K, V]
 
   const int n_qt = (p.Sq + kBwdOwn - 1) / kBwdOwn;
   const int qt = n_qt - 1 - (int)(blockIdx.x / (p.B * p.H));
@@ -152,9 +155,9 @@ void fa_bwd32_dq_kernel(BwdParams p) {
   }
   __syncthreads();
   for (int t = 0; t < n_t; ++t) {
-    const int S = t & 1;
+    const int S = NSTG == 1 ? 0 : t & 1;
     const int kv0 = (t0 + t) * kB32Tile;
-    if (t + 1 < n_t) {
+    if (NSTG == 2 && t + 1 < n_t) {
       kst.load(K, p.k_ss, kv0 + kB32Tile, p.Sk);
       vst.load(V, p.v_ss, kv0 + kB32Tile, p.Sk);
     }
@@ -208,8 +211,13 @@ void fa_bwd32_dq_kernel(BwdParams p) {
           dq[db] = mfma32x32x2f32(Kt[crow(e, g) * RS + db * 32 + j], ds[e], dq[db]);
     }
     if (t + 1 < n_t) {
-      kst.store(lds[S ^ 1][0]);
-      vst.store(lds[S ^ 1][1]);
+      if constexpr (NSTG == 1) {
+        __syncthreads();
+        kst.load(K, p.k_ss, kv0 + kB32Tile, p.Sk);
+        vst.load(V, p.v_ss, kv0 + kB32Tile, p.Sk);
+      }
+      kst.store(lds[NSTG == 1 ? 0 : S ^ 1][0]);
+      vst.store(lds[NSTG == 1 ? 0 : S ^ 1][1]);
     }
     __syncthreads();
   }
@@ -230,7 +238,9 @@ template <int D, bool WANT_K, bool WANT_V, bool DROP = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void fa_bwd32_dkdv_kernel(BwdParams p) {
   constexpr int NQ4 = D / 8, NDB = D / 32, RS = D + 4, TILE = kB32Tile * RS;
-  __shared__ __align__(16) float lds[2][2][TILE];  // [stage][Q, dO]
+  // D = 256: one LDS stage, as in the dQ kernel.
+  constexpr int NSTG = D > 128 ? 1 : 2;
+  __shared__ __align__(16) float lds[NSTG][2][TILE];  // [stage][Q, dO]
   __shared__ __align__(16) float lse_lds[2][kB32Tile];
   __shared__ __align__(16) float dvc_lds[2][kB32Tile];
 
@@ -297,8 +307,8 @@ void fa_bwd32_dkdv_kernel(BwdParams p) {
   }
   __syncthreads();
   for (int u = 0; u < n_steps; ++u) {
-    const int S = u & 1;
-    if (u + 1 < n_steps) load(u + 1);
+    const int S = NSTG == 1 ? 0 : u & 1;
+    if (NSTG == 2 && u + 1 < n_steps) load(u + 1);
     const int qr0 = (t0 + u % n_t) * kB32Tile;
     const bool skip = wk0 >= p.Sk ||
                       (p.win_right >= 0 && wk0 > qr0 + kB32Tile - 1 + p.win_right) ||
@@ -358,7 +368,13 @@ void fa_bwd32_dkdv_kernel(BwdParams p) {
           if constexpr (WANT_K) dk[db] = mfma32x32x2f32(Qt[r], ds[e], dk[db]);
         }
     }
-    if (u + 1 < n_steps) store(S ^ 1);
+    if (u + 1 < n_steps) {
+      if constexpr (NSTG == 1) {
+        __syncthreads();
+        load(u + 1);
+      }
+      store(NSTG == 1 ? 0 : S ^ 1);
+    }
     __syncthreads();
   }
   if (mykey < p.Sk) {
@@ -379,7 +395,7 @@ hipError_t launch_bwd32_d(const BwdParams& p, hipStream_t st) {
   const int n_qt = (p.Sq + kBwdOwn - 1) / kBwdOwn, n_kt = (p.Sk + kBwdOwn - 1) / kBwdOwn;
   hipLaunchKernelGGL((fa_bwd32_dq_kernel<D, DROP>), dim3(p.B * p.H * n_qt), dim3(256), 0, st, p);
   const dim3 grid_kv(p.B * p.H_kv * n_kt);
-  if constexpr (D == 128) {
+  if constexpr (D >= 128) {
     hipLaunchKernelGGL((fa_bwd32_dkdv_kernel<D, true, false, DROP>), grid_kv, dim3(256), 0, st, p);
     hipLaunchKernelGGL((fa_bwd32_dkdv_kernel<D, false, true, DROP>), grid_kv, dim3(256), 0, st, p);
   } else {
@@ -388,9 +404,15 @@ hipError_t launch_bwd32_d(const BwdParams& p, hipStream_t st) {
   return hipGetLastError();
 }
 
+template <bool DROP>
+hipError_t launch_bwd32_drop(const BwdParams& p, int D, hipStream_t st) {
+  if (D == 64) return launch_bwd32_d<64, DROP>(p, st);
+  if (D == 256) return launch_bwd32_d<256, DROP>(p, st);
+  return launch_bwd32_d<128, DROP>(p, st);
+}
+
 hipError_t launch_bwd32(const BwdParams& p, int D, bool drop, hipStream_t st) {
-  if (drop) return D == 64 ? launch_bwd32_d<64, true>(p, st) : launch_bwd32_d<128, true>(p, st);
-  return D == 64 ? launch_bwd32_d<64, false>(p, st) : launch_bwd32_d<128, false>(p, st);
+  return drop ? launch_bwd32_drop<true>(p, D, st) : launch_bwd32_drop<false>(p, D, st);
 }
 
 }  // namespace mpx

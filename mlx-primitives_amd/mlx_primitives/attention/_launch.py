@@ -14,10 +14,11 @@ import torch
 import torch.nn.functional as F
 
 from mlx_primitives import _native
-from mlx_primitives.constants import METAL_ATTENTION_MAX_HEAD_DIM, Layout
+from mlx_primitives.constants import Layout
 
-# Head dims of the kernels (forward, paged, dropout, 16-bit backward); the
-# float32 backward stops at METAL_ATTENTION_MAX_HEAD_DIM (128).
+# Head dims of the kernels (forward, paged, dropout, backward); the reference's
+# Metal kernel stops at METAL_ATTENTION_MAX_HEAD_DIM (128), its other routes
+# take any D.
 _KERNEL_HEAD_DIMS = (32, 64, 128, 256)
 MAX_HEAD_DIM = _KERNEL_HEAD_DIMS[-1]
 
@@ -110,11 +111,8 @@ def _attention_with_grad(q, k, v, layout, scale, causal, window_left, window_rig
             "mlx_primitives (MI355X build) differentiates attention with scale > 0 only "
             f"(got scale={scale}); run it under torch.no_grad()")
     D = q.shape[-1]
-    # Backward kernels: D = 64, 128, and 256 for the 16-bit types.
-    if q.dtype == torch.float32:
-        kernel_head_dim(D, METAL_ATTENTION_MAX_HEAD_DIM, "float32 backward")
-    else:
-        kernel_head_dim(D, MAX_HEAD_DIM, "backward")
+    # Backward kernels: D = 64, 128 and 256.
+    kernel_head_dim(D, MAX_HEAD_DIM, "backward")
     dk = 64 if D <= 64 else (128 if D <= 128 else 256)
     qk, kk, vk = (_prepare(x, dk) for x in (q, k, v))
     o = _FlashAttentionFn.apply(qk, kk, vk, layout, scale, causal, window_left, window_right,

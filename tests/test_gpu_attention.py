@@ -159,8 +159,8 @@ def test_head_dim_limits(device):
     x = torch.zeros(1, 8, 1, 264, device=device)
     with pytest.raises(NotImplementedError, match="256"):
         flash_attention(x, x, x)
-    y = torch.zeros(1, 8, 1, 160, device=device, requires_grad=True)
-    with pytest.raises(NotImplementedError, match="float32 backward.*128"):
+    y = torch.zeros(1, 8, 1, 264, device=device, requires_grad=True)
+    with pytest.raises(NotImplementedError, match="256"):
         flash_attention(y, y, y)
     with pytest.raises(NotImplementedError, match="256"):
         flash_attention(x, x, x, dropout_p=0.1)

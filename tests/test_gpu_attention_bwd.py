@@ -75,13 +75,14 @@ def test_flash_grad(device, dtype, layout, D, causal):
     check_grads(g, q, k, v, d, dtype, scale, causal, layout=layout)
 
 
-@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("layout", ["BSHD", "BHSD"])
 @pytest.mark.parametrize("D", [160, 256])
 @pytest.mark.parametrize("causal", [True, False])
 def test_flash_grad_head_dims_above_128(device, dtype, layout, D, causal):
-    # 16-bit head dims 129 .. 256: the D = 256 backward kernels (one wave per
-    # SIMD, 32-row streamed tiles in dK / dV), inputs zero-padded.
+    # Head dims 129 .. 256: the D = 256 backward kernels (16-bit: one wave per
+    # SIMD, 32-row streamed tiles in dK / dV; float32: one LDS stage), inputs
+    # zero-padded.
     B, S, H = 2, 200, 3
     shape = (B, S, H, D) if layout == "BSHD" else (B, H, S, D)
     q, k, v, dout = (rnd(shape, 70 + i, dtype) for i in range(4))
