@@ -37,7 +37,7 @@ def check(out, ref, dtype):
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("layout", ["BSHD", "BHSD"])
-@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("D", [64, 128, 256])
 @pytest.mark.parametrize("H,H_kv", [(8, 1), (8, 2), (6, 3)])
 def test_flash_gqa(device, dtype, layout, D, H, H_kv):
     B, S = 2, 300
@@ -88,7 +88,7 @@ def paged_inputs(dtype, B, Sq, H, H_kv, D, bs, lens, seed):
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("Sq", [1, 77])
-@pytest.mark.parametrize("H,H_kv,D", [(32, 8, 128), (8, 1, 64), (12, 4, 128)])
+@pytest.mark.parametrize("H,H_kv,D", [(32, 8, 128), (8, 1, 64), (12, 4, 128), (8, 2, 256)])
 def test_paged_gqa(device, dtype, Sq, H, H_kv, D):
     lens = [700, 33, 400]
     q, kp, vp, tables, lens_t = paged_inputs(dtype, 3, Sq, H, H_kv, D, 16, lens, H + D + Sq)
