@@ -1,4 +1,4 @@
-"""The reference-side ctypes binding shown in INTEGRATION.md works as written:
+"""The reference-side ctypes binding of the integration guide works as written:
 its code block is executed against the in-tree library and its results are
 compared with the drop-in API on the same inputs (bit-identical: same kernels).
 """
