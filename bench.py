@@ -873,7 +873,7 @@ def main() -> int:
             "kernel_ms_median": h_med, "kernel_ms_min": h_min, "flop_per_step": hflops,
             "roofline": {"bound": "mfma", "achieved": h_tf, "peak": PEAK_BF16_TFLOPS,
                          "unit": "TFLOP/s", "frac": h_tf / PEAK_BF16_TFLOPS,
-                         "kernel": "fa_fwd16_wide_kernel<256,32,4,bf16>",
+                         "kernel": "fa_fwd16_wide_kernel<256,64,4,bf16> (DMA staging)",
                          "traffic": measured_traffic("flash_d256_bf16"),
                          "traffic_unit": "bytes per launch"},
         },

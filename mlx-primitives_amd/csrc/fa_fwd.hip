@@ -805,11 +805,14 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& pin, const Wor
   constexpr int RPD = 1024 / ROWB;     // rows per DMA instruction (64 lanes x 16 bytes)
   constexpr int RSTEP = RPD * NW;      // rows one DMA instruction of every wave covers
   constexpr int NDMA = BN / RSTEP;     // DMA instructions per wave per K (or V) tile
-  static_assert((NW == 8 || NW == 4) && (D == 128 || D == 64) && NDMA * RSTEP == BN,
+  static_assert((NW == 8 || NW == 4) && (D == 128 || D == 64 || (D == 256 && NW == 4)) &&
+                    NDMA * RSTEP == BN,
                 "each wave stages rows RPD*wave .. +RPD-1, +RSTEP, ...");
   // The row swizzles depend on row bits below RSTEP only (bits 0-3 at D = 128,
-  // 1-3 at D = 64), so every DMA instruction of a lane uses the same chunk.
-  static_assert(RSTEP % 16 == 0, "swizzle period");
+  // 1-3 at D = 64), so every DMA instruction of a lane uses the same chunk. At
+  // D = 256 (RSTEP = 8) the K swizzle takes bits 0-3: a lane's rows of even and
+  // odd instructions differ in bit 3, and each kind has its own chunk.
+  static_assert(RSTEP % 16 == 0 || D == 256, "swizzle period");
   static_assert((NST - 2) * 2 * NDMA <= 15, "vmcnt immediate");
   // Paged: keys exist up to this sequence's context length.
   FwdParams p = pin;
@@ -879,16 +882,24 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& pin, const Wor
   // DMA lane mapping: this wave's first instruction fills LDS rows
   // RPD*wave .. +RPD-1 (lane -> row lr, slot lane % (ROWB/16)); instruction r
   // fills rows lr + RSTEP*r.
-  int lr, kchunk, vchunk;
+  int lr, kchunk, vchunk, kchunk_odd = 0;
   if constexpr (D == 128) {
     lr = 4 * wave + (lane >> 4);
     kchunk = (lane & 15) ^ (lr & 15);
     vchunk = (lane & 15) ^ (4 * (lr & 3));
+  } else if constexpr (D == 256) {
+    // 512-byte rows, two per instruction: instruction r fills rows lr + 8 r,
+    // lr < 8; K row r has chunk c at slot c ^ (r & 15), V row r at c ^ 4 (r & 3).
+    lr = 2 * wave + (lane >> 5);
+    kchunk = (lane & 31) ^ lr;
+    kchunk_odd = (lane & 31) ^ (lr + 8);
+    vchunk = (lane & 31) ^ (4 * (lr & 3));
   } else {
     lr = 8 * wave + (lane >> 3);
     kchunk = vchunk = (lane & 7) ^ swz64(lr);
   }
   const int kgo = (lr * (int)p.k_ss + kchunk * 8) * 2;
+  const int kgo_odd = (lr * (int)p.k_ss + kchunk_odd * 8) * 2;  // (D = 256)
   // Paged, 128-key tiles: the lane part of a DMA offset (row lr % RPD of the
   // instruction's RPD rows, this lane's chunk).
   const int klane = ((lr % RPD) * (int)p.k_ss + kchunk * 8) * 2;
@@ -992,7 +1003,9 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& pin, const Wor
     const int kso = kv0 * (int)p.k_ss * 2, vso = kv0 * (int)p.v_ss * 2;
     if (kv0 + BN <= p.Sk) {
 #pragma unroll
-      for (int r = 0; r < NDMA; ++r) dma16(krs, kdst + r * RSTEP * ROWB, kgo, kso + r * kstep);
+      for (int r = 0; r < NDMA; ++r)
+        dma16(krs, kdst + r * RSTEP * ROWB, (D == 256 && (r & 1)) ? kgo_odd : kgo,
+              kso + r * kstep);
 #pragma unroll
       for (int r = 0; r < NDMA; ++r) dma16(vrs, vdst + r * RSTEP * ROWB, vgo, vso + r * vstep);
     } else {
@@ -1002,7 +1015,8 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& pin, const Wor
 #pragma unroll
       for (int r = 0; r < NDMA; ++r) {
         const int row = min(lr + RSTEP * r, lim);
-        dma16(krs, kdst + r * RSTEP * ROWB, (row * (int)p.k_ss + kchunk * 8) * 2, kso);
+        const int kc = (D == 256 && (r & 1)) ? kchunk_odd : kchunk;
+        dma16(krs, kdst + r * RSTEP * ROWB, (row * (int)p.k_ss + kc * 8) * 2, kso);
         dma16(vrs, vdst + r * RSTEP * ROWB, (row * (int)p.v_ss + vchunk * 8) * 2, vso);
       }
     }
@@ -1011,7 +1025,7 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& pin, const Wor
   // QK operand (A = K rows) of lane (j, g): row nb*32 + krow_perm, logical
   // chunk 2*ks + g, stored at slot (2*ks + g) ^ (row & 15).
   const int krow_perm = (j & ~12) | ((j & 4) << 1) | ((j & 8) >> 1);
-  const int ky = D == 128 ? krow_perm & 15 : swz64(krow_perm);
+  const int ky = D >= 128 ? krow_perm & 15 : swz64(krow_perm);
   int kaddr[NKS];
 #pragma unroll
   for (int ks = 0; ks < NKS; ++ks)
@@ -1022,7 +1036,7 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& pin, const Wor
   int vaddr[NDB], vaddr_hi[NDB];  // rows +16 sl (lo), +16 sl + 4 (hi)
 #pragma unroll
   for (int db = 0; db < NDB; ++db) {
-    if constexpr (D == 128) {
+    if constexpr (D >= 128) {
       vaddr[db] = (8 * g + (s16 >> 2)) * ROWB + 64 * (db ^ (s16 >> 2)) +
                   32 * ((lane >> 4) & 1) + 8 * (s16 & 3);
       vaddr_hi[db] = vaddr[db] + 4 * ROWB;
@@ -1227,7 +1241,9 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& pin, const Wor
     if (pmask) full = false;
     f32x16 s[NB];
     qk_mfma(Kb, s);
-    qk_sched();
+    // (D = 256: the compiler's own order; the pattern's K reads of block nb + 1
+    // under block nb would hold 128 registers of operands)
+    if constexpr (D <= 128) qk_sched();
     max_rescale(s, kv0, full, pmask);
     exp_pv(s, Kb + KBYTES, kv0);
   };
@@ -1395,16 +1411,28 @@ constexpr int kNumWavesWide = 4;
 template <int D, int BN, int NW, bool BF16, bool PAGED = false, bool DROP = false>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void fa_fwd16_wide_kernel(FwdParams p) {
-  constexpr int kLdsBytes = kFa16Stages * fa16_stage_elems<D, BN>() * 2;
-  static_assert(kLdsBytes + (PAGED ? kMaxItemPages * 4 : 0) <= 131072, "LDS budget");
+  // Dense K/V with 64-key tiles: direct (DMA) staging, two stages of 64 KB.
+  constexpr bool kDirect = !PAGED && BN == 64;
+  constexpr int kLdsBytes = kDirect ? 16 : kFa16Stages * fa16_stage_elems<D, BN>() * 2;
+  constexpr int kStageB = kDirect ? 2 * BN * 2 * D : 16;
+  static_assert(kLdsBytes + 2 * kStageB + (PAGED ? kMaxItemPages * 4 : 0) <= 131072 + 16,
+                "LDS budget");
   __shared__ __align__(16) uint16_t smem[kLdsBytes / 2];
+  __shared__ __align__(16) unsigned char dst0[kStageB];
+  __shared__ __align__(16) unsigned char dst1[kStageB];
+  __shared__ __align__(16) unsigned char unused2[16], unused3[16];  // (stages 2, 3: none)
   __shared__ int pages[PAGED ? kMaxItemPages : 1];
   const WorkSlot ws = decode_slot(p);
   const int n_items = slot_items(p, ws);
   // Every item ends with a barrier after its last LDS read.
 #pragma nounroll
-  for (int item = 0; item < n_items; ++item)
-    fa16_rows<D, BN, NW, BF16, PAGED, DROP>(p, slot_item(p, ws, item), smem, pages);
+  for (int item = 0; item < n_items; ++item) {
+    if constexpr (kDirect)
+      fa16_rows_direct<D, BN, NW, BF16, 2, false, DROP>(p, slot_item(p, ws, item), dst0, dst1,
+                                                         unused2, unused3, nullptr);
+    else
+      fa16_rows<D, BN, NW, BF16, PAGED, DROP>(p, slot_item(p, ws, item), smem, pages);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -1810,7 +1838,7 @@ bool paged_wide_tiles(int D, int dtype, int bs_log2, bool alibi) {
 // page sizes, take 64).
 int tile_n(int D, int dtype, bool paged = false, int bs_log2 = -1, bool alibi = false) {
   if (dtype == MPX_F32) return D > 64 ? 32 : 64;
-  if (D > 128) return 32;
+  if (D > 128) return paged ? 32 : 64;
   if (paged) return paged_wide_tiles(D, dtype, bs_log2, alibi) ? 128 : 64;
   return D < 64 || !MPX_FA_DIRECT ? 64 : MPX_FA_BN16;
 }
@@ -1876,13 +1904,15 @@ constexpr int kBN16 = PAGED || D < 64 || !MPX_FA_DIRECT ? 64 : MPX_FA_BN16;
 template <bool PAGED>
 hipError_t dispatch_fwd(const FwdParams& p, int D, int dtype, int grid, hipStream_t st) {
   if (D == 256) {
+    // (16-bit: 64-key DMA-staged tiles dense, 32-key register-staged paged)
+    constexpr int kBNw = PAGED ? 32 : 64;
     if (dtype == MPX_F32) return launch_fwd<256, 32, true, false, PAGED>(p, grid, st);
     if (dtype == MPX_BF16)
-      hipLaunchKernelGGL((fa_fwd16_wide_kernel<256, 32, kNumWavesWide, true, PAGED>), dim3(grid),
-                         dim3(64 * kNumWavesWide), 0, st, p);
+      hipLaunchKernelGGL((fa_fwd16_wide_kernel<256, kBNw, kNumWavesWide, true, PAGED>),
+                         dim3(grid), dim3(64 * kNumWavesWide), 0, st, p);
     else
-      hipLaunchKernelGGL((fa_fwd16_wide_kernel<256, 32, kNumWavesWide, false, PAGED>), dim3(grid),
-                         dim3(64 * kNumWavesWide), 0, st, p);
+      hipLaunchKernelGGL((fa_fwd16_wide_kernel<256, kBNw, kNumWavesWide, false, PAGED>),
+                         dim3(grid), dim3(64 * kNumWavesWide), 0, st, p);
     return hipGetLastError();
   }
   if constexpr (PAGED) {
@@ -1922,10 +1952,10 @@ hipError_t dispatch_fwd_drop(const FwdParams& p, int D, int dtype, int grid, hip
       hipLaunchKernelGGL((fa_fwd32_kernel<256, 32, kNumWaves32, false, true>), dim3(grid),
                          dim3(64 * kNumWaves32), 0, st, p);
     else if (dtype == MPX_BF16)
-      hipLaunchKernelGGL((fa_fwd16_wide_kernel<256, 32, kNumWavesWide, true, false, true>),
+      hipLaunchKernelGGL((fa_fwd16_wide_kernel<256, 64, kNumWavesWide, true, false, true>),
                          dim3(grid), dim3(64 * kNumWavesWide), 0, st, p);
     else
-      hipLaunchKernelGGL((fa_fwd16_wide_kernel<256, 32, kNumWavesWide, false, false, true>),
+      hipLaunchKernelGGL((fa_fwd16_wide_kernel<256, 64, kNumWavesWide, false, false, true>),
                          dim3(grid), dim3(64 * kNumWavesWide), 0, st, p);
     return hipGetLastError();
   }
