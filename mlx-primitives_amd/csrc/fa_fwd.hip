@@ -1402,11 +1402,11 @@ void fa_fwd16_drop_kernel(FwdParams p) {
                                                              dst2, dst3, nullptr);
 }
 
-// Head dims 129 .. 256 (zero-padded to 256): the register-staged rows with
-// 32-key tiles and four waves of one wave per SIMD. The Q fragments (64
-// registers), the O accumulators (128) and the staged tile loads do not fit
-// the 256 registers of two waves per SIMD. PAGED: K/V through the page table
-// (prefill over a paged cache), as the 64-key paged kernels.
+// Head dims 129 .. 256 (zero-padded to 256): four waves of one wave per SIMD,
+// since the Q fragments (64 registers) and the O accumulators (128) leave too
+// little of the 256 registers of two waves per SIMD. Dense K/V: the direct
+// (DMA-staged) rows with 64-key tiles. PAGED (prefill over a paged cache): the
+// register-staged rows with 32-key tiles and the item's page-table slice.
 constexpr int kNumWavesWide = 4;
 template <int D, int BN, int NW, bool BF16, bool PAGED = false, bool DROP = false>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(1, 1)))
