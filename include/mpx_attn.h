@@ -385,7 +385,7 @@ int mpx_attn_bwd_dropout(const void* q, const void* k, const void* v, const void
  * MPX_NOALLOC_SCRATCH_BYTES that the library holds on each GPU it runs on
  * until the process ends. Calls needing more (B * H *
  * ceil(max_blocks * block_size / 512) * (kernel head dim + 2) * 4 bytes,
- * kernel head dim = 32, 64 or 128 >= D) return MPX_EINVAL. Nothing in the
+ * kernel head dim = 32, 64, 128 or 256 >= D) return MPX_EINVAL. Nothing in the
  * array has to start at zero: each call writes every partial it reads. All
  * calls on one GPU share that GPU's array, so two calls that overlap on one
  * GPU (different streams, or threads without ordering) race and corrupt each
