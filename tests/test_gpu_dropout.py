@@ -89,6 +89,26 @@ def test_forward_keep_mask_bit_exact(device, dtype, D, causal):
     assert np.array_equal(np.rint(measured), expected)
 
 
+@pytest.mark.parametrize("p", [0.9, 0.999, 1e-3])
+def test_forward_keep_mask_extreme_rates(device, p):
+    # High and low rates: the threshold's rounding (p * 65536) and both hash
+    # halves at the ends of their range.
+    measured, expected = mask_counts(device, torch.float32, 2, 2, 64, 512, 64, p, 99, False)
+    assert np.array_equal(np.rint(measured), expected)
+    if p > 0.5:
+        assert expected.sum() < 0.2 * 2 * 2 * 64 * 512
+
+
+def test_tiny_rate_keeps_everything(device):
+    # p < 2^-17 rounds to threshold 0: every weight is kept, scaled by 1 / (1 - p).
+    q, k, v = (rnd((2, 200, 4, 64), 60 + i, torch.float32).to(device) for i in range(3))
+    p = 1e-6
+    got = run_attention(q, k, v, Layout.BSHD, 0.125, True, dropout_p=p, dropout_seed_value=5)
+    plain = run_attention(q, k, v, Layout.BSHD, 0.125, True)
+    torch.cuda.synchronize()
+    torch.testing.assert_close(got, plain / (1 - p), rtol=1e-6, atol=1e-6)
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_forward_keep_mask_single_pass_and_window(device, dtype):
     # Many (batch, head) rows: one pass per q-tile (no split), paired causal
