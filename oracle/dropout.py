@@ -74,9 +74,17 @@ def threshold(p: float) -> int:
 
 def keep_mask(B: int, H: int, Sq: int, Sk: int, p: float, seed: int) -> np.ndarray:
     """(B, H, Sq, Sk) bool: True where the kernels keep the weight."""
+    return keep_mask_rows(0, B * H * Sq, Sk, p, seed).reshape(B, H, Sq, Sk)
+
+
+def keep_mask_rows(first_row: int, n_rows: int, Sk: int, p: float, seed: int) -> np.ndarray:
+    """(n_rows, Sk) bool keep mask of rows first_row .. first_row + n_rows - 1,
+    row r = (b * H + h) * Sq + q as above (one (b, h) slice of a large problem
+    without the whole mask)."""
     seed_lo = np.uint32(seed & 0xFFFFFFFF)
     seed_hi = np.uint32((seed >> 32) & 0xFFFFFFFF)
-    rows = (np.arange(B * H * Sq, dtype=np.uint64) & np.uint64(0xFFFFFFFF)).astype(np.uint32)
+    rows = ((np.arange(n_rows, dtype=np.uint64) + np.uint64(first_row)) &
+            np.uint64(0xFFFFFFFF)).astype(np.uint32)
     pairs = np.arange((Sk + 1) // 2, dtype=np.uint32)
     with np.errstate(over="ignore"):
         rk = rows * _G_ROW + seed_lo
@@ -85,10 +93,10 @@ def keep_mask(B: int, H: int, Sq: int, Sk: int, p: float, seed: int) -> np.ndarr
     t = np.uint32(threshold(p))
     lo = (bits & np.uint32(0xFFFF)) >= t
     hi = (bits >> np.uint32(16)) >= t
-    keep = np.empty((B * H * Sq, 2 * pairs.size), dtype=bool)
+    keep = np.empty((n_rows, 2 * pairs.size), dtype=bool)
     keep[:, 0::2] = lo
     keep[:, 1::2] = hi
-    return keep[:, :Sk].reshape(B, H, Sq, Sk)
+    return keep[:, :Sk]
 
 
 def attention_dropout_fwd_bhsd(q, k, v, scale, causal, keep, p, window_left=-1,

@@ -89,6 +89,28 @@ def test_forward_keep_mask_bit_exact(device, dtype, D, causal):
     assert np.array_equal(np.rint(measured), expected)
 
 
+def test_forward_keep_mask_headline_size(device):
+    # The headline shape (4 x 32 heads x 4096, D = 128, causal; paired q-tile
+    # slots, row indices up to 2^19): kept-key counts of two whole (b, h)
+    # slices against the oracle's mask.
+    B, H, S, D, p, seed = 4, 32, 4096, 128, 0.1, 0xABCDEF
+    q = torch.zeros((B, S, H, D), dtype=torch.bfloat16, device=device)
+    k = torch.zeros((B, S, H, D), dtype=torch.bfloat16, device=device)
+    v = torch.zeros((1, S, 1, D), dtype=torch.bfloat16)
+    v[0, torch.arange(S), 0, torch.arange(S) % D] = 1.0
+    v = v.to(device).expand(B, S, H, D)
+    out = run_attention(q, k, v, Layout.BSHD, 1.0, True, dropout_p=p, dropout_seed_value=seed)
+    torch.cuda.synchronize()
+    n = np.arange(1, S + 1, dtype=np.float64)
+    onehot = ((np.arange(S)[:, None] % D) == np.arange(D)[None, :]).astype(np.float64)
+    vis = np.tril(np.ones((S, S), dtype=bool))
+    for b, h in [(0, 0), (3, 31)]:
+        keep = od.keep_mask_rows((b * H + h) * S, S, S, p, seed)
+        expected = (keep & vis).astype(np.float64) @ onehot
+        got = out[b, :, h].double().cpu().numpy() * n[:, None] * (1.0 - p)
+        assert np.abs(got - expected).max() < 0.25, (b, h)
+
+
 @pytest.mark.parametrize("p", [0.9, 0.999, 1e-3])
 def test_forward_keep_mask_extreme_rates(device, p):
     # High and low rates: the threshold's rounding (p * 65536) and both hash

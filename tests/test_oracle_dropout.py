@@ -77,6 +77,9 @@ def test_keep_mask_layout():
     # an odd Sk truncates the last pair's high half
     wide = od.keep_mask(2, 3, 10, 10, 0.5, seed=7)
     assert np.array_equal(wide[..., :9], keep)
+    # a row range of a bigger problem is the same slice of the whole mask
+    rows = od.keep_mask_rows(1 * 3 * 10 + 2 * 10, 10, 9, 0.5, seed=7)
+    assert np.array_equal(rows, keep[1, 2])
 
 
 def _torch_dropout_attention(q, k, v, scale, keep, p, vis):
