@@ -139,6 +139,13 @@ def run_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, layout: Lay
     dk = kernel_head_dim(D)
     dropout = None
     if dropout_p > 0.0:
+        if dropout_seed_value is None and torch.cuda.is_current_stream_capturing():
+            # The seed is a launch argument drawn on the host: a captured graph
+            # would replay this one keep mask on every launch.
+            raise RuntimeError(
+                "mlx_primitives (MI355X build): attention dropout under HIP graph capture "
+                "would reuse one keep mask on every replay; capture without dropout, or "
+                "pass an explicit seed (run_attention(..., dropout_seed_value=...))")
         dropout = (float(dropout_p),
                    dropout_seed() if dropout_seed_value is None else int(dropout_seed_value))
     if q_rope is not None:

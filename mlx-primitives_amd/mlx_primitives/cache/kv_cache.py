@@ -204,11 +204,17 @@ class KVCache:
         if position is None:
             if k.shape[0] == 0:
                 return
-            pt.extend_sequence(lsid, k.shape[0])
         else:
             pt.truncate_sequence(lsid, position)
+        before = pt.get_sequence_metadata(lsid).num_tokens
+        try:
             pt.extend_sequence(lsid, k.shape[0])
-        self._store_kv(sequence_id, k, v, layer_idx, rope=rope)
+            self._store_kv(sequence_id, k, v, layer_idx, rope=rope)
+        except Exception:
+            # Out of blocks (or a rejected write): the sequence keeps no tokens
+            # that no kernel wrote.
+            pt.truncate_sequence(lsid, before)
+            raise
 
     def update_batch(self, sequence_ids: Sequence[int], k: torch.Tensor, v: torch.Tensor,
                      layer_idx: int, num_tokens: Optional[Sequence[int]] = None,
@@ -228,6 +234,9 @@ class KVCache:
         counts = [k.shape[1]] * len(sequence_ids) if num_tokens is None else list(num_tokens)
         if len(counts) != len(sequence_ids) or any(c < 0 or c > k.shape[1] for c in counts):
             raise ValueError(f"num_tokens must give 0..{k.shape[1]} tokens per sequence")
+        if len(set(sequence_ids)) != len(sequence_ids):
+            raise ValueError("update_batch: sequence_ids must be distinct (one append per "
+                             "sequence and step)")
         pt = self._page_tables[layer_idx]
         bs = self._config.block_size
         if rope is not None:
@@ -235,15 +244,23 @@ class KVCache:
                 pt.get_sequence_metadata(self._layer_id(sid, layer_idx)).num_tokens + n
                 for sid, n in zip(sequence_ids, counts)))
         lsids, starts = [], []
-        for sid, n in zip(sequence_ids, counts):
-            lsid = self._layer_id(sid, layer_idx)
-            self._notify("on_access", sid)
-            start = pt.get_sequence_metadata(lsid).num_tokens
-            if n > 0:
-                pt.extend_sequence(lsid, n)
-                pt.make_writable(lsid, start // bs, (start + n - 1) // bs)
-            lsids.append(lsid)
-            starts.append(start)
+        try:
+            for sid, n in zip(sequence_ids, counts):
+                lsid = self._layer_id(sid, layer_idx)
+                self._notify("on_access", sid)
+                start = pt.get_sequence_metadata(lsid).num_tokens
+                lsids.append(lsid)
+                starts.append(start)
+                if n > 0:
+                    pt.extend_sequence(lsid, n)
+                    pt.make_writable(lsid, start // bs, (start + n - 1) // bs)
+        except Exception:
+            # The pool ran out partway: every sequence of the batch goes back to
+            # its length before the call (blocks allocated here are freed), so
+            # none counts tokens that the kernel never wrote.
+            for lsid, start in zip(lsids, starts):
+                pt.truncate_sequence(lsid, start)
+            raise
         if not any(counts):
             return
         tables = pt.get_block_table_tensor(lsids)

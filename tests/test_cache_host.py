@@ -237,3 +237,39 @@ def test_kv_cache_lru_eviction():
     n = c.evict_if_needed(total - used + 1, protected_sequences=[ids[1]])
     assert n == 1 and ids[1] in c.get_all_sequence_ids() and ids[2] not in c.get_all_sequence_ids()
     assert c.evict_if_needed(0) == 0
+
+
+def test_kv_cache_update_batch_rolls_back_when_the_pool_runs_out():
+    # Three 100-block appends into 274 free blocks: the third cannot allocate,
+    # and the two sequences already extended go back to their lengths, so no
+    # sequence counts tokens that were never written.
+    c = small_cache()
+    ids = [c.create_sequence() for _ in range(3)]
+    free = c._allocators[0].num_free_blocks
+    T = 16 * 100
+    assert 2 * 100 <= free < 3 * 100
+    k = torch.zeros((3, T, 8, 64), dtype=torch.float16)
+    with pytest.raises(RuntimeError, match="Cannot allocate"):
+        c.update_batch(ids, k, k, 0)
+    assert [c.get_sequence_length(s) for s in ids] == [0, 0, 0]
+    assert c._allocators[0].num_free_blocks == free
+    with pytest.raises(ValueError, match="distinct"):
+        c.update_batch([ids[0], ids[0]], k[:2], k[:2], 0)
+
+
+def test_kv_cache_update_rolls_back_a_failed_copy_on_write():
+    # A shared, partly filled last block needs a private copy before the next
+    # token is written; with the pool empty the copy fails and the sequence
+    # keeps its length and its table.
+    c = small_cache()
+    a = c.create_sequence()
+    pt, alloc = c._page_tables[0], c._allocators[0]
+    lsid = c._sequence_ids[a][0]
+    pt.extend_sequence(lsid, 150)
+    c.fork_sequence(a)
+    table = pt.get_block_table(lsid)
+    alloc.allocate(alloc.num_free_blocks)
+    one = torch.zeros((1, 8, 64), dtype=torch.float16)
+    with pytest.raises(RuntimeError, match="Cannot allocate"):
+        c.update(a, one, one, 0)
+    assert c.get_sequence_length(a) == 150 and pt.get_block_table(lsid) == table

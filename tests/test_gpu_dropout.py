@@ -3,12 +3,15 @@ mpx_attn_bwd_dropout through flash_attention, sliding_window_attention,
 chunked_cross_attention and autograd) against the CPU oracle
 (oracle/dropout.py) with the same seed.
 
-  * The keep mask bit for bit: with Q = 0 every visible key weighs the same
-    and V[k] = one-hot(k mod D) makes output column d count the kept visible
+  * The keep mask: with Q = 0 every visible key weighs the same and
+    V[k] = one-hot(k mod D) makes output column d count the kept visible
     keys k = d (mod D): O[q, d] * n_visible(q) * (1 - p) is that count (an
     integer: float32 / float16 exactly, bfloat16 to well under 0.5 for the
     counts used), compared with the oracle's mask for every row, column,
-    batch and head, on the split-KV and the single-pass forward.
+    batch and head, on the split-KV and the single-pass forward (kept-key
+    counts per residue class, every dtype). In float32, V[k] =
+    2^(k // D) * one-hot(k mod D) turns each count into a bitmap of the kept
+    keys, compared key by key with the oracle's mask.
   * The forward on random inputs: float32 rtol 1e-4 / atol 1e-5, 16-bit
     max-abs 2e-2 against the float64 oracle (the plain forward's bars).
   * The gradients: the plain backward's bars (tests/test_gpu_attention_bwd.py:
@@ -111,6 +114,60 @@ def test_forward_keep_mask_headline_size(device):
         assert np.abs(got - expected).max() < 0.25, (b, h)
 
 
+def mask_bits(device, B, H, Sq, Sk, D, p, seed, causal, wl=-1):
+    """(measured, expected) per-key keep bitmaps, float32: with Q = 0 and
+    V[k] = 2^(k // D) * one-hot(k mod D), output column d times
+    n_visible * (1 - p) is sum over the kept visible keys k = d (mod D) of
+    2^(k // D), so bit j of its integer value says whether key j * D + d was
+    kept. Sk <= 16 * D keeps every value an exact float32 integer below 2^16."""
+    assert Sk <= 16 * D
+    q = torch.zeros((B, Sq, H, D), dtype=torch.float32, device=device)
+    k = torch.zeros((B, Sk, H, D), dtype=torch.float32, device=device)
+    v = torch.zeros((B, Sk, H, D), dtype=torch.float32)
+    idx = torch.arange(Sk)
+    # (two advanced indices around a slice: the indexed view is (Sk, B, H))
+    v[:, idx, :, idx % D] = (2.0 ** (idx // D).float())[:, None, None]
+    v = v.to(device)
+    out = run_attention(q, k, v, Layout.BSHD, 1.0, causal, wl, -1, dropout_p=p,
+                        dropout_seed_value=seed)
+    torch.cuda.synchronize()
+    vis = visible(Sq, Sk, causal, wl)
+    n = vis.sum(axis=1).astype(np.float64)
+    got = out.double().cpu().numpy().transpose(0, 2, 1, 3)  # (B, H, Sq, D)
+    measured = got * n[None, None, :, None] * (1.0 - p)
+    keep = od.keep_mask(B, H, Sq, Sk, p, seed) & vis[None, None]
+    weight = np.where((np.arange(Sk)[:, None] % D) == np.arange(D)[None, :],
+                      2.0 ** (np.arange(Sk) // D)[:, None], 0.0)
+    expected = keep.astype(np.float64) @ weight
+    return measured, expected
+
+
+@pytest.mark.parametrize("causal,wl", [(False, -1), (True, -1), (True, 300)])
+@pytest.mark.parametrize("D,Sq", [(64, 200), (128, 2048), (128, 300)])
+def test_forward_keep_mask_per_key(device, causal, wl, D, Sq):
+    # Every kept key identified, not only the count per residue class: a tile
+    # order or pair offset error that moves a kept weight to another key of
+    # the same residue changes the bitmap. Sq = 200 runs the split-KV path,
+    # Sq = 2048 (16 q-tiles per head) a single pass per q-tile.
+    B, H, p, seed = 2, 3, 0.3, SEED ^ (D + Sq)
+    Sk = Sq if causal else 1024
+    measured, expected = mask_bits(device, B, H, Sq, Sk, D, p, seed, causal, wl)
+    assert np.abs(measured - expected).max() < 0.25
+    assert np.array_equal(np.rint(measured), expected)
+
+
+def test_dropout_refuses_graph_capture_without_seed(device, monkeypatch):
+    # A seed drawn on the host at capture time would be replayed by every
+    # graph launch (the same keep mask each step), so a capture needs an
+    # explicit dropout seed; the check runs before any launch.
+    q = torch.zeros((1, 64, 2, 64), dtype=torch.bfloat16, device=device)
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: True)
+    with pytest.raises(RuntimeError, match="graph capture"):
+        run_attention(q, q, q, Layout.BSHD, 0.125, True, dropout_p=0.1)
+    with pytest.raises(RuntimeError, match="graph capture"):
+        flash_attention(q, q, q, causal=True, dropout_p=0.1)
+
+
 @pytest.mark.parametrize("p", [0.9, 0.999, 1e-3])
 def test_forward_keep_mask_extreme_rates(device, p):
     # High and low rates: the threshold's rounding (p * 65536) and both hash
@@ -144,7 +201,7 @@ def test_forward_keep_mask_single_pass_and_window(device, dtype):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
-@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("D", [64, 128, 256])
 @pytest.mark.parametrize("causal", [True, False])
 def test_forward_vs_oracle(device, dtype, D, causal):
     B, S, H, p = 2, 333, 4, 0.25
@@ -177,7 +234,7 @@ def check_grads(got, want, dtype, p):
 
 
 @pytest.mark.parametrize("dtype,D", [(dt, d) for dt in DTYPES for d in (64, 128)] +
-                         [(torch.float16, 256), (torch.bfloat16, 256)])
+                         [(dt, 256) for dt in DTYPES])
 @pytest.mark.parametrize("causal,wl,H_kv", [(True, -1, 4), (False, -1, 4), (True, 50, 4),
                                             (True, -1, 2)])
 def test_grad_vs_oracle(device, dtype, D, causal, wl, H_kv):
