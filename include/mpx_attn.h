@@ -136,7 +136,8 @@ size_t mpx_paged_decode_workspace_bytes(int B, int H, int D, int block_size, int
  * t < context_lens[b] and 0 <= block_tables[b, t / block_size] < num_blocks.
  * Exact softmax over the valid, unmasked tokens; a query row with none gets
  * NaN (the reference's softmax over an all -inf row). D in {32, 64, 128, 256};
- * 16-bit pools must be below 4 GiB each (MPX_EUNSUPPORTED otherwise).
+ * pools of any size (from 4 GiB - 256 bytes on, 16-bit pools are read through
+ * 64-bit addresses).
  */
 int mpx_paged_prefill(const void* q, const void* k_pool, const void* v_pool,
                       const int32_t* block_tables, const int32_t* context_lens,

@@ -271,7 +271,8 @@ constexpr int fa16_stage_elems() {
 // Query rows [32*NW*wi.qt, +32*NW) of one (batch, head) against its KV range.
 // PAGED: K/V rows come from pools through the page table (prefill over a
 // paged cache); invalid rows load as zeros and are masked.
-template <int D, int BN, int NW, bool BF16, bool PAGED, bool DROP = false>
+// BIG (paged, pools of 4 GiB and more): page rows through 64-bit addresses.
+template <int D, int BN, int NW, bool BF16, bool PAGED, bool DROP = false, bool BIG = false>
 __device__ __forceinline__ void fa16_rows(const FwdParams& pin, const WorkItem wi,
                                           uint16_t* __restrict__ smem, int* __restrict__ pages) {
   FwdParams p = pin;
@@ -343,6 +344,23 @@ __device__ __forceinline__ void fa16_rows(const FwdParams& pin, const WorkItem w
     }
     return (int)off;
   };
+  // BIG: the same chunk's 64-bit address (missing rows: kZeroChunk).
+  const unsigned char* kbase = (const unsigned char*)p.k + (wi.b * p.k_sb + kvh * p.k_sh) * 2;
+  const unsigned char* vbase = (const unsigned char*)p.v + (wi.b * p.v_sb + kvh * p.v_sh) * 2;
+  auto paged_chunk = [&](const unsigned char* base, int pos, int col, uint32_t row_bytes)
+                         __attribute__((always_inline)) -> u32x4 {
+    const u32x4* a = &kZeroChunk;
+    if (pos < p.Sk) {
+      const int pg = page_of(p, pos);
+      const int page = pages[pg - pg_first];
+      if (page >= 0)
+        a = (const u32x4*)(base +
+                           ((uint64_t)(uint32_t)page * (uint32_t)p.bs + (uint32_t)(pos - pg * p.bs)) *
+                               row_bytes +
+                           (uint32_t)col * 16u);
+    }
+    return *a;
+  };
 
   // Q^T as B operand, k-group g of 16-dim step ks = dims 16*ks + 8*g .. +8.
   // Rows past Sq read the last row (never stored).
@@ -400,9 +418,13 @@ __device__ __forceinline__ void fa16_rows(const FwdParams& pin, const WorkItem w
 #pragma unroll
       for (int i = 0; i < K_PER_T; ++i) {
         const int c = tid + i * NT;
-        if (K_CHUNKS % NT == 0 || c < K_CHUNKS)
-          kbuf[S][i] = __builtin_amdgcn_raw_buffer_load_b128(
-              krs, paged_off(kv0 + c / CPR, c % CPR, (uint32_t)p.k_ss * 2u), 0, 0);
+        if (K_CHUNKS % NT == 0 || c < K_CHUNKS) {
+          if constexpr (BIG)
+            kbuf[S][i] = paged_chunk(kbase, kv0 + c / CPR, c % CPR, (uint32_t)p.k_ss * 2u);
+          else
+            kbuf[S][i] = __builtin_amdgcn_raw_buffer_load_b128(
+                krs, paged_off(kv0 + c / CPR, c % CPR, (uint32_t)p.k_ss * 2u), 0, 0);
+        }
       }
 #pragma unroll
       for (int i = 0; i < V_PER_T; ++i) {
@@ -410,9 +432,13 @@ __device__ __forceinline__ void fa16_rows(const FwdParams& pin, const WorkItem w
         if (V_UNITS % NT == 0 || u < V_UNITS) {
           const int kp = u / CPR, dq = u % CPR;
 #pragma unroll
-          for (int r = 0; r < 2; ++r)
-            vbuf[S][i][r] = __builtin_amdgcn_raw_buffer_load_b128(
-                vrs, paged_off(kv0 + 2 * kp + r, dq, (uint32_t)p.v_ss * 2u), 0, 0);
+          for (int r = 0; r < 2; ++r) {
+            if constexpr (BIG)
+              vbuf[S][i][r] = paged_chunk(vbase, kv0 + 2 * kp + r, dq, (uint32_t)p.v_ss * 2u);
+            else
+              vbuf[S][i][r] = __builtin_amdgcn_raw_buffer_load_b128(
+                  vrs, paged_off(kv0 + 2 * kp + r, dq, (uint32_t)p.v_ss * 2u), 0, 0);
+          }
         }
       }
       return;
@@ -780,7 +806,11 @@ constexpr u32 kNoRowDirect = 0xFFFFFF00u;
 // consecutive rows x 4 consecutive chunks (V^T operands).
 __device__ __forceinline__ int swz64(int r) { return (((r >> 1) & 1) << 2) | ((r >> 2) & 3); }
 
-template <int D, int BN, int NW, bool BF16, int NST, bool PAGED, bool DROP = false>
+// BIG (paged, pools of 4 GiB and more): the page rows are read by the DMA's
+// 64-bit address form (rows without a page from kZeroChunk) instead of 32-bit
+// buffer offsets.
+template <int D, int BN, int NW, bool BF16, int NST, bool PAGED, bool DROP = false,
+          bool BIG = false>
 __device__ __forceinline__ void fa16_rows_direct(const FwdParams& pin, const WorkItem wi,
                                                  unsigned char* __restrict__ st0,
                                                  unsigned char* __restrict__ st1,
@@ -833,6 +863,10 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& pin, const Wor
   const u32 vrec = PAGED ? p.pool_bytes - (u32)(kvh * p.v_sh * 2) : 0x7fffffffu;
   const u32x4 krs = buffer_desc((const uint16_t*)p.k + wi.b * p.k_sb + kvh * p.k_sh, krec);
   const u32x4 vrs = buffer_desc((const uint16_t*)p.v + wi.b * p.v_sb + kvh * p.v_sh, vrec);
+  // BIG: the same bases for 64-bit addresses.
+  const unsigned char* kbase = (const unsigned char*)p.k + (wi.b * p.k_sb + kvh * p.k_sh) * 2;
+  const unsigned char* vbase = (const unsigned char*)p.v + (wi.b * p.v_sb + kvh * p.v_sh) * 2;
+  static_assert(!BIG || PAGED, "64-bit DMA addressing is for paged pools");
 
   // Paged: this item's slice of the page table, validated, in LDS.
   int pg_first = 0;
@@ -955,6 +989,18 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& pin, const Wor
         // part (row lr % RPD, chunk) is fixed. The tile starts on a page
         // boundary, so instruction r reads page entry pg_idx[r] at in-page
         // byte offset pg_in[r], both fixed for the kernel.
+        if constexpr (BIG) {
+          // The page base of instruction r in 64 bits, in scalar registers.
+          const uint64_t page_bytes = (uint64_t)row_bytes << p.bs_log2;
+#pragma unroll
+          for (int r = 0; r < NDMA; ++r) {
+            const u32 page = (u32)__builtin_amdgcn_readlane(pg_cur, pg_idx[r]);
+            const uint64_t off = (uint64_t)page * page_bytes + pg_in[r];
+            dma16_global_s(kdst + r * RSTEP * ROWB, kbase + off, (u32)klane);
+            dma16_global_s(vdst + r * RSTEP * ROWB, vbase + off, (u32)vlane);
+          }
+          return;
+        }
         const u32 pg_bytes = (u32)pg_cur * (row_bytes << p.bs_log2);
 #pragma unroll
         for (int r = 0; r < NDMA; ++r) {
@@ -970,6 +1016,15 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& pin, const Wor
             pg_cur, ((kv0 + RPD * wave + RSTEP * r) >> p.bs_log2) - pg0);
         const int pos = kv0 + lr + RSTEP * r;
         const bool ok = pos < p.Sk && page >= 0 && page < p.num_blocks;
+        if constexpr (BIG) {
+          const uint64_t base =
+              ((uint64_t)((u32)page << p.bs_log2) + (u32)(pos & bmask)) * row_bytes;
+          dma16_global(kdst + r * RSTEP * ROWB,
+                       ok ? (const void*)(kbase + base + (u32)kchunk * 16u) : &kZeroChunk);
+          dma16_global(vdst + r * RSTEP * ROWB,
+                       ok ? (const void*)(vbase + base + (u32)vchunk * 16u) : &kZeroChunk);
+          continue;
+        }
         const u32 base = (((u32)page << p.bs_log2) + (u32)(pos & bmask)) * row_bytes;
         dma16(krs, kdst + r * RSTEP * ROWB, (int)(ok ? base + (u32)kchunk * 16u : kNoRowDirect),
               0);
@@ -985,6 +1040,23 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& pin, const Wor
 #pragma unroll
       for (int r = 0; r < NDMA; ++r) {
         const int pos = kv0 + lr + RSTEP * r;
+        if constexpr (BIG) {
+          const void* ka = &kZeroChunk;
+          const void* va = &kZeroChunk;
+          if (pos < p.Sk) {
+            const int pg = page_of(p, pos);
+            const int page = pages[pg - pg_first];
+            if (page >= 0) {
+              const uint64_t base =
+                  ((uint64_t)(u32)page * (u32)p.bs + (u32)(pos - pg * p.bs)) * row_bytes;
+              ka = kbase + base + (u32)kchunk * 16u;
+              va = vbase + base + (u32)vchunk * 16u;
+            }
+          }
+          dma16_global(kdst + r * RSTEP * ROWB, ka);
+          dma16_global(vdst + r * RSTEP * ROWB, va);
+          continue;
+        }
         u32 koff = kNoRowDirect, voff = kNoRowDirect;
         if (pos < p.Sk) {
           const int pg = page_of(p, pos);
@@ -1338,7 +1410,7 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& pin, const Wor
   }
 }
 
-template <int D, int BN, int NW, bool BF16, bool PAGED>
+template <int D, int BN, int NW, bool BF16, bool PAGED, bool BIG = false>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(MPX_FA_WAVES_PER_EU)))
 void fa_fwd16_kernel(FwdParams p) {
   // Stay within 128 KB of LDS per workgroup (a 136 KB configuration gave wrong
@@ -1372,10 +1444,10 @@ void fa_fwd16_kernel(FwdParams p) {
 #pragma nounroll
   for (int item = 0; item < n_items; ++item) {
     if constexpr (kDirect)
-      fa16_rows_direct<D, BN, NW, BF16, kDStages, PAGED>(p, slot_item(p, ws, item), dst0, dst1,
-                                                    dst2, dst3, pages);
+      fa16_rows_direct<D, BN, NW, BF16, kDStages, PAGED, false, BIG>(
+          p, slot_item(p, ws, item), dst0, dst1, dst2, dst3, pages);
     else
-      fa16_rows<D, BN, NW, BF16, PAGED>(p, slot_item(p, ws, item), smem, pages);
+      fa16_rows<D, BN, NW, BF16, PAGED, false, BIG>(p, slot_item(p, ws, item), smem, pages);
   }
 }
 
@@ -1408,7 +1480,8 @@ void fa_fwd16_drop_kernel(FwdParams p) {
 // (DMA-staged) rows with 64-key tiles. PAGED (prefill over a paged cache): the
 // register-staged rows with 32-key tiles and the item's page-table slice.
 constexpr int kNumWavesWide = 4;
-template <int D, int BN, int NW, bool BF16, bool PAGED = false, bool DROP = false>
+template <int D, int BN, int NW, bool BF16, bool PAGED = false, bool DROP = false,
+          bool BIG = false>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void fa_fwd16_wide_kernel(FwdParams p) {
   // Dense K/V with 64-key tiles: direct (DMA) staging, two stages of 64 KB.
@@ -1431,7 +1504,7 @@ void fa_fwd16_wide_kernel(FwdParams p) {
       fa16_rows_direct<D, BN, NW, BF16, 2, false, DROP>(p, slot_item(p, ws, item), dst0, dst1,
                                                          unused2, unused3, nullptr);
     else
-      fa16_rows<D, BN, NW, BF16, PAGED, DROP>(p, slot_item(p, ws, item), smem, pages);
+      fa16_rows<D, BN, NW, BF16, PAGED, DROP, BIG>(p, slot_item(p, ws, item), smem, pages);
   }
 }
 
@@ -1884,13 +1957,14 @@ Plan make_plan(int B, int H, int Sq, int Sk, int D, int causal, int window_left,
   return pl;
 }
 
-template <int D, int BN, bool F32, bool BF16, bool PAGED>
+// BIG: 16-bit paged pools of 4 GiB and more (p.pool_bytes == 0).
+template <int D, int BN, bool F32, bool BF16, bool PAGED, bool BIG = false>
 hipError_t launch_fwd(const FwdParams& p, int grid, hipStream_t stream) {
   if constexpr (F32) {
     hipLaunchKernelGGL((fa_fwd32_kernel<D, BN, kNumWaves32, PAGED>), dim3(grid),
                        dim3(64 * kNumWaves32), 0, stream, p);
   } else {
-    hipLaunchKernelGGL((fa_fwd16_kernel<D, BN, kNumWaves16, BF16, PAGED>), dim3(grid),
+    hipLaunchKernelGGL((fa_fwd16_kernel<D, BN, kNumWaves16, BF16, PAGED, BIG>), dim3(grid),
                        dim3(64 * kNumWaves16), 0, stream, p);
   }
   return hipGetLastError();
@@ -1901,24 +1975,28 @@ hipError_t launch_fwd(const FwdParams& p, int grid, hipStream_t stream) {
 template <bool PAGED, int D>
 constexpr int kBN16 = PAGED || D < 64 || !MPX_FA_DIRECT ? 64 : MPX_FA_BN16;
 
-template <bool PAGED>
+template <bool PAGED, bool BIG = false>
 hipError_t dispatch_fwd(const FwdParams& p, int D, int dtype, int grid, hipStream_t st) {
+  if constexpr (PAGED && !BIG) {
+    // 16-bit pools of 4 GiB and more: the 64-bit address forms
+    if (dtype != MPX_F32 && p.pool_bytes == 0) return dispatch_fwd<true, true>(p, D, dtype, grid, st);
+  }
   if (D == 256) {
     // (16-bit: 64-key DMA-staged tiles dense, 32-key register-staged paged)
     constexpr int kBNw = PAGED ? 32 : 64;
     if (dtype == MPX_F32) return launch_fwd<256, 32, true, false, PAGED>(p, grid, st);
     if (dtype == MPX_BF16)
-      hipLaunchKernelGGL((fa_fwd16_wide_kernel<256, kBNw, kNumWavesWide, true, PAGED>),
+      hipLaunchKernelGGL((fa_fwd16_wide_kernel<256, kBNw, kNumWavesWide, true, PAGED, false, BIG>),
                          dim3(grid), dim3(64 * kNumWavesWide), 0, st, p);
     else
-      hipLaunchKernelGGL((fa_fwd16_wide_kernel<256, kBNw, kNumWavesWide, false, PAGED>),
+      hipLaunchKernelGGL((fa_fwd16_wide_kernel<256, kBNw, kNumWavesWide, false, PAGED, false, BIG>),
                          dim3(grid), dim3(64 * kNumWavesWide), 0, st, p);
     return hipGetLastError();
   }
   if constexpr (PAGED) {
     if (paged_wide_tiles(D, dtype, p.bs_log2, p.slopes != nullptr)) {
-      return dtype == MPX_BF16 ? launch_fwd<128, 128, false, true, true>(p, grid, st)
-                               : launch_fwd<128, 128, false, false, true>(p, grid, st);
+      return dtype == MPX_BF16 ? launch_fwd<128, 128, false, true, true, BIG>(p, grid, st)
+                               : launch_fwd<128, 128, false, false, true, BIG>(p, grid, st);
     }
   }
   if (dtype == MPX_F32) {
@@ -1929,15 +2007,15 @@ hipError_t dispatch_fwd(const FwdParams& p, int D, int dtype, int grid, hipStrea
     }
   } else if (dtype == MPX_BF16) {
     switch (D) {
-      case 32: return launch_fwd<32, kBN16<PAGED, 32>, false, true, PAGED>(p, grid, st);
-      case 64: return launch_fwd<64, kBN16<PAGED, 64>, false, true, PAGED>(p, grid, st);
-      default: return launch_fwd<128, kBN16<PAGED, 128>, false, true, PAGED>(p, grid, st);
+      case 32: return launch_fwd<32, kBN16<PAGED, 32>, false, true, PAGED, BIG>(p, grid, st);
+      case 64: return launch_fwd<64, kBN16<PAGED, 64>, false, true, PAGED, BIG>(p, grid, st);
+      default: return launch_fwd<128, kBN16<PAGED, 128>, false, true, PAGED, BIG>(p, grid, st);
     }
   } else {
     switch (D) {
-      case 32: return launch_fwd<32, kBN16<PAGED, 32>, false, false, PAGED>(p, grid, st);
-      case 64: return launch_fwd<64, kBN16<PAGED, 64>, false, false, PAGED>(p, grid, st);
-      default: return launch_fwd<128, kBN16<PAGED, 128>, false, false, PAGED>(p, grid, st);
+      case 32: return launch_fwd<32, kBN16<PAGED, 32>, false, false, PAGED, BIG>(p, grid, st);
+      case 64: return launch_fwd<64, kBN16<PAGED, 64>, false, false, PAGED, BIG>(p, grid, st);
+      default: return launch_fwd<128, kBN16<PAGED, 128>, false, false, PAGED, BIG>(p, grid, st);
     }
   }
 }
@@ -2294,10 +2372,6 @@ extern "C" int mpx_paged_prefill_gqa(const void* q, const void* k_pool, const vo
   MPX_CHECK_ARG(max_tokens < (1L << 30), "mpx_paged_prefill: block table too large");
   const int es = dtype == MPX_F32 ? 4 : 2;
   const uint64_t pool_bytes = (uint64_t)num_blocks * block_size * H_kv * D * es;
-  if (dtype != MPX_F32 && pool_bytes >= 0xFFFFFF00ull) {
-    set_error("mpx_paged_prefill: 16-bit pools above 4 GiB are not supported");
-    return MPX_EUNSUPPORTED;
-  }
   hipStream_t st = (hipStream_t)stream;
   if (num_blocks == 0 || max_blocks == 0) {
     // No key exists for any query: every output row is NaN.
@@ -2342,7 +2416,10 @@ extern "C" int mpx_paged_prefill_gqa(const void* q, const void* k_pool, const vo
   p.bs = block_size;
   p.bs_log2 = log2_if_pow2(block_size);
   p.max_blocks = max_blocks; p.num_blocks = num_blocks;
-  p.pool_bytes = (uint32_t)std::min<uint64_t>(pool_bytes, 0xFFFFFFFFull);
+  // 0: a pool of 4 GiB - 256 bytes or more, read through 64-bit addresses (the
+  // 32-bit buffer offsets of the other kernels reach below that; fp32 kernels
+  // always address pools in 64 bits).
+  p.pool_bytes = pool_bytes < 0xFFFFFF00ull ? (uint32_t)pool_bytes : 0u;
   return run_fwd<true>(p, pl, D, dtype, workspace, st);
 }
 

@@ -232,6 +232,27 @@ __device__ __forceinline__ void dma16(u32x4 rsrc, unsigned lds_addr, int voff, i
                : "memory", "m0");
 }
 
+// The same DMA from 64-bit addresses, for pools of 4 GiB and more (the buffer
+// form's offsets are 32-bit): lane l's 16 bytes at `src` (its own address) /
+// at sbase + voff (a wave-uniform base and a per-lane offset) land at LDS
+// address lds_addr + 16*l.
+__device__ __forceinline__ void dma16_global(unsigned lds_addr, const void* src) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off"
+               :
+               : "s"(lds_addr), "v"(src)
+               : "memory", "m0");
+}
+__device__ __forceinline__ void dma16_global_s(unsigned lds_addr, const void* sbase, u32 voff) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
+               :
+               : "s"(lds_addr), "v"(voff), "s"(sbase)
+               : "memory", "m0");
+}
+
+// 16 zero bytes in device memory: the source of rows that have no page in the
+// 64-bit (large pool) loads, which have no range check to turn them into zeros.
+static __device__ const u32x4 kZeroChunk = {0u, 0u, 0u, 0u};
+
 // ds_read_b64_tr_b16: for a group of 16 lanes whose lane s addresses row
 // base + s/4, columns c0 + 4*(s%4) .. +3 of a row-major 16-bit tile, lane s
 // receives column c0 + s of rows base .. base + 3.

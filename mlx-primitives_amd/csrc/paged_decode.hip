@@ -44,7 +44,7 @@ struct DecodeParams {
   int H_kv, kv_group;  // K/V heads of the pools; query heads per K/V head
   int dp;   // head dim of q, the pools and o (elements, <= the kernel's D)
   float c;  // scale * log2(e)
-  u32 pool_bytes;  // bytes of one pool (grouped-query MFMA kernel: < 4 GiB - 256)
+  u32 pool_bytes;  // bytes of one pool; 0: 4 GiB - 256 bytes or more (64-bit addressing)
 };
 
 // Tokens per partition and 16-byte loads in flight per lane (overridable at
@@ -332,7 +332,9 @@ constexpr u32 kGqaNoRow = 0xFFFFFF00u;  // DMA offset past any accepted pool: re
 
 __device__ __forceinline__ int gqa_swz(int row) { return (row & 3) | (((row >> 3) & 3) << 2); }
 
-template <bool BF16>
+// BIG: pools of 4 GiB - 256 bytes and more (pool_bytes == 0), whose rows the
+// DMA reads through 64-bit addresses (rows without a page from kZeroChunk).
+template <bool BF16, bool BIG = false>
 __global__ __launch_bounds__(64 * kGqaWaves) void paged_decode_gqa_kernel(DecodeParams p) {
   constexpr int D = 128, ROWB = 2 * D, TILEB = kGqaTile * ROWB;
   // Per wave: kGqaStages stages of (K tile, V tile).
@@ -382,9 +384,11 @@ __global__ __launch_bounds__(64 * kGqaWaves) void paged_decode_gqa_kernel(Decode
   // DMAs only.
   __builtin_amdgcn_s_waitcnt(0x0F70);
 
-  // Buffers of this K/V head's column of the pools (32-bit offsets: the host
-  // keeps each pool below 4 GiB - 256 bytes).
+  // Buffers of this K/V head's column of the pools (32-bit offsets: pools
+  // below 4 GiB - 256 bytes; BIG: 64-bit addresses from the same bases).
   const u32 rec = p.pool_bytes - (u32)(hk * D * 2);
+  const unsigned char* kbase = (const unsigned char*)p.kpool + (int64_t)hk * D * 2;
+  const unsigned char* vbase = (const unsigned char*)p.vpool + (int64_t)hk * D * 2;
   const u32x4 krs = buffer_desc((const uint16_t*)p.kpool + (int64_t)hk * D, rec);
   const u32x4 vrs = buffer_desc((const uint16_t*)p.vpool + (int64_t)hk * D, rec);
   const u32 row_bytes = (u32)p.H_kv * (u32)D * 2u;
@@ -398,6 +402,13 @@ __global__ __launch_bounds__(64 * kGqaWaves) void paged_decode_gqa_kernel(Decode
       const int r = 4 * v + q4;
       const int t = t0 + r;
       const int pg = t < p1 ? bl[t / p.bs - pg0] : -1;
+      if constexpr (BIG) {
+        const uint64_t off = ((uint64_t)(u32)pg * (u32)p.bs + (u32)(t % p.bs)) * row_bytes +
+                             (u32)((i16 ^ gqa_swz(r)) * 16);
+        dma16_global(kdst + 4 * v * ROWB, pg >= 0 ? (const void*)(kbase + off) : &kZeroChunk);
+        dma16_global(vdst + 4 * v * ROWB, pg >= 0 ? (const void*)(vbase + off) : &kZeroChunk);
+        continue;
+      }
       const u32 off = pg >= 0 ? ((u32)pg * (u32)p.bs + (u32)(t % p.bs)) * row_bytes +
                                     (u32)((i16 ^ gqa_swz(r)) * 16)
                               : kGqaNoRow;
@@ -528,18 +539,22 @@ dim3 merge_grid(const DecodeParams& p, int D) {
 }
 
 // The grouped-query MFMA kernel serves 16-bit pools of head dim 128 with 2 to
-// 16 query heads per K/V head and pools below 4 GiB - 256 bytes
-// (pool_bytes != 0).
+// 16 query heads per K/V head (pools of 4 GiB - 256 bytes and more,
+// pool_bytes == 0, through its 64-bit address form).
 template <int D, int DT>
 constexpr bool kGqaMfmaType = D == 128 && DT != MPX_F32;
 
 template <int D, int DT>
 hipError_t launch_decode(const DecodeParams& p, hipStream_t st) {
   if constexpr (kGqaMfmaType<D, DT>) {
-    if (p.kv_group >= 2 && p.kv_group <= 16 && p.dp == D && p.pool_bytes != 0) {
+    if (p.kv_group >= 2 && p.kv_group <= 16 && p.dp == D) {
       const dim3 grid(p.H_kv, (p.max_parts + kGqaWaves - 1) / kGqaWaves, p.B);
-      hipLaunchKernelGGL((paged_decode_gqa_kernel<DT == MPX_BF16>), grid, dim3(64 * kGqaWaves),
-                         0, st, p);
+      if (p.pool_bytes != 0)
+        hipLaunchKernelGGL((paged_decode_gqa_kernel<DT == MPX_BF16>), grid,
+                           dim3(64 * kGqaWaves), 0, st, p);
+      else
+        hipLaunchKernelGGL((paged_decode_gqa_kernel<DT == MPX_BF16, true>), grid,
+                           dim3(64 * kGqaWaves), 0, st, p);
       hipError_t e = hipGetLastError();
       if (e != hipSuccess) return e;
       hipLaunchKernelGGL(paged_decode_merge_kernel<DT>, merge_grid(p, D), dim3(64), 0, st, p, D);

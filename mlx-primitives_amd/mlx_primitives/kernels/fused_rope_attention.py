@@ -70,9 +70,18 @@ def _rope_attention(q, k, v, scale, cos_cache, sin_cache, rope_base, q_offset, k
                                                      dtype=q.dtype, device=q.device)
     shift = q_offset - kv_offset if position_rule else max(0, seq_kv - seq_q)
     if causal and shift < 0:
-        raise NotImplementedError(
-            "causal fused RoPE attention with kv_offset > q_offset (queries before the first "
-            "key) is not supported by the MI355X kernels")
+        # kv_offset > q_offset: query rows i < -shift are placed before the
+        # first key and see none; the reference kernel writes zeros for them
+        # (its sum stays 0, fused_rope_attention.py:127-131, 176-186). Row
+        # i >= -shift sees keys j <= i + shift: the top-left causal attention
+        # of the rows from -shift on, rotated from position q_offset - shift.
+        n0 = min(-shift, seq_q)
+        out = torch.zeros_like(q)
+        if n0 < seq_q:
+            out[:, n0:] = _rope_attention(q[:, n0:], k, v, scale, cos_cache, sin_cache,
+                                          rope_base, q_offset + n0, kv_offset, causal,
+                                          position_rule)
+        return out
     k_rot = rope(k, cos_cache, sin_cache, kv_offset)
     # kv_offset + j <= q_offset + i  <=>  j <= i + shift
     mask = (dict(causal=False) if not causal else

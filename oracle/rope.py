@@ -55,7 +55,10 @@ def fused_rope_attention(q: np.ndarray, k: np.ndarray, v: np.ndarray,
                          q_offset: int = 0, kv_offset: int = 0,
                          causal: bool = False) -> np.ndarray:
     """rope(Q), rope(K), then softmax(scale * Q K^T + position-causal mask) V
-    (fused_rope_attention.py:637-733 with the mask of 125-131); (B, Sq, H, D)."""
+    (fused_rope_attention.py:637-733 with the mask of 125-131); (B, Sq, H, D).
+    A query placed before every key (kv_offset > q_offset + i) sees none and
+    gets zeros, as the reference kernel writes them (its running sum stays 0,
+    fused_rope_attention.py:176-186)."""
     bsz, seq_q, heads, dim = q.shape
     seq_kv = k.shape[1]
     if scale is None:
@@ -75,6 +78,7 @@ def fused_rope_attention(q: np.ndarray, k: np.ndarray, v: np.ndarray,
         m = np.max(s, axis=-1, keepdims=True)
         e = np.exp(s - m)
         w = e / np.sum(e, axis=-1, keepdims=True)
+    w = np.where(np.isfinite(m), w, 0.0)  # rows without a visible key
     return np.transpose(np.matmul(w, np.transpose(v, (0, 2, 1, 3))), (0, 2, 1, 3))
 
 

@@ -137,11 +137,11 @@ def test_gqa_decode_alibi_ragged(device, dtype, H, H_kv, D):
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("H,H_kv,bs", [(16, 1, 16), (32, 2, 1), (48, 4, 8), (20, 10, 32),
-                                       (34, 2, 64)])
+                                       (34, 2, 64), (12, 3, 24), (16, 2, 48)])
 def test_gqa_mfma_decode_groups_and_pages(device, dtype, H, H_kv, bs):
-    # the MFMA decode kernel: groups 16, 16, 12, 2 and 17 (> 16: per-head
-    # kernel), page sizes 1 .. 64, contexts ending mid-tile and mid-page,
-    # several partitions, a missing page
+    # the MFMA decode kernel: groups 16, 16, 12, 2, 17 (> 16: per-head
+    # kernel), 4 and 8, page sizes 1 .. 64 (24 and 48: not powers of two),
+    # contexts ending mid-tile and mid-page, several partitions, a missing page
     lens = [1537, 31, 512, 2049]
     q, kp, vp, tables, lens_t = paged_inputs(dtype, 4, 1, H, H_kv, 128, bs, lens, H + bs)
     tables[0, 3] = -1

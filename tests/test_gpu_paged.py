@@ -69,7 +69,7 @@ def test_reference_small_cases(device, lens, tables, nb):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
-@pytest.mark.parametrize("bs", [1, 8, 16, 32, 128])
+@pytest.mark.parametrize("bs", [1, 8, 16, 24, 32, 48, 128])
 @pytest.mark.parametrize("D", [32, 64, 128, 256])
 def test_random_tables(device, dtype, bs, D):
     rng = np.random.default_rng(bs * 1000 + D)

@@ -213,3 +213,68 @@ def test_deterministic(device):
     o1, _ = run_case(device, torch.float16, 64, lens, tables, nb, 16, 8, 128, causal=False)
     o2, _ = run_case(device, torch.float16, 64, lens, tables, nb, 16, 8, 128, causal=False)
     assert torch.equal(o1, o2)
+
+
+# Pools of 4 GiB and more: the 16-bit kernels read pages through 64-bit
+# addresses (the 32-bit buffer offsets end below 4 GiB). The pools are left
+# uninitialised except for the referenced pages, which sit both below and above
+# the 4 GiB mark; the oracle runs on those pages alone (a compact pool with the
+# table renumbered), so unreferenced memory cannot reach the result.
+@pytest.mark.parametrize("dtype,D,H,H_kv,bs,alibi,Sq", [
+    (torch.bfloat16, 128, 8, 8, 16, False, 300),   # 128-key tiles, page ids per instruction
+    (torch.float16, 128, 8, 4, 16, True, 300),     # 64-key tiles, page-table slice (ALiBi)
+    (torch.bfloat16, 128, 4, 4, 24, False, 200),   # page size not a power of two
+    (torch.bfloat16, 64, 8, 8, 16, False, 300),
+    (torch.float16, 32, 8, 8, 16, False, 200),     # register-staged tiles
+    (torch.bfloat16, 256, 4, 2, 16, False, 150),   # head dim 256 (register-staged)
+    (torch.float16, 128, 32, 8, 16, False, 1),     # decode: grouped-query MFMA kernel
+    (torch.bfloat16, 128, 16, 4, 24, True, 1),     # the same, page size 24, ALiBi
+    (torch.bfloat16, 64, 8, 8, 16, False, 1),      # decode: per-head kernel
+])
+def test_pool_above_4gib(device, dtype, D, H, H_kv, bs, alibi, Sq):
+    rng = np.random.default_rng(D + bs + H_kv)
+    block_bytes = bs * H_kv * D * 2
+    nb = (4 << 30) // block_bytes + 4096  # 4 GiB + 4096 pages
+    lens = [700, Sq, 1000]
+    pages = [(n + bs - 1) // bs for n in lens]
+    # referenced pages: most of them past 4 GiB, some below, in random order
+    high = rng.choice(np.arange((4 << 30) // block_bytes, nb), sum(pages) - 6, replace=False)
+    low = rng.choice(np.arange(0, 1000), 6, replace=False)
+    ids = rng.permutation(np.concatenate([high, low]))
+    width = max(pages) + 1
+    tables = np.full((3, width), -1, np.int32)
+    off = 0
+    for b, n in enumerate(pages):
+        tables[b, :n] = ids[off:off + n]
+        off += n
+    tables[0, 3] = -1  # a missing page inside the context
+    g = torch.Generator().manual_seed(int(nb))
+    q = torch.randn(3, Sq, H, D, generator=g).to(dtype)
+    kc = torch.randn(len(ids), bs, H_kv, D, generator=g).to(dtype)
+    vc = torch.randn(len(ids), bs, H_kv, D, generator=g).to(dtype)
+    kp = torch.empty((nb, bs, H_kv, D), dtype=dtype, device=device)
+    vp = torch.empty((nb, bs, H_kv, D), dtype=dtype, device=device)
+    assert kp.numel() * 2 >= 4 << 30
+    idx = torch.as_tensor(ids, dtype=torch.long).to(device)
+    kp[idx] = kc.to(device)
+    vp[idx] = vc.to(device)
+    slopes = get_alibi_slopes(H) if alibi else None
+    lens_t = torch.as_tensor(lens, dtype=torch.int32)
+    print(f"pool {kp.numel() * 2 / 2**30:.2f} GiB, {dtype}, D={D}, bs={bs}, Sq={Sq}", flush=True)
+    out = paged_attention(q.to(device), kp, vp, torch.as_tensor(tables).to(device),
+                          lens_t.to(device), block_size=bs, causal=True,
+                          alibi_slopes=slopes.to(device) if alibi else None,
+                          enable_gqa=H != H_kv)
+    torch.cuda.synchronize()
+    del kp, vp
+    # the oracle on the referenced pages: compact pool, renumbered table
+    where = {int(p): i for i, p in enumerate(ids)}
+    ctab = np.vectorize(lambda p: where.get(int(p), -1))(tables).astype(np.int32)
+    ctab[tables < 0] = -1
+    grp = H // H_kv
+    ref = op.paged_attention(q.double().numpy(),
+                             kc.repeat_interleave(grp, dim=2).double().numpy(),
+                             vc.repeat_interleave(grp, dim=2).double().numpy(), ctab,
+                             lens_t.numpy(), block_size=bs, causal=True,
+                             alibi_slopes=slopes.numpy() if alibi else None)
+    check(out, ref, dtype)

@@ -102,6 +102,10 @@ def oracle_attention(q, k, v, dtype, scale, q_off, kv_off, causal, base=10000.0)
     ((2, 1, 4, 64), (2, 64, 4, 64), 63, 0, True),     # q shorter, 189-209
     ((2, 32, 4, 64), (2, 16, 4, 64), 0, 0, False),    # q longer, 211-232
     ((2, 40, 3, 128), (2, 72, 3, 128), 50, 10, True),
+    # kv_offset > q_offset: the first 15 queries precede every key (zeros)
+    ((2, 40, 3, 64), (2, 48, 3, 64), 5, 20, True),
+    ((1, 300, 2, 128), (1, 260, 2, 128), 0, 37, True),
+    ((1, 16, 2, 64), (1, 16, 2, 64), 0, 100, True),    # no query sees a key
 ])
 def test_fused_rope_attention(device, dt, qs, ks, q_off, kv_off, causal):
     dtype = DT[dt]
@@ -168,8 +172,11 @@ def test_given_caches_and_validation(device):
         fused_rope_attention(q[0], k, v)
     with pytest.raises(ValueError, match="exceed"):
         fused_rope_attention(q, k, v, cos_cache=cos[:8], sin_cache=sin[:8])
-    with pytest.raises(NotImplementedError):
-        fused_rope_attention(q, k, v, q_offset=0, kv_offset=4, causal=True)
+    # keys placed after the first queries: those rows are zeros, the rest is
+    # the attention of the later rows (fused_rope_attention.py:127-131, 176-186)
+    z = fused_rope_attention(q, k, v, q_offset=0, kv_offset=4, causal=True)
+    assert torch.equal(z[:, :4], torch.zeros_like(z[:, :4]))
+    assert torch.isfinite(z.float()).all() and z[:, 4:].abs().amax() > 0
 
 
 def test_serving_shape_matches_flash_on_rotated_inputs(device):

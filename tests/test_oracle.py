@@ -527,6 +527,8 @@ def _brute_rope_attention(q, k, v, scale, base, q_off, kv_off, causal, allowed=N
                     js = [j for j in range(Sk) if not causal or allowed(i, j)]
                 else:
                     js = [j for j in range(Sk) if not causal or kv_off + j <= q_off + i]
+                if not js:
+                    continue  # no visible key: zeros (fused_rope_attention.py:176-186)
                 sc = [scale * float(np.dot(qi, ks[j])) for j in js]
                 m = max(sc)
                 w = [math.exp(x - m) for x in sc]
@@ -537,7 +539,8 @@ def _brute_rope_attention(q, k, v, scale, base, q_off, kv_off, causal, allowed=N
 
 
 @pytest.mark.parametrize("q_off,kv_off,causal,sq,sk", [
-    (0, 0, True, 5, 5), (0, 0, False, 4, 6), (3, 0, True, 2, 5), (4, 4, True, 3, 3)])
+    (0, 0, True, 5, 5), (0, 0, False, 4, 6), (3, 0, True, 2, 5), (4, 4, True, 3, 3),
+    (0, 4, True, 6, 5), (1, 9, True, 3, 4)])
 def test_fused_rope_attention_vs_brute(q_off, kv_off, causal, sq, sk):
     rng = np.random.default_rng(51 + q_off + sk)
     q = rng.standard_normal((1, sq, 2, 8)); k = rng.standard_normal((1, sk, 2, 8))
