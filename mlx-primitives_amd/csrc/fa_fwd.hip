@@ -45,6 +45,11 @@ struct FwdParams {
   int win_left, win_right;  // -1 = unbounded
   int n_qtiles, num_splits, tiles_per_split;
   int n_slots;  // q-tile slots per (batch, head)
+  // > 0: every q-tile has its own split count, max(1, ceil(its KV tiles /
+  // tiles_per_split)), and var_split is their sum per (batch, head); 0: every
+  // q-tile has num_splits splits.
+  int var_split;
+  int bm, bn;  // query rows per q-tile, keys per KV tile of the launch
   int paired;   // a slot runs q-tiles n_qtiles-1-slot and slot (causal balance)
   float c;  // |scale| * log2(e)
   int neg;  // scale < 0: Q is negated on load (exact) and |scale| used
@@ -190,9 +195,43 @@ struct WorkItem {
   int b, h, qt, split;
 };
 
+// KV tiles of q-tile qt (rows [qt*BM, +BM) against keys [0, Sk) under the
+// window / causal bounds): the count kv_range gives, on host and device.
+__host__ __device__ inline int qtile_kv_tiles(int qt, int BM, int BN, int Sq, int Sk, int wl,
+                                              int wr) {
+  const int q0 = qt * BM, q_last = (q0 + BM < Sq ? q0 + BM : Sq) - 1;
+  int lo = wl >= 0 ? (q0 - wl > 0 ? q0 - wl : 0) : 0;
+  lo -= lo % BN;
+  const int hi = wr >= 0 ? (Sk < q_last + wr + 1 ? Sk : q_last + wr + 1) : Sk;
+  return hi > lo ? (hi - lo + BN - 1) / BN : 0;
+}
+
+// Splits of q-tile qt when each q-tile has its own count (var_split).
+__host__ __device__ inline int qtile_splits(int qt, int BM, int BN, int Sq, int Sk, int wl, int wr,
+                                            int tiles_per_split) {
+  const int n = qtile_kv_tiles(qt, BM, BN, Sq, Sk, wl, wr);
+  return n > tiles_per_split ? (n + tiles_per_split - 1) / tiles_per_split : 1;
+}
+
 __device__ __forceinline__ WorkSlot decode_slot(const FwdParams& p) {
   const int L = blockIdx.x, N = gridDim.x;
   const int w = (N & 7) == 0 ? (L & 7) * (N >> 3) + (L >> 3) : L;
+  if (p.var_split > 0) {
+    // Slot s is q-tile n_qtiles-1-s (the longest first); the splits of the
+    // slots follow each other within a (batch, head).
+    WorkSlot ws;
+    ws.bh = w / p.var_split;
+    int r = w - ws.bh * p.var_split, slot = 0;
+    for (; slot < p.n_qtiles - 1; ++slot) {
+      const int c = qtile_splits(p.n_qtiles - 1 - slot, p.bm, p.bn, p.Sq, p.Sk, p.win_left,
+                                 p.win_right, p.tiles_per_split);
+      if (r < c) break;
+      r -= c;
+    }
+    ws.slot = slot;
+    ws.split = r;
+    return ws;
+  }
   const int per_bh = p.n_slots * p.num_splits;
   WorkSlot ws;
   ws.bh = w / per_bh;
@@ -1815,19 +1854,29 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd32_kernel(FwdParams pin) {
 // ---------------------------------------------------------------------------
 constexpr int kMergeBatch = 8;
 
+// (The attention launch's split layout: each q-tile's split count when it
+// has its own, var_split, as in decode_slot.)
+struct MergeShape {
+  int var_split, bm, bn, Sk, win_left, win_right, tiles_per_split;
+};
+
 template <int DT>
 __global__ __launch_bounds__(256) void fa_split_merge_kernel(const float* __restrict__ ws_o,
                                                              const float* __restrict__ ws_ml,
                                                              void* o, int64_t o_sb, int64_t o_sh,
                                                              int64_t o_ss, int B, int H, int Sq,
                                                              int D, int splits, float eps,
-                                                             int nan_empty, float* lse) {
+                                                             int nan_empty, float* lse,
+                                                             MergeShape ms) {
   const int chunks = D / 4;
   const int64_t rows = (int64_t)B * H * Sq;
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= rows * chunks) return;
   const int64_t row = idx / chunks;
   const int c4 = (int)(idx - row * chunks);
+  if (ms.var_split > 0)
+    splits = qtile_splits((int)(row % Sq) / ms.bm, ms.bm, ms.bn, Sq, ms.Sk, ms.win_left,
+                          ms.win_right, ms.tiles_per_split);
   float M = -INFINITY, L = 0.f;
   f32x4 acc = {};
   for (int s0 = 0; s0 < splits; s0 += kMergeBatch) {
@@ -1895,6 +1944,7 @@ int target_workgroups(int D, int dtype) {
 struct Plan {
   int BM, BN, n_qtiles, splits, tiles_per_split, win_left, win_right;
   int n_slots, paired;
+  int var_split;  // splits per (batch, head) when each q-tile has its own count, else 0
   size_t ws_bytes;
 };
 
@@ -1927,14 +1977,9 @@ Plan make_plan(int B, int H, int Sq, int Sk, int D, int causal, int window_left,
   pl.n_qtiles = (Sq + pl.BM - 1) / pl.BM;
   // Widest KV range over all q-tiles.
   int max_tiles = 0;
-  for (int qt = 0; qt < pl.n_qtiles; ++qt) {
-    const int q0 = qt * pl.BM, q_last = std::min(q0 + pl.BM, Sq) - 1;
-    int lo = pl.win_left >= 0 ? std::max(0, q0 - pl.win_left) : 0;
-    lo -= lo % pl.BN;
-    const int hi = pl.win_right >= 0 ? std::min(Sk, q_last + pl.win_right + 1) : Sk;
-    const int n = hi > lo ? (hi - lo + pl.BN - 1) / pl.BN : 0;
-    max_tiles = std::max(max_tiles, n);
-  }
+  for (int qt = 0; qt < pl.n_qtiles; ++qt)
+    max_tiles = std::max(max_tiles, qtile_kv_tiles(qt, pl.BM, pl.BN, Sq, Sk, pl.win_left,
+                                                   pl.win_right));
   const long base = (long)B * H * pl.n_qtiles;
   int splits = 1;
   const long target = target_workgroups(D, dtype);
@@ -1954,6 +1999,27 @@ Plan make_plan(int B, int H, int Sq, int Sk, int D, int causal, int window_left,
   pl.paired = dtype != MPX_F32 && splits == 1 && pl.win_left < 0 && pl.win_right >= 0 &&
               pl.n_qtiles >= 2 && (long)B * H * half >= kNumCUs;
   pl.n_slots = pl.paired ? half : pl.n_qtiles;
+  // Ranges of unequal length (causal, windows) split by one tile count leave
+  // short q-tiles with empty splits and long ones with many: instead, each
+  // q-tile gets ceil(its tiles / T) splits of T tiles, with the smallest T (at
+  // least 4) whose launch fits one resident wave of workgroups.
+  pl.var_split = 0;
+  if (splits > 1 && !pl.paired && pl.n_qtiles <= 64) {
+    const int cap = std::max(max_tiles_per_split, 1);
+    for (int T = 4; T <= std::min(max_tiles, cap); ++T) {
+      long per_bh = 0;
+      for (int qt = 0; qt < pl.n_qtiles; ++qt)
+        per_bh += qtile_splits(qt, pl.BM, pl.BN, Sq, Sk, pl.win_left, pl.win_right, T);
+      if ((long)B * H * per_bh > target) continue;
+      if (per_bh < (long)pl.n_qtiles * splits) {
+        pl.var_split = (int)per_bh;
+        pl.tiles_per_split = T;
+        pl.splits = (max_tiles + T - 1) / T;
+        pl.ws_bytes = (size_t)pl.splits * B * H * Sq * (D + 2) * sizeof(float);
+      }
+      break;
+    }
+  }
   return pl;
 }
 
@@ -2064,19 +2130,23 @@ int run_fwd(FwdParams& p, const Plan& pl, int D, int dtype, void* workspace, hip
   p.win_left = pl.win_left; p.win_right = pl.win_right;
   p.n_qtiles = pl.n_qtiles; p.num_splits = pl.splits; p.tiles_per_split = pl.tiles_per_split;
   p.n_slots = pl.n_slots; p.paired = pl.paired;
-  const long grid_l = (long)p.B * p.H * pl.n_slots * pl.splits;
+  p.var_split = pl.var_split; p.bm = pl.BM; p.bn = pl.BN;
+  const long grid_l =
+      (long)p.B * p.H * (pl.var_split > 0 ? pl.var_split : (long)pl.n_slots * pl.splits);
   MPX_CHECK_ARG(grid_l < (1L << 31), "attention: problem too large");
   if (!PAGED && drop)
     MPX_CHECK_HIP(dispatch_fwd_drop(p, D, dtype, (int)grid_l, st));
   else
     MPX_CHECK_HIP(dispatch_fwd<PAGED>(p, D, dtype, (int)grid_l, st));
   if (pl.splits > 1) {
+    const MergeShape ms = {pl.var_split, pl.BM, pl.BN, p.Sk, pl.win_left, pl.win_right,
+                           pl.tiles_per_split};
     const long threads = (long)p.B * p.H * p.Sq * (D / 4);
     const int blocks = (int)((threads + 255) / 256);
 #define MPX_MERGE(DT)                                                                         \
   hipLaunchKernelGGL(fa_split_merge_kernel<DT>, dim3(blocks), dim3(256), 0, st, p.ws_o, p.ws_ml, \
                      p.o, p.o_sb, p.o_sh, p.o_ss, p.B, p.H, p.Sq, D, pl.splits, p.eps,         \
-                     p.nan_empty, p.lse)
+                     p.nan_empty, p.lse, ms)
     if (dtype == MPX_F32)
       MPX_MERGE(MPX_F32);
     else if (dtype == MPX_BF16)
