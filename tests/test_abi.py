@@ -81,6 +81,10 @@ def test_fwd_workspace_sizes(lib):
     # Few q-tiles and a long KV range -> split-KV partials are needed.
     ws = lib.mpx_attn_fwd_workspace_bytes(1, 16, 512, 65536, 64, 0, -1, -1, 2)
     assert ws > 0 and ws % (4 * (64 + 2)) == 0
+    # config 1 (fp32 causal 2 x 12 heads x 1024, D = 64): q-tiles of 128 rows split
+    # 1, 1, 2, 2, 3, 3, 4, 4 ways (pieces of 4 tiles of 64 keys): 4 partial slots
+    assert lib.mpx_attn_fwd_workspace_bytes(2, 12, 1024, 1024, 64, 1, -1, -1, 0) == \
+        4 * 2 * 12 * 1024 * (64 + 2) * 4
     # Enough q-tiles to fill the GPU -> no workspace.
     assert lib.mpx_attn_fwd_workspace_bytes(4, 32, 4096, 4096, 128, 1, -1, -1, 2) == 0
 
