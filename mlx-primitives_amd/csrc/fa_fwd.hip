@@ -50,6 +50,9 @@ struct FwdParams {
   // q-tile has num_splits splits.
   int var_split;
   int bm, bn;  // query rows per q-tile, keys per KV tile of the launch
+  // Windowed launches: the first q-tile whose KV range has the full window
+  // length (slot_qtile), else -1.
+  int win_first;
   int paired;   // a slot runs q-tiles n_qtiles-1-slot and slot (causal balance)
   float c;  // |scale| * log2(e)
   int neg;  // scale < 0: Q is negated on load (exact) and |scale| used
@@ -213,17 +216,23 @@ __host__ __device__ inline int qtile_splits(int qt, int BM, int BN, int Sq, int 
   return n > tiles_per_split ? (n + tiles_per_split - 1) / tiles_per_split : 1;
 }
 
+__device__ __forceinline__ int slot_qtile(const FwdParams& p, int slot) {
+  if (p.win_first < 0) return p.n_qtiles - 1 - slot;
+  const int k = p.win_first, n_long = p.n_qtiles - k;
+  return slot < n_long ? k + slot : k - 1 - (slot - n_long);
+}
+
 __device__ __forceinline__ WorkSlot decode_slot(const FwdParams& p) {
   const int L = blockIdx.x, N = gridDim.x;
   const int w = (N & 7) == 0 ? (L & 7) * (N >> 3) + (L >> 3) : L;
   if (p.var_split > 0) {
-    // Slot s is q-tile n_qtiles-1-s (the longest first); the splits of the
-    // slots follow each other within a (batch, head).
+    // Slot s is q-tile slot_qtile(s); the splits of the slots follow each
+    // other within a (batch, head).
     WorkSlot ws;
     ws.bh = w / p.var_split;
     int r = w - ws.bh * p.var_split, slot = 0;
     for (; slot < p.n_qtiles - 1; ++slot) {
-      const int c = qtile_splits(p.n_qtiles - 1 - slot, p.bm, p.bn, p.Sq, p.Sk, p.win_left,
+      const int c = qtile_splits(slot_qtile(p, slot), p.bm, p.bn, p.Sq, p.Sk, p.win_left,
                                  p.win_right, p.tiles_per_split);
       if (r < c) break;
       r -= c;
@@ -245,13 +254,21 @@ __device__ __forceinline__ WorkSlot decode_slot(const FwdParams& p) {
 // paired launch, then q-tile `slot`: under a causal mask the two ranges add up
 // to the same number of KV tiles for every slot, so all workgroups finish
 // together instead of the last-dispatched long q-tiles trailing the launch.
+// Windowed launches order a head's q-tiles differently: first the q-tiles
+// whose window has its full length, in ascending order, so the workgroups
+// resident on one XCD sweep neighbouring windows left to right together and
+// each K/V tile comes from HBM about once (longest first, their windows drift
+// apart and a head's K/V, 4 MB at 8192 x 128 bf16, is refetched several times
+// through the XCD's 4 MB L2); then the shorter leading q-tiles (prefixes of
+// the sequence, which share their first tiles anyway) in descending order,
+// which fill the end of the launch as the longest-first order does.
 __device__ __forceinline__ int slot_items(const FwdParams& p, const WorkSlot& ws) {
   return p.paired && ws.slot < p.n_qtiles - 1 - ws.slot ? 2 : 1;
 }
 
 __device__ __forceinline__ WorkItem slot_item(const FwdParams& p, const WorkSlot& ws, int item) {
   WorkItem wi;
-  wi.qt = item == 0 ? p.n_qtiles - 1 - ws.slot : ws.slot;
+  wi.qt = item == 0 ? slot_qtile(p, ws.slot) : ws.slot;
   wi.split = ws.split;
   wi.b = ws.bh / p.H;
   wi.h = ws.bh - wi.b * p.H;
@@ -1943,7 +1960,7 @@ int target_workgroups(int D, int dtype) {
 
 struct Plan {
   int BM, BN, n_qtiles, splits, tiles_per_split, win_left, win_right;
-  int n_slots, paired;
+  int n_slots, paired, win_first;
   int var_split;  // splits per (batch, head) when each q-tile has its own count, else 0
   size_t ws_bytes;
 };
@@ -1999,6 +2016,14 @@ Plan make_plan(int B, int H, int Sq, int Sk, int D, int causal, int window_left,
   pl.paired = dtype != MPX_F32 && splits == 1 && pl.win_left < 0 && pl.win_right >= 0 &&
               pl.n_qtiles >= 2 && (long)B * H * half >= kNumCUs;
   pl.n_slots = pl.paired ? half : pl.n_qtiles;
+  pl.win_first = -1;
+  if (!pl.paired && pl.win_left >= 0) {
+    pl.win_first = 0;
+    while (pl.win_first < pl.n_qtiles - 1 &&
+           qtile_kv_tiles(pl.win_first, pl.BM, pl.BN, Sq, Sk, pl.win_left, pl.win_right) <
+               max_tiles)
+      ++pl.win_first;
+  }
   // Ranges of unequal length (causal, windows) split by one tile count leave
   // short q-tiles with empty splits and long ones with many: instead, each
   // q-tile gets ceil(its tiles / T) splits of T tiles, with the smallest T (at
@@ -2130,7 +2155,7 @@ int run_fwd(FwdParams& p, const Plan& pl, int D, int dtype, void* workspace, hip
   p.win_left = pl.win_left; p.win_right = pl.win_right;
   p.n_qtiles = pl.n_qtiles; p.num_splits = pl.splits; p.tiles_per_split = pl.tiles_per_split;
   p.n_slots = pl.n_slots; p.paired = pl.paired;
-  p.var_split = pl.var_split; p.bm = pl.BM; p.bn = pl.BN;
+  p.var_split = pl.var_split; p.bm = pl.BM; p.bn = pl.BN; p.win_first = pl.win_first;
   const long grid_l =
       (long)p.B * p.H * (pl.var_split > 0 ? pl.var_split : (long)pl.n_slots * pl.splits);
   MPX_CHECK_ARG(grid_l < (1L << 31), "attention: problem too large");
