@@ -59,8 +59,8 @@ APPEND_KERNEL = "kv_append_kernel (+ the 12-byte fill that clears the error word
 BWD_KERNELS = "fa_bwd_dq_kernel<128,bf16> (+ Dvec) + fa_bwd_dkdv_fused_kernel<bf16>"
 DROPOUT_P = 0.1
 DROPOUT_KERNEL = "fa_fwd16_drop_kernel<128,128,8,bf16>"
-DROPOUT_BWD_KERNELS = ("fa_bwd_dq_kernel<128,bf16,drop> (+ Dvec) + "
-                       "fa_bwd_dkdv_fused_kernel<bf16,drop>")
+DROPOUT_BWD_KERNELS = ("stored dS: fa_bwd_dvec_kernel + fa_bwd_dkdv_fused_kernel<bf16,drop,ds> "
+                       "+ fa_bwd_dq_ds_kernel<128,bf16>")
 
 
 def measured_traffic(key: str):

@@ -313,7 +313,15 @@ int mpx_attn_fwd_rope(const void* q, const void* k, const void* v, void* o,
  * overlap the inputs. Masks (causal, windows) are those of the forward call.
  * Scope: dtype float32 / float16 / bfloat16, D in {64, 128, 256}, scale > 0.
  * Workspace: mpx_attn_bwd_workspace_bytes(B, H, Sq) bytes, 16-byte aligned
- * (per-row rowsum(dout * o)).
+ * (per-row rowsum(dout * o)). A workspace of at least
+ * mpx_attn_bwd_ds_workspace_bytes(...) bytes (same problem arguments; 0 when
+ * the problem has no such schedule: float32, or D other than 128) selects the
+ * stored-dS schedule: the dK/dV kernel stores dS (16-bit, only the 32 x 32
+ * blocks the mask leaves, about B * H * Sq * Sk bytes under a causal mask)
+ * and dQ is computed from it instead of recomputing S and dP (and, with
+ * dropout, the keep mask). On MI355X it is the faster schedule for
+ * mpx_attn_bwd_dropout (6% over forward and backward at 4 x 32 x 4096 x 128)
+ * and runs level with the other one for mpx_attn_bwd.
  */
 int mpx_attn_fwd_lse(const void* q, const void* k, const void* v, void* o, float* lse,
                      const int64_t* q_strides, const int64_t* k_strides,
@@ -323,6 +331,12 @@ int mpx_attn_fwd_lse(const void* q, const void* k, const void* v, void* o, float
                      void* workspace, size_t workspace_bytes, void* stream);
 
 size_t mpx_attn_bwd_workspace_bytes(int B, int H, int Sq);
+
+/* The workspace of mpx_attn_bwd's stored-dS schedule (no counterpart in the
+ * reference, which differentiates through mx.grad; it is the same backward
+ * with dQ taken from stored dS). */
+size_t mpx_attn_bwd_ds_workspace_bytes(int B, int H, int Sq, int Sk, int D, int dtype,
+                                       int causal, int window_left, int window_right);
 
 int mpx_attn_bwd(const void* q, const void* k, const void* v, const void* o, const void* dout,
                  const float* lse, void* dq, void* dk, void* dv,

@@ -26,11 +26,32 @@ struct BwdParams {
   // words of the keep-mask hash, and the 1 / (1 - p) of the kept weights.
   uint32_t drop_thresh, seed0, seed1;
   float drop_scale;
+  // Stored dS^T (the stored-dS schedule only): ds_tot blocks per query head.
+  void* ds;
+  int64_t ds_tot;
 };
 
 constexpr int kBwdWaves = 4;    // waves per workgroup (one per SIMD)
 constexpr int kBwdOwn = 32 * kBwdWaves;  // rows (or keys) a workgroup owns
 constexpr int kBwdTile = 64;    // streamed rows per step
+
+// Stored dS^T: per query head, 2 KB blocks of 32 keys x 32 queries (16-bit).
+// Key tile kt (kBwdOwn keys, four key blocks) owns the blocks of the 32-row
+// query blocks t0 .. t0 + nt - 1 that its keys' masks reach, query block
+// major, key block minor; its first block is 4 * (sum of nt over the key
+// tiles before it). Blocks that a key block and a query block do not share
+// (outside both window edges, keys past Sk) are never written or read.
+constexpr int kDsBlockBytes = 2048;
+
+__host__ __device__ inline void ds_key_tile(int Sq, int Sk, int win_left, int win_right, int kt,
+                                            int& t0, int& nt) {
+  const int k0 = kt * kBwdOwn;
+  const int k_last = (k0 + kBwdOwn < Sk ? k0 + kBwdOwn : Sk) - 1;
+  const int q_lo = win_right >= 0 ? (k0 - win_right > 0 ? k0 - win_right : 0) : 0;
+  const int q_hi = win_left >= 0 ? (k_last + win_left + 1 < Sq ? k_last + win_left + 1 : Sq) : Sq;
+  t0 = q_lo / 32;
+  nt = q_hi > q_lo ? (q_hi - 1) / 32 - t0 + 1 : 0;
+}
 
 // The float32 backward (rowsum, dQ, dK/dV kernels) for D in {64, 128}, with
 // the forward's dropout when drop is set, enqueued on st; defined in

@@ -572,9 +572,15 @@ void fa_bwd_dkdv_kernel(BwdParams p) {
 // Per tile: S and dP once, P and dS packed as B operands, then dV^T += dO^T P
 // and dK^T += Q^T dS (S is computed twice per backward instead of three times).
 // ---------------------------------------------------------------------------
+// With DS the kernel also stores each step's dS (the wave's 32 keys x the
+// tile's 32 query rows, one 2 KB block) for fa_bwd_dq_ds_kernel; in the block,
+// query half hh (rows 16 hh ..) is 1 KB, and the 16 bytes of key k, rows
+// 16 hh + 8 g' .. + 7 sit at chunk 32 g' + (k ^ 4 (2 hh + g')) of it: each
+// store instruction writes 1 KB contiguously, and the dQ kernel's transposing
+// reads of the block are conflict-free.
 constexpr int kFusedTile = 32;
 
-template <bool BF16, bool DROP = false>
+template <bool BF16, bool DROP = false, bool DS = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void fa_bwd_dkdv_fused_kernel(BwdParams p) {
   constexpr int D = 128, NKS = D / 16, NDB = D / 32, TILE = kFusedTile * D;
@@ -639,9 +645,10 @@ void fa_bwd_dkdv_fused_kernel(BwdParams p) {
     // Visible query rows of this key, cut at Sq (rows past it are clamped
     // copies with a real row's lse): q - q_first <= span as unsigned (no row
     // at all: q_first = 2^30, span 0).
+    // (DS: keys past Sk see no row either, so that their stored dS is zero.)
     const int q_lo_key = p.win_right >= 0 ? mykey - p.win_right : -(1 << 30);
     const int q_last = min(p.win_left >= 0 ? mykey + p.win_left : (1 << 30), p.Sq - 1);
-    const bool no_row = q_last < q_lo_key;
+    const bool no_row = q_last < q_lo_key || (DS && mykey >= p.Sk);
     const int q_first = no_row ? (1 << 30) : q_lo_key;
     const unsigned span = no_row ? 0u : (unsigned)q_last - (unsigned)q_first;
     // Dropout: this key's pair key of the forward's keep-mask hash and the
@@ -664,6 +671,21 @@ void fa_bwd_dkdv_fused_kernel(BwdParams p) {
     for (int db = 0; db < NDB; ++db) {
       dk[db] = (f32x16){};
       dv[db] = (f32x16){};
+    }
+
+    // (DS) The wave's block of the step being computed: the key tile's first
+    // block, query block t0 of head hk * kv_group, key block `wave`; 4 blocks
+    // per step, and a head's blocks ds_tot apart.
+    char* ds_cur = nullptr;
+    if constexpr (DS) {
+      int64_t off = 0;
+      for (int t = 0; t < kt; ++t) {
+        int a, n;
+        ds_key_tile(p.Sq, p.Sk, p.win_left, p.win_right, t, a, n);
+        off += 4 * n;
+      }
+      ds_cur = (char*)p.ds +
+               (((int64_t)(b * p.H + hk * p.kv_group) * p.ds_tot + off + wave) * kDsBlockBytes);
     }
 
     // Step u covers query tile t0 + u % n_t of head hk * kv_group + u / n_t; the
@@ -700,16 +722,20 @@ void fa_bwd_dkdv_fused_kernel(BwdParams p) {
       // (dropout: row key of query qr0 + 8 g of this step's head ch)
       const u32 drop_rk =
           DROP ? drop_row_key((u32)(((int64_t)b * p.H + ch) * p.Sq + qr0 + 8 * g), p.seed0) : 0u;
+      char* const ds_blk = ds_cur;
+      if constexpr (DS) ds_cur += 4 * kDsBlockBytes;
       if (++ct == n_t) {
         ct = 0;
         ++ch;
+        if constexpr (DS) ds_cur += (p.ds_tot - 4 * n_t) * kDsBlockBytes;
       }
       const bool skip = wk0 >= p.Sk ||
                         (p.win_right >= 0 && wk0 > qr0 + kFusedTile - 1 + p.win_right) ||
                         (p.win_left >= 0 && wk0 + 31 < qr0 - p.win_left);
-      const bool full = qr0 + kFusedTile <= p.Sq &&
+      const bool full = qr0 + kFusedTile <= p.Sq && (!DS || wk0 + 32 <= p.Sk) &&
                         (p.win_right < 0 || wk0 + 31 <= qr0 + p.win_right) &&
                         (p.win_left < 0 || wk0 >= qr0 + kFusedTile - 1 - p.win_left);
+      u32x4 dsp[2];
       if (!skip) {
         const float* lsv = vec_lds[S][0];
         const float* dvv = vec_lds[S][1];
@@ -739,7 +765,7 @@ void fa_bwd_dkdv_fused_kernel(BwdParams p) {
           for (int e = 0; e < 16; ++e)
             sb[e] = (unsigned)(qd0 + 16 * (e >> 3) + (e & 7)) <= span ? sb[e] : -INFINITY;
         }
-        u32x4 pp[2], dsp[2];
+        u32x4 pp[2];
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
           const int r8 = 16 * hh + 8 * g;
@@ -789,6 +815,14 @@ void fa_bwd_dkdv_fused_kernel(BwdParams p) {
       }
       wait_all();
       stage_barrier();
+      // (DS) The step's dS goes out after the wait, so that the next step's
+      // wait (vmcnt counts stores too) finds it long written.
+      if (DS && !skip) {
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh)
+          __builtin_nontemporal_store(
+              dsp[hh], (u32x4*)(ds_blk + hh * 1024 + (32 * g + (j ^ (4 * (2 * hh + g)))) * 16));
+      }
     }
     if (mykey < p.Sk) {
       store_row<NDB, BF16>((uint16_t*)p.dk + b * p.dk_sb + hk * p.dk_sh + (int64_t)mykey * p.dk_ss,
@@ -799,10 +833,238 @@ void fa_bwd_dkdv_fused_kernel(BwdParams p) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Dvec = rowsum(dO * O) in float32 for the stored-dS schedule (whose dK/dV
+// kernel runs first): one 16-byte chunk of a row per lane, D / 8 lanes per row.
+// ---------------------------------------------------------------------------
+template <int D, bool BF16>
+__global__ __launch_bounds__(256) void fa_bwd_dvec_kernel(BwdParams p) {
+  constexpr int CPR = D / 8, RPB = 256 / CPR;
+  const int64_t rows = (int64_t)p.B * p.H * p.Sq;
+  const int64_t row = (int64_t)blockIdx.x * RPB + threadIdx.x / CPR;
+  const int c = threadIdx.x % CPR;
+  float part = 0.f;
+  if (row < rows) {
+    const int64_t bh = row / p.Sq;
+    const int s = (int)(row - bh * p.Sq), b = (int)(bh / p.H), h = (int)(bh % p.H);
+    const u32x4 o = *(const u32x4*)((const uint16_t*)p.o + b * p.o_sb + h * p.o_sh +
+                                    (int64_t)s * p.o_ss + 8 * c);
+    const u32x4 d = *(const u32x4*)((const uint16_t*)p.dout + b * p.do_sb + h * p.do_sh +
+                                    (int64_t)s * p.do_ss + 8 * c);
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      part += h2f<BF16>((uint16_t)(o[w] & 0xffffu)) * h2f<BF16>((uint16_t)(d[w] & 0xffffu));
+      part += h2f<BF16>((uint16_t)(o[w] >> 16)) * h2f<BF16>((uint16_t)(d[w] >> 16));
+    }
+  }
+#pragma unroll
+  for (int m = CPR / 2; m >= 1; m >>= 1) part += __shfl_xor(part, m);
+  if (row < rows && c == 0) p.dvec[row] = part;
+}
+
+// ---------------------------------------------------------------------------
+// dQ from the stored dS^T: a workgroup owns query rows [128 QB qt, +128 QB) of
+// one (batch, head) (wave w: the QB query blocks from 4 QB qt + QB w) and
+// streams 64-key steps: the K tile into LDS (shared by the four waves) and
+// each wave's dS^T blocks (two key blocks per query block) into its own LDS,
+// both by DMA. dQ^T += K^T dS^T with both operands from transposing reads
+// (B: column j = query j of the block, k-group = 8 keys); each K^T fragment
+// serves the wave's QB query blocks. The dS^T stream bounds the kernel (one
+// 2 KB block per 32 x 32 products): NST stages, NST - 1 steps in flight, one
+// workgroup per CU.
+// ---------------------------------------------------------------------------
+template <int QB>
+struct DqDsShape {
+  static constexpr int kDsBytes = QB * 4096;                 // a wave's dS^T per step
+  static constexpr int kStage = kBwdTile * 128 * 2 + kBwdWaves * kDsBytes;  // bytes (D = 128)
+  static constexpr int NST = (160 * 1024) / kStage > 4 ? 4 : (160 * 1024) / kStage;
+};
+
+template <int D, bool BF16, int QB>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void fa_bwd_dq_ds_kernel(BwdParams p) {
+  constexpr int NDB = D / 32, TILE = kBwdTile * D;
+  constexpr int NST = DqDsShape<QB>::NST, DSB = DqDsShape<QB>::kDsBytes;
+  constexpr int OWN = kBwdOwn * QB;                      // query rows per workgroup
+  constexpr int NPER = TileDma<D>::NDMA + DSB / 1024;    // DMAs per wave per step
+  static_assert(NST >= 2 && NPER * (NST - 2) <= 63, "stages and vmcnt range");
+  __shared__ __align__(1024) uint16_t kl[NST * TILE];
+  // Stage s, wave w: the wave's blocks at byte (kBwdWaves s + w) * DSB, query
+  // block k's two key blocks at + 4096 k.
+  __shared__ __align__(1024) uint16_t dsl[NST * kBwdWaves * DSB / 2];
+
+  const int n_qt = (p.Sq + OWN - 1) / OWN;
+  // Query tiles n_qt - 1 - pt and pt, as fa_bwd_dq_kernel.
+  const int n_pair = (n_qt + 1) / 2;
+  int pt, bh;
+  grid_tile(p.B * p.H, n_pair, pt, bh);
+  const int b = bh / p.H, h = bh % p.H;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g = lane >> 5;
+  const uint16_t* K = (const uint16_t*)p.k + b * p.k_sb + (h / p.kv_group) * p.k_sh;
+  const char* dsh = (const char*)p.ds + (int64_t)bh * p.ds_tot * kDsBlockBytes;
+  Addr<D> ad;
+  ad.init(lane);
+  TileDma<D> kd;
+  kd.init(p.k_ss, wave, lane);
+  const u32 kbase = lds_addr(kl);
+  const u32 dbase = lds_addr(dsl) + (u32)(wave * DSB);
+  const char* dsw = (const char*)dsl + wave * DSB;
+  // Transposing read of a block (k-step ks of the step: block ks / 2, keys
+  // 16 (ks % 2) + 8 g + 4 hf + s / 4, rows 16 gq + 4 (s % 4) .. + 3, s = lane
+  // % 16, gq = (lane / 16) % 2) at byte (ks / 2) * 2048 + (ks % 2) * 256 +
+  // dtr[hf]: chunk 32 g' + (key ^ 4 (2 gq + g')) of half gq, g' = (s % 4) / 2.
+  const int s = lane & 15, gq = (lane >> 4) & 1, gh = (s & 3) >> 1;
+  int dtr[2];
+#pragma unroll
+  for (int hf = 0; hf < 2; ++hf) {
+    const int kq = 8 * g + 4 * hf + (s >> 2);
+    dtr[hf] = gq * 1024 + (32 * gh + (kq ^ (4 * (2 * gq + gh)))) * 16 + (s & 1) * 8;
+  }
+
+  for (int pass = 0; pass < 2; ++pass) {
+    const int qt = pass == 0 ? n_qt - 1 - pt : pt;
+    if (pass == 1 && qt == n_qt - 1 - pt) break;  // odd n_qt: the middle tile runs alone
+    const int q0 = qt * OWN, wq0 = q0 + wave * 32 * QB;
+    const int qb0 = wq0 / 32;  // the wave's first query block
+    const int q_last = min(q0 + OWN, p.Sq) - 1;
+    const int kv_lo = p.win_left >= 0 ? max(0, q0 - p.win_left) : 0;
+    const int kv_hi = p.win_right >= 0 ? min(p.Sk, q_last + p.win_right + 1) : p.Sk;
+    const int t0 = kv_lo / kBwdTile;
+    const int n_t = kv_hi > kv_lo ? (kv_hi - 1) / kBwdTile - t0 + 1 : 0;
+
+    f32x16 dq[QB][NDB];
+#pragma unroll
+    for (int k = 0; k < QB; ++k)
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) dq[k][db] = (f32x16){};
+
+    // Load cursor: key tile lkt of the step being loaded, its first block and
+    // query block range (steps are consecutive 64-key halves of key tiles).
+    int lkt = t0 / 2, lt0, lnt;
+    int64_t loff = 0;
+    for (int t = 0; t < lkt; ++t) {
+      int a, n;
+      ds_key_tile(p.Sq, p.Sk, p.win_left, p.win_right, t, a, n);
+      loff += 4 * n;
+    }
+    ds_key_tile(p.Sq, p.Sk, p.win_left, p.win_right, lkt, lt0, lnt);
+    auto load = [&](int t) __attribute__((always_inline)) {
+      const int kv0 = (t0 + t) * kBwdTile, kt = kv0 / kBwdOwn, S = t % NST;
+      if (kt != lkt) {
+        loff += 4 * lnt;
+        lkt = kt;
+        ds_key_tile(p.Sq, p.Sk, p.win_left, p.win_right, kt, lt0, lnt);
+      }
+      kd.load(K, kbase + S * TILE * 2, kv0, p.Sk);
+      // A query block the key tile has no blocks for reads (and ignores) the
+      // buffer's first 4 KB, so that every step issues the same DMAs.
+#pragma unroll
+      for (int k = 0; k < QB; ++k) {
+        const int qb = qb0 + k;
+        const bool have = qb >= lt0 && qb < lt0 + lnt;
+        const char* src =
+            have ? dsh + (loff + 4 * (qb - lt0) + ((kv0 / 32) & 3)) * kDsBlockBytes
+                 : (const char*)p.ds;
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          dma16_global_s(dbase + (u32)(S * kBwdWaves * DSB + k * 4096 + r * 1024), src + r * 1024,
+                         (u32)lane * 16u);
+      }
+    };
+    if (n_t > 0) {
+      wait_all();
+      for (int t = 0; t < min(n_t, NST - 1); ++t) load(t);
+    }
+    // Step t: wait for its DMAs, barrier (every wave's part of the K tile has
+    // landed, and every wave finished step t - 1, whose stage the load of step
+    // t + NST - 1 then overwrites), then compute.
+    for (int t = 0; t < n_t; ++t) {
+      const int ahead = min(n_t - 1 - t, NST - 2);
+      if (NST > 3 && ahead >= 2)
+        __builtin_amdgcn_s_waitcnt(0x0F70 | ((2 * NPER) & 15) | (((2 * NPER) >> 4) << 14));
+      else if (ahead >= 1)
+        __builtin_amdgcn_s_waitcnt(0x0F70 | (NPER & 15) | ((NPER >> 4) << 14));
+      else
+        __builtin_amdgcn_s_waitcnt(0x0F70);
+      stage_barrier();
+      if (t + NST - 1 < n_t) load(t + NST - 1);
+      const int S = t % NST;
+      const int kv0 = (t0 + t) * kBwdTile, kt = kv0 / kBwdOwn;
+      int ct0, cnt;
+      ds_key_tile(p.Sq, p.Sk, p.win_left, p.win_right, kt, ct0, cnt);
+      const uint16_t* Kt = kl + S * TILE;
+      const char* Dt = dsw + S * kBwdWaves * DSB;
+#pragma unroll
+      for (int blk = 0; blk < 2; ++blk) {
+        // Query block k uses the key block's dS^T unless the dK/dV kernel
+        // skipped it (no block for the pair, or outside the mask's reach).
+        const int kb0 = kv0 + 32 * blk;
+        bool use[QB];
+        bool any = false;
+#pragma unroll
+        for (int k = 0; k < QB; ++k) {
+          const int qb = qb0 + k, qr = 32 * qb;
+          use[k] = qb >= ct0 && qb < ct0 + cnt && kb0 < p.Sk &&
+                   !(p.win_right >= 0 && kb0 > qr + 31 + p.win_right) &&
+                   !(p.win_left >= 0 && kb0 + 31 < qr - p.win_left);
+          any |= use[k];
+        }
+        if (!any) continue;
+#pragma unroll
+        for (int k2 = 0; k2 < 2; ++k2) {
+          const int ks = 2 * blk + k2;
+          u32x4 dsb[QB];
+#pragma unroll
+          for (int k = 0; k < QB; ++k) {
+            const char* a = Dt + k * 4096 + blk * kDsBlockBytes + k2 * 256;
+            const u32x2 dlo = lds_read_tr16(a + dtr[0]);
+            const u32x2 dhi = lds_read_tr16(a + dtr[1]);
+            // (a block the pair does not use contributes zero)
+            dsb[k] = use[k] ? (u32x4){dlo[0], dlo[1], dhi[0], dhi[1]} : (u32x4){0u, 0u, 0u, 0u};
+          }
+#pragma unroll
+          for (int db = 0; db < NDB; ++db) {
+            const u32x2 lo = lds_read_tr16(Kt + ad.tr[db][0] + 16 * ks * D);
+            const u32x2 hi = lds_read_tr16(Kt + ad.tr[db][1] + 16 * ks * D);
+            const u32x4 ka = {lo[0], lo[1], hi[0], hi[1]};
+#pragma unroll
+            for (int k = 0; k < QB; ++k) dq[k][db] = mfma32x32x16<BF16>(ka, dsb[k], dq[k][db]);
+          }
+        }
+      }
+    }
+    stage_barrier();  // every wave done with the stages before the next pass loads
+#pragma unroll
+    for (int k = 0; k < QB; ++k) {
+      const int myq = wq0 + 32 * k + (lane & 31);
+      if (myq < p.Sq)
+        store_row<NDB, BF16>((uint16_t*)p.dq + b * p.dq_sb + h * p.dq_sh + (int64_t)myq * p.dq_ss,
+                             g, dq[k], p.scale);
+    }
+  }
+}
+
+constexpr int kDqDsQB = 2;  // query blocks per wave of fa_bwd_dq_ds_kernel
+
 template <int D, bool BF16, bool DROP>
 hipError_t launch_bwd(const BwdParams& p, hipStream_t st) {
-  // dQ (which also writes Dvec) before dK / dV, which reads it.
   const int n_qt = (p.Sq + kBwdOwn - 1) / kBwdOwn, n_kt = (p.Sk + kBwdOwn - 1) / kBwdOwn;
+  if constexpr (D == 128) {
+    if (p.ds != nullptr) {
+      // Stored dS: Dvec, then dK / dV (which stores dS), then dQ = scale dS K.
+      const long rows = (long)p.B * p.H * p.Sq;
+      hipLaunchKernelGGL((fa_bwd_dvec_kernel<D, BF16>), dim3((rows + 15) / 16), dim3(256), 0, st,
+                         p);
+      hipLaunchKernelGGL((fa_bwd_dkdv_fused_kernel<BF16, DROP, true>),
+                         dim3(p.B * p.H_kv * ((n_kt + 1) / 2)), dim3(256), 0, st, p);
+      const int n_qt2 = (p.Sq + kBwdOwn * kDqDsQB - 1) / (kBwdOwn * kDqDsQB);
+      hipLaunchKernelGGL((fa_bwd_dq_ds_kernel<D, BF16, kDqDsQB>),
+                         dim3(p.B * p.H * ((n_qt2 + 1) / 2)), dim3(256), 0, st, p);
+      return hipGetLastError();
+    }
+  }
+  // dQ (which also writes Dvec) before dK / dV, which reads it.
   hipLaunchKernelGGL((fa_bwd_dq_kernel<D, BF16, DROP>), dim3(p.B * p.H * ((n_qt + 1) / 2)),
                      dim3(256), 0, st, p);
   const dim3 grid_kv(p.B * p.H_kv * n_kt);
@@ -829,6 +1091,36 @@ using namespace mpx;
 extern "C" size_t mpx_attn_bwd_workspace_bytes(int B, int H, int Sq) {
   if (B <= 0 || H <= 0 || Sq <= 0) return 0;
   return (size_t)B * H * Sq * sizeof(float);
+}
+
+// Stored dS^T blocks per query head (the key tiles' block counts summed).
+static int64_t ds_blocks_per_head(int Sq, int Sk, int win_left, int win_right) {
+  const int n_kt = (Sk + kBwdOwn - 1) / kBwdOwn;
+  int64_t tot = 0;
+  for (int kt = 0; kt < n_kt; ++kt) {
+    int t0, nt;
+    ds_key_tile(Sq, Sk, win_left, win_right, kt, t0, nt);
+    tot += 4 * nt;
+  }
+  return tot;
+}
+
+// Bytes of Dvec rounded up to 256: the stored dS^T starts there.
+static size_t dvec_region_bytes(int B, int H, int Sq) {
+  return (mpx_attn_bwd_workspace_bytes(B, H, Sq) + 255) & ~(size_t)255;
+}
+
+extern "C" size_t mpx_attn_bwd_ds_workspace_bytes(int B, int H, int Sq, int Sk, int D, int dtype,
+                                                  int causal, int window_left,
+                                                  int window_right) {
+  if (B <= 0 || H <= 0 || Sq <= 0 || Sk <= 0 || D != 128 ||
+      (dtype != MPX_F16 && dtype != MPX_BF16))
+    return 0;
+  const int wl = window_left < 0 ? -1 : window_left;
+  const int wr = causal ? 0 : (window_right < 0 ? -1 : window_right);
+  const int64_t blocks = (int64_t)B * H * ds_blocks_per_head(Sq, Sk, wl, wr);
+  // (at least 4 KB: the dQ kernel's placeholder reads)
+  return dvec_region_bytes(B, H, Sq) + (size_t)std::max<int64_t>(blocks, 2) * kDsBlockBytes;
 }
 
 static int attn_bwd_entry(const void* q, const void* k, const void* v, const void* o,
@@ -907,6 +1199,13 @@ static int attn_bwd_entry(const void* q, const void* k, const void* v, const voi
     p.seed0 = (uint32_t)seed;
     p.seed1 = (uint32_t)(seed >> 32);
     p.drop_scale = 1.f / (1.f - dropout_p);
+  }
+  // The stored-dS schedule when the workspace holds it.
+  const size_t ds_need = mpx_attn_bwd_ds_workspace_bytes(B, H, Sq, Sk, D, dtype, causal,
+                                                         window_left, window_right);
+  if (ds_need > 0 && workspace_bytes >= ds_need) {
+    p.ds = (char*)workspace + dvec_region_bytes(B, H, Sq);
+    p.ds_tot = ds_blocks_per_head(Sq, Sk, p.win_left, p.win_right);
   }
   hipStream_t st = (hipStream_t)stream;
   hipError_t e;

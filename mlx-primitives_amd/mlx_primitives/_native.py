@@ -102,6 +102,8 @@ def load() -> ctypes.CDLL:
             ctypes.c_float, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
         lib.mpx_attn_bwd_workspace_bytes.restype = ctypes.c_size_t
         lib.mpx_attn_bwd_workspace_bytes.argtypes = [ctypes.c_int] * 3
+        lib.mpx_attn_bwd_ds_workspace_bytes.restype = ctypes.c_size_t
+        lib.mpx_attn_bwd_ds_workspace_bytes.argtypes = [ctypes.c_int] * 9
         lib.mpx_attn_fwd_workspace_bytes.restype = ctypes.c_size_t
         lib.mpx_attn_fwd_workspace_bytes.argtypes = [ctypes.c_int] * 9
         lib.mpx_paged_decode.restype = ctypes.c_int
@@ -278,19 +280,55 @@ def attn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor,
     _check(rc, "mpx_attn_fwd failed")
 
 
+_DS_LIMIT: dict = {}
+
+
+def _ds_workspace_limit(dev: torch.device) -> int:
+    """An eighth of the device's memory: the largest stored-dS workspace taken
+    without being asked for."""
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    if idx not in _DS_LIMIT:
+        _DS_LIMIT[idx] = torch.cuda.get_device_properties(idx).total_memory // 8
+    return _DS_LIMIT[idx]
+
+
 def attn_bwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor,
              dout: torch.Tensor, lse: torch.Tensor, dq: torch.Tensor, dk: torch.Tensor,
              dv: torch.Tensor, strides: Sequence[Sequence[int]], B: int, H: int, H_kv: int,
              Sq: int, Sk: int, D: int, scale: float, causal: bool, window_left: int = -1,
-             window_right: int = -1, dropout: Optional[tuple] = None) -> None:
+             window_right: int = -1, dropout: Optional[tuple] = None,
+             stored_ds: Optional[bool] = None) -> None:
     """Enqueue mpx_attn_bwd on the current stream. ``strides`` holds the (b, h, s)
     element strides of q, k, v, o, dout, dq, dk, dv in that order; dropout =
-    (dropout_p, seed) of the forward (mpx_attn_bwd_dropout)."""
+    (dropout_p, seed) of the forward (mpx_attn_bwd_dropout).
+
+    stored_ds: the stored-dS schedule (mpx_attn_bwd_ds_workspace_bytes) or the
+    recomputing one. None takes the stored one for the dropout backward (whose
+    dQ kernel would otherwise regenerate the keep mask as well: 6% faster over
+    forward and backward at the headline shape), where the problem has it and
+    its workspace is at most an eighth of the device's memory and can be
+    allocated; without dropout the two schedules run level and the recomputing
+    one needs no workspace. False keeps the recomputing schedule; True requires
+    the stored one."""
     lib = load()
     dev = require_device(q, k, v, o, dout, lse, dq, dk, dv)
     code = dtype_code(q.dtype)
     ws_bytes = int(lib.mpx_attn_bwd_workspace_bytes(B, H, Sq))
-    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=dev)
+    ws = None
+    if stored_ds or (stored_ds is None and dropout is not None):
+        ds_bytes = int(lib.mpx_attn_bwd_ds_workspace_bytes(
+            B, H, Sq, Sk, D, code, int(causal), int(window_left), int(window_right)))
+        if stored_ds and not ds_bytes:
+            raise ValueError("mpx_attn_bwd: no stored-dS schedule for this problem")
+        if ds_bytes and (stored_ds or ds_bytes <= _ds_workspace_limit(dev)):
+            try:
+                ws = torch.empty(ds_bytes, dtype=torch.uint8, device=dev)
+                ws_bytes = ds_bytes
+            except torch.OutOfMemoryError:
+                if stored_ds:
+                    raise
+    if ws is None:
+        ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=dev)
     args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), dout.data_ptr(),
             lse.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
             *[_strides(s) for s in strides],

@@ -58,6 +58,12 @@ def _dims(q: torch.Tensor, k: torch.Tensor, layout: Layout):
     return B, H, k.shape[1], Sq, k.shape[2], D
 
 
+# The backward's schedule (_native.attn_bwd's stored_ds): None = the stored-dS
+# schedule for the dropout backward where it applies and its workspace fits,
+# True = the stored-dS schedule, False = recompute S and dP for dQ.
+BWD_STORED_DS: Optional[bool] = None
+
+
 class _FlashAttentionFn(torch.autograd.Function):
     """Flash forward that keeps each row's log-sum-exp, and the gfx950 backward
     (mpx_attn_bwd) that recomputes the probabilities from it. Inputs arrive
@@ -88,7 +94,8 @@ class _FlashAttentionFn(torch.autograd.Function):
         dv = torch.empty(v.shape, dtype=v.dtype, device=v.device)
         strides = [_bhs(x, layout) for x in (q, k, v, o, dout, dq, dk, dv)]
         _native.attn_bwd(q, k, v, o, dout, lse, dq, dk, dv, strides, B, H, H_kv, Sq, Sk, D,
-                         scale, causal, window_left, window_right, dropout=dropout)
+                         scale, causal, window_left, window_right, dropout=dropout,
+                         stored_ds=BWD_STORED_DS)
         return dq, dk, dv, None, None, None, None, None, None
 
 

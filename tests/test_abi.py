@@ -5,6 +5,7 @@ import ctypes
 import os
 import re
 
+import numpy as np
 import pytest
 import torch  # noqa: F401  (loads the HIP runtime the library links against)
 
@@ -34,7 +35,8 @@ def test_header_declares_expected_entry_points():
         "mpx_paged_prefill_workspace_bytes", "mpx_kv_append", "mpx_rope", "mpx_attn_fwd_gqa",
         "mpx_paged_decode_gqa", "mpx_paged_prefill_gqa", "mpx_attn_fwd_lse", "mpx_attn_bwd",
         "mpx_attn_bwd_workspace_bytes", "mpx_attn_fwd_rope", "mpx_paged_decode_noalloc",
-        "mpx_rope_at", "mpx_kv_append_rope", "mpx_attn_fwd_dropout", "mpx_attn_bwd_dropout"])
+        "mpx_rope_at", "mpx_kv_append_rope", "mpx_attn_fwd_dropout", "mpx_attn_bwd_dropout",
+        "mpx_attn_bwd_ds_workspace_bytes"])
 
 
 def test_library_exports_every_declared_symbol(lib):
@@ -194,6 +196,47 @@ def _bwd(lib, dtype=2, D=64, B=1, H=2, H_kv=2, Sq=8, Sk=8, scale=0.1, ptr=16, ws
     return lib.mpx_attn_bwd(ptr, ptr, ptr, ptr, ptr, ptr, ptr, ptr, ptr, st, st, st, st, st, st,
                             st, st, B, H, H_kv, Sq, Sk, D, scale, 1, -1, -1, dtype, ws, ws_bytes,
                             None)
+
+
+def _ds_blocks_brute(Sq, Sk, causal, wl, wr):
+    """Stored-dS blocks of one head by brute force over the mask: key tile t
+    (128 keys) keeps every 32-row query block from the first to the last one
+    holding a query that sees one of its keys, times its four key blocks."""
+    wr = 0 if causal else wr
+    q = np.arange(Sq)[:, None]
+    kk = np.arange(Sk)[None, :]
+    vis = np.ones((Sq, Sk), bool)
+    if wr >= 0:
+        vis &= kk <= q + wr
+    if wl >= 0:
+        vis &= kk >= q - wl
+    total = 0
+    for t in range(0, Sk, 128):
+        rows = np.nonzero(vis[:, t:t + 128].any(1))[0]
+        if rows.size:
+            total += 4 * (rows[-1] // 32 - rows[0] // 32 + 1)
+    return total
+
+
+@pytest.mark.parametrize("Sq,Sk,causal,wl,wr", [
+    (4096, 4096, 1, -1, -1), (300, 77, 1, -1, -1), (77, 300, 0, -1, 223), (260, 260, 1, 75, -1),
+    (260, 260, 0, 40, 40), (1, 129, 0, -1, -1), (129, 1, 1, -1, -1), (1000, 700, 0, 5, 900),
+    (700, 1000, 0, 0, 0), (513, 513, 1, 127, -1)])
+def test_bwd_ds_workspace_bytes(lib, Sq, Sk, causal, wl, wr):
+    B, H = 2, 3
+    dvec = (B * H * Sq * 4 + 255) // 256 * 256
+    blocks = max(B * H * _ds_blocks_brute(Sq, Sk, causal, wl, wr), 2)
+    for dtype in (1, 2):
+        got = lib.mpx_attn_bwd_ds_workspace_bytes(B, H, Sq, Sk, 128, dtype, causal, wl, wr)
+        assert got == dvec + 2048 * blocks
+    # causal 4096: the 32 x 32 lower triangle (128 * 129 / 2 blocks) plus six unused
+    # blocks on each key tile's diagonal
+    if (Sq, Sk, causal) == (4096, 4096, 1):
+        assert blocks == B * H * (128 * 129 // 2 + 6 * 32)
+    # no stored-dS schedule: float32, head dims other than 128, empty problems
+    assert lib.mpx_attn_bwd_ds_workspace_bytes(B, H, Sq, Sk, 128, 0, causal, wl, wr) == 0
+    assert lib.mpx_attn_bwd_ds_workspace_bytes(B, H, Sq, Sk, 64, 2, causal, wl, wr) == 0
+    assert lib.mpx_attn_bwd_ds_workspace_bytes(0, H, Sq, Sk, 128, 2, causal, wl, wr) == 0
 
 
 def test_bwd_validation(lib):

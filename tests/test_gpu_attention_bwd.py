@@ -23,6 +23,7 @@ import torch
 
 from mlx_primitives.attention import (chunked_cross_attention, flash_attention,
                                       sliding_window_attention)
+from mlx_primitives.attention import _launch
 from oracle import attention_grad as oag
 
 pytestmark = pytest.mark.gpu
@@ -140,6 +141,56 @@ def test_gqa_grad(device, dtype, H, H_kv, D):
     fn = lambda q, k, v: flash_attention(q, k, v, causal=True, enable_gqa=True)
     out, *g = run_grads(fn, device, q, k, v, d)
     check_grads(g, q, k, v, d, dtype, 1 / math.sqrt(D), True)
+
+
+# Both backward schedules at D = 128 (the recomputing one, which autograd takes
+# by default, and the stored-dS one): masks, ragged and tiny sizes, a partial
+# last key block, windows on one and both sides, grouped heads.
+SCHEDULE_CASES = [  # (Sq, Sk, H, H_kv, causal, W): W = sliding window, None = flash
+    (300, 300, 4, 4, True, None), (1000, 1000, 2, 2, True, None),
+    (77, 300, 4, 4, False, None), (300, 77, 4, 4, True, None), (300, 77, 4, 4, False, None),
+    (129, 1, 2, 2, True, None), (1, 129, 2, 2, False, None), (260, 260, 4, 4, True, 75),
+    (260, 260, 4, 4, False, 40), (700, 700, 2, 2, True, 300), (500, 500, 8, 2, True, None),
+]
+
+
+@pytest.mark.parametrize("stored", [True, False])
+@pytest.mark.parametrize("case", SCHEDULE_CASES)
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_backward_schedules_d128(device, monkeypatch, dtype, case, stored):
+    Sq, Sk, H, H_kv, causal, W = case
+    monkeypatch.setattr(_launch, "BWD_STORED_DS", stored)
+    seed = Sq * 7 + Sk + H_kv
+    q, d = rnd((2, Sq, H, 128), seed, dtype), rnd((2, Sq, H, 128), seed + 1, dtype)
+    k, v = rnd((2, Sk, H_kv, 128), seed + 2, dtype), rnd((2, Sk, H_kv, 128), seed + 3, dtype)
+    if W is None:
+        fn = lambda q, k, v: flash_attention(q, k, v, causal=causal, enable_gqa=H != H_kv)
+    else:
+        fn = lambda q, k, v: sliding_window_attention(q, k, v, window_size=W, causal=causal)
+    out, *g = run_grads(fn, device, q, k, v, d)
+    if W is not None:
+        check_grads(g, q, k, v, d, dtype, 1 / math.sqrt(128), causal, W, -1 if causal else W)
+    elif causal and Sk > Sq:
+        check_grads(g, q, k, v, d, dtype, 1 / math.sqrt(128), False, -1, Sk - Sq)
+    else:
+        check_grads(g, q, k, v, d, dtype, 1 / math.sqrt(128), causal)
+
+
+def test_backward_schedules_agree(device, monkeypatch):
+    # The two schedules differ only in summation order and in which kernel forms
+    # Dvec: their gradients agree to a few bf16 rounding units, normwise.
+    q, k, v, d = (rnd((2, 2048, 4, 128), 90 + i, torch.bfloat16) for i in range(4))
+    fn = lambda q, k, v: flash_attention(q, k, v, causal=True)
+    got = {}
+    for stored in (True, False):
+        monkeypatch.setattr(_launch, "BWD_STORED_DS", stored)
+        got[stored] = run_grads(fn, device, q, k, v, d)[1:]
+    for name, a, b in zip(("dq", "dk", "dv"), got[True], got[False]):
+        a, b = a.double(), b.double()
+        assert torch.isfinite(a).all(), name
+        rel = float((a - b).norm() / b.norm())
+        print(f"{name}: stored vs recompute normwise {rel:.2e}")
+        assert rel <= 4e-3, name
 
 
 @pytest.mark.parametrize("dtype", DTYPES)

@@ -31,6 +31,7 @@ import torch
 
 from mlx_primitives.attention import (chunked_cross_attention, flash_attention,
                                       sliding_window_attention)
+from mlx_primitives.attention import _launch
 from mlx_primitives.attention._launch import dropout_seed, run_attention
 from mlx_primitives.constants import Layout
 from oracle import dropout as od
@@ -238,6 +239,19 @@ def check_grads(got, want, dtype, p):
 @pytest.mark.parametrize("causal,wl,H_kv", [(True, -1, 4), (False, -1, 4), (True, 50, 4),
                                             (True, -1, 2)])
 def test_grad_vs_oracle(device, dtype, D, causal, wl, H_kv):
+    grad_vs_oracle(device, dtype, D, causal, wl, H_kv)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("causal,wl,H_kv", [(True, -1, 4), (True, 50, 2)])
+def test_grad_vs_oracle_recompute_schedule(device, monkeypatch, dtype, causal, wl, H_kv):
+    # The dropout backward at D = 128 takes the stored-dS schedule by default;
+    # this runs the other one.
+    monkeypatch.setattr(_launch, "BWD_STORED_DS", False)
+    grad_vs_oracle(device, dtype, 128, causal, wl, H_kv)
+
+
+def grad_vs_oracle(device, dtype, D, causal, wl, H_kv):
     B, Sq, Sk, H, p, seed = 2, 300, 300, 4, 0.2, SEED ^ (D * 31 + H_kv)
     scale = 1 / math.sqrt(D)
     q = rnd((B, Sq, H, D), 10, dtype)
