@@ -118,18 +118,27 @@ __global__ __launch_bounds__(64 * kHeadsPerWG<NT>) void paged_decode_part_kernel
   const int p1 = min(p0 + kPart, ctx);
   const int pg0 = p0 / p.bs;
   const int npg = (p1 - 1) / p.bs - pg0 + 1;
-  for (int i = tid; i < npg; i += 64 * kHeadsPerWG<NT>) {
-    const int blk = p.bt[(int64_t)b * p.max_blocks + pg0 + i];
-    btl[i] = (blk >= 0 && blk < p.num_blocks) ? blk : -1;
-  }
-  __syncthreads();
-  if (h >= p.H) return;
 
   // Lane (tl, cidx): 16-byte chunk cidx of the head row of tokens tl, tl+TPI, ...
   const int cidx = lane % LPT, tl = lane / LPT;
   // Head rows of dp <= D elements: the lanes of chunks past dp read nothing
   // and hold zeros (they add nothing to q.k and their output is not written).
   const bool lane_on = cidx * EPC < p.dp;
+  // The Q chunk and the ALiBi slope are requested before the page table, from
+  // addresses that are always valid (a wave past the last head, a lane past
+  // dp, no ALiBi: a row or word that is read and discarded), so that the
+  // three loads share one latency.
+  const int hq = min(h, p.H - 1);
+  const u32x4 q_raw = *(const u32x4*)((const char*)p.q +
+                                      ((int64_t)b * p.q_sb + (int64_t)hq * p.q_sh +
+                                       (lane_on ? cidx * EPC : 0)) * ES);
+  const float slope_any = *(p.slopes ? p.slopes + hq : (const float*)p.q);
+  for (int i = tid; i < npg; i += 64 * kHeadsPerWG<NT>) {
+    const int blk = p.bt[(int64_t)b * p.max_blocks + pg0 + i];
+    btl[i] = (blk >= 0 && blk < p.num_blocks) ? blk : -1;
+  }
+  __syncthreads();
+  if (h >= p.H) return;
   // Pool token rows hold H_kv heads; query head h reads K/V head h / kv_group.
   const int64_t row_elems = (int64_t)p.H_kv * p.dp;
   const int64_t hoff = (int64_t)(h / p.kv_group) * p.dp + cidx * EPC;
@@ -138,14 +147,11 @@ __global__ __launch_bounds__(64 * kHeadsPerWG<NT>) void paged_decode_part_kernel
 
   float qv[EPC];
   {
-    const u32x4 qr = lane_on ? *(const u32x4*)((const char*)p.q +
-                                               ((int64_t)b * p.q_sb + (int64_t)h * p.q_sh +
-                                                cidx * EPC) * ES)
-                             : (u32x4){0u, 0u, 0u, 0u};
+    const u32x4 qr = lane_on ? q_raw : (u32x4){0u, 0u, 0u, 0u};
 #pragma unroll
     for (int i = 0; i < EPC; ++i) qv[i] = elem<DT>(qr, i) * p.c;
   }
-  const float slope2 = p.slopes ? p.slopes[h] * kLog2e : 0.f;
+  const float slope2 = p.slopes ? slope_any * kLog2e : 0.f;
 
   // One pass over the partition: the K and V rows of a batch of U tokens per
   // lane are requested together; every token group (the LPT lanes of one
@@ -334,7 +340,9 @@ __device__ __forceinline__ int gqa_swz(int row) { return (row & 3) | (((row >> 3
 
 // BIG: pools of 4 GiB - 256 bytes and more (pool_bytes == 0), whose rows the
 // DMA reads through 64-bit addresses (rows without a page from kZeroChunk).
-template <bool BF16, bool BIG = false>
+// POW2: page sizes that are powers of two, whose page index and slot come from
+// a shift and a mask instead of a division.
+template <bool BF16, bool BIG = false, bool POW2 = false>
 __global__ __launch_bounds__(64 * kGqaWaves) void paged_decode_gqa_kernel(DecodeParams p) {
   constexpr int D = 128, ROWB = 2 * D, TILEB = kGqaTile * ROWB;
   // Per wave: kGqaStages stages of (K tile, V tile).
@@ -352,8 +360,31 @@ __global__ __launch_bounds__(64 * kGqaWaves) void paged_decode_gqa_kernel(Decode
   const int p0 = part * kPart;
   if (p0 >= ctx) return;  // uniform over the wave
   const int p1 = min(p0 + kPart, ctx);
-  const int pg0 = p0 / p.bs;
-  const int npg = (p1 - 1) / p.bs - pg0 + 1;
+  const int bsh = POW2 ? __builtin_ctz((unsigned)p.bs) : 0;
+  auto page_of = [&](int t) __attribute__((always_inline)) { return POW2 ? t >> bsh : t / p.bs; };
+  auto slot_of = [&](int t) __attribute__((always_inline)) {
+    return POW2 ? t & (p.bs - 1) : t % p.bs;
+  };
+  const int pg0 = page_of(p0);
+  const int npg = page_of(p1 - 1) - pg0 + 1;
+
+  const int i16 = lane & 15, q4 = lane >> 4;
+  const int G = p.kv_group;
+  const bool hv = i16 < G;        // column i16 is a query head of the group
+  const int h = hk * G + i16;
+  // Q rows first and unconditionally (columns past the group read the
+  // group's first head and are zeroed below), so that the five loads of the
+  // prologue share one latency instead of running one after another.
+  u32x4 qb[4];
+  const uint16_t* qrow = (const uint16_t*)p.q + (int64_t)b * p.q_sb +
+                         (int64_t)(hv ? h : hk * G) * p.q_sh + 8 * q4;
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb) qb[kb] = *(const u32x4*)(qrow + 32 * kb);
+  // (without ALiBi a dummy read of Q's first word, discarded: no branch, no
+  // wait of its own)
+  const float* sp = p.slopes ? p.slopes + (hv ? h : hk * G) : (const float*)p.q;
+  const float slope_any = *sp;
+  const float slope_raw = p.slopes ? slope_any : 0.f;
   int* bl = btl[wave];
   for (int i = lane; i < npg; i += 64) {
     const int blk = p.bt[(int64_t)b * p.max_blocks + pg0 + i];
@@ -361,25 +392,18 @@ __global__ __launch_bounds__(64 * kGqaWaves) void paged_decode_gqa_kernel(Decode
   }
   // (this wave's own LDS writes: its later reads see them in order)
 
-  const int i16 = lane & 15, q4 = lane >> 4;
-  const int G = p.kv_group;
-  const bool hv = i16 < G;        // column i16 is a query head of the group
-  const int h = hk * G + i16;
   // Q^T operand (column i16, dims 32 kb + 8 q4 .. +7) times scale * log2(e),
   // rounded to the storage type: S^T comes out of the MFMAs in log2 units.
-  u32x4 qb[4];
 #pragma unroll
   for (int kb = 0; kb < 4; ++kb) {
-    u32x4 x = {0u, 0u, 0u, 0u};
-    if (hv) x = *(const u32x4*)((const uint16_t*)p.q + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh +
-                               32 * kb + 8 * q4);
+    u32x4 x = hv ? qb[kb] : (u32x4){0u, 0u, 0u, 0u};
 #pragma unroll
     for (int w = 0; w < 4; ++w)
       x[w] = pack2<BF16>(h2f<BF16>((uint16_t)(x[w] & 0xffffu)) * p.c,
                          h2f<BF16>((uint16_t)(x[w] >> 16)) * p.c);
     qb[kb] = x;
   }
-  const float slope2 = (p.slopes && hv) ? p.slopes[h] * kLog2e : 0.f;
+  const float slope2 = hv ? slope_raw * kLog2e : 0.f;
   // Q (and the table) have landed before any DMA, so the waits below count
   // DMAs only.
   __builtin_amdgcn_s_waitcnt(0x0F70);
@@ -401,15 +425,15 @@ __global__ __launch_bounds__(64 * kGqaWaves) void paged_decode_gqa_kernel(Decode
     for (int v = 0; v < kGqaTile / 4; ++v) {
       const int r = 4 * v + q4;
       const int t = t0 + r;
-      const int pg = t < p1 ? bl[t / p.bs - pg0] : -1;
+      const int pg = t < p1 ? bl[page_of(t) - pg0] : -1;
       if constexpr (BIG) {
-        const uint64_t off = ((uint64_t)(u32)pg * (u32)p.bs + (u32)(t % p.bs)) * row_bytes +
+        const uint64_t off = ((uint64_t)(u32)pg * (u32)p.bs + (u32)slot_of(t)) * row_bytes +
                              (u32)((i16 ^ gqa_swz(r)) * 16);
         dma16_global(kdst + 4 * v * ROWB, pg >= 0 ? (const void*)(kbase + off) : &kZeroChunk);
         dma16_global(vdst + 4 * v * ROWB, pg >= 0 ? (const void*)(vbase + off) : &kZeroChunk);
         continue;
       }
-      const u32 off = pg >= 0 ? ((u32)pg * (u32)p.bs + (u32)(t % p.bs)) * row_bytes +
+      const u32 off = pg >= 0 ? ((u32)pg * (u32)p.bs + (u32)slot_of(t)) * row_bytes +
                                     (u32)((i16 ^ gqa_swz(r)) * 16)
                               : kGqaNoRow;
       dma16(krs, kdst + 4 * v * ROWB, (int)off, 0);
@@ -460,7 +484,7 @@ __global__ __launch_bounds__(64 * kGqaWaves) void paged_decode_gqa_kernel(Decode
     }
     // Masks (missing pages, the context end), ALiBi, the tile max of head i16.
     const int tl = t0 + (lane & 31);
-    const uint64_t vm = __ballot(tl < p1 && bl[min(tl, p1 - 1) / p.bs - pg0] >= 0);
+    const uint64_t vm = __ballot(tl < p1 && bl[page_of(min(tl, p1 - 1)) - pg0] >= 0);
     float mx = -INFINITY;
 #pragma unroll
     for (int f = 0; f < 2; ++f)
@@ -549,12 +573,22 @@ hipError_t launch_decode(const DecodeParams& p, hipStream_t st) {
   if constexpr (kGqaMfmaType<D, DT>) {
     if (p.kv_group >= 2 && p.kv_group <= 16 && p.dp == D) {
       const dim3 grid(p.H_kv, (p.max_parts + kGqaWaves - 1) / kGqaWaves, p.B);
-      if (p.pool_bytes != 0)
-        hipLaunchKernelGGL((paged_decode_gqa_kernel<DT == MPX_BF16>), grid,
-                           dim3(64 * kGqaWaves), 0, st, p);
-      else
-        hipLaunchKernelGGL((paged_decode_gqa_kernel<DT == MPX_BF16, true>), grid,
-                           dim3(64 * kGqaWaves), 0, st, p);
+      const bool pow2 = (p.bs & (p.bs - 1)) == 0;
+      if (p.pool_bytes != 0) {
+        if (pow2)
+          hipLaunchKernelGGL((paged_decode_gqa_kernel<DT == MPX_BF16, false, true>), grid,
+                             dim3(64 * kGqaWaves), 0, st, p);
+        else
+          hipLaunchKernelGGL((paged_decode_gqa_kernel<DT == MPX_BF16>), grid,
+                             dim3(64 * kGqaWaves), 0, st, p);
+      } else {
+        if (pow2)
+          hipLaunchKernelGGL((paged_decode_gqa_kernel<DT == MPX_BF16, true, true>), grid,
+                             dim3(64 * kGqaWaves), 0, st, p);
+        else
+          hipLaunchKernelGGL((paged_decode_gqa_kernel<DT == MPX_BF16, true>), grid,
+                             dim3(64 * kGqaWaves), 0, st, p);
+      }
       hipError_t e = hipGetLastError();
       if (e != hipSuccess) return e;
       hipLaunchKernelGGL(paged_decode_merge_kernel<DT>, merge_grid(p, D), dim3(64), 0, st, p, D);
