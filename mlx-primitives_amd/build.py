@@ -26,10 +26,11 @@ LIB_PATH = os.path.join(LIB_DIR, "libmpx_attn.so")
 
 SOURCES = ["abi.hip", "fa_fwd.hip", "fa_bwd.hip", "fa_bwd32.hip", "paged_decode.hip",
            "kv_cache.hip", "rope.hip"]
-# Per-source device-compiler options. The backward kernels hold their MFMA
-# accumulators in arch VGPRs (the default heuristic moves them through AGPRs
-# with a copy per element per tile).
-EXTRA_FLAGS = {"fa_bwd.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
+# Per-source device-compiler options. The backward and grouped-query decode
+# kernels hold their MFMA accumulators in arch VGPRs (the default heuristic
+# moves them through AGPRs with a copy per element per tile).
+EXTRA_FLAGS = {"fa_bwd.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+               "paged_decode.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
 ARCH = "gfx950"
 
 

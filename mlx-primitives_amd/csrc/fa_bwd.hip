@@ -94,15 +94,6 @@ struct TileDma {
 // s_waitcnt vmcnt(0) lgkmcnt(0): every load and LDS access of this wave done.
 __device__ __forceinline__ void wait_all() { __builtin_amdgcn_s_waitcnt(0x0070); }
 
-// One 4-byte-per-lane DMA: lane l's dword lands at LDS address lds_addr + 4 l.
-// Untracked by the compiler like dma16.
-__device__ __forceinline__ void dma4(u32x4 rsrc, unsigned lds_addr, int voff) {
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds"
-               :
-               : "s"(lds_addr), "v"(voff), "s"(rsrc)
-               : "memory", "m0");
-}
-
 // Per-lane LDS element offsets into a swizzled (64, D) tile. row[ks]: A
 // operand rows 32*nb + perm(j), k-step ks (add nb * 32 * D). tr[db][hf]: the
 // transposing read for A = X^T over rows 16*sl + 8g + 4hf + s/4, columns

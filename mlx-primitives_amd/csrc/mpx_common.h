@@ -232,6 +232,15 @@ __device__ __forceinline__ void dma16(u32x4 rsrc, unsigned lds_addr, int voff, i
                : "memory", "m0");
 }
 
+// One 4-byte-per-lane DMA: lane l's dword lands at LDS address lds_addr + 4 l.
+// Untracked by the compiler like dma16.
+__device__ __forceinline__ void dma4(u32x4 rsrc, unsigned lds_addr, int voff) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds"
+               :
+               : "s"(lds_addr), "v"(voff), "s"(rsrc)
+               : "memory", "m0");
+}
+
 // The same DMA from 64-bit addresses, for pools of 4 GiB and more (the buffer
 // form's offsets are 32-bit): lane l's 16 bytes at `src` (its own address) /
 // at sbase + voff (a wave-uniform base and a per-lane offset) land at LDS

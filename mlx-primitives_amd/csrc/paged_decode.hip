@@ -419,13 +419,18 @@ __global__ __launch_bounds__(64 * kGqaWaves) void paged_decode_gqa_kernel(Decode
 
   // K and V rows of the tile at t0 into stage sb: 8 DMA instructions each;
   // lane l fills slot l % 16 of row 4v + l / 16 with its chunk (l % 16) ^ f(row).
+  // The eight page ids are read first (clamped rows, no branch), so that
+  // their LDS reads share one wait.
   auto load_tile = [&](int t0, int sb) __attribute__((always_inline)) {
     const u32 kdst = lds_addr(kvt[wave][sb][0]), vdst = lds_addr(kvt[wave][sb][1]);
+    int pgs[kGqaTile / 4];
+#pragma unroll
+    for (int v = 0; v < kGqaTile / 4; ++v) pgs[v] = bl[page_of(min(t0 + 4 * v + q4, p1 - 1)) - pg0];
 #pragma unroll
     for (int v = 0; v < kGqaTile / 4; ++v) {
       const int r = 4 * v + q4;
       const int t = t0 + r;
-      const int pg = t < p1 ? bl[page_of(t) - pg0] : -1;
+      const int pg = t < p1 ? pgs[v] : -1;
       if constexpr (BIG) {
         const uint64_t off = ((uint64_t)(u32)pg * (u32)p.bs + (u32)slot_of(t)) * row_bytes +
                              (u32)((i16 ^ gqa_swz(r)) * 16);
