@@ -12,6 +12,7 @@ or the tensors are not on a ROCm device, the call raises.
 from __future__ import annotations
 
 import ctypes
+import functools
 import os
 import threading
 from typing import Optional, Sequence
@@ -184,7 +185,14 @@ def _check(rc: int, what: str) -> None:
 
 
 def _strides(vals: Sequence[int]) -> ctypes.Array:
-    return (ctypes.c_int64 * len(vals))(*[int(x) for x in vals])
+    return _strides_of(tuple(int(x) for x in vals))
+
+
+@functools.lru_cache(maxsize=512)
+def _strides_of(vals: tuple) -> ctypes.Array:
+    # One int64[] per distinct stride tuple: the library only reads it during
+    # the call, and nothing here writes it.
+    return (ctypes.c_int64 * len(vals))(*vals)
 
 
 def require_device(*tensors: torch.Tensor) -> torch.device:
@@ -217,14 +225,26 @@ def dtype_code(dtype: torch.dtype) -> int:
         raise ValueError(f"unsupported dtype {dtype}; expected float32, float16 or bfloat16") from None
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def _stream_ptr(dev: torch.device) -> int:
+    """hipStream_t of torch's current stream on dev."""
+    if _raw_stream is not None:
+        return _raw_stream(dev.index if dev.index is not None else torch.cuda.current_device())
     return torch.cuda.current_stream(dev).cuda_stream
+
+
+@functools.lru_cache(maxsize=1024)
+def _fwd_workspace_bytes(*args) -> int:
+    # mpx_attn_fwd_workspace_bytes is a pure function of its arguments.
+    return int(load().mpx_attn_fwd_workspace_bytes(*args))
 
 
 def attn_fwd_workspace_bytes(B: int, H: int, Sq: int, Sk: int, D: int, causal: bool,
                              window_left: int, window_right: int, dtype: torch.dtype) -> int:
-    return int(load().mpx_attn_fwd_workspace_bytes(
-        B, H, Sq, Sk, D, int(causal), window_left, window_right, dtype_code(dtype)))
+    return _fwd_workspace_bytes(B, H, Sq, Sk, D, int(causal), int(window_left),
+                                int(window_right), dtype_code(dtype))
 
 
 def attn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor,
@@ -247,8 +267,8 @@ def attn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor,
             raise ValueError("q_rope and lse cannot be combined")
         cos, sin, q_offset = q_rope
         require_device(q, cos, sin)
-        ws_bytes = int(lib.mpx_attn_fwd_workspace_bytes(
-            B, H, Sq, Sk, D, int(causal), window_left, window_right, code))
+        ws_bytes = _fwd_workspace_bytes(B, H, Sq, Sk, D, int(causal), int(window_left),
+                                        int(window_right), code)
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
         rc = lib.mpx_attn_fwd_rope(
             q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
@@ -263,8 +283,8 @@ def attn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor,
         if (lse.dtype != torch.float32 or not lse.is_contiguous() or lse.device != dev
                 or tuple(lse.shape) != (B, H, Sq)):
             raise ValueError("lse must be a contiguous (B, H, Sq) float32 tensor on the device")
-    ws_bytes = int(lib.mpx_attn_fwd_workspace_bytes(
-        B, H, Sq, Sk, D, int(causal), window_left, window_right, code))
+    ws_bytes = _fwd_workspace_bytes(B, H, Sq, Sk, D, int(causal), int(window_left),
+                                    int(window_right), code)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
     args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
             lse.data_ptr() if lse is not None else None,
