@@ -4,16 +4,19 @@ The hand-picked cases of the per-path tests name the shapes, masks and page
 sizes the kernels branch on; this sweep draws combinations from fixed seeds
 (dtype, layout, head dim, batch, heads, sequence lengths, causal / window /
 chunk, grouped heads, paged decode or prefill, page size, ALiBi, empty
-sequences and missing pages), so
-that combinations nobody listed run too. Every case is small enough for the
-float64 oracle to finish in about a second.
+sequences and missing pages, dropout rate and seed), so that combinations
+nobody listed run too. Every case is small enough for the float64 oracle to
+finish within seconds.
 
 Tolerances, as in the per-path tests: forward and decode float32 rtol 1e-4 /
 atol 1e-5 (the reference's fp32 bar, tests/attention/test_flash.py:72-74),
 16-bit max-abs error <= 2e-2 against the float64 oracle on the same cast
 inputs; gradients float32 rtol 1e-3 / atol 1e-4, float16 1e-2 / 1e-2,
 bfloat16 1e-1 / 1e-1 elementwise (the reference's gradient bar,
-tests/parity/shared/tolerance_config.py:57,363-387).
+tests/parity/shared/tolerance_config.py:57,363-387); with dropout the
+gradients' absolute bar is divided by 1 - p (the kept weights' scale) and a
+normwise relative bar is added (float32 2e-5, float16 2e-3, bfloat16 1.5e-2),
+as in the dropout tests.
 """
 
 import numpy as np
@@ -24,7 +27,10 @@ from mlx_primitives.attention import (chunked_cross_attention, flash_attention,
                                       sliding_window_attention)
 from mlx_primitives.cache import get_alibi_slopes, paged_attention
 from oracle import attention as oa
+from mlx_primitives.attention._launch import run_attention
+from mlx_primitives.constants import Layout
 from oracle import attention_grad as oag
+from oracle import dropout as od
 from oracle import paged as op
 
 pytestmark = pytest.mark.gpu
@@ -32,6 +38,7 @@ pytestmark = pytest.mark.gpu
 DTYPES = [torch.float32, torch.float16, torch.bfloat16]
 GRAD_TOL = {torch.float32: (1e-3, 1e-4), torch.float16: (1e-2, 1e-2),
             torch.bfloat16: (1e-1, 1e-1)}
+GRAD_NORMWISE = {torch.float32: 2e-5, torch.float16: 2e-3, torch.bfloat16: 1.5e-2}
 
 
 def rnd(shape, gen, dtype):
@@ -99,7 +106,7 @@ def test_paged_sweep(device, seed):
     rng = np.random.default_rng(8000 + seed)
     gen = torch.Generator().manual_seed(8000 + seed)
     dtype = DTYPES[int(rng.integers(3))]
-    D = int(rng.choice([64, 128]))
+    D = int(rng.choice([32, 64, 80, 128, 128, 256]))
     H_kv, G = int(rng.choice([1, 2, 4, 8])), int(rng.choice([1, 2, 3, 4, 8]))
     H = H_kv * G
     bs = int(rng.choice([8, 16, 24, 32, 64]))
@@ -168,3 +175,42 @@ def test_backward_sweep(device, seed):
         gn = g.double().cpu().numpy()
         assert np.isfinite(gn).all(), f"{what} {name}"
         np.testing.assert_allclose(gn, w, rtol=rtol, atol=atol, err_msg=f"{what} {name}")
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_dropout_sweep(device, seed):
+    # forward and gradients with dropout: the keep mask of (seed, row, key
+    # pair) regenerated by the backward kernels, against the oracle's mask
+    rng = np.random.default_rng(9500 + seed)
+    gen = torch.Generator().manual_seed(9500 + seed)
+    dtype = DTYPES[int(rng.integers(3))]
+    D = int(rng.choice([32, 64, 96, 128, 256]))
+    B, H_kv, G = int(rng.integers(1, 3)), int(rng.integers(1, 4)), int(rng.choice([1, 2]))
+    S = int(rng.integers(1, 400))
+    causal = bool(rng.integers(2))
+    wl = int(rng.integers(1, 200)) if rng.integers(2) else -1
+    p = float(rng.choice([0.1, 0.3, 0.6]))
+    dseed = int(rng.integers(1 << 62))
+    scale = 1.0 / np.sqrt(D)
+    q, dout = (rnd((B, S, H_kv * G, D), gen, dtype) for _ in range(2))
+    k, v = (rnd((B, S, H_kv, D), gen, dtype) for _ in range(2))
+    qd, kd, vd = (x.to(device).requires_grad_(True) for x in (q, k, v))
+    out = run_attention(qd, kd, vd, Layout.BSHD, scale, causal, wl, -1, dropout_p=p,
+                        dropout_seed_value=dseed)
+    out.backward(dout.to(device))
+    torch.cuda.synchronize()
+    a = lambda x: x.double().numpy()
+    what = (f"dropout {dtype} B={B} H={H_kv * G}/{H_kv} S={S} D={D} causal={causal} "
+            f"window={wl} p={p}")
+    ref = od.attention_dropout(a(q), a(k), a(v), scale, causal, p, dseed, wl)
+    check(out.detach(), ref, dtype, what)
+    want = od.attention_dropout_grad(a(q), a(k), a(v), a(dout), scale, causal, p, dseed, wl)
+    rtol, atol = GRAD_TOL[dtype]
+    atol /= 1.0 - p
+    for name, g, w in zip(("dq", "dk", "dv"), (qd.grad, kd.grad, vd.grad), want):
+        gn = g.double().cpu().numpy()
+        assert gn.shape == w.shape and np.isfinite(gn).all(), f"{what} {name}"
+        np.testing.assert_allclose(gn, w, rtol=rtol, atol=atol, err_msg=f"{what} {name}")
+        if np.linalg.norm(w) / np.sqrt(w.size) > atol:
+            err = np.linalg.norm(gn - w) / np.linalg.norm(w)
+            assert err <= GRAD_NORMWISE[dtype], f"{what} {name}: normwise {err:.3e}"
