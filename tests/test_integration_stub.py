@@ -273,13 +273,15 @@ def test_stub_fused_rope_matches_api(device):
 
 
 @pytest.mark.gpu
-def test_stub_dropout_matches_api(device):
+@pytest.mark.parametrize("D", [64, 128])
+def test_stub_dropout_matches_api(device, D):
+    # (D = 128: both sides take the stored-dS backward)
     from mlx_primitives.attention._launch import run_attention
     from mlx_primitives.constants import Layout
 
     ns = stub_namespace()
     g = torch.Generator().manual_seed(11)
-    B, H, S, D, p, seed = 2, 4, 260, 64, 0.2, 0xDEADBEEF12345678
+    B, H, S, p, seed = 2, 4, 260, 0.2, 0xDEADBEEF12345678
     q, k, v, do = (torch.randn((B, S, H, D), generator=g).to(torch.float16).to(device)
                    for _ in range(4))
     bufs = []
