@@ -1436,7 +1436,51 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& pin, const Wor
   const float f = m_max == -INFINITY ? 0.f : fast_exp2(m_run - m_max);
   // (dropout: kept weights times 1 / (1 - p); the row sums stay unscaled)
   const float fo = DROP ? f * p.drop_scale : f;
-  if (p.num_splits == 1) {
+  if (p.num_splits == 1 && D <= 128) {
+    // O goes out through LDS so that each store instruction writes whole rows
+    // (16 bytes a lane, CPR lanes a row): straight from the accumulators an
+    // instruction would write 8-byte pieces of 32 rows. The stages are free
+    // here (the last tile step ended with no DMA in flight and every wave past
+    // its reads). Wave w's 32 rows sit in its own region, the 16-byte chunk c
+    // of row r at slot c ^ oswz(r), so that the writes (two lanes per row and
+    // chunk) and the row reads are free of bank conflicts.
+    constexpr int CPR = ROWB / 16, RPI = 64 / CPR, OWB = 32 * ROWB;
+    static_assert(D > 128 || NW * OWB <= 2 * STAGEB, "the rows fit two stages");
+    auto oswz = [](int r) { return CPR == 16 ? (r & 15) : ((r >> 1) & 7); };
+    unsigned char* const eb = NW * OWB <= STAGEB
+                                  ? st0 + wave * OWB
+                                  : (wave < NW / 2 ? st0 : st1) + (wave % (NW / 2)) * OWB;
+    // (the lane index taken afresh: addresses derived from it are not hoisted
+    // into registers the tile loop needs)
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    const int jr = ln & 31, gr = ln >> 5;
+    if (myq < p.Sq) {
+      const float inv = m_max == -INFINITY ? (p.nan_empty ? __builtin_nanf("") : 0.f)
+                                           : fo / (l_tot * f + p.eps);
+      if (p.lse && g == 0)
+        p.lse[((int64_t)wi.b * p.H + wi.h) * p.Sq + myq] =
+            m_max == -INFINITY ? INFINITY : m_max + log2f(l_tot * f + p.eps);
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int e4 = 0; e4 < 4; ++e4) {
+          // dims 8c + 4g .. + 3 of row j, c = 4 db + e4
+          const int c = 4 * db + e4;
+          const u32x2 val = {pack2<BF16>(o[db][4 * e4] * inv, o[db][4 * e4 + 1] * inv),
+                             pack2<BF16>(o[db][4 * e4 + 2] * inv, o[db][4 * e4 + 3] * inv)};
+          *(u32x2*)(eb + jr * ROWB + (c ^ oswz(jr)) * 16 + 8 * gr) = val;
+        }
+    }
+    uint16_t* const Ob = (uint16_t*)p.o + wi.b * p.o_sb + wi.h * p.o_sh;
+#pragma unroll
+    for (int i = 0; i < 32 / RPI; ++i) {
+      const int r = RPI * i + ln / CPR, c = ln % CPR;
+      const u32x4 val = *(const u32x4*)(eb + r * ROWB + (c ^ oswz(r)) * 16);
+      if (wq0 + r < p.Sq) *(u32x4*)(Ob + (int64_t)(wq0 + r) * p.o_ss + 8 * c) = val;
+    }
+    stage_barrier();  // every wave's rows read before the next item restages LDS
+  } else if (p.num_splits == 1) {
     if (myq < p.Sq) {
       const float inv = m_max == -INFINITY ? (p.nan_empty ? __builtin_nanf("") : 0.f)
                                            : fo / (l_tot * f + p.eps);
