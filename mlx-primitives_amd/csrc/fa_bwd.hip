@@ -145,6 +145,44 @@ __device__ __forceinline__ void store_row(uint16_t* row, int g, const f32x16 (&a
     }
 }
 
+// The same for the wave's 32 rows (row0 + j) at once, through the wave's own
+// LDS region eb (32 rows of 2 D bytes, free for the wave): each lane writes
+// its 8-byte pieces there, then every store instruction writes whole rows,
+// 16 bytes a lane, instead of 8-byte pieces of 32 rows. Rows at or past
+// `limit` are not written. The 16-byte chunk c of row r sits at slot
+// c ^ oswz(r), which keeps the writes and the row reads free of bank
+// conflicts. The caller puts a barrier between this and the next DMA into the
+// region.
+template <int NDB, bool BF16>
+__device__ __forceinline__ void store_rows_lds(unsigned char* eb, uint16_t* base, int64_t stride,
+                                               int row0, int limit, const f32x16 (&acc)[NDB],
+                                               float mul) {
+  constexpr int ROWB = 64 * NDB, CPR = ROWB / 16, RPI = 64 / CPR;
+  static_assert(RPI >= 1, "rows up to 1 KB");
+  auto oswz = [](int r) { return CPR >= 16 ? (r & 15) : ((r >> 1) & 7); };
+  // (the lane index taken afresh: addresses derived from it are not hoisted
+  // into the registers of the kernel's main loop)
+  int ln = threadIdx.x & 63;
+  asm volatile("" : "+v"(ln));
+  const int jr = ln & 31, gr = ln >> 5;
+#pragma unroll
+  for (int db = 0; db < NDB; ++db)
+#pragma unroll
+    for (int e4 = 0; e4 < 4; ++e4) {
+      // dims 8c + 4g .. + 3 of row j, c = 4 db + e4
+      const int c = 4 * db + e4;
+      const u32x2 val = {pack2<BF16>(acc[db][4 * e4] * mul, acc[db][4 * e4 + 1] * mul),
+                         pack2<BF16>(acc[db][4 * e4 + 2] * mul, acc[db][4 * e4 + 3] * mul)};
+      *(u32x2*)(eb + jr * ROWB + (c ^ oswz(jr)) * 16 + 8 * gr) = val;
+    }
+#pragma unroll
+  for (int i = 0; i < 32 / RPI; ++i) {
+    const int r = RPI * i + ln / CPR, c = ln % CPR;
+    const u32x4 val = *(const u32x4*)(eb + r * ROWB + (c ^ oswz(r)) * 16);
+    if (row0 + r < limit) *(u32x4*)(base + (int64_t)(row0 + r) * stride + 8 * c) = val;
+  }
+}
+
 // Workgroup -> (tile, head) of a launch over n_heads x n_tiles. Workgroup i
 // runs on XCD i % 8; with n_heads a multiple of 8, XCD x takes heads x, x + 8,
 // ... one at a time, all tiles of a head before the next, so the workgroups
@@ -334,9 +372,12 @@ void fa_bwd_dq_kernel(BwdParams p) {
       wait_all();
       stage_barrier();
     }
-    if (myq < p.Sq)
-      store_row<NDB, BF16>((uint16_t*)p.dq + b * p.dq_sb + h * p.dq_sh + (int64_t)myq * p.dq_ss,
-                           g, dq, p.scale);
+    // (the stages are free: the last step ended with every wave past its reads
+    // and no DMA in flight)
+    store_rows_lds<NDB, BF16>((unsigned char*)lds + wave * 64 * D,
+                              (uint16_t*)p.dq + b * p.dq_sb + h * p.dq_sh, p.dq_ss, wq0, p.Sq,
+                              dq, p.scale);
+    stage_barrier();  // every wave's rows read before the next pass stages tiles
   }
 }
 
@@ -1025,14 +1066,16 @@ void fa_bwd_dq_ds_kernel(BwdParams p) {
         }
       }
     }
-    stage_barrier();  // every wave done with the stages before the next pass loads
+    stage_barrier();  // every wave done with the stages (the last step waited for every DMA)
+    // The wave's query blocks go out through its own 64 D bytes of the K tile
+    // stages, one block after the other.
+    static_assert(kBwdWaves * 64 * D <= sizeof(kl), "a region per wave");
 #pragma unroll
-    for (int k = 0; k < QB; ++k) {
-      const int myq = wq0 + 32 * k + (lane & 31);
-      if (myq < p.Sq)
-        store_row<NDB, BF16>((uint16_t*)p.dq + b * p.dq_sb + h * p.dq_sh + (int64_t)myq * p.dq_ss,
-                             g, dq[k], p.scale);
-    }
+    for (int k = 0; k < QB; ++k)
+      store_rows_lds<NDB, BF16>((unsigned char*)kl + wave * 64 * D,
+                                (uint16_t*)p.dq + b * p.dq_sb + h * p.dq_sh, p.dq_ss,
+                                wq0 + 32 * k, p.Sq, dq[k], p.scale);
+    stage_barrier();  // every wave's rows read before the next pass loads
   }
 }
 
