@@ -1436,7 +1436,7 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& pin, const Wor
   const float f = m_max == -INFINITY ? 0.f : fast_exp2(m_run - m_max);
   // (dropout: kept weights times 1 / (1 - p); the row sums stay unscaled)
   const float fo = DROP ? f * p.drop_scale : f;
-  if (p.num_splits == 1 && D <= 128) {
+  if (p.num_splits == 1 && NW * 32 * ROWB <= 2 * STAGEB) {
     // O goes out through LDS so that each store instruction writes whole rows
     // (16 bytes a lane, CPR lanes a row): straight from the accumulators an
     // instruction would write 8-byte pieces of 32 rows. The stages are free
@@ -1445,8 +1445,7 @@ __device__ __forceinline__ void fa16_rows_direct(const FwdParams& pin, const Wor
     // of row r at slot c ^ oswz(r), so that the writes (two lanes per row and
     // chunk) and the row reads are free of bank conflicts.
     constexpr int CPR = ROWB / 16, RPI = 64 / CPR, OWB = 32 * ROWB;
-    static_assert(D > 128 || NW * OWB <= 2 * STAGEB, "the rows fit two stages");
-    auto oswz = [](int r) { return CPR == 16 ? (r & 15) : ((r >> 1) & 7); };
+    auto oswz = [](int r) { return CPR >= 16 ? (r & 15) : ((r >> 1) & 7); };
     unsigned char* const eb = NW * OWB <= STAGEB
                                   ? st0 + wave * OWB
                                   : (wave < NW / 2 ? st0 : st1) + (wave % (NW / 2)) * OWB;
