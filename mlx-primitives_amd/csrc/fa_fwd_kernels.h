@@ -60,6 +60,9 @@ struct FwdParams {
   // length (slot_qtile), else -1.
   int win_first;
   int paired;   // a slot runs q-tiles n_qtiles-1-slot and slot (causal balance)
+  // Paired launches, > 0: the last tail_bh (batch, head)s of every XCD's slice
+  // run their q-tiles one per workgroup, longest first (B * H % 8 == 0).
+  int tail_bh;
   float c;  // |scale| * log2(e)
   int neg;  // scale < 0: Q is negated on load (exact) and |scale| used
   float eps;      // normaliser epsilon: O / (l + eps)
@@ -198,6 +201,7 @@ constexpr float kRescaleThreshold = 8.0f;
 // XCD's L2 for their K/V reads.
 struct WorkSlot {
   int bh, slot, split;
+  int single;  // >= 0: the slot is this one q-tile alone
 };
 
 struct WorkItem {
@@ -230,11 +234,37 @@ __device__ __forceinline__ int slot_qtile(const FwdParams& p, int slot) {
 
 __device__ __forceinline__ WorkSlot decode_slot(const FwdParams& p) {
   const int L = blockIdx.x, N = gridDim.x;
+  if (p.tail_bh > 0) {
+    // XCD L % 8 takes (batch, head)s [x * bpx, (x + 1) * bpx) in dispatch
+    // order L / 8: first the paired slots of all but the last tail_bh of
+    // them, then the q-tiles of those one by one, longest first across the
+    // tail heads. The CUs that finish their last pair early take the long
+    // single q-tiles, the last ones the short ones, so the XCD's CUs end
+    // closer together than after a last round of equal pairs.
+    const int x = L & 7, idx = L >> 3;
+    const int bpx = (p.B * p.H) >> 3, t = p.tail_bh;
+    const int n_pair = (bpx - t) * p.n_slots;
+    WorkSlot ws;
+    ws.split = 0;
+    if (idx < n_pair) {
+      const int hb = idx / p.n_slots;
+      ws.bh = x * bpx + hb;
+      ws.slot = idx - hb * p.n_slots;
+      ws.single = -1;
+    } else {
+      const int k = idx - n_pair, r = k / t;
+      ws.bh = x * bpx + (bpx - t) + (k - r * t);
+      ws.slot = 0;
+      ws.single = p.n_qtiles - 1 - r;
+    }
+    return ws;
+  }
   const int w = (N & 7) == 0 ? (L & 7) * (N >> 3) + (L >> 3) : L;
   if (p.var_split > 0) {
     // Slot s is q-tile slot_qtile(s); the splits of the slots follow each
     // other within a (batch, head).
     WorkSlot ws;
+    ws.single = -1;
     ws.bh = w / p.var_split;
     int r = w - ws.bh * p.var_split, slot = 0;
     for (; slot < p.n_qtiles - 1; ++slot) {
@@ -249,6 +279,7 @@ __device__ __forceinline__ WorkSlot decode_slot(const FwdParams& p) {
   }
   const int per_bh = p.n_slots * p.num_splits;
   WorkSlot ws;
+  ws.single = -1;
   ws.bh = w / per_bh;
   const int r = w - ws.bh * per_bh;
   ws.slot = r / p.num_splits;
@@ -269,12 +300,12 @@ __device__ __forceinline__ WorkSlot decode_slot(const FwdParams& p) {
 // the sequence, which share their first tiles anyway) in descending order,
 // which fill the end of the launch as the longest-first order does.
 __device__ __forceinline__ int slot_items(const FwdParams& p, const WorkSlot& ws) {
-  return p.paired && ws.slot < p.n_qtiles - 1 - ws.slot ? 2 : 1;
+  return p.paired && ws.single < 0 && ws.slot < p.n_qtiles - 1 - ws.slot ? 2 : 1;
 }
 
 __device__ __forceinline__ WorkItem slot_item(const FwdParams& p, const WorkSlot& ws, int item) {
   WorkItem wi;
-  wi.qt = item == 0 ? slot_qtile(p, ws.slot) : ws.slot;
+  wi.qt = ws.single >= 0 ? ws.single : (item == 0 ? slot_qtile(p, ws.slot) : ws.slot);
   wi.split = ws.split;
   wi.b = ws.bh / p.H;
   wi.h = ws.bh - wi.b * p.H;

@@ -111,6 +111,17 @@ def test_flash_paired_causal_slots(device, S, D):
     check(out[:, sel], ref, torch.bfloat16)
 
 
+@pytest.mark.parametrize("BH,S,D", [(136, 768, 128), (96, 1536, 64)])
+def test_flash_paired_single_tail_every_head(device, BH, S, D):
+    # B * H divisible by the 8 XCDs: each XCD's slice of (batch, head)s runs
+    # paired slots first, then the q-tiles of its last heads one per workgroup
+    # (768: 3 q-tiles, 2 slots, 16 of 17 heads per XCD single; 1536: 6
+    # q-tiles, 3 slots, 11 of 12). Every head is checked.
+    (q, k, v), (qn, kn, vn) = inputs([(1, BH, S, D)] * 3, torch.bfloat16, BH + S, device)
+    out = flash_attention(q, k, v, causal=True, layout="BHSD")
+    check(out, oa.flash_attention(qn, kn, vn, causal=True, layout="BHSD"), torch.bfloat16)
+
+
 @pytest.mark.parametrize("D", [1, 8, 16, 40, 80, 96])
 def test_flash_padded_head_dims(device, D):
     (q, k, v), (qn, kn, vn) = inputs([(2, 70, 2, D)] * 3, torch.float32, D, device)
