@@ -183,6 +183,57 @@ __device__ __forceinline__ void store_rows_lds(unsigned char* eb, uint16_t* base
   }
 }
 
+#ifndef MPX_BWD_TAIL_SLOTS
+#define MPX_BWD_TAIL_SLOTS 64
+#endif
+// Paired launches over n_heads x n_tiles tiles (n_pair = ceil(n_tiles / 2)
+// workgroups per head) with n_heads a multiple of the 8 XCDs: the number of
+// heads per XCD whose tiles run one per workgroup at the end of the XCD's
+// share (about one round of the two workgroups per CU, 64 per XCD), or 0.
+// Taken by the stored-dS launches (dropout +0.9% at the headline shape); the
+// recomputing dQ and dK/dV pair measured 2% slower with it (tail = false).
+__host__ __device__ inline int bwd_tail_heads(int n_heads, int n_tiles, bool tail) {
+  const int n_pair = (n_tiles + 1) / 2;
+  if (!tail || MPX_BWD_TAIL_SLOTS <= 0 || n_heads % 8 != 0 || n_pair < 2) return 0;
+  const int t = (MPX_BWD_TAIL_SLOTS + n_pair - 1) / n_pair;
+  return t < n_heads / 8 ? t : 0;
+}
+
+// Workgroups of a paired launch (see grid_pair).
+inline long bwd_pair_grid(int n_heads, int n_tiles, bool tail) {
+  const int n_pair = (n_tiles + 1) / 2, t = bwd_tail_heads(n_heads, n_tiles, tail);
+  return (long)n_heads * n_pair + 8L * t * (n_tiles - n_pair);
+}
+
+// Workgroup -> (tile pair, head) of a paired launch, as grid_tile over
+// n_heads x n_pair, except that the last bwd_tail_heads heads of each XCD run
+// their n_tiles tiles one per workgroup after every pair of the XCD: single
+// = the rank of this workgroup's tile in longest-first order (else -1). The
+// CUs that finish their pairs early take the long tiles, the last ones the
+// short ones.
+__device__ __forceinline__ void grid_tile(int n_heads, int n_tiles, int& tile, int& head);
+
+__device__ __forceinline__ void grid_pair(int n_heads, int n_tiles, bool tail, int& pt,
+                                          int& head, int& single) {
+  const int n_pair = (n_tiles + 1) / 2, t = bwd_tail_heads(n_heads, n_tiles, tail);
+  single = -1;
+  if (t == 0) {
+    grid_tile(n_heads, n_pair, pt, head);
+    return;
+  }
+  const int i = blockIdx.x, xcd = i % 8, local = i / 8;
+  const int n_paired = (n_heads / 8 - t) * n_pair;
+  if (local < n_paired) {
+    pt = local % n_pair;
+    head = (local / n_pair) * 8 + xcd;
+  } else {
+    const int k = local - n_paired, r = k / t;
+    pt = 0;
+    head = (n_heads / 8 - t + (k - r * t)) * 8 + xcd;
+    single = r;
+  }
+}
+
 // Workgroup -> (tile, head) of a launch over n_heads x n_tiles. Workgroup i
 // runs on XCD i % 8; with n_heads a multiple of 8, XCD x takes heads x, x + 8,
 // ... one at a time, all tiles of a head before the next, so the workgroups
@@ -221,9 +272,8 @@ void fa_bwd_dq_kernel(BwdParams p) {
   // A workgroup runs query tiles n_qt - 1 - pt and pt, the longer (under a
   // causal mask, the last) first: their key-tile counts add up to the same
   // total for every pair, so all workgroups carry equal work.
-  const int n_pair = (n_qt + 1) / 2;
-  int pt, bh;
-  grid_tile(p.B * p.H, n_pair, pt, bh);
+  int pt, bh, single;
+  grid_pair(p.B * p.H, n_qt, false, pt, bh, single);
   const int b = bh / p.H, h = bh % p.H;
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int j = lane & 31, g = lane >> 5;
@@ -241,8 +291,9 @@ void fa_bwd_dq_kernel(BwdParams p) {
   const u32 lbase = lds_addr(lds);
 
   for (int pass = 0; pass < 2; ++pass) {
-    const int qt = pass == 0 ? n_qt - 1 - pt : pt;
-    if (pass == 1 && qt == n_qt - 1 - pt) break;  // odd n_qt: the middle tile runs alone
+    const int qt = single >= 0 ? n_qt - 1 - single : (pass == 0 ? n_qt - 1 - pt : pt);
+    // odd n_qt: the middle tile runs alone
+    if (pass == 1 && (single >= 0 || qt == n_qt - 1 - pt)) break;
     const int q0 = qt * kBwdOwn, wq0 = q0 + wave * 32, myq = wq0 + j;
     const int qrow = min(myq, p.Sq - 1);
     u32x4 qf[NKS], df[NKS];
@@ -630,9 +681,8 @@ void fa_bwd_dkdv_fused_kernel(BwdParams p) {
   // causal mask, the first) first: their step counts add up to the same total
   // for every pair, so all workgroups carry equal work and the launch ends
   // without a tail of long tiles that started late.
-  const int n_pair = (n_kt + 1) / 2;
-  int pt, bhk;  // tile pair, (batch, K/V head)
-  grid_tile(p.B * p.H_kv, n_pair, pt, bhk);
+  int pt, bhk, single;  // tile pair, (batch, K/V head), single tile rank
+  grid_pair(p.B * p.H_kv, n_kt, DS, pt, bhk, single);
   // (scalar: the lse / Dvec DMA descriptors are built from them)
   const int b = __builtin_amdgcn_readfirstlane(bhk / p.H_kv);
   const int hk = __builtin_amdgcn_readfirstlane(bhk % p.H_kv);
@@ -670,8 +720,9 @@ void fa_bwd_dkdv_fused_kernel(BwdParams p) {
   const u32 lbase = lds_addr(lds);
 
   for (int pass = 0; pass < 2; ++pass) {
-    const int kt = pass == 0 ? pt : n_kt - 1 - pt;
-    if (pass == 1 && kt == pt) break;  // odd n_kt: the middle tile runs alone
+    const int kt = single >= 0 ? single : (pass == 0 ? pt : n_kt - 1 - pt);
+    // odd n_kt: the middle tile runs alone
+    if (pass == 1 && (single >= 0 || kt == pt)) break;
     const int k0 = kt * kBwdOwn, wk0 = k0 + wave * 32, mykey = wk0 + j;
     const int krow = min(mykey, p.Sk - 1);
     // Visible query rows of this key, cut at Sq (rows past it are clamped
@@ -927,9 +978,8 @@ void fa_bwd_dq_ds_kernel(BwdParams p) {
 
   const int n_qt = (p.Sq + OWN - 1) / OWN;
   // Query tiles n_qt - 1 - pt and pt, as fa_bwd_dq_kernel.
-  const int n_pair = (n_qt + 1) / 2;
-  int pt, bh;
-  grid_tile(p.B * p.H, n_pair, pt, bh);
+  int pt, bh, single;
+  grid_pair(p.B * p.H, n_qt, true, pt, bh, single);
   const int b = bh / p.H, h = bh % p.H;
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g = lane >> 5;
@@ -955,8 +1005,9 @@ void fa_bwd_dq_ds_kernel(BwdParams p) {
   }
 
   for (int pass = 0; pass < 2; ++pass) {
-    const int qt = pass == 0 ? n_qt - 1 - pt : pt;
-    if (pass == 1 && qt == n_qt - 1 - pt) break;  // odd n_qt: the middle tile runs alone
+    const int qt = single >= 0 ? n_qt - 1 - single : (pass == 0 ? n_qt - 1 - pt : pt);
+    // odd n_qt: the middle tile runs alone
+    if (pass == 1 && (single >= 0 || qt == n_qt - 1 - pt)) break;
     const int q0 = qt * OWN, wq0 = q0 + wave * 32 * QB;
     const int qb0 = wq0 / 32;  // the wave's first query block
     const int q_last = min(q0 + OWN, p.Sq) - 1;
@@ -1091,19 +1142,19 @@ hipError_t launch_bwd(const BwdParams& p, hipStream_t st) {
       hipLaunchKernelGGL((fa_bwd_dvec_kernel<D, BF16>), dim3((rows + 15) / 16), dim3(256), 0, st,
                          p);
       hipLaunchKernelGGL((fa_bwd_dkdv_fused_kernel<BF16, DROP, true>),
-                         dim3(p.B * p.H_kv * ((n_kt + 1) / 2)), dim3(256), 0, st, p);
+                         dim3(bwd_pair_grid(p.B * p.H_kv, n_kt, true)), dim3(256), 0, st, p);
       const int n_qt2 = (p.Sq + kBwdOwn * kDqDsQB - 1) / (kBwdOwn * kDqDsQB);
       hipLaunchKernelGGL((fa_bwd_dq_ds_kernel<D, BF16, kDqDsQB>),
-                         dim3(p.B * p.H * ((n_qt2 + 1) / 2)), dim3(256), 0, st, p);
+                         dim3(bwd_pair_grid(p.B * p.H, n_qt2, true)), dim3(256), 0, st, p);
       return hipGetLastError();
     }
   }
   // dQ (which also writes Dvec) before dK / dV, which reads it.
-  hipLaunchKernelGGL((fa_bwd_dq_kernel<D, BF16, DROP>), dim3(p.B * p.H * ((n_qt + 1) / 2)),
-                     dim3(256), 0, st, p);
+  hipLaunchKernelGGL((fa_bwd_dq_kernel<D, BF16, DROP>),
+                     dim3(bwd_pair_grid(p.B * p.H, n_qt, false)), dim3(256), 0, st, p);
   const dim3 grid_kv(p.B * p.H_kv * n_kt);
   if constexpr (D == 128) {
-    const dim3 grid_pairs(p.B * p.H_kv * ((n_kt + 1) / 2));
+    const dim3 grid_pairs(bwd_pair_grid(p.B * p.H_kv, n_kt, false));
     hipLaunchKernelGGL((fa_bwd_dkdv_fused_kernel<BF16, DROP>), grid_pairs, dim3(256), 0, st, p);
   } else {  // D = 64, and D = 256 (one wave per SIMD)
     hipLaunchKernelGGL((fa_bwd_dkdv_kernel<D, BF16, kBoth, DROP>), grid_kv, dim3(256), 0, st, p);

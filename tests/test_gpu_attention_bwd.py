@@ -259,6 +259,25 @@ def test_headline_shape_sampled_heads(device):
                     1 / math.sqrt(D), True, layout="BHSD")
 
 
+@pytest.mark.parametrize("stored", [False, True])
+def test_paired_tiles_single_tail(device, monkeypatch, stored):
+    # 136 (batch, head)s over the 8 XCDs (17 each) with 8 tiles of 128 rows.
+    # Stored dS: each XCD runs the dK/dV tile pairs of its first head, then the
+    # tiles of the other 16 one per workgroup; XCD x holds heads x, x + 8, ...,
+    # so the sample takes both kinds on several XCDs. Recomputing: pairs only.
+    monkeypatch.setattr(_launch, "BWD_STORED_DS", stored)
+    B, H, S, D = 1, 136, 1024, 128
+    q, k, v, d = (rnd((B, H, S, D), 70 + i, torch.bfloat16) for i in range(4))
+    fn = lambda q, k, v: flash_attention(q, k, v, causal=True, layout="BHSD")
+    out, dq, dk, dv = run_grads(fn, device, q, k, v, d)
+    for x in (dq, dk, dv):
+        assert bool(torch.isfinite(x).all())
+    for h in (0, 3, 8, 13, 64, 101, 128, 135):
+        sl = lambda x: x[:, h:h + 1]
+        check_grads((sl(dq), sl(dk), sl(dv)), sl(q), sl(k), sl(v), sl(d), torch.bfloat16,
+                    1 / math.sqrt(D), True, layout="BHSD")
+
+
 def test_forward_matches_no_grad_path(device):
     # the differentiable forward (row log-sum-exp kept) returns the same output
     q, k, v = (rnd((2, 333, 4, 128), 70 + i, torch.bfloat16).to(device) for i in range(3))
