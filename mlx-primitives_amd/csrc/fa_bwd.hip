@@ -186,6 +186,13 @@ __device__ __forceinline__ void store_rows_lds(unsigned char* eb, uint16_t* base
 #ifndef MPX_BWD_TAIL_SLOTS
 #define MPX_BWD_TAIL_SLOTS 64
 #endif
+// The same tail for the recomputing dQ / dK/dV launches (off: see bwd_tail_heads).
+#ifndef MPX_BWD_TAIL_DQ
+#define MPX_BWD_TAIL_DQ 0
+#endif
+#ifndef MPX_BWD_TAIL_DKDV
+#define MPX_BWD_TAIL_DKDV 0
+#endif
 // Paired launches over n_heads x n_tiles tiles (n_pair = ceil(n_tiles / 2)
 // workgroups per head) with n_heads a multiple of the 8 XCDs: the number of
 // heads per XCD whose tiles run one per workgroup at the end of the XCD's
@@ -273,7 +280,7 @@ void fa_bwd_dq_kernel(BwdParams p) {
   // causal mask, the last) first: their key-tile counts add up to the same
   // total for every pair, so all workgroups carry equal work.
   int pt, bh, single;
-  grid_pair(p.B * p.H, n_qt, false, pt, bh, single);
+  grid_pair(p.B * p.H, n_qt, MPX_BWD_TAIL_DQ, pt, bh, single);
   const int b = bh / p.H, h = bh % p.H;
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int j = lane & 31, g = lane >> 5;
@@ -682,7 +689,7 @@ void fa_bwd_dkdv_fused_kernel(BwdParams p) {
   // for every pair, so all workgroups carry equal work and the launch ends
   // without a tail of long tiles that started late.
   int pt, bhk, single;  // tile pair, (batch, K/V head), single tile rank
-  grid_pair(p.B * p.H_kv, n_kt, DS, pt, bhk, single);
+  grid_pair(p.B * p.H_kv, n_kt, DS || MPX_BWD_TAIL_DKDV, pt, bhk, single);
   // (scalar: the lse / Dvec DMA descriptors are built from them)
   const int b = __builtin_amdgcn_readfirstlane(bhk / p.H_kv);
   const int hk = __builtin_amdgcn_readfirstlane(bhk % p.H_kv);
@@ -1151,10 +1158,10 @@ hipError_t launch_bwd(const BwdParams& p, hipStream_t st) {
   }
   // dQ (which also writes Dvec) before dK / dV, which reads it.
   hipLaunchKernelGGL((fa_bwd_dq_kernel<D, BF16, DROP>),
-                     dim3(bwd_pair_grid(p.B * p.H, n_qt, false)), dim3(256), 0, st, p);
+                     dim3(bwd_pair_grid(p.B * p.H, n_qt, MPX_BWD_TAIL_DQ)), dim3(256), 0, st, p);
   const dim3 grid_kv(p.B * p.H_kv * n_kt);
   if constexpr (D == 128) {
-    const dim3 grid_pairs(bwd_pair_grid(p.B * p.H_kv, n_kt, false));
+    const dim3 grid_pairs(bwd_pair_grid(p.B * p.H_kv, n_kt, MPX_BWD_TAIL_DKDV));
     hipLaunchKernelGGL((fa_bwd_dkdv_fused_kernel<BF16, DROP>), grid_pairs, dim3(256), 0, st, p);
   } else {  // D = 64, and D = 256 (one wave per SIMD)
     hipLaunchKernelGGL((fa_bwd_dkdv_kernel<D, BF16, kBoth, DROP>), grid_kv, dim3(256), 0, st, p);
