@@ -90,8 +90,9 @@ Plan make_plan(int B, int H, int Sq, int Sk, int D, int causal, int window_left,
   // One-workgroup-per-CU paired launches end with single q-tiles, longest
   // first, in place of the last ~round of pairs on each XCD (kTailSlots
   // pairs' worth of (batch, head)s): the XCD's CUs then finish within about
-  // one short q-tile of each other. (Measured: config 2 +2.2% with 32 slots,
-  // less with 16 or 64; the head-dim-256 kernel, 128-row q-tiles, -1.3%.)
+  // one short q-tile of each other. (Measured at B=4, H=32, S=4096, D=128
+  // causal bf16: +2.2% with 32 slots, less with 16 or 64; the head-dim-256
+  // kernel, 128-row q-tiles, -1.3%.)
   pl.tail_bh = 0;
   if (pl.paired && kTailSlots > 0 && (long)B * H % kNumXcds == 0 && D <= 128 &&
       target_workgroups(D, dtype) == kNumCUs) {
